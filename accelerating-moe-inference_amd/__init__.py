@@ -1,0 +1,264 @@
+"""Python binding of the gfx950 MoE library (libmoe_amd.so) over its C ABI.
+
+The functions mirror the entry points declared in include/moe_amd.h and the
+reference operators they replace (tensor_ops::matmul_transposed,
+PhiMoE::route, PhiMoE::forward ...).  Arguments are torch tensors on the GPU;
+work is enqueued on torch's current stream.  There is no fallback: if the
+HIP library is missing or fails to load, every call raises.
+
+Load it by path (the directory name is not a Python identifier):
+
+    spec = importlib.util.spec_from_file_location(
+        "moe_amd", "accelerating-moe-inference_amd/__init__.py")
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmoe_amd.so")
+
+OK, ERR_INVALID, ERR_RUNTIME, ERR_UNSUPPORTED = 0, 1, 2, 3
+CONTRACT_NONE, CONTRACT_FMA = 0, 1
+ROUTER_PHI_QUANT, ROUTER_SOFTMAX_TOPK = 0, 1
+ACT_SWIGLU, ACT_SILU_MLP = 0, 1
+
+EXPORTS = (
+    "moe_ctx_create", "moe_ctx_destroy", "moe_ctx_reserve", "moe_ctx_set_timing",
+    "moe_ctx_kernel_times", "moe_ctx_reset_timing", "moe_last_error",
+    "moe_version", "moe_sgemm_nt", "moe_sgemm_nn", "moe_gate_logits",
+    "moe_route", "moe_permute", "moe_expert_ffn_grouped", "moe_combine",
+    "moe_layer_forward",
+)
+
+
+class MoeInvalidArgument(ValueError):
+    """MOE_ERR_INVALID (std::invalid_argument in the C++ drop-in)."""
+
+
+class MoeRuntimeError(RuntimeError):
+    """MOE_ERR_RUNTIME / MOE_ERR_UNSUPPORTED (std::runtime_error)."""
+
+
+class LayerDesc(ctypes.Structure):
+    _fields_ = [("T", ctypes.c_int64), ("d", ctypes.c_int64),
+                ("E", ctypes.c_int64), ("k", ctypes.c_int64),
+                ("d_ff", ctypes.c_int64), ("act", ctypes.c_int32),
+                ("router", ctypes.c_int32), ("quantum", ctypes.c_float),
+                ("tie_eps", ctypes.c_float), ("contract", ctypes.c_int32)]
+
+
+class LayerWeights(ctypes.Structure):
+    _fields_ = [("gate_w", ctypes.c_void_p), ("expert_bias", ctypes.c_void_p),
+                ("w1", ctypes.c_void_p), ("w3", ctypes.c_void_p),
+                ("w2", ctypes.c_void_p)]
+
+
+_lib = None
+
+
+def load_library(path: str = LIB_PATH):
+    """Loads libmoe_amd.so; raises if it was not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise RuntimeError(
+            f"{path} is missing: build it with "
+            "`python accelerating-moe-inference_amd/build.py`")
+    L = ctypes.CDLL(path)
+    P, I64, I = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    F = ctypes.c_float
+    sig = {
+        "moe_ctx_create": ([I, ctypes.POINTER(P)], I),
+        "moe_ctx_destroy": ([P], I),
+        "moe_ctx_reserve": ([P, ctypes.POINTER(LayerDesc)], I),
+        "moe_ctx_set_timing": ([P, I], I),
+        "moe_ctx_kernel_times": ([P, ctypes.POINTER(ctypes.c_char_p),
+                                  ctypes.POINTER(ctypes.c_double),
+                                  ctypes.POINTER(ctypes.c_int64), I], I),
+        "moe_ctx_reset_timing": ([P], I),
+        "moe_last_error": ([], ctypes.c_char_p),
+        "moe_version": ([], ctypes.c_char_p),
+        "moe_sgemm_nt": ([P, P, P, P, P, I64, I64, I64, P], I),
+        "moe_sgemm_nn": ([P, P, P, P, P, I64, I64, I64, P], I),
+        "moe_gate_logits": ([P, P, P, P, I64, I64, I64, I, P], I),
+        "moe_route": ([P, P, P, I64, I64, I64, I, F, F, P, P, P], I),
+        "moe_permute": ([P, P, I64, I64, I64, P, P, P, P], I),
+        "moe_expert_ffn_grouped": ([P, P, P, P, P, P, P, I, I64, I64, I64,
+                                    I64, I64, P, P, P], I),
+        "moe_combine": ([P, P, P, P, P, P, P, I64, I64, I64, I, P], I),
+        "moe_layer_forward": ([P, ctypes.POINTER(LayerDesc),
+                               ctypes.POINTER(LayerWeights), P, P, P, P, P], I),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(L, name)
+        fn.argtypes = args
+        fn.restype = res
+    _lib = L
+    return L
+
+
+def _check(rc: int) -> None:
+    if rc == OK:
+        return
+    msg = _lib.moe_last_error().decode()
+    if rc == ERR_INVALID:
+        raise MoeInvalidArgument(msg)
+    raise MoeRuntimeError(f"[{rc}] {msg}")
+
+
+def _ptr(t):
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise MoeInvalidArgument("tensor must be on the GPU")
+    if not t.is_contiguous():
+        raise MoeInvalidArgument("tensor must be contiguous")
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _f32(t, name):
+    import torch
+    if t is not None and t.dtype != torch.float32:
+        raise MoeInvalidArgument(f"{name} must be float32")
+    return _ptr(t)
+
+
+def _i32(t, name):
+    import torch
+    if t is not None and t.dtype != torch.int32:
+        raise MoeInvalidArgument(f"{name} must be int32")
+    return _ptr(t)
+
+
+def _stream():
+    import torch
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+class Context:
+    """A moe_ctx bound to one device (workspace + optional kernel timing)."""
+
+    def __init__(self, device: int = 0):
+        L = load_library()
+        h = ctypes.c_void_p()
+        _check(L.moe_ctx_create(device, ctypes.byref(h)))
+        self.handle = h
+        self.device = device
+
+    def close(self):
+        if self.handle:
+            _check(_lib.moe_ctx_destroy(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ---- timing
+    def set_timing(self, on: bool):
+        _check(_lib.moe_ctx_set_timing(self.handle, 1 if on else 0))
+
+    def reset_timing(self):
+        _check(_lib.moe_ctx_reset_timing(self.handle))
+
+    def kernel_times(self):
+        """{kernel name: (total ms, launches)} since the last reset."""
+        cap = 64
+        names = (ctypes.c_char_p * cap)()
+        ms = (ctypes.c_double * cap)()
+        n = (ctypes.c_int64 * cap)()
+        cnt = _lib.moe_ctx_kernel_times(self.handle, names, ms, n, cap)
+        if cnt < 0:
+            _check(-cnt)
+        return {names[i].decode(): (ms[i], n[i]) for i in range(min(cnt, cap))}
+
+    def reserve(self, desc: LayerDesc):
+        _check(_lib.moe_ctx_reserve(self.handle, ctypes.byref(desc)))
+
+    # ---- operators
+    def sgemm_nt(self, A, B, C, bias=None):
+        M, K = A.shape
+        N = B.shape[0]
+        _check(_lib.moe_sgemm_nt(self.handle, _f32(A, "A"), _f32(B, "B"),
+                                 _f32(bias, "bias"), _f32(C, "C"), M, N, K,
+                                 _stream()))
+        return C
+
+    def sgemm_nn(self, A, B, C, bias=None):
+        M, K = A.shape
+        N = B.shape[1]
+        _check(_lib.moe_sgemm_nn(self.handle, _f32(A, "A"), _f32(B, "B"),
+                                 _f32(bias, "bias"), _f32(C, "C"), M, N, K,
+                                 _stream()))
+        return C
+
+    def gate_logits(self, x, gate_w, logits, contract=CONTRACT_FMA):
+        T, d = x.shape
+        E = gate_w.shape[0]
+        _check(_lib.moe_gate_logits(self.handle, _f32(x, "x"),
+                                    _f32(gate_w, "gate_w"),
+                                    _f32(logits, "logits"), T, d, E, contract,
+                                    _stream()))
+        return logits
+
+    def route(self, logits, k, topk_idx, topk_w, mode=ROUTER_PHI_QUANT,
+              quantum=1e-3, tie_eps=2e-2, expert_bias=None):
+        T, E = logits.shape
+        _check(_lib.moe_route(self.handle, _f32(logits, "logits"),
+                              _f32(expert_bias, "expert_bias"), T, E, k, mode,
+                              quantum, tie_eps, _i32(topk_idx, "topk_idx"),
+                              _f32(topk_w, "topk_w"), _stream()))
+        return topk_idx, topk_w
+
+    def permute(self, topk_idx, E, offsets, perm, inv):
+        T, k = topk_idx.shape
+        _check(_lib.moe_permute(self.handle, _i32(topk_idx, "topk_idx"), T, k,
+                                E, _i32(offsets, "offsets"), _i32(perm, "perm"),
+                                _i32(inv, "inv"), _stream()))
+        return offsets, perm, inv
+
+    def expert_ffn_grouped(self, x, perm, offsets, w1, w3, w2, k, h, out_rows,
+                           act=ACT_SWIGLU):
+        T, d = x.shape
+        E, d_ff, _ = w1.shape
+        _check(_lib.moe_expert_ffn_grouped(
+            self.handle, _f32(x, "x"), _i32(perm, "perm"),
+            _i32(offsets, "offsets"), _f32(w1, "w1"), _f32(w3, "w3"),
+            _f32(w2, "w2"), act, T, k, d, d_ff, E, _f32(h, "h"),
+            _f32(out_rows, "out_rows"), _stream()))
+        return out_rows
+
+    def combine(self, out_rows, topk_idx, topk_w, inv, y, resid=None,
+                contract=CONTRACT_FMA):
+        T, k = topk_idx.shape
+        d = y.shape[1]
+        _check(_lib.moe_combine(self.handle, _f32(out_rows, "out_rows"),
+                                _i32(topk_idx, "topk_idx"),
+                                _f32(topk_w, "topk_w"), _i32(inv, "inv"),
+                                _f32(resid, "resid"), _f32(y, "y"), T, k, d,
+                                contract, _stream()))
+        return y
+
+    def layer_forward(self, desc: LayerDesc, weights: dict, x, y,
+                      topk_idx=None, topk_w=None):
+        W = LayerWeights(
+            gate_w=_f32(weights["gate_w"], "gate_w"),
+            expert_bias=_f32(weights.get("expert_bias"), "expert_bias"),
+            w1=_f32(weights["w1"], "w1"), w3=_f32(weights.get("w3"), "w3"),
+            w2=_f32(weights["w2"], "w2"))
+        _check(_lib.moe_layer_forward(self.handle, ctypes.byref(desc),
+                                      ctypes.byref(W), _f32(x, "x"),
+                                      _f32(y, "y"), _i32(topk_idx, "topk_idx"),
+                                      _f32(topk_w, "topk_w"), _stream()))
+        return y
+
+
+def make_desc(T, d, E, k, d_ff, act=ACT_SWIGLU, router=ROUTER_PHI_QUANT,
+              quantum=1e-3, tie_eps=2e-2, contract=CONTRACT_FMA) -> LayerDesc:
+    return LayerDesc(T=T, d=d, E=E, k=k, d_ff=d_ff, act=act, router=router,
+                     quantum=quantum, tie_eps=tie_eps, contract=contract)

@@ -1,0 +1,528 @@
+// The C ABI (include/moe_amd.h): argument checks, the grow-only workspace,
+// kernel timing, and the orchestration of the MoE layer forward.
+#include "common.hpp"
+
+#include <algorithm>
+#include <climits>
+#include <cstring>
+
+namespace {
+
+thread_local std::string g_last_error;
+
+template <class F>
+int guarded(F&& f) {
+    try {
+        f();
+        return MOE_OK;
+    } catch (const moe::InvalidArg& e) {
+        g_last_error = e.what();
+        return MOE_ERR_INVALID;
+    } catch (const moe::Unsupported& e) {
+        g_last_error = e.what();
+        return MOE_ERR_UNSUPPORTED;
+    } catch (const std::exception& e) {
+        g_last_error = e.what();
+        return MOE_ERR_RUNTIME;
+    } catch (...) {
+        g_last_error = "unknown error";
+        return MOE_ERR_RUNTIME;
+    }
+}
+
+hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Makes the context's device current for the duration of a call.
+struct DeviceScope {
+    int prev = -1, want;
+    explicit DeviceScope(int d) : want(d) {
+        moe::hip_check(hipGetDevice(&prev), "hipGetDevice");
+        if (prev != want) moe::hip_check(hipSetDevice(want), "hipSetDevice");
+    }
+    ~DeviceScope() {
+        if (prev >= 0 && prev != want) (void)hipSetDevice(prev);
+    }
+};
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Carves typed sub-buffers out of one allocation, 256-byte aligned.
+struct Carve {
+    char* base;
+    size_t off = 0;
+    explicit Carve(void* b) : base(static_cast<char*>(b)) {}
+    template <class T>
+    T* take(int64_t n) {
+        off = (off + 255) & ~size_t(255);
+        T* p = reinterpret_cast<T*>(base + off);
+        off += static_cast<size_t>(n > 0 ? n : 1) * sizeof(T);
+        return p;
+    }
+};
+
+void check_ctx(moe_ctx* ctx) { moe::require(ctx != nullptr, "null moe_ctx"); }
+
+void check_dims(int64_t a, const char* what) {
+    moe::require(a >= 0, std::string(what) + " must be >= 0");
+    moe::require(a <= INT32_MAX, std::string(what) + " exceeds int32 range");
+}
+
+void check_ptr(const void* p, const char* what) {
+    moe::require(p != nullptr, std::string("null pointer: ") + what);
+}
+
+void check_routing(int64_t T, int64_t E, int64_t k) {
+    check_dims(T, "T");
+    moe::require(E >= 1 && E <= moe::kMaxExperts, "E must be in [1, 1024]");
+    moe::require(k >= 1 && k <= E && k <= moe::kMaxTopK, "k must be in [1, min(E, 32)]");
+    moe::require(T * k <= INT32_MAX, "T*k exceeds int32 range");
+}
+
+// ---- dense GEMM
+void sgemm(moe_ctx* ctx, bool nn, const float* A, const float* B,
+           const float* bias, float* C, int64_t M, int64_t N, int64_t K,
+           void* stream) {
+    check_ctx(ctx);
+    check_dims(M, "M");
+    check_dims(N, "N");
+    check_dims(K, "K");
+    if (M == 0 || N == 0) return;
+    check_ptr(C, "C");
+    if (K > 0) {
+        check_ptr(A, "A");
+        check_ptr(B, "B");
+    }
+    const int64_t mt = moe::ceil_div(M, moe::kGemmBM), ntl = moe::ceil_div(N, moe::kGemmBN);
+    moe::require(mt * ntl <= INT32_MAX, "GEMM grid too large");
+    DeviceScope dev(ctx->device);
+    moe::GemmArgs a{};
+    a.A = A;
+    a.lda = K;
+    a.B0 = B;
+    a.B1 = B;
+    a.ldb = nn ? N : K;
+    a.bias = bias;
+    a.C = C;
+    a.ldc = N;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.m_tiles = static_cast<int32_t>(mt);
+    a.n_tiles = static_cast<int32_t>(ntl);
+    const bool vec = (K % 4 == 0) && aligned16(A) && (nn || aligned16(B));
+    // K == 0 leaves the kernel with no K step: C = bias (or 0) still gets written.
+    if (K == 0) {
+        a.A = C;  // any valid pointer; never read
+        a.B0 = a.B1 = C;
+    }
+    hipStream_t s = as_stream(stream);
+    ctx->launch(nn ? "sgemm_nn" : "sgemm_nt", s,
+                [&] { moe::launch_gemm(a, nn, false, moe::EPI_BIAS, vec, s); });
+}
+
+// ---- expert FFN (the part shared by moe_expert_ffn_grouped and the layer)
+void expert_ffn(moe_ctx* ctx, const float* x, const int32_t* perm,
+                const int32_t* offsets, const int32_t* tile_start,
+                const float* w1, const float* w3, const float* w2, int act,
+                int64_t T, int64_t k, int64_t d, int64_t d_ff, int64_t E,
+                float* h, float* out_rows, hipStream_t s) {
+    const int64_t pairs = T * k;
+    if (pairs == 0 || d == 0) return;
+    const int64_t m_tiles = std::min<int64_t>(moe::ceil_div(pairs, moe::kGemmBM) + E, pairs);
+    const bool swiglu = act == MOE_ACT_SWIGLU;
+    if (d_ff > 0) {
+        moe::GemmArgs a{};
+        a.A = x;
+        a.lda = d;
+        a.gather = perm;
+        a.gather_rows = T;
+        a.B0 = w1;
+        a.B1 = swiglu ? w3 : w1;
+        a.ldb = d;
+        a.b_expert_stride = d_ff * d;
+        a.C = h;
+        a.ldc = d_ff;
+        a.N = d_ff;
+        a.K = d;
+        a.offsets = offsets;
+        a.tile_start = tile_start;
+        a.rows_limit = pairs;
+        a.E = static_cast<int32_t>(E);
+        a.m_tiles = static_cast<int32_t>(m_tiles);
+        a.n_tiles = static_cast<int32_t>(moe::ceil_div(d_ff, moe::kGemmBN));
+        moe::require(int64_t(a.m_tiles) * a.n_tiles <= INT32_MAX, "w13 grid too large");
+        const bool vec = d % 4 == 0 && aligned16(x) && aligned16(w1) && (!swiglu || aligned16(w3));
+        ctx->launch(swiglu ? "expert_w13_swiglu" : "expert_w1_silu", s, [&] {
+            moe::launch_gemm(a, false, true, swiglu ? moe::EPI_SWIGLU : moe::EPI_SILU, vec, s);
+        });
+    }
+    moe::GemmArgs b{};
+    b.A = d_ff > 0 ? h : out_rows;
+    b.lda = d_ff;
+    b.B0 = d_ff > 0 ? w2 : out_rows;
+    b.B1 = b.B0;
+    b.ldb = d_ff;
+    b.b_expert_stride = d * d_ff;
+    b.C = out_rows;
+    b.ldc = d;
+    b.N = d;
+    b.K = d_ff;
+    b.offsets = offsets;
+    b.tile_start = tile_start;
+    b.rows_limit = pairs;
+    b.E = static_cast<int32_t>(E);
+    b.m_tiles = static_cast<int32_t>(m_tiles);
+    b.n_tiles = static_cast<int32_t>(moe::ceil_div(d, moe::kGemmBN));
+    moe::require(int64_t(b.m_tiles) * b.n_tiles <= INT32_MAX, "w2 grid too large");
+    const bool vec = d_ff % 4 == 0 && aligned16(h) && aligned16(w2);
+    ctx->launch("expert_w2", s, [&] { moe::launch_gemm(b, false, true, moe::EPI_STORE, vec, s); });
+}
+
+void check_desc(const moe_layer_desc* desc) {
+    check_ptr(desc, "desc");
+    check_routing(desc->T, desc->E, desc->k);
+    check_dims(desc->d, "d");
+    check_dims(desc->d_ff, "d_ff");
+    moe::require(desc->act == MOE_ACT_SWIGLU || desc->act == MOE_ACT_SILU_MLP, "unknown act");
+    moe::require(desc->router == MOE_ROUTER_PHI_QUANT || desc->router == MOE_ROUTER_SOFTMAX_TOPK,
+                 "unknown router mode");
+    moe::require(desc->contract == MOE_CONTRACT_NONE || desc->contract == MOE_CONTRACT_FMA,
+                 "unknown contract mode");
+}
+
+// Workspace layout of moe_layer_forward; with base == nullptr it only sizes.
+struct LayerWs {
+    float* logits;
+    int32_t* idx;
+    float* w;
+    int32_t* counts;
+    int32_t* offsets;
+    int32_t* tile_start;
+    int32_t* perm;
+    int32_t* inv;
+    float* h;
+    float* out_rows;
+    size_t bytes;
+};
+
+LayerWs carve_layer(void* base, const moe_layer_desc& d) {
+    Carve c(base);
+    LayerWs w{};
+    const int64_t pairs = d.T * d.k;
+    const int64_t nb = moe::ceil_div(d.T, moe::kPermTokens);
+    w.logits = c.take<float>(d.T * d.E);
+    w.idx = c.take<int32_t>(pairs);
+    w.w = c.take<float>(pairs);
+    w.counts = c.take<int32_t>(d.E * nb);
+    w.offsets = c.take<int32_t>(d.E + 1);
+    w.tile_start = c.take<int32_t>(d.E + 1);
+    w.perm = c.take<int32_t>(pairs);
+    w.inv = c.take<int32_t>(pairs);
+    w.h = c.take<float>(pairs * d.d_ff);
+    w.out_rows = c.take<float>(pairs * d.d);
+    w.bytes = c.off + 256;
+    return w;
+}
+
+}  // namespace
+
+void* moe_ctx::workspace(size_t bytes) {
+    if (bytes > ws_bytes) {
+        if (ws != nullptr) {
+            // the old buffer may still be read by queued kernels
+            moe::hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+            moe::hip_check(hipFree(ws), "hipFree workspace");
+            ws = nullptr;
+            ws_bytes = 0;
+        }
+        const size_t grow = std::max(bytes, ws_bytes + ws_bytes / 2);
+        moe::hip_check(hipMalloc(&ws, grow), "hipMalloc workspace");
+        ws_bytes = grow;
+    }
+    return ws;
+}
+
+void moe_ctx::collect() {
+    for (auto& p : pending) {
+        moe::hip_check(hipEventSynchronize(p.stop), "hipEventSynchronize");
+        float ms = 0.0f;
+        moe::hip_check(hipEventElapsedTime(&ms, p.start, p.stop), "hipEventElapsedTime");
+        auto& slot = totals[p.name];
+        slot.first += ms;
+        slot.second += 1;
+        event_pool.emplace_back(p.start, p.stop);
+    }
+    pending.clear();
+}
+
+extern "C" {
+
+const char* moe_last_error(void) { return g_last_error.c_str(); }
+
+const char* moe_version(void) { return "moe_amd 0.1 gfx950"; }
+
+int moe_ctx_create(int device, moe_ctx** out) {
+    return guarded([&] {
+        check_ptr(out, "out");
+        *out = nullptr;
+        int n = 0;
+        moe::hip_check(hipGetDeviceCount(&n), "hipGetDeviceCount");
+        moe::require(device >= 0 && device < n, "device ordinal out of range");
+        hipDeviceProp_t prop;
+        moe::hip_check(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+        if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+            throw moe::Unsupported(std::string("kernels are built for gfx950, device is ") +
+                                   prop.gcnArchName);
+        auto* c = new moe_ctx();
+        c->device = device;
+        *out = c;
+    });
+}
+
+int moe_ctx_destroy(moe_ctx* ctx) {
+    return guarded([&] {
+        if (ctx == nullptr) return;
+        DeviceScope dev(ctx->device);
+        moe::hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+        for (auto& p : ctx->pending) ctx->event_pool.emplace_back(p.start, p.stop);
+        for (auto& e : ctx->event_pool) {
+            (void)hipEventDestroy(e.first);
+            (void)hipEventDestroy(e.second);
+        }
+        if (ctx->ws != nullptr) (void)hipFree(ctx->ws);
+        delete ctx;
+    });
+}
+
+int moe_ctx_reserve(moe_ctx* ctx, const moe_layer_desc* desc) {
+    return guarded([&] {
+        check_ctx(ctx);
+        check_desc(desc);
+        DeviceScope dev(ctx->device);
+        ctx->workspace(carve_layer(nullptr, *desc).bytes);
+    });
+}
+
+int moe_ctx_set_timing(moe_ctx* ctx, int enabled) {
+    return guarded([&] {
+        check_ctx(ctx);
+        ctx->timing = enabled != 0;
+    });
+}
+
+int moe_ctx_reset_timing(moe_ctx* ctx) {
+    return guarded([&] {
+        check_ctx(ctx);
+        DeviceScope dev(ctx->device);
+        ctx->collect();
+        ctx->totals.clear();
+    });
+}
+
+int moe_ctx_kernel_times(moe_ctx* ctx, const char** names, double* total_ms,
+                         int64_t* launches, int cap) {
+    int count = 0;
+    const int rc = guarded([&] {
+        check_ctx(ctx);
+        DeviceScope dev(ctx->device);
+        ctx->collect();
+        ctx->name_store.clear();
+        for (auto& kv : ctx->totals) ctx->name_store.push_back(kv.first);
+        int i = 0;
+        for (auto& kv : ctx->totals) {
+            if (i < cap) {
+                if (names) names[i] = ctx->name_store[i].c_str();
+                if (total_ms) total_ms[i] = kv.second.first;
+                if (launches) launches[i] = kv.second.second;
+            }
+            ++i;
+        }
+        count = i;
+    });
+    return rc == MOE_OK ? count : -rc;
+}
+
+int moe_sgemm_nt(moe_ctx* ctx, const float* A, const float* B, const float* bias,
+                 float* C, int64_t M, int64_t N, int64_t K, void* stream) {
+    return guarded([&] { sgemm(ctx, false, A, B, bias, C, M, N, K, stream); });
+}
+
+int moe_sgemm_nn(moe_ctx* ctx, const float* A, const float* B, const float* bias,
+                 float* C, int64_t M, int64_t N, int64_t K, void* stream) {
+    return guarded([&] { sgemm(ctx, true, A, B, bias, C, M, N, K, stream); });
+}
+
+int moe_gate_logits(moe_ctx* ctx, const float* x, const float* gate_w, float* logits,
+                    int64_t T, int64_t d, int64_t E, int contract, void* stream) {
+    return guarded([&] {
+        check_ctx(ctx);
+        check_dims(T, "T");
+        check_dims(d, "d");
+        moe::require(E >= 1 && E <= moe::kMaxExperts, "E must be in [1, 1024]");
+        moe::require(contract == MOE_CONTRACT_NONE || contract == MOE_CONTRACT_FMA,
+                     "unknown contract mode");
+        if (T == 0) return;
+        check_ptr(logits, "logits");
+        if (d > 0) {
+            check_ptr(x, "x");
+            check_ptr(gate_w, "gate_w");
+        }
+        DeviceScope dev(ctx->device);
+        hipStream_t s = as_stream(stream);
+        ctx->launch("gate_logits", s,
+                    [&] { moe::launch_gate_logits(x, gate_w, logits, T, d, E, contract, s); });
+    });
+}
+
+int moe_route(moe_ctx* ctx, const float* logits, const float* expert_bias, int64_t T,
+              int64_t E, int64_t k, int mode, float quantum, float tie_eps,
+              int32_t* topk_idx, float* topk_w, void* stream) {
+    return guarded([&] {
+        check_ctx(ctx);
+        check_routing(T, E, k);
+        moe::require(mode == MOE_ROUTER_PHI_QUANT || mode == MOE_ROUTER_SOFTMAX_TOPK,
+                     "unknown router mode");
+        if (T == 0) return;
+        check_ptr(logits, "logits");
+        check_ptr(topk_idx, "topk_idx");
+        check_ptr(topk_w, "topk_w");
+        DeviceScope dev(ctx->device);
+        hipStream_t s = as_stream(stream);
+        ctx->launch(mode == MOE_ROUTER_PHI_QUANT ? "route_phi" : "route_softmax", s, [&] {
+            moe::launch_route(logits, expert_bias, T, E, k, mode, quantum, tie_eps, topk_idx,
+                              topk_w, s);
+        });
+    });
+}
+
+int moe_permute(moe_ctx* ctx, const int32_t* topk_idx, int64_t T, int64_t k, int64_t E,
+                int32_t* expert_offsets, int32_t* perm, int32_t* inv, void* stream) {
+    return guarded([&] {
+        check_ctx(ctx);
+        check_routing(T, E, k);
+        check_ptr(expert_offsets, "expert_offsets");
+        if (T > 0) {
+            check_ptr(topk_idx, "topk_idx");
+            check_ptr(perm, "perm");
+            check_ptr(inv, "inv");
+        }
+        DeviceScope dev(ctx->device);
+        hipStream_t s = as_stream(stream);
+        const int64_t nb = moe::ceil_div(T, moe::kPermTokens);
+        auto* counts = static_cast<int32_t*>(ctx->workspace(static_cast<size_t>(E * nb + 1) * 4));
+        ctx->launch("perm_count", s, [&] { moe::launch_perm_count(topk_idx, T, k, E, counts, s); });
+        ctx->launch("perm_scan", s,
+                    [&] { moe::launch_perm_scan(counts, nb, E, expert_offsets, nullptr, s); });
+        ctx->launch("perm_place", s,
+                    [&] { moe::launch_perm_place(topk_idx, T, k, E, counts, perm, inv, s); });
+    });
+}
+
+int moe_expert_ffn_grouped(moe_ctx* ctx, const float* x, const int32_t* perm,
+                           const int32_t* expert_offsets, const float* w1, const float* w3,
+                           const float* w2, int act, int64_t T, int64_t k, int64_t d,
+                           int64_t d_ff, int64_t E, float* h, float* out_rows, void* stream) {
+    return guarded([&] {
+        check_ctx(ctx);
+        check_routing(T, E, k);
+        check_dims(d, "d");
+        check_dims(d_ff, "d_ff");
+        moe::require(act == MOE_ACT_SWIGLU || act == MOE_ACT_SILU_MLP, "unknown act");
+        if (T == 0 || d == 0) return;
+        check_ptr(x, "x");
+        check_ptr(perm, "perm");
+        check_ptr(expert_offsets, "expert_offsets");
+        check_ptr(out_rows, "out_rows");
+        if (d_ff > 0) {
+            check_ptr(w1, "w1");
+            check_ptr(w2, "w2");
+            check_ptr(h, "h");
+            if (act == MOE_ACT_SWIGLU) check_ptr(w3, "w3");
+        }
+        DeviceScope dev(ctx->device);
+        hipStream_t s = as_stream(stream);
+        auto* tile_start = static_cast<int32_t*>(ctx->workspace(static_cast<size_t>(E + 1) * 4));
+        ctx->launch("tile_start", s, [&] { moe::launch_tile_start(expert_offsets, E, tile_start, s); });
+        expert_ffn(ctx, x, perm, expert_offsets, tile_start, w1, w3, w2, act, T, k, d, d_ff, E, h,
+                   out_rows, s);
+    });
+}
+
+int moe_combine(moe_ctx* ctx, const float* out_rows, const int32_t* topk_idx,
+                const float* topk_w, const int32_t* inv, const float* resid, float* y,
+                int64_t T, int64_t k, int64_t d, int contract, void* stream) {
+    return guarded([&] {
+        check_ctx(ctx);
+        check_dims(T, "T");
+        check_dims(d, "d");
+        moe::require(k >= 1 && k <= moe::kMaxTopK, "k must be in [1, 32]");
+        moe::require(contract == MOE_CONTRACT_NONE || contract == MOE_CONTRACT_FMA,
+                     "unknown contract mode");
+        if (T == 0 || d == 0) return;
+        check_ptr(out_rows, "out_rows");
+        check_ptr(topk_idx, "topk_idx");
+        check_ptr(topk_w, "topk_w");
+        check_ptr(inv, "inv");
+        check_ptr(y, "y");
+        moe::require(d % 4 != 0 || (aligned16(out_rows) && aligned16(y) &&
+                                    (resid == nullptr || aligned16(resid))),
+                     "combine: rows of width d % 4 == 0 must be 16-byte aligned");
+        DeviceScope dev(ctx->device);
+        hipStream_t s = as_stream(stream);
+        ctx->launch("combine", s, [&] {
+            moe::launch_combine(out_rows, topk_idx, topk_w, inv, resid, y, T, k, d, T * k,
+                                contract, s);
+        });
+    });
+}
+
+int moe_layer_forward(moe_ctx* ctx, const moe_layer_desc* desc,
+                      const moe_layer_weights* weights, const float* x, float* y,
+                      int32_t* topk_idx_out, float* topk_w_out, void* stream) {
+    return guarded([&] {
+        check_ctx(ctx);
+        check_desc(desc);
+        check_ptr(weights, "weights");
+        const moe_layer_desc& D = *desc;
+        if (D.T == 0) return;
+        check_ptr(x, "x");
+        check_ptr(y, "y");
+        check_ptr(weights->gate_w, "gate_w");
+        if (D.d_ff > 0) {
+            check_ptr(weights->w1, "w1");
+            check_ptr(weights->w2, "w2");
+            if (D.act == MOE_ACT_SWIGLU) check_ptr(weights->w3, "w3");
+        }
+        moe::require(D.d % 4 != 0 || (aligned16(x) && aligned16(y)),
+                     "layer: x and y must be 16-byte aligned");
+        DeviceScope dev(ctx->device);
+        hipStream_t s = as_stream(stream);
+        LayerWs ws = carve_layer(ctx->workspace(carve_layer(nullptr, D).bytes), D);
+        int32_t* idx = topk_idx_out != nullptr ? topk_idx_out : ws.idx;
+        float* w = topk_w_out != nullptr ? topk_w_out : ws.w;
+        const int64_t nb = moe::ceil_div(D.T, moe::kPermTokens);
+
+        ctx->launch("gate_logits", s, [&] {
+            moe::launch_gate_logits(x, weights->gate_w, ws.logits, D.T, D.d, D.E, D.contract, s);
+        });
+        ctx->launch(D.router == MOE_ROUTER_PHI_QUANT ? "route_phi" : "route_softmax", s, [&] {
+            moe::launch_route(ws.logits, weights->expert_bias, D.T, D.E, D.k, D.router, D.quantum,
+                              D.tie_eps, idx, w, s);
+        });
+        ctx->launch("perm_count", s, [&] { moe::launch_perm_count(idx, D.T, D.k, D.E, ws.counts, s); });
+        ctx->launch("perm_scan", s, [&] {
+            moe::launch_perm_scan(ws.counts, nb, D.E, ws.offsets, ws.tile_start, s);
+        });
+        ctx->launch("perm_place", s, [&] {
+            moe::launch_perm_place(idx, D.T, D.k, D.E, ws.counts, ws.perm, ws.inv, s);
+        });
+        expert_ffn(ctx, x, ws.perm, ws.offsets, ws.tile_start, weights->w1, weights->w3,
+                   weights->w2, D.act, D.T, D.k, D.d, D.d_ff, D.E, ws.h, ws.out_rows, s);
+        ctx->launch("combine", s, [&] {
+            moe::launch_combine(ws.out_rows, idx, w, ws.inv, nullptr, y, D.T, D.k, D.d,
+                                D.T * D.k, D.contract, s);
+        });
+    });
+}
+
+}  // extern "C"

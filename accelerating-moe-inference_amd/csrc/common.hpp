@@ -1,0 +1,140 @@
+// Shared definitions of the gfx950 MoE library: the context, error
+// propagation to the C ABI, and the launch wrapper that can bracket every
+// kernel with HIP events.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <map>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/moe_amd.h"
+
+namespace moe {
+
+// A shape or argument the caller got wrong (MOE_ERR_INVALID).
+struct InvalidArg : std::invalid_argument {
+    using std::invalid_argument::invalid_argument;
+};
+// An argument the kernels do not support (MOE_ERR_UNSUPPORTED).
+struct Unsupported : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+inline void hip_check(hipError_t e, const char* what) {
+    if (e != hipSuccess)
+        throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+inline void require(bool ok, const std::string& what) {
+    if (!ok) throw InvalidArg(what);
+}
+
+constexpr int kNumXcd = 8;  // MI355X: 8 XCDs, workgroups dealt round-robin
+
+// GEMM tile constants shared by the host (grid sizing) and the kernels.
+constexpr int kGemmBM = 128;
+constexpr int kGemmBN = 128;
+constexpr int kGemmBK = 16;
+constexpr int kGemmThreads = 256;
+
+// Routing constants.
+constexpr int kPermTokens = 256;    // tokens per permutation block
+constexpr int kMaxExperts = 1024;   // bitmap in LDS: E * 4 * 8 B = 32 KiB
+constexpr int kMaxTopK = 32;
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Kernel launch arguments of the GEMM engine (one struct, passed by value).
+struct GemmArgs {
+    const float* A;          // [rows, K] row-major, leading dim lda
+    int64_t lda;
+    const int32_t* gather;   // grouped: packed row -> token of A, or nullptr
+    int64_t gather_rows;     // rows of A the gather may address (clamp)
+    const float* B0;         // NT: [N, K]; NN: [K, N]
+    const float* B1;         // second operand of the dual (SwiGLU) kernel
+    int64_t ldb;
+    int64_t b_expert_stride; // grouped: elements between experts' matrices
+    const float* bias;       // [N] or nullptr
+    float* C;                // output, leading dim ldc
+    int64_t ldc;
+    int64_t M, N, K;         // dense: M rows; grouped: per-expert N, K
+    const int32_t* offsets;  // grouped: expert_offsets[E+1]
+    const int32_t* tile_start; // grouped: first m-tile of each expert [E+1]
+    int64_t rows_limit;      // grouped: packed rows of A / C (T*k); bounds every tile
+    int32_t E;
+    int32_t m_tiles;         // m-tiles covered by the grid (upper bound)
+    int32_t n_tiles;
+};
+
+enum Epilogue : int { EPI_STORE = 0, EPI_BIAS = 1, EPI_SILU = 2, EPI_SWIGLU = 3 };
+
+// Launchers implemented in the .hip files.
+void launch_gemm(const GemmArgs& a, bool nn, bool grouped, int epi, bool vec,
+                 hipStream_t s);
+void launch_gate_logits(const float* x, const float* w, float* logits,
+                        int64_t T, int64_t d, int64_t E, int contract,
+                        hipStream_t s);
+void launch_route(const float* logits, const float* bias, int64_t T, int64_t E,
+                  int64_t k, int mode, float quantum, float tie_eps,
+                  int32_t* idx, float* w, hipStream_t s);
+void launch_perm_count(const int32_t* idx, int64_t T, int64_t k, int64_t E,
+                       int32_t* counts, hipStream_t s);
+void launch_perm_scan(int32_t* counts, int64_t nblocks, int64_t E,
+                      int32_t* offsets, int32_t* tile_start, hipStream_t s);
+void launch_perm_place(const int32_t* idx, int64_t T, int64_t k, int64_t E,
+                       const int32_t* base, int32_t* perm, int32_t* inv,
+                       hipStream_t s);
+void launch_tile_start(const int32_t* offsets, int64_t E, int32_t* tile_start,
+                       hipStream_t s);
+void launch_combine(const float* out_rows, const int32_t* idx, const float* w,
+                    const int32_t* inv, const float* resid, float* y,
+                    int64_t T, int64_t k, int64_t d, int64_t rows_total,
+                    int contract, hipStream_t s);
+
+}  // namespace moe
+
+// The context: the device it is bound to, a grow-only workspace (so frees
+// never land inside a timed region), and the optional per-kernel timers.
+struct moe_ctx {
+    int device = 0;
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+    bool timing = false;
+    struct Pending {
+        const char* name;
+        hipEvent_t start, stop;
+    };
+    std::vector<Pending> pending;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> event_pool;
+    std::map<std::string, std::pair<double, int64_t>> totals;
+    std::vector<std::string> name_store;  // keeps returned names alive
+
+    void* workspace(size_t bytes);
+
+    template <class F>
+    void launch(const char* name, hipStream_t s, F&& f) {
+        if (!timing) {
+            f();
+            moe::hip_check(hipGetLastError(), name);
+            return;
+        }
+        std::pair<hipEvent_t, hipEvent_t> ev;
+        if (!event_pool.empty()) {
+            ev = event_pool.back();
+            event_pool.pop_back();
+        } else {
+            moe::hip_check(hipEventCreate(&ev.first), "hipEventCreate");
+            moe::hip_check(hipEventCreate(&ev.second), "hipEventCreate");
+        }
+        moe::hip_check(hipEventRecord(ev.first, s), "hipEventRecord");
+        f();
+        moe::hip_check(hipGetLastError(), name);
+        moe::hip_check(hipEventRecord(ev.second, s), "hipEventRecord");
+        pending.push_back({name, ev.first, ev.second});
+    }
+    void collect();
+};

@@ -1,0 +1,164 @@
+/*
+ * moe_amd.h -- C ABI of the MI355X (gfx950) MoE forward hot path.
+ *
+ * Every entry point takes device pointers (fp32 / int32, row-major), plain
+ * sizes and a stream given as `void*` (a hipStream_t; NULL = the default
+ * stream).  Work is enqueued on that stream and the call returns without
+ * synchronising.  Return value: MOE_OK, or an error code whose message
+ * moe_last_error() returns (thread-local).  The C++ drop-in layer rethrows
+ * MOE_ERR_INVALID as std::invalid_argument and the others as
+ * std::runtime_error, the reference's exception types.
+ *
+ * Replaces (paths relative to the songsnim/accelerating-MoE-inference root):
+ *   moe_sgemm_nt        tensor_ops::matmul_transposed     src/tensor.cu:136-148
+ *                       and the GPU gemm_nt_body/gemm_nt_bias src/model.cu:182-460
+ *   moe_sgemm_nn        tensor_ops::matmul (declared only) include/tensor.h:61
+ *   moe_gate_logits     router gate GEMM                   src/layer.cu:84,
+ *                       gemm_gate                          src/model.cu:505-616
+ *   moe_route           PhiMoE::route                      src/layer.cu:47-70,
+ *                       route_top2                         src/model.cu:878-904
+ *   moe_permute         assignments[e] build               src/layer.cu:86-92,
+ *                       route_count/scan/place             src/model.cu:921-1030
+ *   moe_expert_ffn_grouped  per-expert PhiMLP::forward     src/layer.cu:32-45,93-98,
+ *                       gemm_grouped / w2 launches         src/model.cu:625-667
+ *   moe_combine         y[t] += w * out in expert order    src/layer.cu:99-101,
+ *                       gemm_grouped_combine epilogue      src/model.cu:436-447
+ *   moe_layer_forward   PhiMoE::forward                    src/layer.cu:80-103,
+ *                       the MoE block of generate()        src/model.cu:1976-2021
+ *   moe_ctx_*           DeviceBuffer / Scratch workspace   src/model.cu:45-68,1294-1324
+ */
+#ifndef MOE_AMD_H
+#define MOE_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MOE_OK 0
+#define MOE_ERR_INVALID 1     /* bad shape / argument (std::invalid_argument) */
+#define MOE_ERR_RUNTIME 2     /* HIP runtime failure (std::runtime_error)     */
+#define MOE_ERR_UNSUPPORTED 3 /* argument outside what the kernels support    */
+
+/* Floating-point contraction of `acc += a*b` in the bit-exact kernels (gate
+ * logits, combine).  FMA: one rounding per step, what the reference's GPU
+ * gate and its CPU build on an FMA host compute.  NONE: product and sum
+ * rounded separately, what the reference's CPU build on a host without FMA
+ * computes. */
+#define MOE_CONTRACT_NONE 0
+#define MOE_CONTRACT_FMA 1
+
+/* PHI_QUANT: PhiMoE::route (quantise to `quantum`, sequential select with
+ * `tie_eps`, fixed weights 1/k = 0.5 for k = 2).  SOFTMAX_TOPK: k largest
+ * logits (ties to the lower index), softmax over the selected k. */
+#define MOE_ROUTER_PHI_QUANT 0
+#define MOE_ROUTER_SOFTMAX_TOPK 1
+
+/* SWIGLU: w2 (silu(x w1^T) * (x w3^T)) (PhiMLP).  SILU_MLP: w2 silu(x w1^T). */
+#define MOE_ACT_SWIGLU 0
+#define MOE_ACT_SILU_MLP 1
+
+typedef struct moe_ctx moe_ctx;
+
+typedef struct moe_layer_desc {
+    int64_t T;        /* tokens (rows of x)                         */
+    int64_t d;        /* model width                                */
+    int64_t E;        /* experts, 1..1024                           */
+    int64_t k;        /* experts per token, 1..min(E, 32)           */
+    int64_t d_ff;     /* expert hidden width                        */
+    int32_t act;      /* MOE_ACT_*                                  */
+    int32_t router;   /* MOE_ROUTER_*                               */
+    float quantum;    /* PHI_QUANT score quantum (1e-3 in the reference)   */
+    float tie_eps;    /* PHI_QUANT tie margin (2e-2 in the reference)      */
+    int32_t contract; /* MOE_CONTRACT_* for gate logits and combine         */
+} moe_layer_desc;
+
+typedef struct moe_layer_weights {
+    const float* gate_w;      /* [E, d]                         */
+    const float* expert_bias; /* [E] added to logits, or NULL   */
+    const float* w1;          /* [E, d_ff, d]                   */
+    const float* w3;          /* [E, d_ff, d]; NULL for SILU_MLP */
+    const float* w2;          /* [E, d, d_ff]                   */
+} moe_layer_weights;
+
+/* ---- context: device binding, grow-only workspace, optional kernel timing.
+ * Replaces the reference's DeviceBuffer/Scratch (src/model.cu:45-68,
+ * 1294-1324).  A context is not safe for concurrent calls from several
+ * threads (the reference's generate() is not either, include/model.h:124-127). */
+int moe_ctx_create(int device, moe_ctx** out);
+int moe_ctx_destroy(moe_ctx* ctx);
+/* Grow the workspace so that moe_layer_forward(desc) allocates nothing. */
+int moe_ctx_reserve(moe_ctx* ctx, const moe_layer_desc* desc);
+/* Kernel timing (the reference's APS_PROFILE stage timers,
+ * src/model.cu:1584-1622): when on, every launch is bracketed by HIP events
+ * on its stream.  moe_ctx_kernel_times() synchronises, then returns the
+ * number of named kernels and fills up to `cap` entries of names / total
+ * milliseconds / launch counts accumulated since the last reset. */
+int moe_ctx_set_timing(moe_ctx* ctx, int enabled);
+int moe_ctx_kernel_times(moe_ctx* ctx, const char** names, double* total_ms,
+                         int64_t* launches, int cap);
+int moe_ctx_reset_timing(moe_ctx* ctx);
+const char* moe_last_error(void);
+const char* moe_version(void);
+
+/* ---- dense SGEMM, fp32 MFMA.
+ * NT: C[M,N] = A[M,K] B[N,K]^T (+ bias[N]); NN: C = A[M,K] B[K,N] (+ bias).
+ * Any M, N, K >= 0; K = 0 gives C = bias (or 0).  bias may be NULL. */
+int moe_sgemm_nt(moe_ctx* ctx, const float* A, const float* B,
+                 const float* bias, float* C, int64_t M, int64_t N, int64_t K,
+                 void* stream);
+int moe_sgemm_nn(moe_ctx* ctx, const float* A, const float* B,
+                 const float* bias, float* C, int64_t M, int64_t N, int64_t K,
+                 void* stream);
+
+/* ---- router gate logits[T,E] = x[T,d] Wg[E,d]^T with one k-ascending fp32
+ * accumulator per output: bit-identical to the CPU path under `contract`. */
+int moe_gate_logits(moe_ctx* ctx, const float* x, const float* gate_w,
+                    float* logits, int64_t T, int64_t d, int64_t E,
+                    int contract, void* stream);
+
+/* ---- top-k routing of logits[T,E] (+ expert_bias[E] when not NULL).
+ * topk_idx[T,k] (int32, selection order) and topk_w[T,k]. */
+int moe_route(moe_ctx* ctx, const float* logits, const float* expert_bias,
+              int64_t T, int64_t E, int64_t k, int mode, float quantum,
+              float tie_eps, int32_t* topk_idx, float* topk_w, void* stream);
+
+/* ---- stable bucket sort of the T*k (token, slot) pairs by expert.
+ * expert_offsets[E+1]; perm[T*k]: token of each packed row, tokens ascending
+ * within an expert; inv[T*k]: packed row of pair (t, s) at t*k+s.
+ * Every row of topk_idx must hold k distinct experts in [0, E). */
+int moe_permute(moe_ctx* ctx, const int32_t* topk_idx, int64_t T, int64_t k,
+                int64_t E, int32_t* expert_offsets, int32_t* perm,
+                int32_t* inv, void* stream);
+
+/* ---- expert FFN over packed rows, one grouped launch per projection.
+ * Packed row r of expert e (expert_offsets[e] <= r < expert_offsets[e+1])
+ * reads x[perm[r], :].  h[T*k, d_ff] is the hidden activation (written),
+ * out_rows[T*k, d] the expert outputs in packed order.
+ * w1, w3: [E, d_ff, d]; w2: [E, d, d_ff]; w3 is ignored for SILU_MLP. */
+int moe_expert_ffn_grouped(moe_ctx* ctx, const float* x, const int32_t* perm,
+                           const int32_t* expert_offsets, const float* w1,
+                           const float* w3, const float* w2, int act,
+                           int64_t T, int64_t k, int64_t d, int64_t d_ff,
+                           int64_t E, float* h, float* out_rows, void* stream);
+
+/* ---- y[t,:] = sum over t's experts in ascending expert id of
+ * topk_w[t,s] * out_rows[inv[t,s], :], starting from zero (+ resid[t,:]
+ * added last when resid is not NULL). */
+int moe_combine(moe_ctx* ctx, const float* out_rows, const int32_t* topk_idx,
+                const float* topk_w, const int32_t* inv, const float* resid,
+                float* y, int64_t T, int64_t k, int64_t d, int contract,
+                void* stream);
+
+/* ---- the whole MoE layer: gate -> route -> permute -> expert FFN ->
+ * combine.  topk_idx_out [T,k] / topk_w_out [T,k] may be NULL. */
+int moe_layer_forward(moe_ctx* ctx, const moe_layer_desc* desc,
+                      const moe_layer_weights* weights, const float* x,
+                      float* y, int32_t* topk_idx_out, float* topk_w_out,
+                      void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,60 @@
+"""CPU-side checks of the C ABI: the library builds for gfx950, loads, and
+exports every function include/moe_amd.h declares; the Python binding maps
+the same names.  No compute call runs here (there is no GPU)."""
+import ctypes
+import os
+import subprocess
+
+import pytest
+
+from helpers import PKG_DIR, header_functions, load_pkg
+
+
+@pytest.fixture(scope="module")
+def lib_path():
+    path = os.path.join(PKG_DIR, "libmoe_amd.so")
+    if not os.path.exists(path):
+        subprocess.run(["python", os.path.join(PKG_DIR, "build.py")], check=True)
+    return path
+
+
+def test_header_declares_the_boundary():
+    names = header_functions()
+    for n in ("moe_sgemm_nt", "moe_sgemm_nn", "moe_gate_logits", "moe_route",
+              "moe_permute", "moe_expert_ffn_grouped", "moe_combine",
+              "moe_layer_forward", "moe_ctx_create", "moe_last_error"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol(lib_path):
+    lib = ctypes.CDLL(lib_path)
+    missing = [n for n in header_functions() if not hasattr(lib, n)]
+    assert not missing, f"not exported: {missing}"
+    out = subprocess.run(["nm", "-D", "--defined-only", lib_path],
+                         capture_output=True, text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    assert set(header_functions()) <= exported
+
+
+def test_binding_covers_the_header(lib_path):
+    pkg = load_pkg()
+    assert set(pkg.EXPORTS) == set(header_functions())
+    lib = pkg.load_library()
+    assert lib.moe_version().decode().endswith("gfx950")
+
+
+def test_library_is_built_for_gfx950(lib_path):
+    # the offload bundle ids of the library's device code name the target
+    with open(lib_path, "rb") as f:
+        blob = f.read()
+    assert b"amdgcn-amd-amdhsa--gfx950" in blob
+
+
+def test_errors_without_context(lib_path):
+    pkg = load_pkg()
+    lib = pkg.load_library()
+    rc = lib.moe_sgemm_nt(None, None, None, None, None, 1, 1, 1, None)
+    assert rc == pkg.ERR_INVALID
+    assert "moe_ctx" in lib.moe_last_error().decode()
+    rc = lib.moe_route(None, None, None, 4, 8, 2, 0, 1e-3, 2e-2, None, None, None)
+    assert rc == pkg.ERR_INVALID

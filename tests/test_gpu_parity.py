@@ -1,0 +1,404 @@
+"""GPU parity: every entry point of the C ABI against the CPU oracle on the
+same seeded inputs.
+
+Bar: routing indices, expert assignment, offsets, permutations and gate
+logits bit-exact; activations within REL_TOL = 1e-4 normwise relative error
+(helpers.REL_TOL); the combine is bit-exact given identical inputs.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from helpers import REL_TOL, assert_close, load_pkg, normal, rel_err, zipf_bias
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as _t
+    assert _t.cuda.is_available(), "GPU tests need the MI355X"
+    return _t
+
+
+@pytest.fixture(scope="module")
+def pkg():
+    return load_pkg()
+
+
+@pytest.fixture(scope="module")
+def ctx(pkg, torch):
+    c = pkg.Context(0)
+    yield c
+    c.close()
+
+
+def dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
+
+
+def host(t):
+    return t.detach().cpu().numpy()
+
+
+# ------------------------------------------------------------------ SGEMM
+SGEMM_SHAPES = [(1, 1, 1), (7, 5, 33), (129, 130, 17), (128, 128, 128),
+                (256, 384, 512), (33, 200, 1000), (300, 64, 4), (5, 700, 2)]
+
+
+@pytest.mark.parametrize("m,n,k", SGEMM_SHAPES)
+def test_sgemm_nt_vs_oracle(ctx, torch, orc, m, n, k):
+    print(f"sgemm_nt {m}x{n}x{k}", flush=True)
+    rng = np.random.default_rng(m * 7 + n * 3 + k)
+    a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    b = rng.uniform(-1, 1, (n, k)).astype(np.float32)
+    bias = rng.uniform(-1, 1, n).astype(np.float32)
+    c = torch.empty((m, n), device="cuda")
+    ctx.sgemm_nt(dev(torch, a), dev(torch, b), c)
+    ref = orc.matmul_nt(a, b)
+    assert_close(host(c), ref, what="nt")
+    ctx.sgemm_nt(dev(torch, a), dev(torch, b), c, bias=dev(torch, bias))
+    assert_close(host(c), ref + bias, what="nt+bias")
+
+
+@pytest.mark.parametrize("m,n,k", SGEMM_SHAPES)
+def test_sgemm_nn_vs_oracle(ctx, torch, orc, m, n, k):
+    print(f"sgemm_nn {m}x{n}x{k}", flush=True)
+    rng = np.random.default_rng(m * 5 + n * 11 + k)
+    a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    b = rng.uniform(-1, 1, (k, n)).astype(np.float32)
+    c = torch.empty((m, n), device="cuda")
+    ctx.sgemm_nn(dev(torch, a), dev(torch, b), c)
+    assert_close(host(c), orc.matmul_nn(a, b), what="nn")
+
+
+def test_sgemm_unaligned_k(ctx, torch, orc):
+    # K % 4 != 0 takes the scalar-load path; a view at a 4-byte offset too
+    rng = np.random.default_rng(9)
+    a = rng.uniform(-1, 1, (70, 37)).astype(np.float32)
+    b = rng.uniform(-1, 1, (90, 37)).astype(np.float32)
+    c = torch.empty((70, 90), device="cuda")
+    ctx.sgemm_nt(dev(torch, a), dev(torch, b), c)
+    assert_close(host(c), orc.matmul_nt(a, b), what="K=37")
+    big = torch.zeros(1 + 70 * 36, device="cuda")
+    a2 = big[1:].view(70, 36)
+    a2.copy_(dev(torch, a[:, :36]))
+    ctx.sgemm_nt(a2, dev(torch, b[:, :36].copy()), c)
+    assert_close(host(c), orc.matmul_nt(a[:, :36], b[:, :36]), what="offset A")
+
+
+def test_sgemm_k_zero_gives_bias(ctx, torch):
+    c = torch.full((3, 5), 7.0, device="cuda")
+    bias = torch.arange(5, dtype=torch.float32, device="cuda")
+    ctx.sgemm_nt(torch.empty((3, 0), device="cuda"), torch.empty((5, 0), device="cuda"),
+                 c, bias=bias)
+    assert np.array_equal(host(c), np.tile(np.arange(5, dtype=np.float32), (3, 1)))
+
+
+@pytest.mark.parametrize("n", [1024, 2048])
+def test_sgemm_square_config2(ctx, torch, orc, n):
+    """Config-2 square shapes, fully checked against the oracle."""
+    print(f"sgemm square {n}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(n)
+    a = torch.rand((n, n), device="cuda", generator=g) * 2 - 1
+    b = torch.rand((n, n), device="cuda", generator=g) * 2 - 1
+    c = torch.empty((n, n), device="cuda")
+    ctx.sgemm_nn(a, b, c)
+    assert_close(host(c), orc.matmul_nn(host(a), host(b)), what=f"nn {n}")
+    ctx.sgemm_nt(a, b, c)
+    assert_close(host(c), orc.matmul_nt(host(a), host(b)), what=f"nt {n}")
+
+
+@pytest.mark.parametrize("m", [16, 64, 256, 512])
+def test_sgemm_skinny_config2_row_sample(ctx, torch, orc, m):
+    """Config-2 skinny expert shapes M x 14336 x 4096 at full size; the oracle
+    recomputes a sample of rows (each output row depends only on its A row)."""
+    print(f"sgemm skinny {m}", flush=True)
+    n, k = 14336, 4096
+    g = torch.Generator(device="cuda").manual_seed(m)
+    a = torch.rand((m, k), device="cuda", generator=g) * 2 - 1
+    b = torch.rand((k, n), device="cuda", generator=g) * 2 - 1
+    c = torch.empty((m, n), device="cuda")
+    ctx.sgemm_nn(a, b, c)
+    rows = np.unique(np.linspace(0, m - 1, 8).astype(int))
+    ref = orc.matmul_nn(host(a)[rows], host(b))
+    assert_close(host(c)[rows], ref, what=f"skinny {m}")
+
+
+# ------------------------------------------------------------------- gate
+@pytest.mark.parametrize("contract", [0, 1])
+@pytest.mark.parametrize("T,d,E", [(64, 512, 4), (300, 4096, 16), (1000, 2048, 64),
+                                   (33, 100, 7), (5, 1, 3), (70, 130, 130)])
+def test_gate_logits_bit_exact(ctx, torch, orc, contract, T, d, E):
+    print(f"gate {T}x{d}x{E} contract={contract}", flush=True)
+    rng = np.random.default_rng(T + d + E)
+    x = normal(rng, (T, d))
+    w = normal(rng, (E, d), 0.02)
+    logits = torch.empty((T, E), device="cuda")
+    ctx.gate_logits(dev(torch, x), dev(torch, w), logits, contract=contract)
+    ref = orc.matmul_nt(x, w, contract=contract)
+    assert np.array_equal(host(logits).view(np.int32), ref.view(np.int32))
+
+
+@pytest.mark.parametrize("contract", [0, 1])
+def test_routing_histogram_kat_on_gpu(ctx, torch, orc, contract):
+    """The reference's published per-expert row counts
+    (docs/microworld/exp-003-moe.html:399-405), recomputed by the GPU gate and
+    router."""
+    with open(os.path.join(GOLDEN, "exp003_routing_histogram.json")) as f:
+        kat = json.load(f)
+    gw = dev(torch, orc.lcg_fill((16, 4096), 101))
+    for T_str, want in kat["rows_per_expert"].items():
+        T = int(T_str)
+        print(f"KAT T={T} contract={contract}", flush=True)
+        x = dev(torch, orc.lcg_fill((T, 4096), 7 + T))
+        logits = torch.empty((T, 16), device="cuda")
+        ctx.gate_logits(x, gw, logits, contract=contract)
+        idx = torch.empty((T, 2), dtype=torch.int32, device="cuda")
+        w = torch.empty((T, 2), device="cuda")
+        ctx.route(logits, 2, idx, w)
+        got = np.bincount(host(idx).ravel(), minlength=16).tolist()
+        assert got == want, f"T={T}"
+        offsets = torch.empty(17, dtype=torch.int32, device="cuda")
+        perm = torch.empty(2 * T, dtype=torch.int32, device="cuda")
+        inv = torch.empty((T, 2), dtype=torch.int32, device="cuda")
+        ctx.permute(idx, 16, offsets, perm, inv)
+        assert np.diff(host(offsets)).tolist() == want
+
+
+# ---------------------------------------------------------------- routing
+@pytest.mark.parametrize("E,k", [(4, 2), (16, 2), (8, 2), (64, 8), (7, 3), (128, 4), (1, 1)])
+@pytest.mark.parametrize("mode", [0, 1])
+def test_route_vs_oracle(ctx, torch, orc, E, k, mode):
+    print(f"route E={E} k={k} mode={mode}", flush=True)
+    rng = np.random.default_rng(E * 10 + k + mode)
+    T = 1000
+    logits = normal(rng, (T, E), 0.1)
+    logits[::5, :min(E, 3)] = logits[::5, :1]          # exact ties
+    logits[1::9] = np.round(logits[1::9], 2)           # quantisation boundaries
+    if E >= 3:
+        logits[2::11, 2] = np.nan                      # NaN ranks as -inf (softmax)
+    bias = zipf_bias(E) if E == 64 else None
+    idx = torch.empty((T, k), dtype=torch.int32, device="cuda")
+    w = torch.empty((T, k), device="cuda")
+    ctx.route(dev(torch, logits), k, idx, w, mode=mode,
+              expert_bias=None if bias is None else dev(torch, bias))
+    ridx, rw = orc.route(logits, k, mode=mode, expert_bias=bias)
+    assert np.array_equal(host(idx), ridx)
+    if mode == 0:
+        assert np.array_equal(host(w), rw)
+    else:
+        diff = np.abs(host(w).view(np.int32).astype(np.int64) - rw.view(np.int32))
+        assert diff.max() <= 1, "softmax weights beyond 1 ulp"
+
+
+def test_route_phi_hand_cases(ctx, torch, orc):
+    rows = np.array([[0.0, 0.025, 0.04, -1.0], [0.5, 0.5, 0.5, 0.5],
+                     [0.0, 0.0196, -1.0, -1.0], [0.0, 0.0194, -1.0, -1.0],
+                     [-0.3, -0.2, -0.25, -0.9], [-0.0, 0.0, -1.0, -1.0]], np.float32)
+    idx = torch.empty((6, 2), dtype=torch.int32, device="cuda")
+    w = torch.empty((6, 2), device="cuda")
+    ctx.route(dev(torch, rows), 2, idx, w)
+    assert host(idx).tolist() == [[1, 2], [0, 1], [1, 0], [0, 1], [1, 2], [0, 1]]
+
+
+# ------------------------------------------------------------ permutation
+def _rand_topk(rng, T, E, k, skew=False):
+    if skew:
+        p = np.arange(1, E + 1, dtype=np.float64) ** -1.2
+        p /= p.sum()
+        return np.stack([rng.choice(E, size=k, replace=False, p=p) for _ in range(T)]).astype(np.int32)
+    return np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
+
+
+@pytest.mark.parametrize("T,E,k,skew", [(1, 4, 2, False), (255, 4, 2, False), (256, 8, 2, False),
+                                        (1000, 64, 8, True), (3000, 16, 2, False),
+                                        (777, 1024, 4, True), (513, 8, 8, False)])
+def test_permute_bit_exact(ctx, torch, orc, T, E, k, skew):
+    print(f"permute T={T} E={E} k={k}", flush=True)
+    rng = np.random.default_rng(T + E + k)
+    topk = _rand_topk(rng, T, E, k, skew)
+    offsets = torch.empty(E + 1, dtype=torch.int32, device="cuda")
+    perm = torch.empty(T * k, dtype=torch.int32, device="cuda")
+    inv = torch.empty((T, k), dtype=torch.int32, device="cuda")
+    ctx.permute(dev(torch, topk), E, offsets, perm, inv)
+    roff, rperm, rinv = orc.permute(topk, E)
+    assert np.array_equal(host(offsets), roff)
+    assert np.array_equal(host(perm), rperm)
+    assert np.array_equal(host(inv), rinv)
+
+
+def test_permute_all_tokens_one_expert(ctx, torch, orc):
+    T, E = 600, 8
+    topk = np.stack([np.full(T, 5), np.full(T, 2)], axis=1).astype(np.int32)
+    offsets = torch.empty(E + 1, dtype=torch.int32, device="cuda")
+    perm = torch.empty(2 * T, dtype=torch.int32, device="cuda")
+    inv = torch.empty((T, 2), dtype=torch.int32, device="cuda")
+    ctx.permute(dev(torch, topk), E, offsets, perm, inv)
+    roff, rperm, rinv = orc.permute(topk, E)
+    assert np.array_equal(host(offsets), roff)
+    assert np.array_equal(host(perm), rperm) and np.array_equal(host(inv), rinv)
+
+
+# --------------------------------------------------------- FFN and combine
+def _ffn_case(rng, T, d, E, k, d_ff, act, skew=False):
+    x = normal(rng, (T, d))
+    w1 = normal(rng, (E, d_ff, d), 0.02)
+    w3 = normal(rng, (E, d_ff, d), 0.02) if act == 0 else None
+    w2 = normal(rng, (E, d, d_ff), 0.02)
+    topk = _rand_topk(rng, T, E, k, skew)
+    return x, w1, w3, w2, topk
+
+
+@pytest.mark.parametrize("T,d,E,k,d_ff,act,skew", [
+    (64, 512, 4, 2, 1024, 1, False),     # config-1 expert shape, SiLU MLP
+    (200, 256, 8, 2, 384, 0, False),
+    (300, 128, 64, 8, 96, 0, True),      # ragged, tiny experts
+    (50, 132, 4, 2, 70, 0, False),       # d, d_ff not multiples of the tile
+    (33, 36, 16, 3, 17, 1, True),
+])
+def test_expert_ffn_vs_oracle(ctx, torch, orc, T, d, E, k, d_ff, act, skew):
+    print(f"ffn T={T} d={d} E={E} k={k} d_ff={d_ff} act={act}", flush=True)
+    rng = np.random.default_rng(T + d + E + d_ff)
+    x, w1, w3, w2, topk = _ffn_case(rng, T, d, E, k, d_ff, act, skew)
+    roff, rperm, rinv = orc.permute(topk, E)
+    ref = orc.expert_ffn(x, rperm, roff, w1, w3, w2, act=act)
+    h = torch.empty((T * k, d_ff), device="cuda")
+    out = torch.empty((T * k, d), device="cuda")
+    ctx.expert_ffn_grouped(dev(torch, x), dev(torch, rperm), dev(torch, roff), dev(torch, w1),
+                           None if w3 is None else dev(torch, w3), dev(torch, w2), k, h, out,
+                           act=act)
+    assert_close(host(out), ref, what="expert rows")
+
+
+@pytest.mark.parametrize("contract", [0, 1])
+def test_combine_bit_exact(ctx, torch, orc, contract):
+    rng = np.random.default_rng(11)
+    T, k, d = 500, 8, 260
+    topk = _rand_topk(rng, T, 64, k)
+    roff, rperm, rinv = orc.permute(topk, 64)
+    rows = normal(rng, (T * k, d))
+    w = rng.uniform(0, 1, (T, k)).astype(np.float32)
+    y = torch.empty((T, d), device="cuda")
+    ctx.combine(dev(torch, rows), dev(torch, topk), dev(torch, w), dev(torch, rinv), y,
+                contract=contract)
+    ref = orc.combine(rows, topk, w, rinv, contract=contract)
+    assert np.array_equal(host(y), ref)
+    resid = normal(rng, (T, d))
+    ctx.combine(dev(torch, rows), dev(torch, topk), dev(torch, w), dev(torch, rinv), y,
+                resid=dev(torch, resid), contract=contract)
+    assert np.array_equal(host(y), ref + resid)
+
+
+# ------------------------------------------------------------ whole layer
+def _layer(ctx, pkg, torch, x, gw, w1, w3, w2, k, act, mode, contract=1, bias=None):
+    T, d = x.shape
+    E, d_ff, _ = w1.shape
+    desc = pkg.make_desc(T, d, E, k, d_ff, act=act, router=mode, contract=contract)
+    y = torch.empty((T, d), device="cuda")
+    idx = torch.empty((T, k), dtype=torch.int32, device="cuda")
+    w = torch.empty((T, k), device="cuda")
+    weights = {"gate_w": gw, "w1": w1, "w3": w3, "w2": w2, "expert_bias": bias}
+    ctx.layer_forward(desc, weights, x, y, idx, w)
+    return y, idx, w
+
+
+def test_layer_config1(ctx, pkg, torch, orc):
+    """Config 1: 64 tokens x 512, gate 512->4, top-2 softmax over the selected
+    logits, SiLU-MLP experts 512->1024->512, weights N(0,0.02), x N(0,1), seed 0."""
+    rng = np.random.default_rng(0)
+    T, d, E, k, d_ff = 64, 512, 4, 2, 1024
+    x = normal(rng, (T, d))
+    gw = normal(rng, (E, d), 0.02)
+    w1 = normal(rng, (E, d_ff, d), 0.02)
+    w2 = normal(rng, (E, d, d_ff), 0.02)
+    y, idx, w = _layer(ctx, pkg, torch, dev(torch, x), dev(torch, gw), dev(torch, w1), None,
+                       dev(torch, w2), k, act=1, mode=1)
+    ry, ridx, rw = orc.moe_forward(x, gw, w1, None, w2, k, act=1, router_mode=1)
+    assert np.array_equal(host(idx), ridx)
+    assert np.max(np.abs(host(w).view(np.int32).astype(np.int64) - rw.view(np.int32))) <= 1
+    assert_close(host(y), ry, what="config1 y")
+
+
+@pytest.mark.parametrize("contract", [0, 1])
+def test_layer_phi_router_swiglu(ctx, pkg, torch, orc, contract):
+    """The reference's own layer semantics: quantised top-2 with 0.5/0.5
+    weights and SwiGLU experts (src/layer.cu:32-103), 16 experts."""
+    rng = np.random.default_rng(5)
+    T, d, E, k, d_ff = 300, 256, 16, 2, 448
+    x = normal(rng, (T, d))
+    gw = normal(rng, (E, d), 0.02)
+    w1 = normal(rng, (E, d_ff, d), 0.02)
+    w3 = normal(rng, (E, d_ff, d), 0.02)
+    w2 = normal(rng, (E, d, d_ff), 0.02)
+    y, idx, w = _layer(ctx, pkg, torch, dev(torch, x), dev(torch, gw), dev(torch, w1),
+                       dev(torch, w3), dev(torch, w2), k, act=0, mode=0, contract=contract)
+    ry, ridx, rw = orc.moe_forward(x, gw, w1, w3, w2, k, act=0, router_mode=0,
+                                   contract=contract)
+    assert np.array_equal(host(idx), ridx) and np.array_equal(host(w), rw)
+    assert_close(host(y), ry, what="phi layer y")
+
+
+def test_layer_deterministic(ctx, pkg, torch):
+    rng = np.random.default_rng(6)
+    T, d, E, k, d_ff = 500, 128, 8, 2, 256
+    args = [dev(torch, normal(rng, s, sd)) for s, sd in
+            [((T, d), 1.0), ((E, d), 0.02), ((E, d_ff, d), 0.02), ((E, d_ff, d), 0.02),
+             ((E, d, d_ff), 0.02)]]
+    y1, i1, w1 = _layer(ctx, pkg, torch, *args, k, act=0, mode=1)
+    y2, i2, w2 = _layer(ctx, pkg, torch, *args, k, act=0, mode=1)
+    assert torch.equal(y1, y2) and torch.equal(i1, i2) and torch.equal(w1, w2)
+
+
+def _big_layer(ctx, pkg, torch, orc, T, d, E, k, d_ff, mode, bias, sample, seed):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    x = torch.randn((T, d), device="cuda", generator=g)
+    gw = torch.randn((E, d), device="cuda", generator=g) * 0.02
+    w1 = torch.randn((E, d_ff, d), device="cuda", generator=g) * 0.02
+    w3 = torch.randn((E, d_ff, d), device="cuda", generator=g) * 0.02
+    w2 = torch.randn((E, d, d_ff), device="cuda", generator=g) * 0.02
+    bias_t = None if bias is None else dev(torch, bias)
+    y, idx, w = _layer(ctx, pkg, torch, x, gw, w1, w3, w2, k, act=0, mode=mode, bias=bias_t)
+    counts = np.bincount(host(idx).ravel(), minlength=E)
+    assert counts.sum() == T * k
+    xs = host(x)[:sample]
+    ry, ridx, rw = orc.moe_forward(xs, host(gw), host(w1), host(w3), host(w2), k, act=0,
+                                   router_mode=mode, expert_bias=bias)
+    assert np.array_equal(host(idx)[:sample], ridx)
+    assert_close(host(y)[:sample], ry, what="sampled tokens")
+    return counts
+
+
+def test_layer_mixtral_config3_full_size(ctx, pkg, torch, orc):
+    """Config 3 at full size (4096 x 4096, E=8, top-2 softmax, SwiGLU 14336);
+    the oracle recomputes the first 24 tokens (routing is per token, so their
+    routing and outputs are exactly the full layer's)."""
+    counts = _big_layer(ctx, pkg, torch, orc, 4096, 4096, 8, 2, 14336, mode=1, bias=None,
+                        sample=24, seed=3)
+    assert counts.min() > 0
+
+
+def test_layer_skewed_config4_full_size(ctx, pkg, torch, orc):
+    """Config 4 at full size (16384 x 2048, E=64, top-8, SwiGLU 1408, Zipf(1.2)
+    router bias); the oracle recomputes the first 48 tokens."""
+    counts = _big_layer(ctx, pkg, torch, orc, 16384, 2048, 64, 8, 1408, mode=1,
+                        bias=zipf_bias(64), sample=48, seed=4)
+    assert counts.max() > 4 * counts.mean()  # heavily imbalanced loads
+
+
+# ------------------------------------------------------------------ errors
+def test_errors_are_reported(ctx, pkg, torch):
+    c = torch.empty((4, 4), device="cuda")
+    with pytest.raises(pkg.MoeInvalidArgument):
+        ctx.sgemm_nt(torch.empty((4, 3), device="cuda"), torch.empty((4, 3), device="cuda"),
+                     c.to(torch.float64))
+    with pytest.raises(pkg.MoeInvalidArgument):
+        ctx.route(torch.empty((4, 4), device="cuda"), 5,
+                  torch.empty((4, 5), dtype=torch.int32, device="cuda"),
+                  torch.empty((4, 5), device="cuda"))
+    with pytest.raises(pkg.MoeInvalidArgument):
+        pkg._check(pkg.load_library().moe_gate_logits(
+            ctx.handle, None, None, None, 4, 8, 2000, 1, None))

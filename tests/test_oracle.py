@@ -1,0 +1,270 @@
+"""Pins the CPU oracle (oracle/moe_oracle.c) before anything is checked
+against it.
+
+Every check is chosen so that a plausible mistake fails it: the published
+routing histograms of the reference (a known answer computed by the reference
+itself), closed-form sums whose value depends on the summation order or on
+the contraction, float64 brute force, and invariants.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+F32 = np.float32
+
+
+# ---------------------------------------------------------------- LCG + KAT
+def test_lcg_first_values(orc):
+    # s1 = 101*1664525 + 1013904223 mod 2^32; v = ((s1>>8)&0xFFFF)/32768 - 1
+    s = 101
+    vals = []
+    for _ in range(3):
+        s = (s * 1664525 + 1013904223) & 0xFFFFFFFF
+        vals.append(np.float32(((s >> 8) & 0xFFFF) / 32768.0 - 1.0))
+    got = orc.lcg_fill((3,), 101)
+    assert got.tolist() == vals
+
+
+@pytest.mark.parametrize("contract", [0, 1])
+def test_routing_histogram_matches_reference(orc, contract):
+    """The reference's own per-expert row counts for its LCG-seeded MoE layer
+    (docs/microworld/exp-003-moe.html:399-405) pin the LCG, the k-ascending
+    gate GEMM and PhiMoE::route together, at six token counts."""
+    with open(os.path.join(GOLDEN, "exp003_routing_histogram.json")) as f:
+        kat = json.load(f)
+    gw = orc.lcg_fill((16, 4096), 101)
+    for T_str, want in kat["rows_per_expert"].items():
+        T = int(T_str)
+        x = orc.lcg_fill((T, 4096), 7 + T)
+        logits = orc.matmul_nt(x, gw, contract=contract)
+        idx, w = orc.route(logits, 2)
+        assert np.all(w == F32(0.5))
+        got = np.bincount(idx.ravel(), minlength=16).tolist()
+        assert got == want, f"T={T}"
+        assert np.all(idx[:, 0] != idx[:, 1])
+
+
+# ------------------------------------------------------------------ SGEMM
+def test_matmul_order_known_answer(orc):
+    # [1e8, 1, -1e8, 1] . ones: k-ascending single accumulator gives
+    # ((1e8+1)->1e8, -1e8 -> 0, +1) = 1; reversed gives 0, pairwise 0, exact 2.
+    a = np.array([[1e8, 1.0, -1e8, 1.0]], dtype=F32)
+    b = np.ones((1, 4), dtype=F32)
+    for c in (0, 1):
+        assert orc.matmul_nt(a, b, contract=c)[0, 0] == F32(1.0)
+        assert orc.matmul_nn(a, b.T.copy(), contract=c)[0, 0] == F32(1.0)
+
+
+def test_matmul_contraction_known_answer(orc):
+    # acc = -(1+2^-11); then acc + (1+2^-12)^2.  The exact product is
+    # 1 + 2^-11 + 2^-24: a fused multiply-add keeps the 2^-24, a separately
+    # rounded product (ties-to-even) drops it.
+    u = F32(1 + 2.0 ** -12)
+    a = np.array([[F32(1 + 2.0 ** -11), u]], dtype=F32)
+    b = np.array([[-1.0, u]], dtype=F32)
+    assert orc.matmul_nt(a, b, contract=1)[0, 0] == F32(2.0 ** -24)
+    assert orc.matmul_nt(a, b, contract=0)[0, 0] == F32(0.0)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 1, 1), (7, 5, 33), (33, 17, 64), (64, 48, 257)])
+def test_matmul_vs_float64(orc, m, n, k):
+    rng = np.random.default_rng(m * 1000 + n * 10 + k)
+    a = rng.uniform(-1, 1, (m, k)).astype(F32)
+    b = rng.uniform(-1, 1, (n, k)).astype(F32)
+    ref = a.astype(np.float64) @ b.astype(np.float64).T
+    bound = k * 2.0 ** -23 * (np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64).T) + 1e-30
+    for c in (0, 1):
+        got = orc.matmul_nt(a, b, contract=c)
+        assert np.all(np.abs(got - ref) <= bound)
+        # NN is the same loop nest over b read as [K, N]: bit-identical.
+        assert np.array_equal(orc.matmul_nn(a, b.T.copy(), contract=c), got)
+
+
+def test_matmul_empty(orc):
+    c = orc.matmul_nt(np.zeros((0, 4), F32), np.zeros((3, 4), F32))
+    assert c.shape == (0, 3)
+    c = orc.matmul_nt(np.zeros((2, 0), F32), np.zeros((3, 0), F32))
+    assert c.shape == (2, 3) and np.all(c == 0)
+
+
+# ------------------------------------------------------------------- SiLU
+def test_silu_properties(orc):
+    x = np.linspace(-20, 20, 4001).astype(F32)
+    y = orc.silu(x)
+    assert orc.silu(np.zeros(1, F32))[0] == 0.0
+    exact = x.astype(np.float64) / (1.0 + np.exp(-x.astype(np.float64)))
+    # three roundings (exp to float, the add, the division): within 3 ulp
+    ulp = np.spacing(np.abs(exact).astype(F32)).astype(np.float64)
+    assert np.all(np.abs(y - exact) <= 3 * ulp + 1e-45)
+    # silu(x) - silu(-x) = x
+    assert np.allclose(y - orc.silu(-x), x, rtol=1e-6, atol=1e-6)
+
+
+def test_mul(orc):
+    a = np.array([1.5, -2.0, 3.0], F32)
+    b = np.array([2.0, 0.25, -1.0], F32)
+    assert orc.mul(a, b).tolist() == [3.0, -0.5, -3.0]
+
+
+# ---------------------------------------------------------------- routing
+def _phi(orc, row, k=2):
+    idx, w = orc.route(np.array([row], F32), k)
+    return tuple(idx[0].tolist())
+
+
+def test_phi_route_hand_cases(orc):
+    # Not an argmax: expert 1 beats 0 by > 0.02, expert 2 does not beat 1.
+    assert _phi(orc, [0.0, 0.025, 0.04, -1.0]) == (1, 2)
+    # Exact ties keep the lower index.
+    assert _phi(orc, [0.5, 0.5, 0.5, 0.5]) == (0, 1)
+    # 0.0196 quantises to 20 quanta, whose float value exceeds 0 + 0.02f.
+    # An unquantised comparison would give (0, 1).
+    assert _phi(orc, [0.0, 0.0196, -1.0, -1.0]) == (1, 0)
+    # 0.0194 quantises to 19 quanta: not enough.
+    assert _phi(orc, [0.0, 0.0194, -1.0, -1.0]) == (0, 1)
+    # Signs are restored after quantising |s|.
+    assert _phi(orc, [-0.3, -0.2, -0.25, -0.9]) == (1, 2)
+    # -0 and +0 tie.
+    assert _phi(orc, [-0.0, 0.0, -1.0, -1.0]) == (0, 1)
+    # A quantum of 1e-3 makes 0.10004 and 0.1 equal.
+    assert _phi(orc, [0.1, 0.10004, 0.13, 0.0]) == (2, 0)
+
+
+def test_phi_route_weights(orc):
+    rng = np.random.default_rng(0)
+    idx, w = orc.route(rng.normal(size=(50, 16)).astype(F32), 2)
+    assert np.all(w == F32(0.5))
+    idx, w = orc.route(rng.normal(size=(50, 16)).astype(F32), 4)
+    assert np.all(w == F32(0.25))
+    assert all(len(set(r)) == 4 for r in idx.tolist())
+
+
+def test_phi_route_bias_shifts_selection(orc):
+    logits = np.zeros((3, 4), F32)
+    bias = np.array([0.0, 0.0, 0.5, 0.3], F32)
+    idx, _ = orc.route(logits, 2, expert_bias=bias)
+    assert idx.tolist() == [[2, 3]] * 3
+
+
+def test_softmax_topk_vs_brute_force(orc):
+    rng = np.random.default_rng(1)
+    for E, k in [(4, 2), (8, 2), (64, 8), (16, 16)]:
+        logits = rng.normal(size=(200, E)).astype(F32)
+        logits[::7, 1] = logits[::7, 0]  # exact ties
+        bias = rng.normal(size=E).astype(F32) if E == 64 else None
+        idx, w = orc.route(logits, k, mode=orc.ROUTER_SOFTMAX_TOPK,
+                           expert_bias=bias)
+        v = logits + (bias if bias is not None else 0)
+        for t in range(v.shape[0]):
+            order = sorted(range(E), key=lambda e: (-float(v[t, e]), e))[:k]
+            assert idx[t].tolist() == order
+            sel = v[t, order].astype(np.float64)
+            ex = np.exp(sel - sel[0])
+            ref = (ex / ex.sum()).astype(F32)
+            assert np.all(np.abs(w[t].view(np.int32) - ref.view(np.int32)) <= 1)
+        assert np.allclose(w.sum(axis=1), 1.0, atol=1e-6)
+
+
+def test_softmax_topk_nan_ranks_last(orc):
+    logits = np.array([[np.nan, 1.0, 2.0, np.nan]], F32)
+    idx, w = orc.route(logits, 3, mode=orc.ROUTER_SOFTMAX_TOPK)
+    assert idx[0].tolist() == [2, 1, 0]
+
+
+def test_route_rejects_bad_k(orc):
+    with pytest.raises(ValueError):
+        orc.route(np.zeros((2, 4), F32), 5)
+    with pytest.raises(ValueError):
+        orc.route(np.zeros((2, 4), F32), 0)
+
+
+# ------------------------------------------------------------ permutation
+def test_permute_invariants_and_brute_force(orc):
+    rng = np.random.default_rng(2)
+    T, E, k = 300, 16, 4
+    idx = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
+    offsets, perm, inv = orc.permute(idx, E)
+    counts = np.bincount(idx.ravel(), minlength=E)
+    assert offsets.tolist() == [0] + np.cumsum(counts).tolist()
+    for e in range(E):
+        want = [t for t in range(T) if e in idx[t]]
+        assert perm[offsets[e]:offsets[e + 1]].tolist() == want
+    for t in range(T):
+        for s in range(k):
+            r = inv[t, s]
+            assert perm[r] == t and offsets[idx[t, s]] <= r < offsets[idx[t, s] + 1]
+
+
+def test_permute_empty_experts_and_tokens(orc):
+    idx = np.array([[3, 1], [3, 1]], np.int32)
+    offsets, perm, inv = orc.permute(idx, 6)
+    assert offsets.tolist() == [0, 0, 2, 2, 4, 4, 4]
+    assert perm.tolist() == [0, 1, 0, 1]
+    offsets, perm, inv = orc.permute(np.zeros((0, 2), np.int32), 4)
+    assert offsets.tolist() == [0] * 5 and perm.size == 0
+
+
+def test_permute_rejects_out_of_range(orc):
+    with pytest.raises(ValueError):
+        orc.permute(np.array([[0, 4]], np.int32), 4)
+
+
+# ---------------------------------------------------------------- combine
+def test_combine_ascending_expert_order(orc):
+    # One token, experts listed as (2, 0, 1), unit weights; rows e0=1e8, e1=1,
+    # e2=-1e8.  Ascending expert order: (1e8 + 1) -> 1e8, -1e8 -> 0.
+    # Slot order would give (-1e8 + 1e8) + 1 = 1.
+    out_rows = np.array([[-1e8], [1e8], [1.0]], F32)   # packed rows
+    topk_idx = np.array([[2, 0, 1]], np.int32)
+    inv = np.array([[0, 1, 2]], np.int32)
+    w = np.ones((1, 3), F32)
+    for c in (0, 1):
+        assert orc.combine(out_rows, topk_idx, w, inv, contract=c)[0, 0] == 0.0
+
+
+def test_combine_top2_closed_form(orc):
+    rng = np.random.default_rng(3)
+    rows = rng.normal(size=(8, 32)).astype(F32)
+    topk_idx = np.array([[5, 1], [0, 7], [2, 3], [6, 4]], np.int32)
+    inv = np.array([[0, 1], [2, 3], [4, 5], [6, 7]], np.int32)
+    w = np.full((4, 2), 0.5, F32)
+    y = orc.combine(rows, topk_idx, w, inv)
+    want = F32(0.5) * rows[0::2] + F32(0.5) * rows[1::2]
+    assert np.array_equal(y, want)
+
+
+# ------------------------------------------------------- FFN and the layer
+def _f64_layer(x, gw, w1, w3, w2, idx, w, act):
+    x64 = x.astype(np.float64)
+    T, d = x.shape
+    y = np.zeros((T, d))
+    for t in range(T):
+        for s in range(idx.shape[1]):
+            e = idx[t, s]
+            g = w1[e].astype(np.float64) @ x64[t]
+            h = g / (1 + np.exp(-g))
+            if act == 0:
+                h = h * (w3[e].astype(np.float64) @ x64[t])
+            y[t] += float(w[t, s]) * (w2[e].astype(np.float64) @ h)
+    return y
+
+
+@pytest.mark.parametrize("act", [0, 1])
+@pytest.mark.parametrize("mode", [0, 1])
+def test_moe_forward_vs_float64(orc, act, mode):
+    rng = np.random.default_rng(4 + act + 2 * mode)
+    T, d, E, k, d_ff = 40, 64, 4, 2, 96
+    x = rng.normal(size=(T, d)).astype(F32)
+    gw = (0.02 * rng.normal(size=(E, d))).astype(F32)
+    w1 = (0.02 * rng.normal(size=(E, d_ff, d))).astype(F32)
+    w3 = (0.02 * rng.normal(size=(E, d_ff, d))).astype(F32)
+    w2 = (0.02 * rng.normal(size=(E, d, d_ff))).astype(F32)
+    y, idx, w = orc.moe_forward(x, gw, w1, w3 if act == 0 else None, w2, k,
+                                act=act, router_mode=mode)
+    ridx, rw = orc.route(orc.matmul_nt(x, gw), k, mode=mode)
+    assert np.array_equal(idx, ridx) and np.array_equal(w, rw)
+    ref = _f64_layer(x, gw, w1, w3, w2, idx, w, act)
+    assert np.max(np.abs(y - ref)) <= 1e-5 * np.max(np.abs(ref))
