@@ -27,7 +27,8 @@ ACT_SWIGLU, ACT_SILU_MLP = 0, 1
 EXPORTS = (
     "moe_ctx_create", "moe_ctx_destroy", "moe_ctx_reserve", "moe_ctx_set_timing",
     "moe_ctx_kernel_times", "moe_ctx_reset_timing", "moe_last_error",
-    "moe_version", "moe_sgemm_nt", "moe_sgemm_nn", "moe_gate_logits",
+    "moe_version", "moe_sgemm_nt", "moe_sgemm_nn", "moe_silu", "moe_mul",
+    "moe_gate_logits",
     "moe_route", "moe_permute", "moe_expert_ffn_grouped", "moe_combine",
     "moe_layer_forward",
 )
@@ -83,6 +84,8 @@ def load_library(path: str = LIB_PATH):
         "moe_version": ([], ctypes.c_char_p),
         "moe_sgemm_nt": ([P, P, P, P, P, I64, I64, I64, P], I),
         "moe_sgemm_nn": ([P, P, P, P, P, I64, I64, I64, P], I),
+        "moe_silu": ([P, P, P, I64, P], I),
+        "moe_mul": ([P, P, P, P, I64, P], I),
         "moe_gate_logits": ([P, P, P, P, I64, I64, I64, I, P], I),
         "moe_route": ([P, P, P, I64, I64, I64, I, F, F, P, P, P], I),
         "moe_permute": ([P, P, I64, I64, I64, P, P, P, P], I),
@@ -196,6 +199,16 @@ class Context:
                                  _f32(bias, "bias"), _f32(C, "C"), M, N, K,
                                  _stream()))
         return C
+
+    def silu(self, x, y):
+        _check(_lib.moe_silu(self.handle, _f32(x, "x"), _f32(y, "y"), x.numel(),
+                             _stream()))
+        return y
+
+    def mul(self, a, b, c):
+        _check(_lib.moe_mul(self.handle, _f32(a, "a"), _f32(b, "b"), _f32(c, "c"),
+                            a.numel(), _stream()))
+        return c
 
     def gate_logits(self, x, gate_w, logits, contract=CONTRACT_FMA):
         T, d = x.shape

@@ -18,7 +18,10 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libmoe_amd.so")
-HIP_SOURCES = ["gemm.hip", "route.hip", "capi.hip"]
+HIP_SOURCES = ["gemm.hip", "route.hip", "elementwise.hip", "capi.hip"]
+DROPIN_LIB = os.path.join(HERE, "libmoe_dropin.so")
+DROPIN_SOURCES = ["device.cpp", "tensor.cpp", "model_loader.cpp", "layer.cpp"]
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 HIP_FLAGS = [
@@ -43,18 +46,35 @@ def _compile(src: str) -> str:
     return obj
 
 
+def _run(cmd, what):
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"{what} failed:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+
+
+def build_dropin() -> str:
+    """The C++ drop-in of the reference host API (Tensor, tensor_ops, Linear,
+    PhiMLP, PhiMoE, ModelLoader): host code over the C ABI, built with g++."""
+    srcs = [os.path.join(HERE, "host", f) for f in DROPIN_SOURCES]
+    tmp = DROPIN_LIB + ".tmp"
+    _run(["g++", "-std=c++17", "-O2", "-fPIC", "-shared", "-Wall", "-Wextra",
+          "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", *srcs, "-o", tmp,
+          f"-L{HERE}", "-lmoe_amd", f"-L{ROCM}/lib", "-lamdhip64",
+          "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{ROCM}/lib"], "drop-in build")
+    os.replace(tmp, DROPIN_LIB)
+    return DROPIN_LIB
+
+
 def build(verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
     with cf.ThreadPoolExecutor(max_workers=len(HIP_SOURCES)) as ex:
         objs = list(ex.map(_compile, HIP_SOURCES))
     tmp = LIB + ".tmp"
-    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs]
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs], "link")
     os.replace(tmp, LIB)
+    build_dropin()
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB}\nbuilt {DROPIN_LIB}")
     return LIB
 
 

@@ -352,6 +352,33 @@ int moe_sgemm_nn(moe_ctx* ctx, const float* A, const float* B, const float* bias
     return guarded([&] { sgemm(ctx, true, A, B, bias, C, M, N, K, stream); });
 }
 
+int moe_silu(moe_ctx* ctx, const float* x, float* y, int64_t n, void* stream) {
+    return guarded([&] {
+        check_ctx(ctx);
+        moe::require(n >= 0, "n must be >= 0");
+        if (n == 0) return;
+        check_ptr(x, "x");
+        check_ptr(y, "y");
+        DeviceScope dev(ctx->device);
+        hipStream_t s = as_stream(stream);
+        ctx->launch("silu", s, [&] { moe::launch_silu(x, y, n, s); });
+    });
+}
+
+int moe_mul(moe_ctx* ctx, const float* a, const float* b, float* c, int64_t n, void* stream) {
+    return guarded([&] {
+        check_ctx(ctx);
+        moe::require(n >= 0, "n must be >= 0");
+        if (n == 0) return;
+        check_ptr(a, "a");
+        check_ptr(b, "b");
+        check_ptr(c, "c");
+        DeviceScope dev(ctx->device);
+        hipStream_t s = as_stream(stream);
+        ctx->launch("mul", s, [&] { moe::launch_mul(a, b, c, n, s); });
+    });
+}
+
 int moe_gate_logits(moe_ctx* ctx, const float* x, const float* gate_w, float* logits,
                     int64_t T, int64_t d, int64_t E, int contract, void* stream) {
     return guarded([&] {

@@ -90,6 +90,8 @@ void launch_perm_place(const int32_t* idx, int64_t T, int64_t k, int64_t E,
                        hipStream_t s);
 void launch_tile_start(const int32_t* offsets, int64_t E, int32_t* tile_start,
                        hipStream_t s);
+void launch_silu(const float* x, float* y, int64_t n, hipStream_t s);
+void launch_mul(const float* a, const float* b, float* c, int64_t n, hipStream_t s);
 void launch_combine(const float* out_rows, const int32_t* idx, const float* w,
                     const int32_t* inv, const float* resid, float* y,
                     int64_t T, int64_t k, int64_t d, int64_t rows_total,

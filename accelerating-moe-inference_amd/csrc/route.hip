@@ -18,13 +18,16 @@ namespace moe {
 namespace {
 
 // ---------------------------------------------------------------- gate
-// Workgroup: 32 token rows x a chunk of up to 64 experts.  Thread (r, g)
-// owns row r and experts g, g+8, ..., g+56 of the chunk: up to 8 independent
-// accumulator chains.  K streams through LDS 64 columns at a time with
-// coalesced loads; x rows are read once per expert chunk.
-constexpr int GATE_ROWS = 32;
-constexpr int GATE_EXPERTS = 64;
+// The gate is a row-times-[E, d] product whose every output must be the
+// CPU's sequential k-ascending chain, so its parallelism is the T*E outputs:
+// one thread per output.  A workgroup covers R = 256/EB token rows x EB
+// experts (EB = E rounded up to a power of two, 8..64); in a wave the lanes
+// sharing a row (or an expert) read the same LDS word, so both operand reads
+// are broadcasts.  K streams through a double-buffered LDS tile of R + EB
+// rows x 64 columns; the next chunk's coalesced global loads are in flight
+// while the current one is consumed, 4 columns per 16-byte LDS read.
 constexpr int GATE_KC = 64;
+constexpr int GATE_LDS = GATE_KC + 4;  // 16-byte aligned, conflict-free rows
 
 template <int CONTRACT>
 __device__ __forceinline__ float mac(float acc, float a, float b) {
@@ -33,57 +36,87 @@ __device__ __forceinline__ float mac(float acc, float a, float b) {
     return acc + prod;
 }
 
-template <int CONTRACT>
+template <int CONTRACT, int EB>
 __global__ __launch_bounds__(256) void gate_logits_kernel(
         const float* __restrict__ x, const float* __restrict__ w,
         float* __restrict__ logits, int64_t T, int64_t d, int64_t E) {
-    __shared__ float xs[GATE_ROWS][GATE_KC + 1];
-    __shared__ float ws[GATE_EXPERTS][GATE_KC + 1];
-    const int tid = threadIdx.x;
-    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * GATE_ROWS;
-    const int64_t e0 = static_cast<int64_t>(blockIdx.y) * GATE_EXPERTS;
-    const int r = tid & (GATE_ROWS - 1);
-    const int g = tid >> 5;  // 0..7
-    float acc[GATE_EXPERTS / 8];
-#pragma unroll
-    for (int j = 0; j < GATE_EXPERTS / 8; ++j) acc[j] = 0.0f;
+    constexpr int R = 256 / EB;               // token rows per workgroup
+    constexpr int ROWS = R + EB;              // staged rows: x rows, then w rows
+    constexpr int PER = ROWS * GATE_KC / 256; // staged floats per thread
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    __shared__ __align__(16) float tile[2][ROWS * GATE_LDS];
 
-    for (int64_t k0 = 0; k0 < d; k0 += GATE_KC) {
+    const int tid = threadIdx.x;
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * R;
+    const int64_t e0 = static_cast<int64_t>(blockIdx.y) * EB;
+    const int el = tid % EB, r = tid / EB;
+
+    // Staging: element i*256 + tid of the tile -> (row, col); 64 lanes of a
+    // wave read 64 consecutive floats of one row (256 contiguous bytes).
+    const float* src[PER];
+    bool ok[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int idx = i * 256 + tid;
+        const int row = idx / GATE_KC, col = idx % GATE_KC;
+        if (row < R) {
+            const int64_t t = t0 + row;
+            ok[i] = t < T;
+            src[i] = x + (ok[i] ? t : 0) * d + col;
+        } else {
+            const int64_t e = e0 + (row - R);
+            ok[i] = e < E;
+            src[i] = w + (ok[i] ? e : 0) * d + col;
+        }
+    }
+    float stage[PER];
+    auto gload = [&](int64_t k0) {
+        const int64_t kn = d - k0;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int col = (i * 256 + tid) % GATE_KC;
+            stage[i] = (ok[i] && col < kn) ? src[i][k0] : 0.0f;
+        }
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int idx = i * 256 + tid;
+            tile[buf][(idx / GATE_KC) * GATE_LDS + idx % GATE_KC] = stage[i];
+        }
+    };
+
+    float acc = 0.0f;
+    const int64_t nchunks = (d + GATE_KC - 1) / GATE_KC;
+    if (nchunks > 0) {
+        gload(0);
+        lstore(0);
+        __syncthreads();
+    }
+    for (int64_t c = 0; c < nchunks; ++c) {
+        const int buf = static_cast<int>(c & 1);
+        const int64_t k0 = c * GATE_KC;
+        if (c + 1 < nchunks) gload(k0 + GATE_KC);
+        // Only the kn real columns enter the sum: the chain is exactly the
+        // CPU's, with no padding term.
         const int kn = static_cast<int>(d - k0 < GATE_KC ? d - k0 : GATE_KC);
-        // stage x[t0.., k0..] and w[e0.., k0..]: 64 consecutive floats per row
-#pragma unroll
-        for (int i = 0; i < GATE_ROWS * GATE_KC / 256; ++i) {
-            const int idx = tid + 256 * i;
-            const int rr = idx / GATE_KC, cc = idx % GATE_KC;
-            const int64_t t = t0 + rr;
-            xs[rr][cc] = (t < T && cc < kn) ? x[t * d + k0 + cc] : 0.0f;
+        const float* xr = &tile[buf][r * GATE_LDS];
+        const float* wr = &tile[buf][(R + el) * GATE_LDS];
+        int kk = 0;
+        for (; kk + 4 <= kn; kk += 4) {
+            const f4 xv = *reinterpret_cast<const f4*>(xr + kk);
+            const f4 wv = *reinterpret_cast<const f4*>(wr + kk);
+            acc = mac<CONTRACT>(acc, xv[0], wv[0]);
+            acc = mac<CONTRACT>(acc, xv[1], wv[1]);
+            acc = mac<CONTRACT>(acc, xv[2], wv[2]);
+            acc = mac<CONTRACT>(acc, xv[3], wv[3]);
         }
-#pragma unroll
-        for (int i = 0; i < GATE_EXPERTS * GATE_KC / 256; ++i) {
-            const int idx = tid + 256 * i;
-            const int ee = idx / GATE_KC, cc = idx % GATE_KC;
-            const int64_t e = e0 + ee;
-            ws[ee][cc] = (e < E && cc < kn) ? w[e * d + k0 + cc] : 0.0f;
-        }
-        __syncthreads();
-        // Only the kn real columns are accumulated: no padding term ever
-        // enters a sum, so the chain is exactly the CPU's.
-        for (int kk = 0; kk < kn; ++kk) {
-            const float xv = xs[r][kk];
-#pragma unroll
-            for (int j = 0; j < GATE_EXPERTS / 8; ++j)
-                acc[j] = mac<CONTRACT>(acc[j], xv, ws[g + 8 * j][kk]);
-        }
+        for (; kk < kn; ++kk) acc = mac<CONTRACT>(acc, xr[kk], wr[kk]);
+        if (c + 1 < nchunks) lstore(buf ^ 1);
         __syncthreads();
     }
-    const int64_t t = t0 + r;
-    if (t < T) {
-#pragma unroll
-        for (int j = 0; j < GATE_EXPERTS / 8; ++j) {
-            const int64_t e = e0 + g + 8 * j;
-            if (e < E) logits[t * E + e] = acc[j];
-        }
-    }
+    const int64_t t = t0 + r, e = e0 + el;
+    if (t < T && e < E) logits[t * E + e] = acc;
 }
 
 // -------------------------------------------------------------- routers
@@ -375,12 +408,23 @@ void launch_gate_logits(const float* x, const float* w, float* logits,
                         int64_t T, int64_t d, int64_t E, int contract,
                         hipStream_t s) {
     if (T == 0 || E == 0) return;
-    const dim3 grid(static_cast<unsigned>(ceil_div(T, GATE_ROWS)),
-                    static_cast<unsigned>(ceil_div(E, GATE_EXPERTS)));
-    if (contract)
-        hipLaunchKernelGGL(gate_logits_kernel<1>, grid, dim3(256), 0, s, x, w, logits, T, d, E);
-    else
-        hipLaunchKernelGGL(gate_logits_kernel<0>, grid, dim3(256), 0, s, x, w, logits, T, d, E);
+    int eb = 8;
+    while (eb < E && eb < 64) eb <<= 1;
+    const dim3 grid(static_cast<unsigned>(ceil_div(T, 256 / eb)),
+                    static_cast<unsigned>(ceil_div(E, eb)));
+    auto go = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, x, w, logits, T, d, E);
+    };
+    switch (eb * 2 + (contract ? 1 : 0)) {
+        case 16: go(gate_logits_kernel<0, 8>); break;
+        case 17: go(gate_logits_kernel<1, 8>); break;
+        case 32: go(gate_logits_kernel<0, 16>); break;
+        case 33: go(gate_logits_kernel<1, 16>); break;
+        case 64: go(gate_logits_kernel<0, 32>); break;
+        case 65: go(gate_logits_kernel<1, 32>); break;
+        case 128: go(gate_logits_kernel<0, 64>); break;
+        default: go(gate_logits_kernel<1, 64>); break;
+    }
 }
 
 void launch_route(const float* logits, const float* bias, int64_t T, int64_t E,

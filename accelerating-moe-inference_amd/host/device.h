@@ -1,0 +1,45 @@
+// Internal helpers of the drop-in host layer: the process-wide moe_ctx,
+// status-to-exception mapping, and an RAII device buffer.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+
+#include "../../include/moe_amd.h"
+
+namespace moe_dropin {
+
+// The context every drop-in call uses: device $MOE_DEVICE (default 0),
+// created on first use, destroyed at exit.
+moe_ctx* context();
+
+// MOE_ERR_INVALID -> std::invalid_argument, any other error ->
+// std::runtime_error, carrying moe_last_error().
+void check(int status);
+
+// Waits for the work the drop-in enqueued (it uses the default stream).
+void synchronize();
+
+class DeviceBuffer {
+public:
+    DeviceBuffer() = default;
+    explicit DeviceBuffer(std::size_t bytes);
+    ~DeviceBuffer();
+    DeviceBuffer(const DeviceBuffer&) = delete;
+    DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+    DeviceBuffer(DeviceBuffer&& o) noexcept;
+    DeviceBuffer& operator=(DeviceBuffer&& o) noexcept;
+
+    void* get() const { return p_; }
+    std::size_t bytes() const { return n_; }
+    template <class T>
+    T* as() const { return static_cast<T*>(p_); }
+    void upload(const void* src, std::size_t bytes, std::size_t offset = 0);
+    void download(void* dst, std::size_t bytes) const;
+
+private:
+    void* p_ = nullptr;
+    std::size_t n_ = 0;
+};
+
+}  // namespace moe_dropin

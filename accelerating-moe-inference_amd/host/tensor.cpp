@@ -1,0 +1,207 @@
+// Tensor (host storage) and the GPU-backed tensor_ops of the drop-in API.
+#include "tensor.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <stdexcept>
+#include <string>
+
+#include "device.h"
+
+namespace {
+
+std::size_t count_of(const std::vector<std::size_t>& shape) {
+    std::size_t n = 1;
+    for (std::size_t d : shape) n *= d;
+    return n;
+}
+
+}  // namespace
+
+Tensor::Tensor(std::vector<std::size_t> shape, Alloc alloc)
+    : shape_(std::move(shape)), alloc_(alloc) {
+    const std::size_t n = count_of(shape_);
+    if (alloc_ == Alloc::Pinned) {
+        void* p = nullptr;
+        const hipError_t e = hipHostMalloc(&p, std::max<std::size_t>(n, 1) * sizeof(float),
+                                           hipHostMallocDefault);
+        if (e != hipSuccess)
+            throw std::runtime_error(std::string("hipHostMalloc tensor: ") + hipGetErrorString(e));
+        data_ = static_cast<float*>(p);
+    } else {
+        data_ = new float[std::max<std::size_t>(n, 1)];
+    }
+    size_ = capacity_ = n;
+    std::fill(data_, data_ + n, 0.0f);
+}
+
+void Tensor::release() {
+    if (data_ == nullptr) return;
+    if (alloc_ == Alloc::Pinned) {
+        const hipError_t e = hipHostFree(data_);
+        if (e != hipSuccess) std::fprintf(stderr, "hipHostFree tensor: %s\n", hipGetErrorString(e));
+    } else {
+        delete[] data_;
+    }
+    data_ = nullptr;
+    size_ = capacity_ = 0;
+}
+
+Tensor::~Tensor() { release(); }
+
+Tensor::Tensor(const Tensor& other) : shape_(other.shape_) {
+    if (other.size_ != 0) {
+        data_ = new float[other.size_];
+        std::copy(other.data_, other.data_ + other.size_, data_);
+        size_ = capacity_ = other.size_;
+    }
+}
+
+Tensor& Tensor::operator=(const Tensor& other) {
+    if (this != &other) {
+        Tensor copy(other);
+        *this = std::move(copy);
+    }
+    return *this;
+}
+
+Tensor::Tensor(Tensor&& other) noexcept
+    : shape_(std::move(other.shape_)), data_(other.data_), size_(other.size_),
+      capacity_(other.capacity_), alloc_(other.alloc_) {
+    other.shape_.clear();
+    other.data_ = nullptr;
+    other.size_ = other.capacity_ = 0;
+}
+
+Tensor& Tensor::operator=(Tensor&& other) noexcept {
+    if (this != &other) {
+        release();
+        shape_ = std::move(other.shape_);
+        data_ = other.data_;
+        size_ = other.size_;
+        capacity_ = other.capacity_;
+        alloc_ = other.alloc_;
+        other.shape_.clear();
+        other.data_ = nullptr;
+        other.size_ = other.capacity_ = 0;
+    }
+    return *this;
+}
+
+std::size_t Tensor::size(std::size_t dim) const {
+    if (dim >= shape_.size()) throw std::out_of_range("Tensor dimension");
+    return shape_[dim];
+}
+
+std::size_t Tensor::index(std::initializer_list<std::size_t> idx) const {
+    if (idx.size() != shape_.size()) throw std::invalid_argument("Tensor rank mismatch");
+    std::size_t flat = 0;
+    std::size_t d = 0;
+    for (std::size_t i : idx) {
+        if (i >= shape_[d]) throw std::out_of_range("Tensor index");
+        flat = flat * shape_[d] + i;
+        ++d;
+    }
+    return flat;
+}
+
+float& Tensor::at(std::size_t i) { return data_[index({i})]; }
+float& Tensor::at(std::size_t i, std::size_t j) { return data_[index({i, j})]; }
+float& Tensor::at(std::size_t i, std::size_t j, std::size_t k) { return data_[index({i, j, k})]; }
+float& Tensor::at(std::size_t i, std::size_t j, std::size_t k, std::size_t l) {
+    return data_[index({i, j, k, l})];
+}
+const float& Tensor::at(std::size_t i) const { return data_[index({i})]; }
+const float& Tensor::at(std::size_t i, std::size_t j) const { return data_[index({i, j})]; }
+const float& Tensor::at(std::size_t i, std::size_t j, std::size_t k) const {
+    return data_[index({i, j, k})];
+}
+const float& Tensor::at(std::size_t i, std::size_t j, std::size_t k, std::size_t l) const {
+    return data_[index({i, j, k, l})];
+}
+
+void Tensor::reshape(std::vector<std::size_t> shape) {
+    if (count_of(shape) != size_) throw std::invalid_argument("reshape changes tensor size");
+    shape_ = std::move(shape);
+}
+
+void Tensor::reshape_within_capacity(std::vector<std::size_t> shape) {
+    const std::size_t n = count_of(shape);
+    if (n > capacity_) throw std::invalid_argument("reshape exceeds tensor capacity");
+    shape_ = std::move(shape);
+    size_ = n;
+}
+
+void Tensor::fill(float value) { std::fill(data_, data_ + size_, value); }
+
+namespace tensor_ops {
+namespace {
+
+using moe_dropin::check;
+using moe_dropin::DeviceBuffer;
+
+DeviceBuffer to_device(const Tensor& t) {
+    DeviceBuffer b(t.size() * sizeof(float));
+    b.upload(t.data(), t.size() * sizeof(float));
+    return b;
+}
+
+void gemm(bool nn, const Tensor& a, const Tensor& b, Tensor& c, const char* what) {
+    const std::size_t m = a.size(0), k = a.size(1);
+    const std::size_t n = nn ? b.size(1) : b.size(0);
+    const std::size_t bk = nn ? b.size(0) : b.size(1);
+    if (a.ndim() != 2 || b.ndim() != 2 || c.ndim() != 2 || bk != k || c.size(0) != m ||
+        c.size(1) != n)
+        throw std::invalid_argument(what);
+    DeviceBuffer da = to_device(a), db = to_device(b), dc(m * n * sizeof(float));
+    moe_ctx* ctx = moe_dropin::context();
+    const auto M = static_cast<int64_t>(m), N = static_cast<int64_t>(n), K = static_cast<int64_t>(k);
+    check(nn ? moe_sgemm_nn(ctx, da.as<float>(), db.as<float>(), nullptr, dc.as<float>(), M, N, K,
+                            nullptr)
+             : moe_sgemm_nt(ctx, da.as<float>(), db.as<float>(), nullptr, dc.as<float>(), M, N, K,
+                            nullptr));
+    dc.download(c.data(), m * n * sizeof(float));
+}
+
+[[noreturn]] void outside(const char* op) {
+    throw std::logic_error(std::string("tensor_ops::") + op +
+                           " is outside the MoE hot path this library implements");
+}
+
+}  // namespace
+
+void matmul(const Tensor& a, const Tensor& b, Tensor& c) { gemm(true, a, b, c, "matmul shape"); }
+
+void matmul_transposed(const Tensor& a, const Tensor& b, Tensor& c) {
+    gemm(false, a, b, c, "matmul_transposed shape");
+}
+
+void mul(const Tensor& a, const Tensor& b, Tensor& c) {
+    if (a.size() != b.size() || c.size() != a.size()) throw std::invalid_argument("mul shape");
+    DeviceBuffer da = to_device(a), db = to_device(b), dc(c.size() * sizeof(float));
+    check(moe_mul(moe_dropin::context(), da.as<float>(), db.as<float>(), dc.as<float>(),
+                  static_cast<int64_t>(a.size()), nullptr));
+    dc.download(c.data(), c.size() * sizeof(float));
+}
+
+void silu(const Tensor& x, Tensor& y) {
+    if (x.size() != y.size()) throw std::invalid_argument("silu shape");
+    DeviceBuffer dx = to_device(x);
+    check(moe_silu(moe_dropin::context(), dx.as<float>(), dx.as<float>(),
+                   static_cast<int64_t>(x.size()), nullptr));
+    dx.download(y.data(), y.size() * sizeof(float));
+}
+
+void add_inplace(Tensor&, const Tensor&) { outside("add_inplace"); }
+void add_bias_inplace(Tensor&, const Tensor&) { outside("add_bias_inplace"); }
+void softmax_last_dim(const Tensor&, Tensor&) { outside("softmax_last_dim"); }
+void layer_norm(const Tensor&, const Tensor&, const Tensor&, float, Tensor&) {
+    outside("layer_norm");
+}
+void apply_rope(Tensor&, Tensor&, std::size_t, std::size_t, std::size_t, std::size_t, float) {
+    outside("apply_rope");
+}
+
+}  // namespace tensor_ops

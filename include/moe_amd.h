@@ -112,6 +112,14 @@ int moe_sgemm_nn(moe_ctx* ctx, const float* A, const float* B,
                  const float* bias, float* C, int64_t M, int64_t N, int64_t K,
                  void* stream);
 
+/* ---- elementwise ops of the expert MLP, bit-identical to the CPU loops:
+ * moe_silu: y = x / (1 + float(exp(double(-x))))  tensor_ops::silu, src/tensor.cu:169-173
+ * moe_mul:  c = a * b                              tensor_ops::mul,  src/tensor.cu:163-167
+ * (in place is allowed: y == x, c == a or c == b). */
+int moe_silu(moe_ctx* ctx, const float* x, float* y, int64_t n, void* stream);
+int moe_mul(moe_ctx* ctx, const float* a, const float* b, float* c, int64_t n,
+            void* stream);
+
 /* ---- router gate logits[T,E] = x[T,d] Wg[E,d]^T with one k-ascending fp32
  * accumulator per output: bit-identical to the CPU path under `contract`. */
 int moe_gate_logits(moe_ctx* ctx, const float* x, const float* gate_w,

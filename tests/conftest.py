@@ -11,6 +11,11 @@ if ROOT not in sys.path:
 def pytest_configure(config):
     config.addinivalue_line(
         "markers", "gpu: needs an MI355X (gfx950) GPU; runs on the GPU box")
+    # torch bundles its own HIP runtime (SONAME libamdhip64.so.7).  Importing
+    # it before any of our libraries makes them bind to that same runtime; if
+    # one of ours loaded first, the system runtime and torch's would both be
+    # mapped and torch could not initialise the GPU.
+    import torch  # noqa: F401
 
 
 @pytest.fixture(scope="session")

@@ -1,0 +1,206 @@
+// Test shim: drives the C++ drop-in API (Tensor, tensor_ops, ModelLoader,
+// Linear, PhiMLP, PhiMoE) exactly as reference code would, and exposes each
+// scenario as an extern "C" function for tests/test_dropin.py (ctypes).
+// Exceptions come back as codes: 1 invalid_argument, 2 runtime_error,
+// 3 logic_error, 4 out_of_range, 5 other; shim_error() holds the message.
+#include <cstdint>
+#include <cstring>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "layer.h"
+#include "model_loader.h"
+#include "tensor.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+template <class F>
+int guarded(F&& f) {
+    try {
+        f();
+        return 0;
+    } catch (const std::invalid_argument& e) {
+        g_err = e.what();
+        return 1;
+    } catch (const std::out_of_range& e) {
+        g_err = e.what();
+        return 4;
+    } catch (const std::logic_error& e) {
+        g_err = e.what();
+        return 3;
+    } catch (const std::runtime_error& e) {
+        g_err = e.what();
+        return 2;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return 5;
+    }
+}
+
+void expect(bool ok, const char* what) {
+    if (!ok) throw std::runtime_error(std::string("expectation failed: ") + what);
+}
+
+template <class E, class F>
+void expect_throw(F&& f, const char* what) {
+    try {
+        f();
+    } catch (const E&) {
+        return;
+    }
+    throw std::runtime_error(std::string("expected exception: ") + what);
+}
+
+Tensor make(const float* p, std::vector<std::size_t> shape) {
+    Tensor t(std::move(shape));
+    std::memcpy(t.data(), p, t.size() * sizeof(float));
+    return t;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* shim_error() { return g_err.c_str(); }
+
+// Tensor semantics of the reference's tensor.h:7-58.  Pinned allocation
+// needs the HIP runtime to see a device, so it is checked only on request.
+int shim_tensor_semantics(int with_pinned) {
+    return guarded([&] {
+        Tensor t({2, 3});
+        expect(t.size() == 6 && t.ndim() == 2 && t.size(1) == 3, "shape");
+        for (std::size_t i = 0; i < 6; ++i) expect(t[i] == 0.0f, "zero-initialised");
+        expect_throw<std::out_of_range>([&] { (void)t.size(2); }, "size(dim) past rank");
+        t.at(1, 2) = 5.0f;
+        expect(t[5] == 5.0f, "row-major at()");
+        expect_throw<std::out_of_range>([&] { (void)t.at(2, 0); }, "at() out of range");
+        expect_throw<std::invalid_argument>([&] { (void)t.at(1); }, "at() rank mismatch");
+        Tensor c = t;
+        c.at(0, 0) = 1.0f;
+        expect(t.at(0, 0) == 0.0f && c.at(1, 2) == 5.0f, "deep copy");
+        Tensor m = std::move(c);
+        expect(c.size() == 0 && c.data() == nullptr && m.at(0, 0) == 1.0f, "move");
+        m.reshape({3, 2});
+        expect(m.size(0) == 3 && m.at(2, 1) == 5.0f, "reshape");
+        expect_throw<std::invalid_argument>([&] { m.reshape({4}); }, "reshape size change");
+        m.reshape_within_capacity({1, 2});
+        expect(m.size() == 2 && m.capacity() == 6, "reshape within capacity");
+        expect_throw<std::invalid_argument>([&] { m.reshape_within_capacity({7}); },
+                                            "reshape past capacity");
+        m.fill(2.5f);
+        expect(m[0] == 2.5f && m[1] == 2.5f, "fill");
+        if (with_pinned) {
+            Tensor p({4}, Tensor::Alloc::Pinned);
+            p.at(3) = 1.0f;
+            Tensor pc = p;
+            expect(p.alloc() == Tensor::Alloc::Pinned && pc.alloc() == Tensor::Alloc::Host &&
+                       pc.at(3) == 1.0f,
+                   "copy of pinned is host");
+        }
+    });
+}
+
+int shim_loader_shape(const char* path, const char* name, int64_t* dims, int* ndim) {
+    return guarded([&] {
+        ModelLoader l(path);
+        expect(l.has(name), "has()");
+        const auto& s = l.shape(name);
+        *ndim = static_cast<int>(s.size());
+        for (std::size_t i = 0; i < s.size(); ++i) dims[i] = static_cast<int64_t>(s[i]);
+    });
+}
+
+int shim_loader_load(const char* path, const char* name, float* out, int64_t n) {
+    return guarded([&] {
+        ModelLoader l(path);
+        const Tensor t = l.load(name);
+        expect(static_cast<int64_t>(t.size()) == n, "element count");
+        std::memcpy(out, t.data(), t.size() * sizeof(float));
+    });
+}
+
+int shim_matmul_transposed(const float* a, int64_t m, int64_t k, const float* b, int64_t n,
+                           float* c) {
+    return guarded([&] {
+        Tensor A = make(a, {size_t(m), size_t(k)}), B = make(b, {size_t(n), size_t(k)});
+        Tensor C({size_t(m), size_t(n)});
+        tensor_ops::matmul_transposed(A, B, C);
+        std::memcpy(c, C.data(), C.size() * sizeof(float));
+    });
+}
+
+int shim_matmul(const float* a, int64_t m, int64_t k, const float* b, int64_t n, float* c) {
+    return guarded([&] {
+        Tensor A = make(a, {size_t(m), size_t(k)}), B = make(b, {size_t(k), size_t(n)});
+        Tensor C({size_t(m), size_t(n)});
+        tensor_ops::matmul(A, B, C);
+        std::memcpy(c, C.data(), C.size() * sizeof(float));
+    });
+}
+
+int shim_matmul_bad_shape() {
+    return guarded([] {
+        Tensor A({2, 3}), B({4, 5}), C({2, 4});
+        tensor_ops::matmul_transposed(A, B, C);
+    });
+}
+
+int shim_silu_mul(const float* x, const float* u, int64_t n, float* s, float* p) {
+    return guarded([&] {
+        Tensor X = make(x, {size_t(n)}), U = make(u, {size_t(n)}), S({size_t(n)}), P({size_t(n)});
+        tensor_ops::silu(X, S);
+        tensor_ops::mul(S, U, P);
+        std::memcpy(s, S.data(), n * sizeof(float));
+        std::memcpy(p, P.data(), n * sizeof(float));
+    });
+}
+
+int shim_outside_op() {
+    return guarded([] {
+        Tensor x({2, 4}), w({4}), b({4}), y({2, 4});
+        tensor_ops::layer_norm(x, w, b, 1e-5f, y);
+    });
+}
+
+int shim_linear(const char* path, const char* weight, const char* bias, const float* x,
+                int64_t rows, int64_t in, float* y, int64_t out) {
+    return guarded([&] {
+        ModelLoader l(path);
+        Linear lin(l, weight, bias);
+        Tensor X = make(x, {size_t(rows), size_t(in)}), Y;
+        lin.forward(X, Y);
+        expect(Y.ndim() == 2 && Y.size(0) == size_t(rows) && Y.size(1) == size_t(out), "y shape");
+        std::memcpy(y, Y.data(), Y.size() * sizeof(float));
+    });
+}
+
+int shim_mlp(const char* path, const char* prefix, const float* x, int64_t rows, int64_t h,
+             float* y) {
+    return guarded([&] {
+        ModelLoader l(path);
+        PhiMLP mlp(l, prefix);
+        Tensor X = make(x, {size_t(rows), size_t(h)}), Y;
+        mlp.forward(X, Y);
+        expect(Y.shape() == X.shape(), "y shaped like x");
+        std::memcpy(y, Y.data(), Y.size() * sizeof(float));
+    });
+}
+
+int shim_moe(const char* path, int64_t layer, int contract, const float* x, int64_t rows,
+             int64_t h, float* y, int32_t* topk) {
+    return guarded([&] {
+        ModelLoader l(path);
+        PhiMoE moe(l, size_t(layer), contract);
+        Tensor X = make(x, {size_t(rows), size_t(h)}), Y;
+        std::vector<int32_t> idx;
+        moe.forward(X, Y, &idx);
+        expect(Y.ndim() == 2 && Y.size(0) == size_t(rows) && Y.size(1) == size_t(h), "y shape");
+        std::memcpy(y, Y.data(), Y.size() * sizeof(float));
+        std::memcpy(topk, idx.data(), idx.size() * sizeof(int32_t));
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,201 @@
+"""The C++ drop-in of the reference host API (Tensor, tensor_ops, ModelLoader,
+Linear, PhiMLP, PhiMoE), driven through tests/cpp/dropin_shim.cpp.
+
+CPU tests: Tensor semantics and every ModelLoader error path.  GPU tests:
+each layer against the oracle on a model.bin written in the reference format
+(src/model_loader.cu:14-30)."""
+import ctypes
+import os
+import struct
+import subprocess
+
+import numpy as np
+import pytest
+
+from helpers import ROOT, assert_close, normal
+
+SHIM_DIR = os.path.join(ROOT, "tests", "cpp")
+SHIM = os.path.join(SHIM_DIR, "libdropin_shim.so")
+INVALID, RUNTIME, LOGIC, OUT_OF_RANGE = 1, 2, 3, 4
+
+
+@pytest.fixture(scope="module")
+def shim():
+    if not os.path.exists(SHIM):
+        subprocess.run(["make", "-s", "-C", SHIM_DIR], check=True)
+    L = ctypes.CDLL(SHIM)
+    L.shim_error.restype = ctypes.c_char_p
+    return L
+
+
+def err(shim):
+    return shim.shim_error().decode()
+
+
+def write_model_bin(path, tensors):
+    """model.bin: u32 count; per tensor u32 name_len, name, u32 ndim,
+    u32 dims[ndim], u64 offset, u64 bytes; fp32 data at the offsets."""
+    header = 4 + sum(4 + len(n.encode()) + 4 + 4 * a.ndim + 16 for n, a in tensors.items())
+    blob = bytearray(struct.pack("<I", len(tensors)))
+    off = header
+    datas = []
+    for name, a in tensors.items():
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        nb = name.encode()
+        blob += struct.pack("<I", len(nb)) + nb + struct.pack("<I", a.ndim)
+        blob += struct.pack(f"<{a.ndim}I", *a.shape)
+        blob += struct.pack("<QQ", off, a.nbytes)
+        datas.append(a.tobytes())
+        off += a.nbytes
+    assert len(blob) == header
+    with open(path, "wb") as f:
+        f.write(bytes(blob))
+        for d in datas:
+            f.write(d)
+
+
+def fptr(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+# ---------------------------------------------------------------- CPU side
+def test_tensor_semantics(shim):
+    assert shim.shim_tensor_semantics(0) == 0, err(shim)
+
+
+def test_loader_reads_shapes_and_values(shim, tmp_path):
+    rng = np.random.default_rng(0)
+    a = normal(rng, (3, 5))
+    b = normal(rng, (7,))
+    path = str(tmp_path / "model.bin")
+    write_model_bin(path, {"a.weight": a, "layer.b": b})
+    dims = (ctypes.c_int64 * 8)()
+    nd = ctypes.c_int()
+    assert shim.shim_loader_shape(path.encode(), b"a.weight", dims, ctypes.byref(nd)) == 0
+    assert list(dims[:nd.value]) == [3, 5]
+    out = np.empty(7, np.float32)
+    assert shim.shim_loader_load(path.encode(), b"layer.b", fptr(out), ctypes.c_int64(7)) == 0
+    assert np.array_equal(out, b)
+
+
+def test_loader_error_paths(shim, tmp_path):
+    path = str(tmp_path / "model.bin")
+    write_model_bin(path, {"w": np.ones((2, 2), np.float32)})
+    out = np.empty(4, np.float32)
+    rc = shim.shim_loader_load(path.encode(), b"nope", fptr(out), ctypes.c_int64(4))
+    assert rc == RUNTIME and err(shim) == "missing tensor: nope"
+    rc = shim.shim_loader_load(str(tmp_path / "absent.bin").encode(), b"w", fptr(out),
+                               ctypes.c_int64(4))
+    assert rc == RUNTIME and err(shim).startswith("cannot open model")
+    raw = open(path, "rb").read()
+    trunc = str(tmp_path / "trunc_header.bin")
+    open(trunc, "wb").write(raw[:10])
+    rc = shim.shim_loader_load(trunc.encode(), b"w", fptr(out), ctypes.c_int64(4))
+    assert rc == RUNTIME and err(shim) == "truncated model.bin"
+    trunc = str(tmp_path / "trunc_data.bin")
+    open(trunc, "wb").write(raw[:-4])
+    rc = shim.shim_loader_load(trunc.encode(), b"w", fptr(out), ctypes.c_int64(4))
+    assert rc == RUNTIME and err(shim) == "truncated tensor: w"
+    # bytes field that is not 4 * elements: not fp32
+    bad = bytearray(raw)
+    hdr = 4 + 4 + 1 + 4 + 8
+    bad[hdr + 8:hdr + 16] = struct.pack("<Q", 8)
+    badp = str(tmp_path / "bad.bin")
+    open(badp, "wb").write(bytes(bad))
+    rc = shim.shim_loader_load(badp.encode(), b"w", fptr(out), ctypes.c_int64(4))
+    assert rc == RUNTIME and err(shim) == "tensor is not float32: w"
+
+
+def test_shape_errors_before_any_device_work(shim):
+    assert shim.shim_matmul_bad_shape() == INVALID
+    assert err(shim) == "matmul_transposed shape"
+    assert shim.shim_outside_op() == LOGIC
+    assert "outside the MoE hot path" in err(shim)
+
+
+# ---------------------------------------------------------------- GPU side
+@pytest.mark.gpu
+def test_tensor_pinned(shim):
+    assert shim.shim_tensor_semantics(1) == 0, err(shim)
+
+
+@pytest.mark.gpu
+def test_tensor_ops_vs_oracle(shim, orc):
+    rng = np.random.default_rng(1)
+    m, k, n = 37, 70, 29
+    a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    bt = rng.uniform(-1, 1, (n, k)).astype(np.float32)
+    c = np.empty((m, n), np.float32)
+    I = ctypes.c_int64
+    assert shim.shim_matmul_transposed(fptr(a), I(m), I(k), fptr(bt), I(n), fptr(c)) == 0, err(shim)
+    assert_close(c, orc.matmul_nt(a, bt), what="matmul_transposed")
+    b = np.ascontiguousarray(bt.T)
+    assert shim.shim_matmul(fptr(a), I(m), I(k), fptr(b), I(n), fptr(c)) == 0, err(shim)
+    assert_close(c, orc.matmul_nn(a, b), what="matmul")
+    x = np.linspace(-30, 30, 1001).astype(np.float32)
+    u = normal(rng, (1001,))
+    s = np.empty_like(x)
+    p = np.empty_like(x)
+    assert shim.shim_silu_mul(fptr(x), fptr(u), I(1001), fptr(s), fptr(p)) == 0, err(shim)
+    assert np.array_equal(s, orc.silu(x))           # bit-exact
+    assert np.array_equal(p, orc.mul(orc.silu(x), u))
+
+
+@pytest.mark.gpu
+def test_linear_mlp_moe_vs_oracle(shim, orc, tmp_path):
+    rng = np.random.default_rng(2)
+    h, ff, E, rows = 256, 192, 16, 300
+    base = "model.layers.3.block_sparse_moe"
+    tensors = {"proj.weight": normal(rng, (96, h), 0.02), "proj.bias": normal(rng, (96,), 0.1),
+               f"{base}.gate.weight": normal(rng, (E, h), 0.02)}
+    for e in range(E):
+        tensors[f"{base}.experts.{e}.w1.weight"] = normal(rng, (ff, h), 0.02)
+        tensors[f"{base}.experts.{e}.w3.weight"] = normal(rng, (ff, h), 0.02)
+        tensors[f"{base}.experts.{e}.w2.weight"] = normal(rng, (h, ff), 0.02)
+    path = str(tmp_path / "model.bin").encode()
+    write_model_bin(path.decode(), tensors)
+    x = normal(rng, (rows, h))
+    I = ctypes.c_int64
+
+    y = np.empty((rows, 96), np.float32)
+    assert shim.shim_linear(path, b"proj.weight", b"proj.bias", fptr(x), I(rows), I(h), fptr(y),
+                            I(96)) == 0, err(shim)
+    assert_close(y, orc.matmul_nt(x, tensors["proj.weight"]) + tensors["proj.bias"],
+                 what="Linear")
+
+    y = np.empty((rows, h), np.float32)
+    pre = f"{base}.experts.5".encode()
+    assert shim.shim_mlp(path, pre, fptr(x), I(rows), I(h), fptr(y)) == 0, err(shim)
+    w1 = tensors[f"{base}.experts.5.w1.weight"]
+    w3 = tensors[f"{base}.experts.5.w3.weight"]
+    w2 = tensors[f"{base}.experts.5.w2.weight"]
+    ref = orc.matmul_nt(orc.mul(orc.silu(orc.matmul_nt(x, w1)), orc.matmul_nt(x, w3)), w2)
+    assert_close(y, ref, what="PhiMLP")
+
+    stack = lambda n: np.stack([tensors[f"{base}.experts.{e}.{n}.weight"] for e in range(E)])
+    for contract in (0, 1):
+        topk = np.empty((rows, 2), np.int32)
+        assert shim.shim_moe(path, I(3), contract, fptr(x), I(rows), I(h), fptr(y),
+                             fptr(topk)) == 0, err(shim)
+        ry, ridx, _ = orc.moe_forward(x, tensors[f"{base}.gate.weight"], stack("w1"),
+                                      stack("w3"), stack("w2"), 2, contract=contract)
+        assert np.array_equal(topk, ridx)
+        assert_close(y, ry, what=f"PhiMoE contract={contract}")
+
+
+def test_moe_missing_expert_raises(shim, tmp_path):
+    # PhiMoE loads every expert before it uploads anything: no device needed
+    rng = np.random.default_rng(3)
+    base = "model.layers.0.block_sparse_moe"
+    tensors = {f"{base}.gate.weight": normal(rng, (2, 8))}
+    tensors[f"{base}.experts.0.w1.weight"] = normal(rng, (4, 8))
+    tensors[f"{base}.experts.0.w3.weight"] = normal(rng, (4, 8))
+    tensors[f"{base}.experts.0.w2.weight"] = normal(rng, (8, 4))
+    path = str(tmp_path / "model.bin")
+    write_model_bin(path, tensors)
+    x = normal(rng, (4, 8))
+    y = np.empty((4, 8), np.float32)
+    topk = np.empty((4, 2), np.int32)
+    I = ctypes.c_int64
+    rc = shim.shim_moe(path.encode(), I(0), 1, fptr(x), I(4), I(8), fptr(y), fptr(topk))
+    assert rc == RUNTIME and err(shim) == f"missing tensor: {base}.experts.1.w1.weight"

@@ -128,6 +128,23 @@ def test_sgemm_skinny_config2_row_sample(ctx, torch, orc, m):
     assert_close(host(c)[rows], ref, what=f"skinny {m}")
 
 
+# ------------------------------------------------------------ elementwise
+def test_silu_mul_bit_exact(ctx, torch, orc):
+    rng = np.random.default_rng(12)
+    x = np.concatenate([np.linspace(-90, 90, 20001), rng.normal(size=5000) * 3,
+                        [0.0, -0.0, 1e-30, -1e-30, 88.7, -88.7]]).astype(np.float32)
+    u = normal(rng, x.shape)
+    y = torch.empty(x.shape, device="cuda")
+    ctx.silu(dev(torch, x), y)
+    assert np.array_equal(host(y).view(np.int32), orc.silu(x).view(np.int32))
+    p = torch.empty(x.shape, device="cuda")
+    ctx.mul(y, dev(torch, u), p)
+    assert np.array_equal(host(p), orc.mul(orc.silu(x), u))
+    xt = dev(torch, x)
+    ctx.silu(xt, xt)  # in place
+    assert np.array_equal(host(xt).view(np.int32), orc.silu(x).view(np.int32))
+
+
 # ------------------------------------------------------------------- gate
 @pytest.mark.parametrize("contract", [0, 1])
 @pytest.mark.parametrize("T,d,E", [(64, 512, 4), (300, 4096, 16), (1000, 2048, 64),
