@@ -40,6 +40,9 @@ constexpr int kGemmBM = 128;
 constexpr int kGemmBN = 128;
 constexpr int kGemmBK = 16;
 constexpr int kGemmThreads = 256;
+// Default raster group (m-tiles per n-sweep); 0 = every m-tile (m-fastest),
+// the measured best for the grouped expert GEMMs on MI355X.
+constexpr int kGemmGroupM = 0;
 
 // Routing constants.
 constexpr int kPermTokens = 256;    // tokens per permutation block
@@ -68,6 +71,7 @@ struct GemmArgs {
     int32_t E;
     int32_t m_tiles;         // m-tiles covered by the grid (upper bound)
     int32_t n_tiles;
+    int32_t group_m;         // raster: m-tiles that sweep the n-tiles together
 };
 
 enum Epilogue : int { EPI_STORE = 0, EPI_BIAS = 1, EPI_SILU = 2, EPI_SWIGLU = 3 };

@@ -29,6 +29,8 @@
 // load, src/model.cu:1340-1365).
 #include "common.hpp"
 
+#include <cstdlib>
+
 namespace moe {
 namespace {
 
@@ -48,6 +50,20 @@ __device__ __forceinline__ int xcd_remap(int bid, int nb) {
     const int per = nb / kNumXcd, rem = nb % kNumXcd;
     return xcd < rem ? xcd * (per + 1) + slot
                      : rem * (per + 1) + (xcd - rem) * per + slot;
+}
+
+// Logical tile order: groups of `group` consecutive m-tiles sweep the
+// n-tiles together, `group` m-tiles per n-tile.  With group = 8 the ~64
+// workgroups an XCD runs at once cover about 8 m-tiles x 8 n-tiles, so each
+// A panel and each B panel in flight is shared by 8 of them; group = m_tiles
+// is the m-fastest order (every m-tile of one n-tile, then the next n-tile).
+__device__ __forceinline__ void tile_of(int logical, int m_tiles, int n_tiles, int group,
+                                        int& mt, int& nt) {
+    const int per_group = group * n_tiles;
+    const int g = logical / per_group, r = logical % per_group;
+    const int rows = m_tiles - g * group < group ? m_tiles - g * group : group;
+    nt = r / rows;
+    mt = g * group + r % rows;
 }
 
 // The reference's SiLU: x / (1 + float(exp(double(-x)))) (src/tensor.cu:
@@ -76,9 +92,8 @@ __global__ __launch_bounds__(kGemmThreads, 2) void gemm_kernel(const GemmArgs p)
     __shared__ __align__(16) float Bs[2][NB][BN * LDS];
 
     const int tid = threadIdx.x;
-    const int logical = xcd_remap(blockIdx.x, gridDim.x);
-    const int mt = logical % p.m_tiles;
-    const int nt = logical / p.m_tiles;
+    int mt, nt;
+    tile_of(xcd_remap(blockIdx.x, gridDim.x), p.m_tiles, p.n_tiles, p.group_m, mt, nt);
 
     // ---- which rows / which expert this workgroup owns
     int64_t row0;
@@ -279,9 +294,19 @@ void launch_vec(const GemmArgs& a, bool vec, hipStream_t s) {
 
 }  // namespace
 
-void launch_gemm(const GemmArgs& a, bool nn, bool grouped, int epi, bool vec,
+void launch_gemm(const GemmArgs& args, bool nn, bool grouped, int epi, bool vec,
                  hipStream_t s) {
-    if (a.m_tiles <= 0 || a.n_tiles <= 0) return;
+    if (args.m_tiles <= 0 || args.n_tiles <= 0) return;
+    GemmArgs a = args;
+    // Raster group (m-tiles per n-sweep).  MOE_GEMM_GROUP_M overrides the
+    // default for tuning; values outside [1, m_tiles] mean m_tiles.
+    static const int env_group = [] {
+        const char* v = std::getenv("MOE_GEMM_GROUP_M");
+        return v != nullptr ? std::atoi(v) : 0;
+    }();
+    int group = env_group != 0 ? env_group : kGemmGroupM;
+    if (group < 1 || group > a.m_tiles) group = a.m_tiles;
+    a.group_m = group;
     if (!grouped) {
         if (epi != EPI_BIAS) throw Unsupported("dense GEMM epilogue");
         if (nn) launch_vec<true, false, 1, EPI_BIAS>(a, vec, s);

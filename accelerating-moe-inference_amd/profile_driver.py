@@ -1,0 +1,71 @@
+"""Workloads to run under rocprofv3 for counter collection.
+
+    rocprofv3 --pmc FETCH_SIZE -d OUT -o copy -- python3 profile_driver.py copy --mib 1024
+    rocprofv3 --pmc FETCH_SIZE -d OUT -o c3   -- python3 profile_driver.py layer --config c3
+
+`copy` launches one elementwise kernel that reads and writes exactly
+--mib MiB (torch.neg into a second buffer): the calibration of the TCC byte
+counters against a known traffic.  `layer` runs --steps MoE layer forwards
+of a bench configuration (same seeded data as bench.py) after one warm-up.
+"""
+from __future__ import annotations
+
+import argparse
+import importlib.util
+import os
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("what", choices=["copy", "layer"])
+    ap.add_argument("--mib", type=int, default=1024)
+    ap.add_argument("--config", default="c3")
+    ap.add_argument("--steps", type=int, default=2)
+    args = ap.parse_args()
+
+    import torch
+
+    if args.what == "copy":
+        n = args.mib * (1 << 20) // 4
+        a = torch.ones(n, device="cuda")
+        b = torch.empty_like(a)
+        torch.cuda.synchronize()
+        torch.neg(a, out=b)
+        torch.cuda.synchronize()
+        print(f"copy: read {args.mib} MiB, wrote {args.mib} MiB", flush=True)
+        return
+
+    spec = importlib.util.spec_from_file_location("bench", os.path.join(ROOT, "bench.py"))
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    cfg = bench.CONFIGS[args.config]
+    pkg = bench.load_pkg()
+    T, d, E, k, d_ff = cfg["T"], cfg["d"], cfg["E"], cfg["k"], cfg["d_ff"]
+    g = torch.Generator(device="cuda").manual_seed(0)
+    x = torch.randn((T, d), device="cuda", generator=g)
+    weights = {
+        "gate_w": torch.randn((E, d), device="cuda", generator=g) * 0.02,
+        "w1": torch.randn((E, d_ff, d), device="cuda", generator=g) * 0.02,
+        "w3": torch.randn((E, d_ff, d), device="cuda", generator=g) * 0.02,
+        "w2": torch.randn((E, d, d_ff), device="cuda", generator=g) * 0.02,
+        "expert_bias": None,
+    }
+    if cfg["zipf"] is not None:
+        weights["expert_bias"] = torch.from_numpy(bench.zipf_bias(E, cfg["zipf"])).cuda()
+    y = torch.empty((T, d), device="cuda")
+    desc = pkg.make_desc(T, d, E, k, d_ff, act=pkg.ACT_SWIGLU, router=pkg.ROUTER_SOFTMAX_TOPK)
+    ctx = pkg.Context(0)
+    ctx.reserve(desc)
+    for i in range(1 + args.steps):
+        ctx.layer_forward(desc, weights, x, y)
+        torch.cuda.synchronize()
+        print(f"layer {args.config} step {i} done", flush=True)
+    ctx.close()
+
+
+if __name__ == "__main__":
+    sys.exit(main())
