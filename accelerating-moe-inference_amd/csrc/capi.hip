@@ -92,7 +92,8 @@ void sgemm(moe_ctx* ctx, bool nn, const float* A, const float* B,
         check_ptr(A, "A");
         check_ptr(B, "B");
     }
-    const int64_t mt = moe::ceil_div(M, moe::kGemmBM), ntl = moe::ceil_div(N, moe::kGemmBN);
+    const moe::GemmTile tile = moe::gemm_tile(moe::GemmUse::Dense);
+    const int64_t mt = moe::ceil_div(M, tile.bm), ntl = moe::ceil_div(N, tile.bn);
     moe::require(mt * ntl <= INT32_MAX, "GEMM grid too large");
     DeviceScope dev(ctx->device);
     moe::GemmArgs a{};
@@ -121,16 +122,21 @@ void sgemm(moe_ctx* ctx, bool nn, const float* A, const float* B,
 }
 
 // ---- expert FFN (the part shared by moe_expert_ffn_grouped and the layer)
+// Upper bound of sum_e ceil(n_e / bm) over the experts: the grouped
+// kernels launch this many m-tiles and the surplus ones exit at once.
+int64_t grouped_m_tiles(int64_t pairs, int64_t E, int bm) {
+    return std::min<int64_t>(moe::ceil_div(pairs, bm) + E, pairs);
+}
+
 void expert_ffn(moe_ctx* ctx, const float* x, const int32_t* perm,
-                const int32_t* offsets, const int32_t* tile_start,
-                const float* w1, const float* w3, const float* w2, int act,
-                int64_t T, int64_t k, int64_t d, int64_t d_ff, int64_t E,
-                float* h, float* out_rows, hipStream_t s) {
+                const int32_t* offsets, const float* w1, const float* w3,
+                const float* w2, int act, int64_t T, int64_t k, int64_t d,
+                int64_t d_ff, int64_t E, float* h, float* out_rows, hipStream_t s) {
     const int64_t pairs = T * k;
     if (pairs == 0 || d == 0) return;
-    const int64_t m_tiles = std::min<int64_t>(moe::ceil_div(pairs, moe::kGemmBM) + E, pairs);
     const bool swiglu = act == MOE_ACT_SWIGLU;
     if (d_ff > 0) {
+        const moe::GemmTile tile = moe::gemm_tile(moe::GemmUse::W13);
         moe::GemmArgs a{};
         a.A = x;
         a.lda = d;
@@ -145,17 +151,17 @@ void expert_ffn(moe_ctx* ctx, const float* x, const int32_t* perm,
         a.N = d_ff;
         a.K = d;
         a.offsets = offsets;
-        a.tile_start = tile_start;
         a.rows_limit = pairs;
         a.E = static_cast<int32_t>(E);
-        a.m_tiles = static_cast<int32_t>(m_tiles);
-        a.n_tiles = static_cast<int32_t>(moe::ceil_div(d_ff, moe::kGemmBN));
+        a.m_tiles = static_cast<int32_t>(grouped_m_tiles(pairs, E, tile.bm));
+        a.n_tiles = static_cast<int32_t>(moe::ceil_div(d_ff, tile.bn));
         moe::require(int64_t(a.m_tiles) * a.n_tiles <= INT32_MAX, "w13 grid too large");
         const bool vec = d % 4 == 0 && aligned16(x) && aligned16(w1) && (!swiglu || aligned16(w3));
         ctx->launch(swiglu ? "expert_w13_swiglu" : "expert_w1_silu", s, [&] {
             moe::launch_gemm(a, false, true, swiglu ? moe::EPI_SWIGLU : moe::EPI_SILU, vec, s);
         });
     }
+    const moe::GemmTile tile = moe::gemm_tile(moe::GemmUse::W2);
     moe::GemmArgs b{};
     b.A = d_ff > 0 ? h : out_rows;
     b.lda = d_ff;
@@ -168,11 +174,10 @@ void expert_ffn(moe_ctx* ctx, const float* x, const int32_t* perm,
     b.N = d;
     b.K = d_ff;
     b.offsets = offsets;
-    b.tile_start = tile_start;
     b.rows_limit = pairs;
     b.E = static_cast<int32_t>(E);
-    b.m_tiles = static_cast<int32_t>(m_tiles);
-    b.n_tiles = static_cast<int32_t>(moe::ceil_div(d, moe::kGemmBN));
+    b.m_tiles = static_cast<int32_t>(grouped_m_tiles(pairs, E, tile.bm));
+    b.n_tiles = static_cast<int32_t>(moe::ceil_div(d, tile.bn));
     moe::require(int64_t(b.m_tiles) * b.n_tiles <= INT32_MAX, "w2 grid too large");
     const bool vec = d_ff % 4 == 0 && aligned16(h) && aligned16(w2);
     ctx->launch("expert_w2", s, [&] { moe::launch_gemm(b, false, true, moe::EPI_STORE, vec, s); });
@@ -197,7 +202,6 @@ struct LayerWs {
     float* w;
     int32_t* counts;
     int32_t* offsets;
-    int32_t* tile_start;
     int32_t* perm;
     int32_t* inv;
     float* h;
@@ -215,7 +219,6 @@ LayerWs carve_layer(void* base, const moe_layer_desc& d) {
     w.w = c.take<float>(pairs);
     w.counts = c.take<int32_t>(d.E * nb);
     w.offsets = c.take<int32_t>(d.E + 1);
-    w.tile_start = c.take<int32_t>(d.E + 1);
     w.perm = c.take<int32_t>(pairs);
     w.inv = c.take<int32_t>(pairs);
     w.h = c.take<float>(pairs * d.d_ff);
@@ -439,7 +442,7 @@ int moe_permute(moe_ctx* ctx, const int32_t* topk_idx, int64_t T, int64_t k, int
         auto* counts = static_cast<int32_t*>(ctx->workspace(static_cast<size_t>(E * nb + 1) * 4));
         ctx->launch("perm_count", s, [&] { moe::launch_perm_count(topk_idx, T, k, E, counts, s); });
         ctx->launch("perm_scan", s,
-                    [&] { moe::launch_perm_scan(counts, nb, E, expert_offsets, nullptr, s); });
+                    [&] { moe::launch_perm_scan(counts, nb, E, expert_offsets, s); });
         ctx->launch("perm_place", s,
                     [&] { moe::launch_perm_place(topk_idx, T, k, E, counts, perm, inv, s); });
     });
@@ -468,10 +471,8 @@ int moe_expert_ffn_grouped(moe_ctx* ctx, const float* x, const int32_t* perm,
         }
         DeviceScope dev(ctx->device);
         hipStream_t s = as_stream(stream);
-        auto* tile_start = static_cast<int32_t*>(ctx->workspace(static_cast<size_t>(E + 1) * 4));
-        ctx->launch("tile_start", s, [&] { moe::launch_tile_start(expert_offsets, E, tile_start, s); });
-        expert_ffn(ctx, x, perm, expert_offsets, tile_start, w1, w3, w2, act, T, k, d, d_ff, E, h,
-                   out_rows, s);
+        expert_ffn(ctx, x, perm, expert_offsets, w1, w3, w2, act, T, k, d, d_ff, E, h, out_rows,
+                   s);
     });
 }
 
@@ -538,13 +539,13 @@ int moe_layer_forward(moe_ctx* ctx, const moe_layer_desc* desc,
         });
         ctx->launch("perm_count", s, [&] { moe::launch_perm_count(idx, D.T, D.k, D.E, ws.counts, s); });
         ctx->launch("perm_scan", s, [&] {
-            moe::launch_perm_scan(ws.counts, nb, D.E, ws.offsets, ws.tile_start, s);
+            moe::launch_perm_scan(ws.counts, nb, D.E, ws.offsets, s);
         });
         ctx->launch("perm_place", s, [&] {
             moe::launch_perm_place(idx, D.T, D.k, D.E, ws.counts, ws.perm, ws.inv, s);
         });
-        expert_ffn(ctx, x, ws.perm, ws.offsets, ws.tile_start, weights->w1, weights->w3,
-                   weights->w2, D.act, D.T, D.k, D.d, D.d_ff, D.E, ws.h, ws.out_rows, s);
+        expert_ffn(ctx, x, ws.perm, ws.offsets, weights->w1, weights->w3, weights->w2, D.act,
+                   D.T, D.k, D.d, D.d_ff, D.E, ws.h, ws.out_rows, s);
         ctx->launch("combine", s, [&] {
             moe::launch_combine(ws.out_rows, idx, w, ws.inv, nullptr, y, D.T, D.k, D.d,
                                 D.T * D.k, D.contract, s);

@@ -35,14 +35,16 @@ inline void require(bool ok, const std::string& what) {
 
 constexpr int kNumXcd = 8;  // MI355X: 8 XCDs, workgroups dealt round-robin
 
-// GEMM tile constants shared by the host (grid sizing) and the kernels.
-constexpr int kGemmBM = 128;
-constexpr int kGemmBN = 128;
-constexpr int kGemmBK = 16;
-constexpr int kGemmThreads = 256;
-// Default raster group (m-tiles per n-sweep); 0 = every m-tile (m-fastest),
-// the measured best for the grouped expert GEMMs on MI355X.
+// Default GEMM raster group (m-tiles per n-sweep); 0 = every m-tile
+// (m-fastest), the measured best for the grouped expert GEMMs on MI355X.
 constexpr int kGemmGroupM = 0;
+
+// The GEMM uses whose tile shape the host needs for grid sizing.
+enum class GemmUse { Dense, W13, W2 };
+struct GemmTile {
+    int bm, bn;
+};
+GemmTile gemm_tile(GemmUse use);
 
 // Routing constants.
 constexpr int kPermTokens = 256;    // tokens per permutation block
@@ -66,7 +68,6 @@ struct GemmArgs {
     int64_t ldc;
     int64_t M, N, K;         // dense: M rows; grouped: per-expert N, K
     const int32_t* offsets;  // grouped: expert_offsets[E+1]
-    const int32_t* tile_start; // grouped: first m-tile of each expert [E+1]
     int64_t rows_limit;      // grouped: packed rows of A / C (T*k); bounds every tile
     int32_t E;
     int32_t m_tiles;         // m-tiles covered by the grid (upper bound)
@@ -88,11 +89,9 @@ void launch_route(const float* logits, const float* bias, int64_t T, int64_t E,
 void launch_perm_count(const int32_t* idx, int64_t T, int64_t k, int64_t E,
                        int32_t* counts, hipStream_t s);
 void launch_perm_scan(int32_t* counts, int64_t nblocks, int64_t E,
-                      int32_t* offsets, int32_t* tile_start, hipStream_t s);
+                      int32_t* offsets, hipStream_t s);
 void launch_perm_place(const int32_t* idx, int64_t T, int64_t k, int64_t E,
                        const int32_t* base, int32_t* perm, int32_t* inv,
-                       hipStream_t s);
-void launch_tile_start(const int32_t* offsets, int64_t E, int32_t* tile_start,
                        hipStream_t s);
 void launch_silu(const float* x, float* y, int64_t n, hipStream_t s);
 void launch_mul(const float* a, const float* b, float* c, int64_t n, hipStream_t s);

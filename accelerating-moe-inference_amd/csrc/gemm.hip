@@ -8,17 +8,17 @@
 //             through the permutation, one launch for all experts:
 //             w1/w3 with the SwiGLU (or SiLU) epilogue, then w2.
 //
-// Workgroup: 256 threads = 4 wave64s in a 2x2 arrangement, 128x128 output
-// tile, each wave a 64x64 quadrant held as 2x2 MFMA blocks of 32x32 in
-// accumulator registers.  K advances 16 at a time through double-buffered
-// LDS tiles ([rows][16+4] floats: the 4-float pad makes the 16-byte fragment
-// reads and writes bank-conflict free), with the next tile's global loads in
-// flight while the matrix cores work on the current one: one barrier per
-// K step.
+// A workgroup of WM x WN wave64s computes a BM x BN output tile (per B
+// operand); each wave holds its (BM/WM) x (BN/WN) quadrant as 32x32 MFMA
+// blocks in accumulator registers.  K advances BK at a time through
+// double-buffered LDS tiles ([rows][BK+4] floats: the 4-float pad makes the
+// 16-byte fragment reads conflict-free), with the next tile's global loads
+// in flight in registers while the matrix cores work on the current one:
+// one barrier per K step.
 //
-// Within a 16-wide K step, lane half h (lanes 32h..32h+31) feeds K columns
-// 8h..8h+7, so each lane fetches its A and B fragments for 4 MFMAs with one
-// 16-byte LDS read; both operands use the same column order, so every
+// Within each 16-column slice of a K step, lane half h (lanes 32h..32h+31)
+// feeds columns 8h..8h+7, so one 16-byte LDS read gives a lane its A (or B)
+// operand for 4 MFMAs; both operands use the same column order, so every
 // product pairs the same k.  Products are accumulated in fp32 by the MFMA
 // unit; the order differs from the reference's single sequential
 // accumulator, within the 1e-4 relative-error budget of the activations.
@@ -31,16 +31,69 @@
 
 #include <cstdlib>
 
+// Tile configurations (index into CFG_TABLE below) chosen per use; the
+// defaults are the measured best on MI355X and can be overridden at build
+// time for tuning (-DMOE_W13_CFG=n ...).
+#ifndef MOE_W13_CFG
+#define MOE_W13_CFG 0
+#endif
+#ifndef MOE_W2_CFG
+#define MOE_W2_CFG 0
+#endif
+#ifndef MOE_DENSE_CFG
+#define MOE_DENSE_CFG 0
+#endif
+// Main-loop schedule per use, a bit mask of SCHED_* (below).  Defaults are
+// the measured best on MI355X: direct loads for both expert GEMMs, raised
+// priority for w1/w3 only (it slows w2, which runs 4 waves per SIMD).
+#ifndef MOE_W13_SCHED
+#define MOE_W13_SCHED 7
+#endif
+#ifndef MOE_W2_SCHED
+#define MOE_W2_SCHED 6
+#endif
+#ifndef MOE_DENSE_SCHED
+#define MOE_DENSE_SCHED 6
+#endif
+
 namespace moe {
 namespace {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int BM = kGemmBM;
-constexpr int BN = kGemmBN;
-constexpr int BK = kGemmBK;
-constexpr int LDS = BK + 4;
+// Schedule bits: SCHED_PRIO raises the wave's issue priority during its
+// matrix-core burst; SCHED_MIDSTORE (register-staged path) stores the next
+// tile to LDS halfway through the burst instead of after it; SCHED_DIRECT
+// takes the direct global->LDS path where it applies.
+constexpr int SCHED_PRIO = 1, SCHED_MIDSTORE = 2, SCHED_DIRECT = 4;
+
+template <int BM_, int BN_, int BK_, int WM_, int WN_>
+struct Cfg {
+    static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
+    static constexpr int THREADS = 64 * WM * WN;
+    static constexpr int FM = BM / WM / 32;   // 32x32 blocks per wave along m
+    static constexpr int FN = BN / WN / 32;   // ... along n (per B operand)
+    static constexpr int LDS = BK + 4;        // LDS row stride in floats
+    static constexpr int KQ = BK / 4;         // 16-byte chunks per row and K step
+    static constexpr int A_LD = BM * KQ / THREADS;  // A chunks per thread
+    static constexpr int B_LD = BN * KQ / THREADS;  // B chunks per thread (per operand)
+    static_assert(FM >= 1 && FN >= 1 && BM % (32 * WM) == 0 && BN % (32 * WN) == 0, "tile");
+    static_assert(BK % 16 == 0, "K step is a multiple of 16");
+    static_assert(A_LD * THREADS == BM * KQ && B_LD * THREADS == BN * KQ && A_LD >= 1 &&
+                      B_LD >= 1,
+                  "staging divides evenly");
+};
+
+template <int ID> struct CfgOf;
+template <> struct CfgOf<0> { using T = Cfg<128, 128, 16, 2, 2>; };
+template <> struct CfgOf<1> { using T = Cfg<128, 128, 32, 2, 2>; };
+template <> struct CfgOf<2> { using T = Cfg<256, 128, 16, 4, 2>; };
+template <> struct CfgOf<3> { using T = Cfg<128, 64, 16, 2, 2>; };
+template <> struct CfgOf<4> { using T = Cfg<128, 256, 16, 2, 2>; };
+template <> struct CfgOf<5> { using T = Cfg<256, 128, 32, 4, 2>; };
+template <> struct CfgOf<6> { using T = Cfg<256, 256, 16, 4, 2>; };
+template <> struct CfgOf<7> { using T = Cfg<64, 128, 16, 1, 2>; };
 
 // Workgroup ids are dealt round-robin over the XCDs.  Renumber them so each
 // XCD works through a contiguous run of logical tiles: tiles that share an
@@ -66,6 +119,42 @@ __device__ __forceinline__ void tile_of(int logical, int m_tiles, int n_tiles, i
     mt = g * group + r % rows;
 }
 
+// Grouped GEMMs: the expert owning m-tile `mt` when each expert e is split
+// into ceil(n_e / BM) tiles in expert order.  Every wave computes it with a
+// wave-wide scan of the per-expert tile counts (64 experts per step), so no
+// tile table is needed and each kernel may use its own BM.  Returns false
+// for the surplus tiles of the worst-case grid.
+template <int BM>
+__device__ __forceinline__ bool find_expert(const int32_t* __restrict__ offsets, int E, int mt,
+                                            int& expert, int& first_tile) {
+    const int lane = threadIdx.x & 63;
+    int carry = 0;
+    for (int e0 = 0; e0 < E; e0 += 64) {
+        const int e = e0 + lane;
+        int cnt = 0;
+        if (e < E) {
+            const int n = offsets[e + 1] - offsets[e];
+            cnt = n > 0 ? (n + BM - 1) / BM : 0;
+        }
+        int incl = cnt;
+        for (int off = 1; off < 64; off <<= 1) {
+            const int o = __shfl_up(incl, off, 64);
+            if (lane >= off) incl += o;
+        }
+        const int start = carry + incl - cnt;
+        const bool hit = cnt > 0 && mt >= start && mt < start + cnt;
+        const unsigned long long m = __ballot(hit);
+        if (m != 0ull) {
+            const int l = __ffsll(static_cast<long long>(m)) - 1;
+            expert = e0 + l;
+            first_tile = __shfl(start, l, 64);
+            return true;
+        }
+        carry += __shfl(incl, 63, 64);
+    }
+    return false;
+}
+
 // The reference's SiLU: x / (1 + float(exp(double(-x)))) (src/tensor.cu:
 // 132-134,169-173); exp in double, one rounding to float.
 __device__ __forceinline__ float silu_ref(float g) {
@@ -86,8 +175,10 @@ __device__ __forceinline__ f32x4 load_k4(const float* row, int64_t k, int64_t K)
     return v;
 }
 
-template <bool NN, bool VEC, bool GROUPED, int NB, int EPI>
-__global__ __launch_bounds__(kGemmThreads, 2) void gemm_kernel(const GemmArgs p) {
+template <class C, int SCHED, bool NN, bool VEC, bool GROUPED, int NB, int EPI>
+__global__ __launch_bounds__(C::THREADS, 2) void gemm_kernel(const GemmArgs p) {
+    constexpr int BM = C::BM, BN = C::BN, BK = C::BK, LDS = C::LDS, KQ = C::KQ;
+    constexpr int FM = C::FM, FN = C::FN;
     __shared__ __align__(16) float As[2][BM * LDS];
     __shared__ __align__(16) float Bs[2][NB][BN * LDS];
 
@@ -100,19 +191,15 @@ __global__ __launch_bounds__(kGemmThreads, 2) void gemm_kernel(const GemmArgs p)
     int rows;
     const float* B[NB];
     if (GROUPED) {
-        if (mt >= p.tile_start[p.E]) return;  // surplus tile of the worst-case grid
-        int lo = 0, hi = p.E;                 // last expert whose first tile <= mt
-        while (hi - lo > 1) {
-            const int mid = (lo + hi) >> 1;
-            if (p.tile_start[mid] <= mt) lo = mid; else hi = mid;
-        }
-        int64_t e_end = p.offsets[lo + 1];
+        int e, first;
+        if (!find_expert<BM>(p.offsets, p.E, mt, e, first)) return;  // surplus tile
+        int64_t e_end = p.offsets[e + 1];
         e_end = e_end < p.rows_limit ? e_end : p.rows_limit;
-        row0 = p.offsets[lo] + static_cast<int64_t>(mt - p.tile_start[lo]) * BM;
+        row0 = p.offsets[e] + static_cast<int64_t>(mt - first) * BM;
         if (row0 < 0 || row0 >= e_end) return;  // only reachable with inconsistent offsets
         rows = static_cast<int>(e_end - row0 < BM ? e_end - row0 : BM);
-        B[0] = p.B0 + lo * p.b_expert_stride;
-        if (NB == 2) B[NB - 1] = p.B1 + lo * p.b_expert_stride;
+        B[0] = p.B0 + e * p.b_expert_stride;
+        if (NB == 2) B[NB - 1] = p.B1 + e * p.b_expert_stride;
     } else {
         row0 = static_cast<int64_t>(mt) * BM;
         rows = static_cast<int>(p.M - row0 < BM ? p.M - row0 : BM);
@@ -122,14 +209,14 @@ __global__ __launch_bounds__(kGemmThreads, 2) void gemm_kernel(const GemmArgs p)
     const int64_t n0 = static_cast<int64_t>(nt) * BN;
     const int64_t N = p.N, K = p.K;
 
-    // ---- global -> register staging assignment
-    // A (always [rows, K]): thread covers rows lrow and lrow + 64, 4 columns.
-    const int lrow = tid >> 2;
-    const int lk = (tid & 3) * 4;
-    const float* arow[2];
+    // ---- global -> register staging.  Chunk c = tid + THREADS*i of a tile:
+    // A and NT B rows are c / KQ, the 4 columns (c % KQ) * 4; consecutive
+    // threads read consecutive 16 bytes of a row.
+    const float* arow[C::A_LD];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        int r = lrow + 64 * i;
+    for (int i = 0; i < C::A_LD; ++i) {
+        const int c = tid + C::THREADS * i;
+        int r = c / KQ;
         r = r < rows ? r : rows - 1;  // rows past the edge: any valid row, masked at the store
         int64_t src = row0 + r;
         if (GROUPED && p.gather != nullptr) {
@@ -139,108 +226,110 @@ __global__ __launch_bounds__(kGemmThreads, 2) void gemm_kernel(const GemmArgs p)
         }
         arow[i] = p.A + src * p.lda;
     }
-    // B, NT ([N, K]): like A.  NN ([K, N]): thread owns one column and 8 of
-    // the 16 k rows (kq..kq+3 and 8+kq..8+kq+3), transposed into LDS.
-    const float* bptr[NB][2];
-    const int ncol = tid & (BN - 1);
-    const int kq = (tid >> 7) * 4;
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-        if (!NN) {
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                int64_t n = n0 + lrow + 64 * i;
-                n = n < N ? n : N - 1;
-                bptr[nb][i] = B[nb] + n * p.ldb;
-            }
-        } else {
-            int64_t n = n0 + ncol;
-            n = n < N ? n : N - 1;
-            bptr[nb][0] = B[nb] + n;
-            bptr[nb][1] = B[nb] + n;
-        }
-    }
-
-    f32x4 ra[2], rb[NB][2];
-    auto gload = [&](int64_t k0) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i) ra[i] = load_k4<VEC>(arow[i], k0 + lk, K);
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            if (!NN) {
-#pragma unroll
-                for (int i = 0; i < 2; ++i) rb[nb][i] = load_k4<VEC>(bptr[nb][i], k0 + lk, K);
-            } else {
-#pragma unroll
-                for (int h = 0; h < 2; ++h)
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const int64_t k = k0 + 8 * h + kq + j;
-                        rb[nb][h][j] = k < K ? bptr[nb][h][k * p.ldb] : 0.0f;
-                    }
-            }
-        }
-    };
-    auto lstore = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-            *reinterpret_cast<f32x4*>(&As[buf][(lrow + 64 * i) * LDS + lk]) = ra[i];
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            if (!NN) {
-#pragma unroll
-                for (int i = 0; i < 2; ++i)
-                    *reinterpret_cast<f32x4*>(&Bs[buf][nb][(lrow + 64 * i) * LDS + lk]) = rb[nb][i];
-            } else {
-                *reinterpret_cast<f32x4*>(&Bs[buf][nb][ncol * LDS + kq]) = rb[nb][0];
-                *reinterpret_cast<f32x4*>(&Bs[buf][nb][ncol * LDS + 8 + kq]) = rb[nb][1];
-            }
-        }
-    };
-
-    // ---- matrix-core main loop
-    const int lane = tid & 63, wave = tid >> 6;
-    const int wm = wave & 1, wn = wave >> 1;
-    const int lr = lane & 31, lh = lane >> 5;
-
-    f32x16 acc[NB][2][2];
+    // B, NT ([N, K]): like A.  NN ([K, N]): chunk c is 4 consecutive k rows of
+    // column c % BN, k quad c / BN, transposed into LDS.
+    const float* bptr[NB][C::B_LD];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-        for (int bi = 0; bi < 2; ++bi)
-#pragma unroll
-            for (int bj = 0; bj < 2; ++bj)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[nb][bi][bj][r] = 0.0f;
+        for (int i = 0; i < C::B_LD; ++i) {
+            const int c = tid + C::THREADS * i;
+            int64_t n = NN ? n0 + c % BN : n0 + c / KQ;
+            n = n < N ? n : N - 1;
+            bptr[nb][i] = NN ? B[nb] + n : B[nb] + n * p.ldb;
+        }
 
-    auto compute = [&](int buf) {
-        f32x4 a[2][2], b[NB][2][2];
+    f32x4 ra[C::A_LD], rb[NB][C::B_LD];
+    auto gload = [&](int64_t k0) {
 #pragma unroll
-        for (int bi = 0; bi < 2; ++bi) {
-            const float* src = &As[buf][(wm * 64 + bi * 32 + lr) * LDS + 8 * lh];
-            a[bi][0] = *reinterpret_cast<const f32x4*>(src);
-            a[bi][1] = *reinterpret_cast<const f32x4*>(src + 4);
+        for (int i = 0; i < C::A_LD; ++i)
+            ra[i] = load_k4<VEC>(arow[i], k0 + ((tid + C::THREADS * i) % KQ) * 4, K);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int i = 0; i < C::B_LD; ++i) {
+                const int c = tid + C::THREADS * i;
+                if (!NN) {
+                    rb[nb][i] = load_k4<VEC>(bptr[nb][i], k0 + (c % KQ) * 4, K);
+                } else {
+                    const int64_t kb = k0 + (c / BN) * 4;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        rb[nb][i][j] = kb + j < K ? bptr[nb][i][(kb + j) * p.ldb] : 0.0f;
+                }
+            }
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < C::A_LD; ++i) {
+            const int c = tid + C::THREADS * i;
+            *reinterpret_cast<f32x4*>(&As[buf][(c / KQ) * LDS + (c % KQ) * 4]) = ra[i];
         }
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-            for (int bj = 0; bj < 2; ++bj) {
-                const float* src = &Bs[buf][nb][(wn * 64 + bj * 32 + lr) * LDS + 8 * lh];
-                b[nb][bj][0] = *reinterpret_cast<const f32x4*>(src);
-                b[nb][bj][1] = *reinterpret_cast<const f32x4*>(src + 4);
+            for (int i = 0; i < C::B_LD; ++i) {
+                const int c = tid + C::THREADS * i;
+                const int at = NN ? (c % BN) * LDS + (c / BN) * 4 : (c / KQ) * LDS + (c % KQ) * 4;
+                *reinterpret_cast<f32x4*>(&Bs[buf][nb][at]) = rb[nb][i];
+            }
+    };
+
+    // ---- matrix-core main loop
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave % C::WM, wn = wave / C::WM;
+    const int lr = lane & 31, lh = lane >> 5;
+    const int arow0 = wm * (BM / C::WM), bcol0 = wn * (BN / C::WN);
+
+    f32x16 acc[NB][FM][FN];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int bi = 0; bi < FM; ++bi)
+#pragma unroll
+            for (int bj = 0; bj < FN; ++bj)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[nb][bi][bj][r] = 0.0f;
+
+    // One K step on LDS buffer `buf`.  `mid` runs between the two halves of
+    // the matrix-core burst (the schedule may place the next tile's LDS
+    // stores there, SCHED_MIDSTORE); SCHED_PRIO raises the burst's priority.
+    auto compute = [&](int buf, auto&& mid) {
+        if (SCHED & SCHED_PRIO) __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+        for (int sl = 0; sl < BK / 16; ++sl) {  // 16-column slices of the K step
+            f32x4 a[FM][2], b[NB][FN][2];
+#pragma unroll
+            for (int bi = 0; bi < FM; ++bi) {
+                const float* src = &As[buf][(arow0 + bi * 32 + lr) * LDS + sl * 16 + 8 * lh];
+                a[bi][0] = *reinterpret_cast<const f32x4*>(src);
+                a[bi][1] = *reinterpret_cast<const f32x4*>(src + 4);
             }
 #pragma unroll
-        for (int q = 0; q < 2; ++q)
+            for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-            for (int s = 0; s < 4; ++s)
+                for (int bj = 0; bj < FN; ++bj) {
+                    const float* src =
+                        &Bs[buf][nb][(bcol0 + bj * 32 + lr) * LDS + sl * 16 + 8 * lh];
+                    b[nb][bj][0] = *reinterpret_cast<const f32x4*>(src);
+                    b[nb][bj][1] = *reinterpret_cast<const f32x4*>(src + 4);
+                }
 #pragma unroll
-                for (int nb = 0; nb < NB; ++nb)
+            for (int q = 0; q < 2; ++q) {
+                if (sl == BK / 16 - 1 && q == 1) mid();
 #pragma unroll
-                    for (int bi = 0; bi < 2; ++bi)
+                for (int s = 0; s < 4; ++s)
 #pragma unroll
-                        for (int bj = 0; bj < 2; ++bj)
-                            acc[nb][bi][bj] = __builtin_amdgcn_mfma_f32_32x32x2f32(
-                                a[bi][q][s], b[nb][bj][q][s], acc[nb][bi][bj], 0, 0, 0);
+                    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                        for (int bi = 0; bi < FM; ++bi)
+#pragma unroll
+                            for (int bj = 0; bj < FN; ++bj)
+                                acc[nb][bi][bj] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                                    a[bi][q][s], b[nb][bj][q][s], acc[nb][bi][bj], 0, 0, 0);
+            }
+        }
+        if (SCHED & SCHED_PRIO) __builtin_amdgcn_s_setprio(0);
     };
 
     const int64_t nk = (K + BK - 1) / BK;
@@ -250,9 +339,16 @@ __global__ __launch_bounds__(kGemmThreads, 2) void gemm_kernel(const GemmArgs p)
         __syncthreads();
         for (int64_t kt = 0; kt < nk; ++kt) {
             const int cur = static_cast<int>(kt & 1);
-            if (kt + 1 < nk) gload((kt + 1) * BK);
-            compute(cur);
-            if (kt + 1 < nk) lstore(cur ^ 1);
+            const bool more = kt + 1 < nk;
+            if (more) gload((kt + 1) * BK);
+            if (SCHED & SCHED_MIDSTORE) {
+                compute(cur, [&] {
+                    if (more) lstore(cur ^ 1);
+                });
+            } else {
+                compute(cur, [] {});
+                if (more) lstore(cur ^ 1);
+            }
             __syncthreads();
         }
     }
@@ -260,13 +356,13 @@ __global__ __launch_bounds__(kGemmThreads, 2) void gemm_kernel(const GemmArgs p)
     // ---- epilogue.  32x32 accumulator layout: lane l, register r holds
     // row 8*(r/4) + 4*(l/32) + r%4, column l%32 of its block.
 #pragma unroll
-    for (int bi = 0; bi < 2; ++bi)
+    for (int bi = 0; bi < FM; ++bi)
 #pragma unroll
-        for (int bj = 0; bj < 2; ++bj)
+        for (int bj = 0; bj < FN; ++bj)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int i = wm * 64 + bi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                const int64_t n = n0 + wn * 64 + bj * 32 + lr;
+                const int i = arow0 + bi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                const int64_t n = n0 + bcol0 + bj * 32 + lr;
                 if (i < rows && n < N) {
                     float v = acc[0][bi][bj][r];
                     if (EPI == EPI_BIAS) {
@@ -281,18 +377,221 @@ __global__ __launch_bounds__(kGemmThreads, 2) void gemm_kernel(const GemmArgs p)
             }
 }
 
-template <bool NN, bool GROUPED, int NB, int EPI>
-void launch_vec(const GemmArgs& a, bool vec, hipStream_t s) {
-    const dim3 grid(static_cast<unsigned>(a.m_tiles) * static_cast<unsigned>(a.n_tiles));
-    if (vec)
-        hipLaunchKernelGGL((gemm_kernel<NN, true, GROUPED, NB, EPI>), grid,
-                           dim3(kGemmThreads), 0, s, a);
-    else
-        hipLaunchKernelGGL((gemm_kernel<NN, false, GROUPED, NB, EPI>), grid,
-                           dim3(kGemmThreads), 0, s, a);
+// ---------------------------------------------------------------------------
+// NT GEMM with direct global->LDS loads (gfx950 global_load_lds_dwordx4).
+//
+// Lane L of a load instruction writes its 16 bytes at LDS base + 16*L, from
+// any global address it chooses, so each lane fetches the chunk that belongs
+// at its slot: tiles are stored unpadded, 4 chunks of 16 bytes per row of
+// the 16-wide K step, chunk c of row r at slot c ^ ((r >> 2) & 3).  The
+// swizzle keeps the 16-byte fragment reads conflict-free.  The data goes
+// from L2 straight to LDS -- no staging registers, no LDS store
+// instructions -- and lands while the matrix cores run: each K step reads
+// all fragments of the current stage, issues the next stage's loads, runs
+// the MFMA burst, then waits for its loads and meets the other waves at the
+// barrier.  Requires K % 16 == 0 and 16-byte aligned rows.
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) const void glb_void;
+
+__device__ __forceinline__ int swz(int row) { return (row >> 2) & 3; }
+
+template <class C, int SCHED, bool GROUPED, int NB, int EPI>
+__global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmArgs p) {
+    constexpr int BM = C::BM, BN = C::BN, BK = C::BK;
+    constexpr int FM = C::FM, FN = C::FN;
+    constexpr int NW = C::THREADS / 64;
+    constexpr int A_INS = BM / 16 / NW;  // 1 KiB load instructions per wave, A
+    constexpr int B_INS = BN / 16 / NW;  // ... per B operand
+    static_assert(BK == 16, "direct path: 16-wide K steps");
+    static_assert(A_INS * NW * 16 == BM && B_INS * NW * 16 == BN, "load split");
+    __shared__ __align__(16) float As[2][BM * BK];
+    __shared__ __align__(16) float Bs[2][NB][BN * BK];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    int mt, nt;
+    tile_of(xcd_remap(blockIdx.x, gridDim.x), p.m_tiles, p.n_tiles, p.group_m, mt, nt);
+
+    int64_t row0;
+    int rows;
+    const float* B[NB];
+    if (GROUPED) {
+        int e, first;
+        if (!find_expert<BM>(p.offsets, p.E, mt, e, first)) return;  // surplus tile
+        int64_t e_end = p.offsets[e + 1];
+        e_end = e_end < p.rows_limit ? e_end : p.rows_limit;
+        row0 = p.offsets[e] + static_cast<int64_t>(mt - first) * BM;
+        if (row0 < 0 || row0 >= e_end) return;  // only reachable with inconsistent offsets
+        rows = static_cast<int>(e_end - row0 < BM ? e_end - row0 : BM);
+        B[0] = p.B0 + e * p.b_expert_stride;
+        if (NB == 2) B[NB - 1] = p.B1 + e * p.b_expert_stride;
+    } else {
+        row0 = static_cast<int64_t>(mt) * BM;
+        rows = static_cast<int>(p.M - row0 < BM ? p.M - row0 : BM);
+        B[0] = p.B0;
+        if (NB == 2) B[NB - 1] = p.B1;
+    }
+    const int64_t n0 = static_cast<int64_t>(nt) * BN;
+    const int64_t N = p.N, K = p.K;
+
+    // Per-lane source of each load instruction: instruction j of this wave
+    // fills rows 16*J .. 16*J+15 (J = wave*INS + j); lane L writes slot L%4
+    // of row 16*J + L/4, i.e. global chunk (L%4) ^ swz(row).
+    const int lrow = lane >> 2, lslot = lane & 3;
+    const float* asrc[A_INS];
+#pragma unroll
+    for (int j = 0; j < A_INS; ++j) {
+        const int r = 16 * (wave * A_INS + j) + lrow;
+        const int rr = r < rows ? r : rows - 1;  // past the edge: a valid row, masked at the store
+        int64_t src = row0 + rr;
+        if (GROUPED && p.gather != nullptr) {
+            int64_t tok = p.gather[row0 + rr];
+            tok = tok < 0 ? 0 : (tok >= p.gather_rows ? p.gather_rows - 1 : tok);
+            src = tok;
+        }
+        asrc[j] = p.A + src * p.lda + 4 * (lslot ^ swz(r));
+    }
+    const float* bsrc[NB][B_INS];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int j = 0; j < B_INS; ++j) {
+            const int r = 16 * (wave * B_INS + j) + lrow;
+            int64_t n = n0 + r;
+            n = n < N ? n : N - 1;
+            bsrc[nb][j] = B[nb] + n * p.ldb + 4 * (lslot ^ swz(r));
+        }
+    auto issue = [&](int buf, int64_t k0) {
+#pragma unroll
+        for (int j = 0; j < A_INS; ++j)
+            __builtin_amdgcn_global_load_lds((glb_void*)(asrc[j] + k0),
+                                             (lds_void*)&As[buf][(wave * A_INS + j) * 256], 16,
+                                             0, 0);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int j = 0; j < B_INS; ++j)
+                __builtin_amdgcn_global_load_lds((glb_void*)(bsrc[nb][j] + k0),
+                                                 (lds_void*)&Bs[buf][nb][(wave * B_INS + j) * 256],
+                                                 16, 0, 0);
+    };
+
+    const int wm = wave % C::WM, wn = wave / C::WM;
+    const int lr = lane & 31, lh = lane >> 5;
+    const int arow0 = wm * (BM / C::WM), bcol0 = wn * (BN / C::WN);
+
+    f32x16 acc[NB][FM][FN];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int bi = 0; bi < FM; ++bi)
+#pragma unroll
+            for (int bj = 0; bj < FN; ++bj)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[nb][bi][bj][r] = 0.0f;
+
+    const int64_t nk = K / BK;
+    if (nk > 0) {
+        issue(0, 0);
+        __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0): this wave's loads landed
+        __syncthreads();                      // ... and every other wave's
+    }
+    for (int64_t kt = 0; kt < nk; ++kt) {
+        const int cur = static_cast<int>(kt & 1);
+        // all fragments of this K step first (no LDS read may follow the
+        // next stage's loads: they would have to wait for them)
+        f32x4 a[FM][2], b[NB][FN][2];
+#pragma unroll
+        for (int bi = 0; bi < FM; ++bi) {
+            const int r = arow0 + bi * 32 + lr;
+            const float* base = &As[cur][r * BK];
+            a[bi][0] = *reinterpret_cast<const f32x4*>(base + 4 * ((2 * lh) ^ swz(r)));
+            a[bi][1] = *reinterpret_cast<const f32x4*>(base + 4 * ((2 * lh + 1) ^ swz(r)));
+        }
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int bj = 0; bj < FN; ++bj) {
+                const int r = bcol0 + bj * 32 + lr;
+                const float* base = &Bs[cur][nb][r * BK];
+                b[nb][bj][0] = *reinterpret_cast<const f32x4*>(base + 4 * ((2 * lh) ^ swz(r)));
+                b[nb][bj][1] = *reinterpret_cast<const f32x4*>(base + 4 * ((2 * lh + 1) ^ swz(r)));
+            }
+        if (kt + 1 < nk) issue(cur ^ 1, (kt + 1) * BK);
+        if (SCHED & SCHED_PRIO) __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                    for (int bi = 0; bi < FM; ++bi)
+#pragma unroll
+                        for (int bj = 0; bj < FN; ++bj)
+                            acc[nb][bi][bj] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                                a[bi][q][s], b[nb][bj][q][s], acc[nb][bi][bj], 0, 0, 0);
+        if (SCHED & SCHED_PRIO) __builtin_amdgcn_s_setprio(0);
+        __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int bi = 0; bi < FM; ++bi)
+#pragma unroll
+        for (int bj = 0; bj < FN; ++bj)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int i = arow0 + bi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                const int64_t n = n0 + bcol0 + bj * 32 + lr;
+                if (i < rows && n < N) {
+                    float v = acc[0][bi][bj][r];
+                    if (EPI == EPI_BIAS) {
+                        if (p.bias != nullptr) v = v + p.bias[n];
+                    } else if (EPI == EPI_SILU) {
+                        v = silu_ref(v);
+                    } else if (EPI == EPI_SWIGLU) {
+                        v = silu_ref(v) * acc[NB - 1][bi][bj][r];
+                    }
+                    p.C[(row0 + i) * p.ldc + n] = v;
+                }
+            }
 }
 
+template <class C, int SCHED, bool NN, bool GROUPED, int NB, int EPI>
+void launch_cfg(const GemmArgs& a, bool vec, hipStream_t s) {
+    // direct global->LDS path: NT, 16-byte aligned rows, K a multiple of 16
+    if constexpr ((SCHED & SCHED_DIRECT) != 0 && !NN && C::BK == 16) {
+        if (vec && a.K % 16 == 0) {
+            hipLaunchKernelGGL(
+                (gemm_direct_kernel<C, SCHED, GROUPED, NB, EPI>),
+                dim3(static_cast<unsigned>(a.m_tiles) * static_cast<unsigned>(a.n_tiles)),
+                dim3(C::THREADS), 0, s, a);
+            return;
+        }
+    }
+    const dim3 grid(static_cast<unsigned>(a.m_tiles) * static_cast<unsigned>(a.n_tiles));
+    if (vec)
+        hipLaunchKernelGGL((gemm_kernel<C, SCHED, NN, true, GROUPED, NB, EPI>), grid, dim3(C::THREADS),
+                           0, s, a);
+    else
+        hipLaunchKernelGGL((gemm_kernel<C, SCHED, NN, false, GROUPED, NB, EPI>), grid, dim3(C::THREADS),
+                           0, s, a);
+}
+
+using DenseCfg = CfgOf<MOE_DENSE_CFG>::T;
+using W13Cfg = CfgOf<MOE_W13_CFG>::T;
+using W2Cfg = CfgOf<MOE_W2_CFG>::T;
+
 }  // namespace
+
+GemmTile gemm_tile(GemmUse use) {
+    switch (use) {
+        case GemmUse::Dense: return {DenseCfg::BM, DenseCfg::BN};
+        case GemmUse::W13: return {W13Cfg::BM, W13Cfg::BN};
+        default: return {W2Cfg::BM, W2Cfg::BN};
+    }
+}
 
 void launch_gemm(const GemmArgs& args, bool nn, bool grouped, int epi, bool vec,
                  hipStream_t s) {
@@ -309,15 +608,15 @@ void launch_gemm(const GemmArgs& args, bool nn, bool grouped, int epi, bool vec,
     a.group_m = group;
     if (!grouped) {
         if (epi != EPI_BIAS) throw Unsupported("dense GEMM epilogue");
-        if (nn) launch_vec<true, false, 1, EPI_BIAS>(a, vec, s);
-        else launch_vec<false, false, 1, EPI_BIAS>(a, vec, s);
+        if (nn) launch_cfg<DenseCfg, MOE_DENSE_SCHED, true, false, 1, EPI_BIAS>(a, vec, s);
+        else launch_cfg<DenseCfg, MOE_DENSE_SCHED, false, false, 1, EPI_BIAS>(a, vec, s);
         return;
     }
     if (nn) throw Unsupported("grouped NN GEMM");
     switch (epi) {
-        case EPI_SWIGLU: launch_vec<false, true, 2, EPI_SWIGLU>(a, vec, s); break;
-        case EPI_SILU: launch_vec<false, true, 1, EPI_SILU>(a, vec, s); break;
-        case EPI_STORE: launch_vec<false, true, 1, EPI_STORE>(a, vec, s); break;
+        case EPI_SWIGLU: launch_cfg<W13Cfg, MOE_W13_SCHED, false, true, 2, EPI_SWIGLU>(a, vec, s); break;
+        case EPI_SILU: launch_cfg<W13Cfg, MOE_W13_SCHED, false, true, 1, EPI_SILU>(a, vec, s); break;
+        case EPI_STORE: launch_cfg<W2Cfg, MOE_W2_SCHED, false, true, 1, EPI_STORE>(a, vec, s); break;
         default: throw Unsupported("grouped GEMM epilogue");
     }
 }

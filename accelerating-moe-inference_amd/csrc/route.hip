@@ -254,10 +254,10 @@ __global__ __launch_bounds__(256) void perm_count_kernel(
 }
 
 // Exclusive scan of counts[E * nb] in place (one workgroup of 1024 threads),
-// then the per-expert offsets and the per-expert first GEMM m-tile.
+// then the per-expert offsets.
 __global__ __launch_bounds__(1024) void perm_scan_kernel(
         int32_t* __restrict__ counts, int64_t nb, int64_t E,
-        int32_t* __restrict__ offsets, int32_t* __restrict__ tile_start) {
+        int32_t* __restrict__ offsets) {
     __shared__ int32_t wave_sums[16];
     __shared__ int32_t carry;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -284,15 +284,6 @@ __global__ __launch_bounds__(1024) void perm_scan_kernel(
     // offsets[e] = base of (e, block 0); offsets[E] = total pairs
     for (int64_t e = tid; e < E; e += 1024) offsets[e] = nb > 0 ? counts[e * nb] : 0;
     if (tid == 0) offsets[E] = carry;
-    __syncthreads();
-    if (tile_start != nullptr && tid == 0) {
-        int32_t acc = 0;
-        for (int64_t e = 0; e < E; ++e) {
-            tile_start[e] = acc;
-            acc += (offsets[e + 1] - offsets[e] + kGemmBM - 1) / kGemmBM;
-        }
-        tile_start[E] = acc;
-    }
 }
 
 __global__ __launch_bounds__(256) void perm_place_kernel(
@@ -319,18 +310,6 @@ __global__ __launch_bounds__(256) void perm_place_kernel(
     }
 }
 
-// First GEMM m-tile of each expert from the offsets (for callers that
-// bring their own offsets to the grouped FFN).
-__global__ void tile_start_kernel(const int32_t* __restrict__ offsets, int64_t E,
-                                  int32_t* __restrict__ tile_start) {
-    if (threadIdx.x != 0 || blockIdx.x != 0) return;
-    int32_t acc = 0;
-    for (int64_t e = 0; e < E; ++e) {
-        tile_start[e] = acc;
-        acc += (offsets[e + 1] - offsets[e] + kGemmBM - 1) / kGemmBM;
-    }
-    tile_start[E] = acc;
-}
 
 // -------------------------------------------------------------- combine
 // One workgroup per token.  The token's slots are ordered by ascending
@@ -452,9 +431,9 @@ void launch_perm_count(const int32_t* idx, int64_t T, int64_t k, int64_t E,
 }
 
 void launch_perm_scan(int32_t* counts, int64_t nblocks, int64_t E,
-                      int32_t* offsets, int32_t* tile_start, hipStream_t s) {
+                      int32_t* offsets, hipStream_t s) {
     hipLaunchKernelGGL(perm_scan_kernel, dim3(1), dim3(1024), 0, s, counts, nblocks, E,
-                       offsets, tile_start);
+                       offsets);
 }
 
 void launch_perm_place(const int32_t* idx, int64_t T, int64_t k, int64_t E,
@@ -466,10 +445,6 @@ void launch_perm_place(const int32_t* idx, int64_t T, int64_t k, int64_t E,
                        idx, T, k, E, base, perm, inv);
 }
 
-void launch_tile_start(const int32_t* offsets, int64_t E, int32_t* tile_start,
-                       hipStream_t s) {
-    hipLaunchKernelGGL(tile_start_kernel, dim3(1), dim3(64), 0, s, offsets, E, tile_start);
-}
 
 void launch_combine(const float* out_rows, const int32_t* idx, const float* w,
                     const int32_t* inv, const float* resid, float* y,

@@ -73,10 +73,16 @@ def cpu_baseline(x, weights, cfg, pkg_outputs, target_s):
                                        expert_bias=bias)
         return time.perf_counter() - t0, y, idx
 
-    probe = 4
-    dt, _, _ = run(probe)
-    n = int(max(probe, min(cfg["T"], round(target_s / max(dt / probe, 1e-9)))))
-    dt, y, idx = run(n)
+    # Grow the prefix until it takes about target_s: small prefixes leave
+    # most of the threads idle (the reference parallelises over an expert's
+    # rows), so the per-token time only settles once experts hold >= threads
+    # rows each.
+    n = 16
+    while True:
+        dt, y, idx = run(n)
+        if dt >= 0.5 * target_s or n >= cfg["T"]:
+            break
+        n = int(min(cfg["T"], max(2 * n, round(0.9 * n * target_s / max(dt, 1e-9)))))
     gy, gidx = pkg_outputs
     ref_scale = float(np.max(np.abs(y))) or 1.0
     parity = {
