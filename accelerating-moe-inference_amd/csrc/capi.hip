@@ -4,6 +4,7 @@
 
 #include <algorithm>
 #include <climits>
+#include <cstdlib>
 #include <cstring>
 
 namespace {
@@ -128,10 +129,31 @@ int64_t grouped_m_tiles(int64_t pairs, int64_t E, int bm) {
     return std::min<int64_t>(moe::ceil_div(pairs, bm) + E, pairs);
 }
 
+// K splits of the layer's w2: 2 when its tile grid would fill the GPU's
+// workgroup slots fewer than 4 times over (the last, partly filled round of
+// long-K tiles then costs a large share of the launch), else 1.
+// MOE_W2_SPLITS (1 or 2) overrides for tuning.
+int choose_w2_splits(moe_ctx* ctx, int64_t pairs, int64_t d, int64_t d_ff, int64_t E) {
+    static const int env = [] {
+        const char* v = std::getenv("MOE_W2_SPLITS");
+        return v != nullptr ? std::atoi(v) : 0;
+    }();
+    if (d_ff % 32 != 0 || d_ff == 0) return 1;  // each split a multiple of 16 columns
+    if (env == 1 || env == moe::kMaxW2Splits) return env;
+    if (ctx->w2_blocks_per_cu == 0) ctx->w2_blocks_per_cu = moe::gemm_blocks_per_cu(moe::GemmUse::W2);
+    const moe::GemmTile tile = moe::gemm_tile(moe::GemmUse::W2);
+    const int64_t tiles = grouped_m_tiles(pairs, E, tile.bm) * moe::ceil_div(d, tile.bn);
+    const int64_t slots = int64_t(ctx->cus) * ctx->w2_blocks_per_cu;
+    return tiles < 4 * slots ? moe::kMaxW2Splits : 1;
+}
+
+// w2_splits > 1 (layer path only): out_rows holds w2_splits partial row
+// buffers of pairs x d, one per K range, that the combine adds up.
 void expert_ffn(moe_ctx* ctx, const float* x, const int32_t* perm,
                 const int32_t* offsets, const float* w1, const float* w3,
                 const float* w2, int act, int64_t T, int64_t k, int64_t d,
-                int64_t d_ff, int64_t E, float* h, float* out_rows, hipStream_t s) {
+                int64_t d_ff, int64_t E, float* h, float* out_rows, hipStream_t s,
+                int w2_splits = 1) {
     const int64_t pairs = T * k;
     if (pairs == 0 || d == 0) return;
     const bool swiglu = act == MOE_ACT_SWIGLU;
@@ -178,7 +200,13 @@ void expert_ffn(moe_ctx* ctx, const float* x, const int32_t* perm,
     b.E = static_cast<int32_t>(E);
     b.m_tiles = static_cast<int32_t>(grouped_m_tiles(pairs, E, tile.bm));
     b.n_tiles = static_cast<int32_t>(moe::ceil_div(d, tile.bn));
-    moe::require(int64_t(b.m_tiles) * b.n_tiles <= INT32_MAX, "w2 grid too large");
+    if (w2_splits > 1) {
+        b.k_splits = w2_splits;
+        b.k_split_len = moe::ceil_div(moe::ceil_div(d_ff, w2_splits), 16) * 16;
+        b.c_split_stride = pairs * d;
+    }
+    moe::require(int64_t(b.m_tiles) * b.n_tiles * std::max(w2_splits, 1) <= INT32_MAX,
+                 "w2 grid too large");
     const bool vec = d_ff % 4 == 0 && aligned16(h) && aligned16(w2);
     ctx->launch("expert_w2", s, [&] { moe::launch_gemm(b, false, true, moe::EPI_STORE, vec, s); });
 }
@@ -222,7 +250,7 @@ LayerWs carve_layer(void* base, const moe_layer_desc& d) {
     w.perm = c.take<int32_t>(pairs);
     w.inv = c.take<int32_t>(pairs);
     w.h = c.take<float>(pairs * d.d_ff);
-    w.out_rows = c.take<float>(pairs * d.d);
+    w.out_rows = c.take<float>(pairs * d.d * moe::kMaxW2Splits);
     w.bytes = c.off + 256;
     return w;
 }
@@ -278,6 +306,7 @@ int moe_ctx_create(int device, moe_ctx** out) {
                                    prop.gcnArchName);
         auto* c = new moe_ctx();
         c->device = device;
+        c->cus = prop.multiProcessorCount;
         *out = c;
     });
 }
@@ -499,7 +528,7 @@ int moe_combine(moe_ctx* ctx, const float* out_rows, const int32_t* topk_idx,
         hipStream_t s = as_stream(stream);
         ctx->launch("combine", s, [&] {
             moe::launch_combine(out_rows, topk_idx, topk_w, inv, resid, y, T, k, d, T * k,
-                                contract, s);
+                                contract, 1, 0, s);
         });
     });
 }
@@ -544,11 +573,12 @@ int moe_layer_forward(moe_ctx* ctx, const moe_layer_desc* desc,
         ctx->launch("perm_place", s, [&] {
             moe::launch_perm_place(idx, D.T, D.k, D.E, ws.counts, ws.perm, ws.inv, s);
         });
+        const int splits = choose_w2_splits(ctx, D.T * D.k, D.d, D.d_ff, D.E);
         expert_ffn(ctx, x, ws.perm, ws.offsets, weights->w1, weights->w3, weights->w2, D.act,
-                   D.T, D.k, D.d, D.d_ff, D.E, ws.h, ws.out_rows, s);
+                   D.T, D.k, D.d, D.d_ff, D.E, ws.h, ws.out_rows, s, splits);
         ctx->launch("combine", s, [&] {
             moe::launch_combine(ws.out_rows, idx, w, ws.inv, nullptr, y, D.T, D.k, D.d,
-                                D.T * D.k, D.contract, s);
+                                D.T * D.k, D.contract, splits, D.T * D.k * D.d, s);
         });
     });
 }

@@ -45,6 +45,9 @@ struct GemmTile {
     int bm, bn;
 };
 GemmTile gemm_tile(GemmUse use);
+// Workgroups of the grouped kernel of `use` one CU holds at once.
+int gemm_blocks_per_cu(GemmUse use);
+constexpr int kMaxW2Splits = 2;  // split-K of the layer's w2 (partials summed by the combine)
 
 // Routing constants.
 constexpr int kPermTokens = 256;    // tokens per permutation block
@@ -73,6 +76,9 @@ struct GemmArgs {
     int32_t m_tiles;         // m-tiles covered by the grid (upper bound)
     int32_t n_tiles;
     int32_t group_m;         // raster: m-tiles that sweep the n-tiles together
+    int32_t k_splits;        // K ranges computed by separate tiles (>= 1)
+    int64_t k_split_len;     // K per split (a multiple of 16)
+    int64_t c_split_stride;  // elements between the outputs of consecutive splits
 };
 
 enum Epilogue : int { EPI_STORE = 0, EPI_BIAS = 1, EPI_SILU = 2, EPI_SWIGLU = 3 };
@@ -95,10 +101,12 @@ void launch_perm_place(const int32_t* idx, int64_t T, int64_t k, int64_t E,
                        hipStream_t s);
 void launch_silu(const float* x, float* y, int64_t n, hipStream_t s);
 void launch_mul(const float* a, const float* b, float* c, int64_t n, hipStream_t s);
+// out_rows holds `parts` partial row buffers of rows_total x d, part_stride
+// elements apart; a row's value is their sum in part order.
 void launch_combine(const float* out_rows, const int32_t* idx, const float* w,
                     const int32_t* inv, const float* resid, float* y,
                     int64_t T, int64_t k, int64_t d, int64_t rows_total,
-                    int contract, hipStream_t s);
+                    int contract, int parts, int64_t part_stride, hipStream_t s);
 
 }  // namespace moe
 
@@ -106,6 +114,8 @@ void launch_combine(const float* out_rows, const int32_t* idx, const float* w,
 // never land inside a timed region), and the optional per-kernel timers.
 struct moe_ctx {
     int device = 0;
+    int cus = 0;               // compute units of the device
+    int w2_blocks_per_cu = 0;  // occupancy of the grouped w2 kernel (lazily queried)
     void* ws = nullptr;
     size_t ws_bytes = 0;
     bool timing = false;

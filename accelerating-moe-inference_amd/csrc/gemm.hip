@@ -30,6 +30,7 @@
 #include "common.hpp"
 
 #include <cstdlib>
+#include <type_traits>
 
 // Tile configurations (index into CFG_TABLE below) chosen per use; the
 // defaults are the measured best on MI355X and can be overridden at build
@@ -184,7 +185,10 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_kernel(const GemmArgs p) {
 
     const int tid = threadIdx.x;
     int mt, nt;
-    tile_of(xcd_remap(blockIdx.x, gridDim.x), p.m_tiles, p.n_tiles, p.group_m, mt, nt);
+    const int tiles_mn = p.m_tiles * p.n_tiles;
+    const int logical = xcd_remap(blockIdx.x, gridDim.x);
+    const int split = logical / tiles_mn;  // K range of this tile (split-K)
+    tile_of(logical % tiles_mn, p.m_tiles, p.n_tiles, p.group_m, mt, nt);
 
     // ---- which rows / which expert this workgroup owns
     int64_t row0;
@@ -207,7 +211,10 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_kernel(const GemmArgs p) {
         if (NB == 2) B[NB - 1] = p.B1;
     }
     const int64_t n0 = static_cast<int64_t>(nt) * BN;
-    const int64_t N = p.N, K = p.K;
+    const int64_t N = p.N;
+    // K columns [kbeg, K) of this split; loads are bounded by K
+    const int64_t kbeg = split * p.k_split_len;
+    const int64_t K = p.K - kbeg < p.k_split_len ? p.K : kbeg + p.k_split_len;
 
     // ---- global -> register staging.  Chunk c = tid + THREADS*i of a tile:
     // A and NT B rows are c / KQ, the 4 columns (c % KQ) * 4; consecutive
@@ -332,15 +339,15 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_kernel(const GemmArgs p) {
         if (SCHED & SCHED_PRIO) __builtin_amdgcn_s_setprio(0);
     };
 
-    const int64_t nk = (K + BK - 1) / BK;
+    const int64_t nk = (K - kbeg + BK - 1) / BK;
     if (nk > 0) {
-        gload(0);
+        gload(kbeg);
         lstore(0);
         __syncthreads();
         for (int64_t kt = 0; kt < nk; ++kt) {
             const int cur = static_cast<int>(kt & 1);
             const bool more = kt + 1 < nk;
-            if (more) gload((kt + 1) * BK);
+            if (more) gload(kbeg + (kt + 1) * BK);
             if (SCHED & SCHED_MIDSTORE) {
                 compute(cur, [&] {
                     if (more) lstore(cur ^ 1);
@@ -372,7 +379,7 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_kernel(const GemmArgs p) {
                     } else if (EPI == EPI_SWIGLU) {
                         v = silu_ref(v) * acc[NB - 1][bi][bj][r];
                     }
-                    p.C[(row0 + i) * p.ldc + n] = v;
+                    p.C[split * p.c_split_stride + (row0 + i) * p.ldc + n] = v;
                 }
             }
 }
@@ -410,7 +417,10 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     int mt, nt;
-    tile_of(xcd_remap(blockIdx.x, gridDim.x), p.m_tiles, p.n_tiles, p.group_m, mt, nt);
+    const int tiles_mn = p.m_tiles * p.n_tiles;
+    const int logical = xcd_remap(blockIdx.x, gridDim.x);
+    const int split = logical / tiles_mn;  // K range of this tile (split-K)
+    tile_of(logical % tiles_mn, p.m_tiles, p.n_tiles, p.group_m, mt, nt);
 
     int64_t row0;
     int rows;
@@ -432,7 +442,10 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
         if (NB == 2) B[NB - 1] = p.B1;
     }
     const int64_t n0 = static_cast<int64_t>(nt) * BN;
-    const int64_t N = p.N, K = p.K;
+    const int64_t N = p.N;
+    // K columns [kbeg, K) of this split; loads are bounded by K
+    const int64_t kbeg = split * p.k_split_len;
+    const int64_t K = p.K - kbeg < p.k_split_len ? p.K : kbeg + p.k_split_len;
 
     // Per-lane source of each load instruction: instruction j of this wave
     // fills rows 16*J .. 16*J+15 (J = wave*INS + j); lane L writes slot L%4
@@ -490,9 +503,13 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[nb][bi][bj][r] = 0.0f;
 
-    const int64_t nk = K / BK;
+    // 32-row blocks of this wave that hold at least one real row
+    const int live_rows = rows - arow0;
+    const int live = live_rows <= 0 ? 0 : (live_rows >= FM * 32 ? FM : (live_rows + 31) / 32);
+
+    const int64_t nk = (K - kbeg) / BK;
     if (nk > 0) {
-        issue(0, 0);
+        issue(0, kbeg);
         __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0): this wave's loads landed
         __syncthreads();                      // ... and every other wave's
     }
@@ -517,20 +534,29 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
                 b[nb][bj][0] = *reinterpret_cast<const f32x4*>(base + 4 * ((2 * lh) ^ swz(r)));
                 b[nb][bj][1] = *reinterpret_cast<const f32x4*>(base + 4 * ((2 * lh + 1) ^ swz(r)));
             }
-        if (kt + 1 < nk) issue(cur ^ 1, (kt + 1) * BK);
+        if (kt + 1 < nk) issue(cur ^ 1, kbeg + (kt + 1) * BK);
         if (SCHED & SCHED_PRIO) __builtin_amdgcn_s_setprio(1);
+        // the burst over the first NBLK 32-row blocks of this wave
+        auto burst = [&](auto nblk) {
+            constexpr int NBLK = decltype(nblk)::value;
 #pragma unroll
-        for (int q = 0; q < 2; ++q)
+            for (int q = 0; q < 2; ++q)
 #pragma unroll
-            for (int s = 0; s < 4; ++s)
+                for (int s = 0; s < 4; ++s)
 #pragma unroll
-                for (int nb = 0; nb < NB; ++nb)
+                    for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-                    for (int bi = 0; bi < FM; ++bi)
+                        for (int bi = 0; bi < NBLK; ++bi)
 #pragma unroll
-                        for (int bj = 0; bj < FN; ++bj)
-                            acc[nb][bi][bj] = __builtin_amdgcn_mfma_f32_32x32x2f32(
-                                a[bi][q][s], b[nb][bj][q][s], acc[nb][bi][bj], 0, 0, 0);
+                            for (int bj = 0; bj < FN; ++bj)
+                                acc[nb][bi][bj] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                                    a[bi][q][s], b[nb][bj][q][s], acc[nb][bi][bj], 0, 0, 0);
+        };
+        // Blocks whose 32 rows all lie past the tile's last real row (the
+        // ragged end of an expert) are skipped: wave-uniform branches.
+        if (live == FM) burst(std::integral_constant<int, FM>{});
+        else if (FM > 1 && live == 1) burst(std::integral_constant<int, 1>{});
+        else if (live > 0) burst(std::integral_constant<int, FM>{});
         if (SCHED & SCHED_PRIO) __builtin_amdgcn_s_setprio(0);
         __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
         __syncthreads();
@@ -553,7 +579,7 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
                     } else if (EPI == EPI_SWIGLU) {
                         v = silu_ref(v) * acc[NB - 1][bi][bj][r];
                     }
-                    p.C[(row0 + i) * p.ldc + n] = v;
+                    p.C[split * p.c_split_stride + (row0 + i) * p.ldc + n] = v;
                 }
             }
 }
@@ -562,15 +588,17 @@ template <class C, int SCHED, bool NN, bool GROUPED, int NB, int EPI>
 void launch_cfg(const GemmArgs& a, bool vec, hipStream_t s) {
     // direct global->LDS path: NT, 16-byte aligned rows, K a multiple of 16
     if constexpr ((SCHED & SCHED_DIRECT) != 0 && !NN && C::BK == 16) {
-        if (vec && a.K % 16 == 0) {
+        if (vec && a.K % 16 == 0 && a.k_split_len % 16 == 0) {
             hipLaunchKernelGGL(
                 (gemm_direct_kernel<C, SCHED, GROUPED, NB, EPI>),
-                dim3(static_cast<unsigned>(a.m_tiles) * static_cast<unsigned>(a.n_tiles)),
+                dim3(static_cast<unsigned>(a.m_tiles) * static_cast<unsigned>(a.n_tiles) *
+                     static_cast<unsigned>(a.k_splits)),
                 dim3(C::THREADS), 0, s, a);
             return;
         }
     }
-    const dim3 grid(static_cast<unsigned>(a.m_tiles) * static_cast<unsigned>(a.n_tiles));
+    const dim3 grid(static_cast<unsigned>(a.m_tiles) * static_cast<unsigned>(a.n_tiles) *
+                     static_cast<unsigned>(a.k_splits));
     if (vec)
         hipLaunchKernelGGL((gemm_kernel<C, SCHED, NN, true, GROUPED, NB, EPI>), grid, dim3(C::THREADS),
                            0, s, a);
@@ -584,6 +612,33 @@ using W13Cfg = CfgOf<MOE_W13_CFG>::T;
 using W2Cfg = CfgOf<MOE_W2_CFG>::T;
 
 }  // namespace
+
+int gemm_blocks_per_cu(GemmUse use) {
+    int n = 0;
+    hipError_t e = hipSuccess;
+    auto query = [&](auto kernel, int threads) {
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, 0);
+    };
+    switch (use) {
+        case GemmUse::W2:
+            if constexpr ((MOE_W2_SCHED & SCHED_DIRECT) != 0 && W2Cfg::BK == 16)
+                query(gemm_direct_kernel<W2Cfg, MOE_W2_SCHED, true, 1, EPI_STORE>, W2Cfg::THREADS);
+            else
+                query(gemm_kernel<W2Cfg, MOE_W2_SCHED, false, true, true, 1, EPI_STORE>,
+                      W2Cfg::THREADS);
+            break;
+        default:
+            if constexpr ((MOE_W13_SCHED & SCHED_DIRECT) != 0 && W13Cfg::BK == 16)
+                query(gemm_direct_kernel<W13Cfg, MOE_W13_SCHED, true, 2, EPI_SWIGLU>,
+                      W13Cfg::THREADS);
+            else
+                query(gemm_kernel<W13Cfg, MOE_W13_SCHED, false, true, true, 2, EPI_SWIGLU>,
+                      W13Cfg::THREADS);
+            break;
+    }
+    hip_check(e, "hipOccupancyMaxActiveBlocksPerMultiprocessor");
+    return n > 0 ? n : 1;
+}
 
 GemmTile gemm_tile(GemmUse use) {
     switch (use) {
@@ -606,6 +661,11 @@ void launch_gemm(const GemmArgs& args, bool nn, bool grouped, int epi, bool vec,
     int group = env_group != 0 ? env_group : kGemmGroupM;
     if (group < 1 || group > a.m_tiles) group = a.m_tiles;
     a.group_m = group;
+    if (a.k_splits <= 1) {
+        a.k_splits = 1;
+        a.k_split_len = a.K;
+        a.c_split_stride = 0;
+    }
     if (!grouped) {
         if (epi != EPI_BIAS) throw Unsupported("dense GEMM epilogue");
         if (nn) launch_cfg<DenseCfg, MOE_DENSE_SCHED, true, false, 1, EPI_BIAS>(a, vec, s);

@@ -315,13 +315,15 @@ __global__ __launch_bounds__(256) void perm_place_kernel(
 // One workgroup per token.  The token's slots are ordered by ascending
 // expert (ties by slot), then y = 0 + w*row, + w*row, ... in that order: the
 // order of the reference's expert loop (src/layer.cu:93-101).  resid, when
-// given, is added last (the decoder's add_inplace, src/layer.cu:160).
-template <int CONTRACT>
+// given, is added last (the decoder's add_inplace, src/layer.cu:160).  When
+// the w2 GEMM ran split-K, a row is the sum of its PARTS partial rows, added
+// in part order before weighting.
+template <int CONTRACT, int PARTS>
 __global__ __launch_bounds__(256) void combine_kernel(
         const float* __restrict__ out_rows, const int32_t* __restrict__ idx,
         const float* __restrict__ wts, const int32_t* __restrict__ inv,
         const float* __restrict__ resid, float* __restrict__ y, int64_t T,
-        int64_t k, int64_t d, int64_t rows_total) {
+        int64_t k, int64_t d, int64_t rows_total, int64_t part_stride) {
     __shared__ int32_t order_row[kMaxTopK];
     __shared__ float order_w[kMaxTopK];
     __shared__ int n_live;
@@ -358,7 +360,14 @@ __global__ __launch_bounds__(256) void combine_kernel(
         for (int64_t j = threadIdx.x; j < d4; j += blockDim.x) {
             f4 acc = {0.f, 0.f, 0.f, 0.f};
             for (int q = 0; q < n; ++q) {
-                const f4 v = reinterpret_cast<const f4*>(out_rows + order_row[q] * d)[j];
+                f4 v = reinterpret_cast<const f4*>(out_rows + order_row[q] * d)[j];
+#pragma unroll
+                for (int p = 1; p < PARTS; ++p) {
+                    const f4 u =
+                        reinterpret_cast<const f4*>(out_rows + p * part_stride + order_row[q] * d)[j];
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) v[c] = v[c] + u[c];
+                }
                 const float wq = order_w[q];
 #pragma unroll
                 for (int c = 0; c < 4; ++c) acc[c] = mac<CONTRACT>(acc[c], wq, v[c]);
@@ -373,8 +382,12 @@ __global__ __launch_bounds__(256) void combine_kernel(
     } else {
         for (int64_t j = threadIdx.x; j < d; j += blockDim.x) {
             float acc = 0.0f;
-            for (int q = 0; q < n; ++q)
-                acc = mac<CONTRACT>(acc, order_w[q], out_rows[order_row[q] * d + j]);
+            for (int q = 0; q < n; ++q) {
+                float v = out_rows[order_row[q] * d + j];
+#pragma unroll
+                for (int p = 1; p < PARTS; ++p) v = v + out_rows[p * part_stride + order_row[q] * d + j];
+                acc = mac<CONTRACT>(acc, order_w[q], v);
+            }
             if (resid != nullptr) acc = acc + resid[t * d + j];
             y[t * d + j] = acc;
         }
@@ -449,14 +462,18 @@ void launch_perm_place(const int32_t* idx, int64_t T, int64_t k, int64_t E,
 void launch_combine(const float* out_rows, const int32_t* idx, const float* w,
                     const int32_t* inv, const float* resid, float* y,
                     int64_t T, int64_t k, int64_t d, int64_t rows_total,
-                    int contract, hipStream_t s) {
+                    int contract, int parts, int64_t part_stride, hipStream_t s) {
     if (T == 0 || d == 0) return;
-    if (contract)
-        hipLaunchKernelGGL(combine_kernel<1>, dim3(static_cast<unsigned>(T)), dim3(256), 0, s,
-                           out_rows, idx, w, inv, resid, y, T, k, d, rows_total);
-    else
-        hipLaunchKernelGGL(combine_kernel<0>, dim3(static_cast<unsigned>(T)), dim3(256), 0, s,
-                           out_rows, idx, w, inv, resid, y, T, k, d, rows_total);
+    static_assert(kMaxW2Splits == 2, "combine instantiates 1 and 2 parts");
+    auto go = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(T)), dim3(256), 0, s, out_rows, idx,
+                           w, inv, resid, y, T, k, d, rows_total, part_stride);
+    };
+    if (parts == 2) {
+        if (contract) go(combine_kernel<1, 2>); else go(combine_kernel<0, 2>);
+    } else {
+        if (contract) go(combine_kernel<1, 1>); else go(combine_kernel<0, 1>);
+    }
 }
 
 }  // namespace moe
