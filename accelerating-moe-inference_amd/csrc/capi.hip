@@ -3,6 +3,7 @@
 #include "common.hpp"
 
 #include <algorithm>
+#include <cmath>
 #include <climits>
 #include <cstdlib>
 #include <cstring>
@@ -129,22 +130,37 @@ int64_t grouped_m_tiles(int64_t pairs, int64_t E, int bm) {
     return std::min<int64_t>(moe::ceil_div(pairs, bm) + E, pairs);
 }
 
-// K splits of the layer's w2: 2 when its tile grid would fill the GPU's
-// workgroup slots fewer than 4 times over (the last, partly filled round of
-// long-K tiles then costs a large share of the launch), else 1.
-// MOE_W2_SPLITS (1 or 2) overrides for tuning.
+// K splits S of the layer's w2.  Its tiles run in rounds of `slots`
+// concurrent workgroups; a last, partly filled round of long-K tiles wastes
+// the rest of the GPU for a whole tile time.  Splitting K S ways makes the
+// rounds S times shorter, so the fill is w / ceil(w) with w = tiles * S /
+// slots.  The smallest S in {1, 2, 4} whose fill reaches 95 % is taken (else
+// the best); each split must be a multiple of 16 columns.  MOE_W2_SPLITS
+// overrides for tuning.
 int choose_w2_splits(moe_ctx* ctx, int64_t pairs, int64_t d, int64_t d_ff, int64_t E) {
     static const int env = [] {
         const char* v = std::getenv("MOE_W2_SPLITS");
         return v != nullptr ? std::atoi(v) : 0;
     }();
-    if (d_ff % 32 != 0 || d_ff == 0) return 1;  // each split a multiple of 16 columns
-    if (env == 1 || env == moe::kMaxW2Splits) return env;
+    auto allowed = [&](int S) { return S == 1 || (d_ff > 0 && d_ff % (16 * S) == 0); };
+    if (env == 1 || env == 2 || env == 4) return allowed(env) ? env : 1;
     if (ctx->w2_blocks_per_cu == 0) ctx->w2_blocks_per_cu = moe::gemm_blocks_per_cu(moe::GemmUse::W2);
     const moe::GemmTile tile = moe::gemm_tile(moe::GemmUse::W2);
-    const int64_t tiles = grouped_m_tiles(pairs, E, tile.bm) * moe::ceil_div(d, tile.bn);
-    const int64_t slots = int64_t(ctx->cus) * ctx->w2_blocks_per_cu;
-    return tiles < 4 * slots ? moe::kMaxW2Splits : 1;
+    const double tiles = double(grouped_m_tiles(pairs, E, tile.bm) * moe::ceil_div(d, tile.bn));
+    const double slots = double(int64_t(ctx->cus) * ctx->w2_blocks_per_cu);
+    int best = 1;
+    double best_fill = 0.0;
+    for (int S : {1, 2, 4}) {
+        if (S > moe::kMaxW2Splits || !allowed(S)) continue;
+        const double w = tiles * S / slots;
+        const double fill = w / std::ceil(w);
+        if (fill >= 0.95) return S;
+        if (fill > best_fill) {
+            best = S;
+            best_fill = fill;
+        }
+    }
+    return best;
 }
 
 // w2_splits > 1 (layer path only): out_rows holds w2_splits partial row

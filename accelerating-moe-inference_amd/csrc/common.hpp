@@ -47,7 +47,7 @@ struct GemmTile {
 GemmTile gemm_tile(GemmUse use);
 // Workgroups of the grouped kernel of `use` one CU holds at once.
 int gemm_blocks_per_cu(GemmUse use);
-constexpr int kMaxW2Splits = 2;  // split-K of the layer's w2 (partials summed by the combine)
+constexpr int kMaxW2Splits = 4;  // split-K of the layer's w2 (partials summed by the combine)
 
 // Routing constants.
 constexpr int kPermTokens = 256;    // tokens per permutation block

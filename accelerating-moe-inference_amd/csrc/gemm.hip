@@ -39,7 +39,7 @@
 #define MOE_W13_CFG 0
 #endif
 #ifndef MOE_W2_CFG
-#define MOE_W2_CFG 0
+#define MOE_W2_CFG 4
 #endif
 #ifndef MOE_DENSE_CFG
 #define MOE_DENSE_CFG 0

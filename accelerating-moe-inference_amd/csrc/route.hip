@@ -464,15 +464,19 @@ void launch_combine(const float* out_rows, const int32_t* idx, const float* w,
                     int64_t T, int64_t k, int64_t d, int64_t rows_total,
                     int contract, int parts, int64_t part_stride, hipStream_t s) {
     if (T == 0 || d == 0) return;
-    static_assert(kMaxW2Splits == 2, "combine instantiates 1 and 2 parts");
+    static_assert(kMaxW2Splits == 4, "combine instantiates 1, 2 and 4 parts");
     auto go = [&](auto kernel) {
         hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(T)), dim3(256), 0, s, out_rows, idx,
                            w, inv, resid, y, T, k, d, rows_total, part_stride);
     };
-    if (parts == 2) {
+    if (parts == 4) {
+        if (contract) go(combine_kernel<1, 4>); else go(combine_kernel<0, 4>);
+    } else if (parts == 2) {
         if (contract) go(combine_kernel<1, 2>); else go(combine_kernel<0, 2>);
-    } else {
+    } else if (parts == 1) {
         if (contract) go(combine_kernel<1, 1>); else go(combine_kernel<0, 1>);
+    } else {
+        throw Unsupported("combine: partial-row count must be 1, 2 or 4");
     }
 }
 
