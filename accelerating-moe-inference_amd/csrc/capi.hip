@@ -81,6 +81,84 @@ void check_routing(int64_t T, int64_t E, int64_t k) {
 }
 
 // ---- dense GEMM
+int env_int(const char* name, int fallback) {
+    const char* v = std::getenv(name);
+    return v != nullptr ? std::atoi(v) : fallback;
+}
+
+// Tile shape and K splits of a dense SGEMM, from a cost model fitted to a
+// tile x split sweep of the SGEMM shapes on MI355X (every choice it makes
+// there is within 10 % of the best measured one, about twice the sweep's
+// run-to-run spread).  Per CU, the workgroups
+// dealt to it run `occupancy` at a time; each K step of the resident ones
+// costs the larger of their matrix-core time (the rows a wave really
+// computes: 32-row blocks past M are skipped) and the latency of one load
+// stage; HBM time counts A once, B once per m-tile and the split partials
+// twice; launches and the split reduction add fixed costs.  Small and
+// skinny products thereby get small tiles and a few K splits that fill all
+// CUs; large ones keep the 128 x 128 tile.  MOE_DENSE_TILE /
+// MOE_DENSE_SPLITS pin the choice for tuning.
+struct DensePlan {
+    int tile = 0, splits = 1;
+};
+
+constexpr int64_t kDenseSplitBytes = int64_t(512) << 20;  // cap on the partials
+
+DensePlan plan_dense(moe_ctx* ctx, bool nn, bool direct, int64_t M, int64_t N, int64_t K) {
+    DensePlan best;
+    if (!direct || K == 0) return best;  // the register-staged kernel: 128 x 128, one pass
+    static const int env_tile = env_int("MOE_DENSE_TILE", -1);
+    static const int env_splits = env_int("MOE_DENSE_SPLITS", 0);
+    auto split_ok = [&](int S) {
+        return S == 1 || (K % (16 * S) == 0 && K / S >= 64 &&
+                          int64_t(S) * M * N * 4 <= kDenseSplitBytes);
+    };
+    // fitted constants: MFMA efficiency per tile shape, latency of one load
+    // stage, start-up and drain of a round of workgroups, achievable HBM
+    // bandwidth, launch and reduction overheads
+    static constexpr double kEff[moe::kDenseTiles] = {0.80, 0.70, 0.60};
+    constexpr double kStageLatency = 0.5e-6, kRound = 4e-6, kHbm = 5.0e12, kLaunch = 2e-6,
+                     kReduce = 5e-6;
+    // each tile shape runs 4 waves, one per SIMD
+    const double simd_rate = 157.3e12 / (4.0 * ctx->cus);
+    double best_t = 1e30;
+    for (int t = 0; t < moe::kDenseTiles; ++t) {
+        if (env_tile >= 0 && t != env_tile) continue;
+        int& occ = ctx->dense_blocks_per_cu[nn ? 1 : 0][t];
+        if (occ == 0) occ = moe::dense_blocks_per_cu(t, nn);
+        const moe::GemmTile g = moe::dense_tile(t);
+        const int wm = g.bm >= 64 ? 2 : 1;  // wave grid: 2x2, or 1x4 for the 32-row tile
+        const int wn = 4 / wm;
+        const int64_t mt = moe::ceil_div(M, g.bm), nt = moe::ceil_div(N, g.bn);
+        const int64_t rows_w = std::min<int64_t>(g.bm / wm, 32 * moe::ceil_div(std::min<int64_t>(M, g.bm), 32));
+        const double step_mma = 2.0 * rows_w * (g.bn / wn) * 16 / (kEff[t] * simd_rate);
+        for (int S = 1; S <= moe::kMaxDenseSplits; S *= 2) {
+            if (env_splits > 0 && S != env_splits) continue;
+            if (!split_ok(S) || mt * nt * S > INT32_MAX) continue;
+            const int64_t blocks = mt * nt * S;
+            const double steps = double(K / S / 16);
+            // rounds of `occ` resident workgroups, then a last partial round
+            const int64_t per_cu = moe::ceil_div(blocks, ctx->cus);
+            const int64_t full = per_cu / occ, rest = per_cu % occ;
+            double t_cu = full * (steps * std::max(occ * step_mma, kStageLatency) + kRound);
+            if (rest > 0) t_cu += steps * std::max(rest * step_mma, kStageLatency) + kRound;
+            double bytes = 4.0 * (double(M) * K + double(K) * N * mt + double(M) * N);
+            if (S > 1) bytes += 8.0 * S * double(M) * N;
+            double est = std::max(t_cu, bytes / kHbm) + kLaunch;
+            // the split reduction: a second launch reading every partial once,
+            // and the partial stores, which the model cannot hide under the MFMAs
+            const double part_bytes = 4.0 * S * double(M) * N;
+            if (S > 1) est += kReduce + (part_bytes + 4.0 * M * N) / 4e12 + part_bytes / kHbm;
+            if (est < best_t) {
+                best_t = est;
+                best.tile = t;
+                best.splits = S;
+            }
+        }
+    }
+    return best;
+}
+
 void sgemm(moe_ctx* ctx, bool nn, const float* A, const float* B,
            const float* bias, float* C, int64_t M, int64_t N, int64_t K,
            void* stream) {
@@ -94,10 +172,14 @@ void sgemm(moe_ctx* ctx, bool nn, const float* A, const float* B,
         check_ptr(A, "A");
         check_ptr(B, "B");
     }
-    const moe::GemmTile tile = moe::gemm_tile(moe::GemmUse::Dense);
-    const int64_t mt = moe::ceil_div(M, tile.bm), ntl = moe::ceil_div(N, tile.bn);
-    moe::require(mt * ntl <= INT32_MAX, "GEMM grid too large");
     DeviceScope dev(ctx->device);
+    const bool vec = (K % 4 == 0) && aligned16(A) && (nn || aligned16(B));
+    // the direct-load kernels (every tile shape; split K): see launch_cfg
+    const bool direct = vec && K % 16 == 0 && (!nn || (N % 4 == 0 && aligned16(B)));
+    const DensePlan plan = plan_dense(ctx, nn, direct, M, N, K);
+    const moe::GemmTile tile = moe::dense_tile(plan.tile);
+    const int64_t mt = moe::ceil_div(M, tile.bm), ntl = moe::ceil_div(N, tile.bn);
+    moe::require(mt * ntl * plan.splits <= INT32_MAX, "GEMM grid too large");
     moe::GemmArgs a{};
     a.A = A;
     a.lda = K;
@@ -112,15 +194,29 @@ void sgemm(moe_ctx* ctx, bool nn, const float* A, const float* B,
     a.K = K;
     a.m_tiles = static_cast<int32_t>(mt);
     a.n_tiles = static_cast<int32_t>(ntl);
-    const bool vec = (K % 4 == 0) && aligned16(A) && (nn || aligned16(B));
+    a.tile = plan.tile;
     // K == 0 leaves the kernel with no K step: C = bias (or 0) still gets written.
     if (K == 0) {
         a.A = C;  // any valid pointer; never read
         a.B0 = a.B1 = C;
     }
     hipStream_t s = as_stream(stream);
-    ctx->launch(nn ? "sgemm_nn" : "sgemm_nt", s,
-                [&] { moe::launch_gemm(a, nn, false, moe::EPI_BIAS, vec, s); });
+    float* parts = nullptr;
+    if (plan.splits > 1) {
+        // split K: each split writes its partial product to the workspace,
+        // [splits, M, N]; the reduction adds them in order, then the bias.
+        parts = static_cast<float*>(ctx->workspace(size_t(plan.splits) * M * N * sizeof(float)));
+        a.C = parts;
+        a.ldc = N;
+        a.bias = nullptr;
+        a.k_splits = plan.splits;
+        a.k_split_len = K / plan.splits;
+        a.c_split_stride = M * N;
+    }
+    ctx->launch(nn ? "sgemm_nn" : "sgemm_nt", s, [&] {
+        moe::launch_gemm(a, nn, false, moe::EPI_BIAS, vec, s);
+        if (parts != nullptr) moe::launch_split_sum(parts, plan.splits, M * N, bias, C, M, N, s);
+    });
 }
 
 // ---- expert FFN (the part shared by moe_expert_ffn_grouped and the layer)

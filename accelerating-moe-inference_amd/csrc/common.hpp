@@ -49,6 +49,15 @@ GemmTile gemm_tile(GemmUse use);
 int gemm_blocks_per_cu(GemmUse use);
 constexpr int kMaxW2Splits = 4;  // split-K of the layer's w2 (partials summed by the combine)
 
+// Dense SGEMM tile shapes, GemmArgs::tile: 0 = 128x128 (any shape), 1 =
+// 64x128 and 2 = 32x128 (direct-load path only: 16-byte aligned rows,
+// K % 16 == 0, and for NN N % 4 == 0).
+constexpr int kDenseTiles = 3;
+GemmTile dense_tile(int tile);
+// Workgroups of dense tile shape `tile` (direct-load kernel) one CU holds at once.
+int dense_blocks_per_cu(int tile, bool nn);
+constexpr int kMaxDenseSplits = 16;  // split-K of a dense SGEMM (partials in the workspace)
+
 // Routing constants.
 constexpr int kPermTokens = 256;    // tokens per permutation block
 constexpr int kMaxExperts = 1024;   // bitmap in LDS: E * 4 * 8 B = 32 KiB
@@ -79,6 +88,7 @@ struct GemmArgs {
     int32_t k_splits;        // K ranges computed by separate tiles (>= 1)
     int64_t k_split_len;     // K per split (a multiple of 16)
     int64_t c_split_stride;  // elements between the outputs of consecutive splits
+    int32_t tile;            // dense: tile shape (kDenseTiles)
 };
 
 enum Epilogue : int { EPI_STORE = 0, EPI_BIAS = 1, EPI_SILU = 2, EPI_SWIGLU = 3 };
@@ -101,6 +111,10 @@ void launch_perm_place(const int32_t* idx, int64_t T, int64_t k, int64_t E,
                        hipStream_t s);
 void launch_silu(const float* x, float* y, int64_t n, hipStream_t s);
 void launch_mul(const float* a, const float* b, float* c, int64_t n, hipStream_t s);
+// c[rows, cols] (contiguous) = sum over `splits` partials part_stride apart,
+// in order, + bias[cols] (nullable).
+void launch_split_sum(const float* parts, int splits, int64_t part_stride, const float* bias,
+                      float* c, int64_t rows, int64_t cols, hipStream_t s);
 // out_rows holds `parts` partial row buffers of rows_total x d, part_stride
 // elements apart; a row's value is their sum in part order.
 void launch_combine(const float* out_rows, const int32_t* idx, const float* w,
@@ -116,6 +130,7 @@ struct moe_ctx {
     int device = 0;
     int cus = 0;               // compute units of the device
     int w2_blocks_per_cu = 0;  // occupancy of the grouped w2 kernel (lazily queried)
+    int dense_blocks_per_cu[2][moe::kDenseTiles] = {};  // [nn][tile], lazily queried
     void* ws = nullptr;
     size_t ws_bytes = 0;
     bool timing = false;

@@ -81,9 +81,9 @@ struct Cfg {
     static constexpr int B_LD = BN * KQ / THREADS;  // B chunks per thread (per operand)
     static_assert(FM >= 1 && FN >= 1 && BM % (32 * WM) == 0 && BN % (32 * WN) == 0, "tile");
     static_assert(BK % 16 == 0, "K step is a multiple of 16");
-    static_assert(A_LD * THREADS == BM * KQ && B_LD * THREADS == BN * KQ && A_LD >= 1 &&
-                      B_LD >= 1,
-                  "staging divides evenly");
+    // the register-staged kernel deals whole 16-byte chunks to every thread
+    static constexpr bool STAGED = A_LD * THREADS == BM * KQ && B_LD * THREADS == BN * KQ &&
+                                   A_LD >= 1 && B_LD >= 1;
 };
 
 template <int ID> struct CfgOf;
@@ -95,6 +95,8 @@ template <> struct CfgOf<4> { using T = Cfg<128, 256, 16, 2, 2>; };
 template <> struct CfgOf<5> { using T = Cfg<256, 128, 32, 4, 2>; };
 template <> struct CfgOf<6> { using T = Cfg<256, 256, 16, 4, 2>; };
 template <> struct CfgOf<7> { using T = Cfg<64, 128, 16, 1, 2>; };
+template <> struct CfgOf<8> { using T = Cfg<64, 128, 16, 2, 2>; };  // direct only
+template <> struct CfgOf<9> { using T = Cfg<32, 128, 16, 1, 4>; };  // direct only
 
 // Workgroup ids are dealt round-robin over the XCDs.  Renumber them so each
 // XCD works through a contiguous run of logical tiles: tiles that share an
@@ -180,6 +182,7 @@ template <class C, int SCHED, bool NN, bool VEC, bool GROUPED, int NB, int EPI>
 __global__ __launch_bounds__(C::THREADS, 2) void gemm_kernel(const GemmArgs p) {
     constexpr int BM = C::BM, BN = C::BN, BK = C::BK, LDS = C::LDS, KQ = C::KQ;
     constexpr int FM = C::FM, FN = C::FN;
+    static_assert(C::STAGED, "staging divides evenly");
     __shared__ __align__(16) float As[2][BM * LDS];
     __shared__ __align__(16) float Bs[2][NB][BN * LDS];
 
@@ -385,34 +388,60 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_kernel(const GemmArgs p) {
 }
 
 // ---------------------------------------------------------------------------
-// NT GEMM with direct global->LDS loads (gfx950 global_load_lds_dwordx4).
+// GEMM with direct global->LDS loads (gfx950 global_load_lds_dwordx4).
 //
 // Lane L of a load instruction writes its 16 bytes at LDS base + 16*L, from
 // any global address it chooses, so each lane fetches the chunk that belongs
-// at its slot: tiles are stored unpadded, 4 chunks of 16 bytes per row of
-// the 16-wide K step, chunk c of row r at slot c ^ ((r >> 2) & 3).  The
-// swizzle keeps the 16-byte fragment reads conflict-free.  The data goes
+// at its slot: A (and NT B) tiles are stored unpadded, 4 chunks of 16 bytes
+// per row of the 16-wide K step, chunk c of row r at slot c ^ ((r >> 2) & 3).
+// The swizzle keeps the 16-byte fragment reads conflict-free.  The data goes
 // from L2 straight to LDS -- no staging registers, no LDS store
 // instructions -- and lands while the matrix cores run: each K step reads
 // all fragments of the current stage, issues the next stage's loads, runs
 // the MFMA burst, then waits for its loads and meets the other waves at the
 // barrier.  Requires K % 16 == 0 and 16-byte aligned rows.
+//
+// NN B ([K, N] row-major) stays k-major in LDS: one load instruction moves
+// 256 consecutive floats of the tile, 256 / BN k-rows of BN columns, and
+// instructions sit NN_PAD floats apart so that k-rows 8 apart (the two lane
+// halves of a fragment read) fall on opposite halves of the 64 banks.  A
+// lane then gathers its column's 8 k values with 4-byte reads.  Requires
+// N % 4 == 0 as well.
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(1))) const void glb_void;
 
 __device__ __forceinline__ int swz(int row) { return (row >> 2) & 3; }
 
-template <class C, int SCHED, bool GROUPED, int NB, int EPI>
+template <int BN>
+struct NnB {
+    static constexpr int RPI = 256 / BN;        // k-rows per load instruction
+    static constexpr int PAD = 4 * RPI;         // floats between instructions' rows
+    static constexpr int STRIDE = 256 + PAD;    // LDS floats per load instruction
+    static_assert(BN <= 256 && 256 % BN == 0, "NN direct tiles: BN divides 256");
+    // LDS index of element (k, n) of the 16 x BN tile
+    static __device__ __forceinline__ int at(int k, int n) {
+        return (k / RPI) * STRIDE + (k % RPI) * BN + n;
+    }
+};
+
+template <class C, int SCHED, bool NN, bool GROUPED, int NB, int EPI>
 __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmArgs p) {
     constexpr int BM = C::BM, BN = C::BN, BK = C::BK;
     constexpr int FM = C::FM, FN = C::FN;
     constexpr int NW = C::THREADS / 64;
-    constexpr int A_INS = BM / 16 / NW;  // 1 KiB load instructions per wave, A
-    constexpr int B_INS = BN / 16 / NW;  // ... per B operand
+    // 1 KiB load instructions per tile (16 rows x 16 k, or 256 floats of an
+    // NN B tile), dealt to the waves: INS per wave, the last ones idle when
+    // the tile has fewer instructions than waves.
+    constexpr int A_TOT = BM / 16, B_TOT = BN / 16;
+    constexpr int A_INS = (A_TOT + NW - 1) / NW;
+    constexpr int B_INS = (B_TOT + NW - 1) / NW;
     static_assert(BK == 16, "direct path: 16-wide K steps");
-    static_assert(A_INS * NW * 16 == BM && B_INS * NW * 16 == BN, "load split");
+    static_assert(A_TOT * 16 == BM && B_TOT * 16 == BN, "load split");
+    static_assert(A_INS * NW == A_TOT || A_TOT < NW, "A load split");
+    static_assert(B_INS * NW == B_TOT || B_TOT < NW, "B load split");
+    constexpr int B_SIZE = NN ? B_TOT * NnB<BN>::STRIDE : BN * BK;
     __shared__ __align__(16) float As[2][BM * BK];
-    __shared__ __align__(16) float Bs[2][NB][BN * BK];
+    __shared__ __align__(16) float Bs[2][NB][B_SIZE];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -454,7 +483,8 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
     const float* asrc[A_INS];
 #pragma unroll
     for (int j = 0; j < A_INS; ++j) {
-        const int r = 16 * (wave * A_INS + j) + lrow;
+        int r = 16 * (wave * A_INS + j) + lrow;
+        r = r < BM ? r : BM - 1;  // an idle wave's instruction (never issued)
         const int rr = r < rows ? r : rows - 1;  // past the edge: a valid row, masked at the store
         int64_t src = row0 + rr;
         if (GROUPED && p.gather != nullptr) {
@@ -464,29 +494,46 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
         }
         asrc[j] = p.A + src * p.lda + 4 * (lslot ^ swz(r));
     }
+    // B: NT rows n like A's rows.  NN: instruction J's lane L holds floats
+    // 256 J + 4 L .. +3 of the k-major tile, i.e. k-row (256 J + 4 L) / BN,
+    // columns n0 + (256 J + 4 L) % BN (past N: the last 4 columns, masked at
+    // the store); its source advances by k0 rows.
     const float* bsrc[NB][B_INS];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
         for (int j = 0; j < B_INS; ++j) {
-            const int r = 16 * (wave * B_INS + j) + lrow;
-            int64_t n = n0 + r;
-            n = n < N ? n : N - 1;
-            bsrc[nb][j] = B[nb] + n * p.ldb + 4 * (lslot ^ swz(r));
+            int J = wave * B_INS + j;
+            J = J < B_TOT ? J : B_TOT - 1;
+            if (NN) {
+                const int flat = 256 * J + 4 * lane;
+                int64_t n = n0 + flat % BN;
+                n = n < N ? n : N - 4;
+                bsrc[nb][j] = B[nb] + static_cast<int64_t>(flat / BN) * p.ldb + n;
+            } else {
+                const int r = 16 * J + lrow;
+                int64_t n = n0 + r;
+                n = n < N ? n : N - 1;
+                bsrc[nb][j] = B[nb] + n * p.ldb + 4 * (lslot ^ swz(r));
+            }
         }
     auto issue = [&](int buf, int64_t k0) {
 #pragma unroll
         for (int j = 0; j < A_INS; ++j)
-            __builtin_amdgcn_global_load_lds((glb_void*)(asrc[j] + k0),
-                                             (lds_void*)&As[buf][(wave * A_INS + j) * 256], 16,
-                                             0, 0);
+            if (A_INS * NW == A_TOT || wave * A_INS + j < A_TOT)
+                __builtin_amdgcn_global_load_lds((glb_void*)(asrc[j] + k0),
+                                                 (lds_void*)&As[buf][(wave * A_INS + j) * 256],
+                                                 16, 0, 0);
+        const int64_t boff = NN ? k0 * p.ldb : k0;
+        constexpr int BSTEP = NN ? NnB<BN>::STRIDE : 256;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
             for (int j = 0; j < B_INS; ++j)
-                __builtin_amdgcn_global_load_lds((glb_void*)(bsrc[nb][j] + k0),
-                                                 (lds_void*)&Bs[buf][nb][(wave * B_INS + j) * 256],
-                                                 16, 0, 0);
+                if (B_INS * NW == B_TOT || wave * B_INS + j < B_TOT)
+                    __builtin_amdgcn_global_load_lds(
+                        (glb_void*)(bsrc[nb][j] + boff),
+                        (lds_void*)&Bs[buf][nb][(wave * B_INS + j) * BSTEP], 16, 0, 0);
     };
 
     const int wm = wave % C::WM, wn = wave / C::WM;
@@ -530,9 +577,19 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
 #pragma unroll
             for (int bj = 0; bj < FN; ++bj) {
                 const int r = bcol0 + bj * 32 + lr;
-                const float* base = &Bs[cur][nb][r * BK];
-                b[nb][bj][0] = *reinterpret_cast<const f32x4*>(base + 4 * ((2 * lh) ^ swz(r)));
-                b[nb][bj][1] = *reinterpret_cast<const f32x4*>(base + 4 * ((2 * lh + 1) ^ swz(r)));
+                if (NN) {
+                    // the same k order as A: slot s of half q is k = 8 lh + 4 q + s
+#pragma unroll
+                    for (int q = 0; q < 2; ++q)
+#pragma unroll
+                        for (int s = 0; s < 4; ++s)
+                            b[nb][bj][q][s] = Bs[cur][nb][NnB<BN>::at(8 * lh + 4 * q + s, r)];
+                } else {
+                    const float* base = &Bs[cur][nb][r * BK];
+                    b[nb][bj][0] = *reinterpret_cast<const f32x4*>(base + 4 * ((2 * lh) ^ swz(r)));
+                    b[nb][bj][1] =
+                        *reinterpret_cast<const f32x4*>(base + 4 * ((2 * lh + 1) ^ swz(r)));
+                }
             }
         if (kt + 1 < nk) issue(cur ^ 1, kbeg + (kt + 1) * BK);
         if (SCHED & SCHED_PRIO) __builtin_amdgcn_s_setprio(1);
@@ -586,32 +643,75 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
 
 template <class C, int SCHED, bool NN, bool GROUPED, int NB, int EPI>
 void launch_cfg(const GemmArgs& a, bool vec, hipStream_t s) {
-    // direct global->LDS path: NT, 16-byte aligned rows, K a multiple of 16
-    if constexpr ((SCHED & SCHED_DIRECT) != 0 && !NN && C::BK == 16) {
-        if (vec && a.K % 16 == 0 && a.k_split_len % 16 == 0) {
+    // direct global->LDS path: 16-byte aligned rows, K a multiple of 16 (NN:
+    // B's rows, of N floats, 16-byte aligned too)
+    if constexpr ((SCHED & SCHED_DIRECT) != 0 && C::BK == 16) {
+        const bool b_ok = !NN || (a.ldb % 4 == 0 && a.N % 4 == 0 &&
+                                  reinterpret_cast<uintptr_t>(a.B0) % 16 == 0);
+        if (vec && b_ok && a.K % 16 == 0 && a.k_split_len % 16 == 0) {
             hipLaunchKernelGGL(
-                (gemm_direct_kernel<C, SCHED, GROUPED, NB, EPI>),
+                (gemm_direct_kernel<C, SCHED, NN, GROUPED, NB, EPI>),
                 dim3(static_cast<unsigned>(a.m_tiles) * static_cast<unsigned>(a.n_tiles) *
                      static_cast<unsigned>(a.k_splits)),
                 dim3(C::THREADS), 0, s, a);
             return;
         }
     }
-    const dim3 grid(static_cast<unsigned>(a.m_tiles) * static_cast<unsigned>(a.n_tiles) *
-                     static_cast<unsigned>(a.k_splits));
-    if (vec)
-        hipLaunchKernelGGL((gemm_kernel<C, SCHED, NN, true, GROUPED, NB, EPI>), grid, dim3(C::THREADS),
-                           0, s, a);
-    else
-        hipLaunchKernelGGL((gemm_kernel<C, SCHED, NN, false, GROUPED, NB, EPI>), grid, dim3(C::THREADS),
-                           0, s, a);
+    if constexpr (C::STAGED) {
+        const dim3 grid(static_cast<unsigned>(a.m_tiles) * static_cast<unsigned>(a.n_tiles) *
+                        static_cast<unsigned>(a.k_splits));
+        if (vec)
+            hipLaunchKernelGGL((gemm_kernel<C, SCHED, NN, true, GROUPED, NB, EPI>), grid,
+                               dim3(C::THREADS), 0, s, a);
+        else
+            hipLaunchKernelGGL((gemm_kernel<C, SCHED, NN, false, GROUPED, NB, EPI>), grid,
+                               dim3(C::THREADS), 0, s, a);
+    } else {
+        throw Unsupported("GEMM tile shape needs aligned rows and K % 16 == 0");
+    }
 }
 
 using DenseCfg = CfgOf<MOE_DENSE_CFG>::T;
+using DenseMidCfg = CfgOf<8>::T;
+using DenseSmallCfg = CfgOf<9>::T;
 using W13Cfg = CfgOf<MOE_W13_CFG>::T;
 using W2Cfg = CfgOf<MOE_W2_CFG>::T;
 
+template <class C, bool NN>
+void launch_dense(const GemmArgs& a, bool vec, hipStream_t s) {
+    launch_cfg<C, MOE_DENSE_SCHED | SCHED_DIRECT, NN, false, 1, EPI_BIAS>(a, vec, s);
+}
+
+template <class C>
+int dense_occupancy(bool nn) {
+    constexpr int SCHED = MOE_DENSE_SCHED | SCHED_DIRECT;
+    int n = 0;
+    const hipError_t e =
+        nn ? hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                 &n, gemm_direct_kernel<C, SCHED, true, false, 1, EPI_BIAS>, C::THREADS, 0)
+           : hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                 &n, gemm_direct_kernel<C, SCHED, false, false, 1, EPI_BIAS>, C::THREADS, 0);
+    hip_check(e, "hipOccupancyMaxActiveBlocksPerMultiprocessor");
+    return n > 0 ? n : 1;
+}
+
 }  // namespace
+
+GemmTile dense_tile(int tile) {
+    switch (tile) {
+        case 1: return {DenseMidCfg::BM, DenseMidCfg::BN};
+        case 2: return {DenseSmallCfg::BM, DenseSmallCfg::BN};
+        default: return {DenseCfg::BM, DenseCfg::BN};
+    }
+}
+
+int dense_blocks_per_cu(int tile, bool nn) {
+    switch (tile) {
+        case 1: return dense_occupancy<DenseMidCfg>(nn);
+        case 2: return dense_occupancy<DenseSmallCfg>(nn);
+        default: return dense_occupancy<DenseCfg>(nn);
+    }
+}
 
 int gemm_blocks_per_cu(GemmUse use) {
     int n = 0;
@@ -622,14 +722,15 @@ int gemm_blocks_per_cu(GemmUse use) {
     switch (use) {
         case GemmUse::W2:
             if constexpr ((MOE_W2_SCHED & SCHED_DIRECT) != 0 && W2Cfg::BK == 16)
-                query(gemm_direct_kernel<W2Cfg, MOE_W2_SCHED, true, 1, EPI_STORE>, W2Cfg::THREADS);
+                query(gemm_direct_kernel<W2Cfg, MOE_W2_SCHED, false, true, 1, EPI_STORE>,
+                      W2Cfg::THREADS);
             else
                 query(gemm_kernel<W2Cfg, MOE_W2_SCHED, false, true, true, 1, EPI_STORE>,
                       W2Cfg::THREADS);
             break;
         default:
             if constexpr ((MOE_W13_SCHED & SCHED_DIRECT) != 0 && W13Cfg::BK == 16)
-                query(gemm_direct_kernel<W13Cfg, MOE_W13_SCHED, true, 2, EPI_SWIGLU>,
+                query(gemm_direct_kernel<W13Cfg, MOE_W13_SCHED, false, true, 2, EPI_SWIGLU>,
                       W13Cfg::THREADS);
             else
                 query(gemm_kernel<W13Cfg, MOE_W13_SCHED, false, true, true, 2, EPI_SWIGLU>,
@@ -668,8 +769,21 @@ void launch_gemm(const GemmArgs& args, bool nn, bool grouped, int epi, bool vec,
     }
     if (!grouped) {
         if (epi != EPI_BIAS) throw Unsupported("dense GEMM epilogue");
-        if (nn) launch_cfg<DenseCfg, MOE_DENSE_SCHED, true, false, 1, EPI_BIAS>(a, vec, s);
-        else launch_cfg<DenseCfg, MOE_DENSE_SCHED, false, false, 1, EPI_BIAS>(a, vec, s);
+        switch (a.tile) {
+            case 0:
+                if (nn) launch_cfg<DenseCfg, MOE_DENSE_SCHED, true, false, 1, EPI_BIAS>(a, vec, s);
+                else launch_cfg<DenseCfg, MOE_DENSE_SCHED, false, false, 1, EPI_BIAS>(a, vec, s);
+                break;
+            case 1:
+                if (nn) launch_dense<DenseMidCfg, true>(a, vec, s);
+                else launch_dense<DenseMidCfg, false>(a, vec, s);
+                break;
+            case 2:
+                if (nn) launch_dense<DenseSmallCfg, true>(a, vec, s);
+                else launch_dense<DenseSmallCfg, false>(a, vec, s);
+                break;
+            default: throw Unsupported("dense GEMM tile shape");
+        }
         return;
     }
     if (nn) throw Unsupported("grouped NN GEMM");

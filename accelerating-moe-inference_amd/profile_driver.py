@@ -23,7 +23,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("what", choices=["copy", "layer"])
     ap.add_argument("--mib", type=int, default=1024)
-    ap.add_argument("--config", default="c3")
+    ap.add_argument("--config", default="c3", choices=["c3", "c4", "c5"])
     ap.add_argument("--steps", type=int, default=2)
     args = ap.parse_args()
 

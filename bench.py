@@ -35,7 +35,53 @@ CONFIGS = {
                workload="mixtral_moe_layer_fp32"),
     "c4": dict(T=16384, d=2048, E=64, k=8, d_ff=1408, zipf=1.2,
                workload="fine_grained_zipf_moe_layer_fp32"),
+    # the MoE FFN of config 5's decoder (batch 8 x seq 512 tokens, d 1024)
+    "c5": dict(T=4096, d=1024, E=8, k=2, d_ff=2816, zipf=None,
+               workload="decoder_prefill_moe_ffn_fp32"),
 }
+
+# Config 2: standalone SGEMM sweep (NN, row-major, A and B ~ U[-1, 1]).
+SGEMM_SHAPES = [(1024, 1024, 1024), (2048, 2048, 2048), (4096, 4096, 4096), (8192, 8192, 8192),
+                (16, 14336, 4096), (64, 14336, 4096), (256, 14336, 4096), (512, 14336, 4096)]
+
+
+def sgemm_sweep(args):
+    """One JSON line per config-2 shape: TFLOP/s against the fp32 MFMA peak
+    and the HBM roofline (max of flop time and byte time)."""
+    import torch
+    pkg = load_pkg()
+    ctx = pkg.Context(0)
+    g = torch.Generator(device="cuda").manual_seed(0)
+    for layout in ("nn", "nt"):
+        for M, N, K in SGEMM_SHAPES:
+            a = torch.rand((M, K), device="cuda", generator=g) * 2 - 1
+            b = (torch.rand((K, N), device="cuda", generator=g) * 2 - 1) if layout == "nn" else \
+                (torch.rand((N, K), device="cuda", generator=g) * 2 - 1)
+            c = torch.empty((M, N), device="cuda")
+            fn = ctx.sgemm_nn if layout == "nn" else ctx.sgemm_nt
+            for _ in range(args.warmup):
+                fn(a, b, c)
+            ctx.reset_timing()
+            ctx.set_timing(True)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(args.steps):
+                fn(a, b, c)
+            torch.cuda.synchronize()
+            wall = (time.perf_counter() - t0) / args.steps
+            ctx.set_timing(False)
+            ms, n = ctx.kernel_times()[f"sgemm_{layout}"]
+            t = ms / n * 1e-3
+            flops = 2.0 * M * N * K
+            nbytes = 4.0 * (M * K + K * N + M * N)
+            floor = max(flops / (FP32_MFMA_PEAK_TFLOPS * 1e12), nbytes / (HBM_PEAK_GBS * 1e9))
+            print(json.dumps({"workload": "sgemm", "layout": layout, "M": M, "N": N, "K": K,
+                              "kernel_ms": t * 1e3, "wall_ms": wall * 1e3,
+                              "tflops": flops / t / 1e12,
+                              "frac_fp32_mfma_peak": flops / t / 1e12 / FP32_MFMA_PEAK_TFLOPS,
+                              "frac_of_roofline_time": floor / t}), flush=True)
+            del a, b, c
+    ctx.close()
 
 
 def load_pkg():
@@ -108,12 +154,17 @@ def main():
     ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="target CPU time of the cpu_baseline sample (0 = skip)")
+    ap.add_argument("--sgemm", action="store_true",
+                    help="config-2 SGEMM sweep instead of the layer (one JSON line per shape)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported "
               "(this build targets a single MI355X; see DESIGN.md for sharding)",
               file=sys.stderr)
         sys.exit(2)
+    if args.sgemm:
+        sgemm_sweep(args)
+        return
 
     import numpy as np
     import torch

@@ -45,8 +45,15 @@ def host(t):
 
 
 # ------------------------------------------------------------------ SGEMM
+# Besides edge shapes, these reach every dense tile shape and split-K path of
+# the planner on a 256-CU MI355X: (40, 384, 4096) and (100, 300, 512) take the
+# 32x128 tile with K splits, (64, 1408, 2048) the 64x128 tile with splits,
+# (200, 520, 64) the 32x128 tile unsplit, (33, 250, 512) ragged M and N on a
+# small tile, (64, 130, 256) an NN B whose rows are not 16-byte multiples.
 SGEMM_SHAPES = [(1, 1, 1), (7, 5, 33), (129, 130, 17), (128, 128, 128),
-                (256, 384, 512), (33, 200, 1000), (300, 64, 4), (5, 700, 2)]
+                (256, 384, 512), (33, 200, 1000), (300, 64, 4), (5, 700, 2),
+                (40, 384, 4096), (100, 300, 512), (64, 1408, 2048), (200, 520, 64),
+                (33, 250, 512), (64, 130, 256)]
 
 
 @pytest.mark.parametrize("m,n,k", SGEMM_SHAPES)
@@ -70,9 +77,13 @@ def test_sgemm_nn_vs_oracle(ctx, torch, orc, m, n, k):
     rng = np.random.default_rng(m * 5 + n * 11 + k)
     a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
     b = rng.uniform(-1, 1, (k, n)).astype(np.float32)
+    bias = rng.uniform(-1, 1, n).astype(np.float32)
     c = torch.empty((m, n), device="cuda")
     ctx.sgemm_nn(dev(torch, a), dev(torch, b), c)
-    assert_close(host(c), orc.matmul_nn(a, b), what="nn")
+    ref = orc.matmul_nn(a, b)
+    assert_close(host(c), ref, what="nn")
+    ctx.sgemm_nn(dev(torch, a), dev(torch, b), c, bias=dev(torch, bias))
+    assert_close(host(c), ref + bias, what="nn+bias")
 
 
 def test_sgemm_unaligned_k(ctx, torch, orc):
@@ -126,6 +137,10 @@ def test_sgemm_skinny_config2_row_sample(ctx, torch, orc, m):
     rows = np.unique(np.linspace(0, m - 1, 8).astype(int))
     ref = orc.matmul_nn(host(a)[rows], host(b))
     assert_close(host(c)[rows], ref, what=f"skinny {m}")
+    # split-K partials are summed in a fixed order: a second call is identical
+    c2 = torch.empty_like(c)
+    ctx.sgemm_nn(a, b, c2)
+    assert torch.equal(c, c2)
 
 
 # ------------------------------------------------------------ elementwise
