@@ -23,12 +23,13 @@ OK, ERR_INVALID, ERR_RUNTIME, ERR_UNSUPPORTED = 0, 1, 2, 3
 CONTRACT_NONE, CONTRACT_FMA = 0, 1
 ROUTER_PHI_QUANT, ROUTER_SOFTMAX_TOPK = 0, 1
 ACT_SWIGLU, ACT_SILU_MLP = 0, 1
+NORM_NONE, NORM_LAYER = 0, 1
 
 EXPORTS = (
     "moe_ctx_create", "moe_ctx_destroy", "moe_ctx_reserve", "moe_ctx_set_timing",
     "moe_ctx_kernel_times", "moe_ctx_reset_timing", "moe_last_error",
     "moe_version", "moe_sgemm_nt", "moe_sgemm_nn", "moe_silu", "moe_mul",
-    "moe_gate_logits",
+    "moe_layer_norm", "moe_gate_logits",
     "moe_route", "moe_permute", "moe_expert_ffn_grouped", "moe_combine",
     "moe_layer_forward",
 )
@@ -47,13 +48,16 @@ class LayerDesc(ctypes.Structure):
                 ("E", ctypes.c_int64), ("k", ctypes.c_int64),
                 ("d_ff", ctypes.c_int64), ("act", ctypes.c_int32),
                 ("router", ctypes.c_int32), ("quantum", ctypes.c_float),
-                ("tie_eps", ctypes.c_float), ("contract", ctypes.c_int32)]
+                ("tie_eps", ctypes.c_float), ("contract", ctypes.c_int32),
+                ("norm", ctypes.c_int32), ("norm_eps", ctypes.c_float),
+                ("residual", ctypes.c_int32)]
 
 
 class LayerWeights(ctypes.Structure):
     _fields_ = [("gate_w", ctypes.c_void_p), ("expert_bias", ctypes.c_void_p),
                 ("w1", ctypes.c_void_p), ("w3", ctypes.c_void_p),
-                ("w2", ctypes.c_void_p)]
+                ("w2", ctypes.c_void_p), ("norm_w", ctypes.c_void_p),
+                ("norm_b", ctypes.c_void_p)]
 
 
 _lib = None
@@ -86,6 +90,7 @@ def load_library(path: str = LIB_PATH):
         "moe_sgemm_nn": ([P, P, P, P, P, I64, I64, I64, P], I),
         "moe_silu": ([P, P, P, I64, P], I),
         "moe_mul": ([P, P, P, P, I64, P], I),
+        "moe_layer_norm": ([P, P, P, P, F, I64, I64, I, P, P, P, P], I),
         "moe_gate_logits": ([P, P, P, P, I64, I64, I64, I, P], I),
         "moe_route": ([P, P, P, I64, I64, I64, I, F, F, P, P, P], I),
         "moe_permute": ([P, P, I64, I64, I64, P, P, P, P], I),
@@ -210,6 +215,17 @@ class Context:
                             a.numel(), _stream()))
         return c
 
+    def layer_norm(self, x, weight, bias, y=None, eps=1e-5, contract=CONTRACT_FMA,
+                   row_mean=None, row_inv=None):
+        """Layer norm over the last axis; y / row_mean / row_inv may be None."""
+        h = x.shape[-1]
+        rows = x.numel() // h if h else 0
+        _check(_lib.moe_layer_norm(self.handle, _f32(x, "x"), _f32(weight, "weight"),
+                                   _f32(bias, "bias"), eps, rows, h, contract,
+                                   _f32(y, "y"), _f32(row_mean, "row_mean"),
+                                   _f32(row_inv, "row_inv"), _stream()))
+        return y
+
     def gate_logits(self, x, gate_w, logits, contract=CONTRACT_FMA):
         T, d = x.shape
         E = gate_w.shape[0]
@@ -263,7 +279,9 @@ class Context:
             gate_w=_f32(weights["gate_w"], "gate_w"),
             expert_bias=_f32(weights.get("expert_bias"), "expert_bias"),
             w1=_f32(weights["w1"], "w1"), w3=_f32(weights.get("w3"), "w3"),
-            w2=_f32(weights["w2"], "w2"))
+            w2=_f32(weights["w2"], "w2"),
+            norm_w=_f32(weights.get("norm_w"), "norm_w"),
+            norm_b=_f32(weights.get("norm_b"), "norm_b"))
         _check(_lib.moe_layer_forward(self.handle, ctypes.byref(desc),
                                       ctypes.byref(W), _f32(x, "x"),
                                       _f32(y, "y"), _i32(topk_idx, "topk_idx"),
@@ -272,6 +290,8 @@ class Context:
 
 
 def make_desc(T, d, E, k, d_ff, act=ACT_SWIGLU, router=ROUTER_PHI_QUANT,
-              quantum=1e-3, tie_eps=2e-2, contract=CONTRACT_FMA) -> LayerDesc:
+              quantum=1e-3, tie_eps=2e-2, contract=CONTRACT_FMA, norm=NORM_NONE,
+              norm_eps=1e-5, residual=False) -> LayerDesc:
     return LayerDesc(T=T, d=d, E=E, k=k, d_ff=d_ff, act=act, router=router,
-                     quantum=quantum, tie_eps=tie_eps, contract=contract)
+                     quantum=quantum, tie_eps=tie_eps, contract=contract, norm=norm,
+                     norm_eps=norm_eps, residual=int(bool(residual)))

@@ -197,8 +197,19 @@ void silu(const Tensor& x, Tensor& y) {
 void add_inplace(Tensor&, const Tensor&) { outside("add_inplace"); }
 void add_bias_inplace(Tensor&, const Tensor&) { outside("add_bias_inplace"); }
 void softmax_last_dim(const Tensor&, Tensor&) { outside("softmax_last_dim"); }
-void layer_norm(const Tensor&, const Tensor&, const Tensor&, float, Tensor&) {
-    outside("layer_norm");
+// The post-attention norm in front of the MoE block (src/tensor.cu:175-189):
+// bit-identical to the CPU loop built with FMA contraction, the drop-in's
+// default (PhiMoE's `contract`).
+void layer_norm(const Tensor& x, const Tensor& weight, const Tensor& bias, float eps, Tensor& y) {
+    const std::size_t h = x.ndim() > 0 ? x.size(x.ndim() - 1) : 0;
+    if (h == 0 || weight.size() != h || bias.size() != h || y.size() != x.size())
+        throw std::invalid_argument("layer norm shape");
+    const std::size_t rows = x.size() / h;
+    DeviceBuffer dx = to_device(x), dw = to_device(weight), db = to_device(bias);
+    check(moe_layer_norm(moe_dropin::context(), dx.as<float>(), dw.as<float>(), db.as<float>(),
+                         eps, static_cast<int64_t>(rows), static_cast<int64_t>(h),
+                         MOE_CONTRACT_FMA, dx.as<float>(), nullptr, nullptr, nullptr));
+    dx.download(y.data(), y.size() * sizeof(float));
 }
 void apply_rope(Tensor&, Tensor&, std::size_t, std::size_t, std::size_t, std::size_t, float) {
     outside("apply_rope");

@@ -70,13 +70,15 @@ void matmul_transposed(const Tensor& a, const Tensor& b, Tensor& c);
 // GPU elementwise, bit-identical to the reference's CPU loops.
 void mul(const Tensor& a, const Tensor& b, Tensor& c);
 void silu(const Tensor& x, Tensor& y);
+// GPU layer norm over the last axis (the MoE block's post-attention norm),
+// bit-identical to the reference's CPU loop under FMA contraction.
+void layer_norm(const Tensor& x, const Tensor& weight, const Tensor& bias,
+                float eps, Tensor& y);
 // Outside the MoE hot path this library accelerates: declared for source
 // compatibility with the reference header, they throw std::logic_error.
 void add_inplace(Tensor& a, const Tensor& b);
 void add_bias_inplace(Tensor& a, const Tensor& bias);
 void softmax_last_dim(const Tensor& x, Tensor& y);
-void layer_norm(const Tensor& x, const Tensor& weight, const Tensor& bias,
-                float eps, Tensor& y);
 void apply_rope(Tensor& q, Tensor& k, std::size_t seq_len,
                 std::size_t q_heads, std::size_t kv_heads, std::size_t head_dim,
                 float theta);

@@ -23,8 +23,10 @@
  *                       gemm_grouped / w2 launches         src/model.cu:625-667
  *   moe_combine         y[t] += w * out in expert order    src/layer.cu:99-101,
  *                       gemm_grouped_combine epilogue      src/model.cu:436-447
+ *   moe_layer_norm      tensor_ops::layer_norm             src/tensor.cu:175-189,
+ *                       layer_norm_rows / forward_stats    src/model.cu:720-846,1440-1480
  *   moe_layer_forward   PhiMoE::forward                    src/layer.cu:80-103,
- *                       the MoE block of generate()        src/model.cu:1976-2021
+ *                       the MoE block of generate()        src/model.cu:1968-2021
  *   moe_ctx_*           DeviceBuffer / Scratch workspace   src/model.cu:45-68,1294-1324
  */
 #ifndef MOE_AMD_H
@@ -59,6 +61,15 @@ extern "C" {
 #define MOE_ACT_SWIGLU 0
 #define MOE_ACT_SILU_MLP 1
 
+/* Norm in front of the experts (moe_layer_desc.norm).  NONE: gate and
+ * experts read x.  LAYER: they read layer_norm(x, norm_w, norm_b, norm_eps),
+ * the reference's post-attention norm (src/model.cu:1968-2002), computed
+ * bit-identically to tensor_ops::layer_norm under desc.contract; the layer
+ * keeps only its per-row statistics and normalises x where the gate and the
+ * w1/w3 GEMM read it. */
+#define MOE_NORM_NONE 0
+#define MOE_NORM_LAYER 1
+
 typedef struct moe_ctx moe_ctx;
 
 typedef struct moe_layer_desc {
@@ -71,7 +82,11 @@ typedef struct moe_layer_desc {
     int32_t router;   /* MOE_ROUTER_*                               */
     float quantum;    /* PHI_QUANT score quantum (1e-3 in the reference)   */
     float tie_eps;    /* PHI_QUANT tie margin (2e-2 in the reference)      */
-    int32_t contract; /* MOE_CONTRACT_* for gate logits and combine         */
+    int32_t contract; /* MOE_CONTRACT_* for the norm, gate logits, combine   */
+    int32_t norm;     /* MOE_NORM_*                                         */
+    float norm_eps;   /* layer norm epsilon (MOE_NORM_LAYER)                */
+    int32_t residual; /* 1: y = x + MoE(...), x un-normalised (the block's
+                         residual, src/model.cu:2009-2012); 0: y = MoE(...) */
 } moe_layer_desc;
 
 typedef struct moe_layer_weights {
@@ -80,6 +95,8 @@ typedef struct moe_layer_weights {
     const float* w1;          /* [E, d_ff, d]                   */
     const float* w3;          /* [E, d_ff, d]; NULL for SILU_MLP */
     const float* w2;          /* [E, d, d_ff]                   */
+    const float* norm_w;      /* [d] layer norm weight (MOE_NORM_LAYER) */
+    const float* norm_b;      /* [d] layer norm bias   (MOE_NORM_LAYER) */
 } moe_layer_weights;
 
 /* ---- context: device binding, grow-only workspace, optional kernel timing.
@@ -120,6 +137,16 @@ int moe_silu(moe_ctx* ctx, const float* x, float* y, int64_t n, void* stream);
 int moe_mul(moe_ctx* ctx, const float* a, const float* b, float* c, int64_t n,
             void* stream);
 
+/* ---- layer norm over the last axis of x[rows, h], bit-identical to
+ * tensor_ops::layer_norm under `contract`: row_mean[r] and row_inv[r] =
+ * 1 / sqrt(var + eps) from the CPU loop's sequential sums, and
+ * y = (x - mean) * inv * weight + bias.  y, row_mean and row_inv may each be
+ * NULL (statistics only: y NULL; the statistics are then still computed). */
+int moe_layer_norm(moe_ctx* ctx, const float* x, const float* weight,
+                   const float* bias, float eps, int64_t rows, int64_t h,
+                   int contract, float* y, float* row_mean, float* row_inv,
+                   void* stream);
+
 /* ---- router gate logits[T,E] = x[T,d] Wg[E,d]^T with one k-ascending fp32
  * accumulator per output: bit-identical to the CPU path under `contract`. */
 int moe_gate_logits(moe_ctx* ctx, const float* x, const float* gate_w,
@@ -159,8 +186,9 @@ int moe_combine(moe_ctx* ctx, const float* out_rows, const int32_t* topk_idx,
                 float* y, int64_t T, int64_t k, int64_t d, int contract,
                 void* stream);
 
-/* ---- the whole MoE layer: gate -> route -> permute -> expert FFN ->
- * combine.  topk_idx_out [T,k] / topk_w_out [T,k] may be NULL. */
+/* ---- the whole MoE layer: [norm statistics ->] gate -> route -> permute ->
+ * expert FFN -> combine [+ x].  topk_idx_out [T,k] / topk_w_out [T,k] may be
+ * NULL. */
 int moe_layer_forward(moe_ctx* ctx, const moe_layer_desc* desc,
                       const moe_layer_weights* weights, const float* x,
                       float* y, int32_t* topk_idx_out, float* topk_w_out,

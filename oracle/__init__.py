@@ -54,6 +54,8 @@ def lib():
         L.orc_silu.restype = None
         L.orc_mul.argtypes = [P, P, P, S]
         L.orc_mul.restype = None
+        L.orc_layer_norm.argtypes = [P, P, P, F, S, S, I, P, P, P]
+        L.orc_layer_norm.restype = I
         L.orc_route.argtypes = [P, P, S, S, S, I, F, F, P, P]
         L.orc_route.restype = I
         L.orc_permute.argtypes = [P, S, S, S, P, P, P]
@@ -136,6 +138,20 @@ def mul(a, b):
     c = np.empty_like(a)
     lib().orc_mul(_p(a), _p(b), _p(c), a.size)
     return c
+
+
+def layer_norm(x, weight, bias, eps=1e-5, contract=CONTRACT_FMA):
+    """tensor_ops::layer_norm over the last axis; returns (y, row_mean, row_inv)."""
+    x, weight, bias = _f32(x), _f32(weight), _f32(bias)
+    h = x.shape[-1]
+    rows = x.size // h if h else 0
+    assert weight.size == h and bias.size == h
+    y = np.empty_like(x)
+    mean = np.empty(rows, np.float32)
+    inv = np.empty(rows, np.float32)
+    _check(lib().orc_layer_norm(_p(x), _p(weight), _p(bias), float(eps), rows, h,
+                                int(contract), _p(y), _p(mean), _p(inv)), "layer_norm")
+    return y, mean, inv
 
 
 def route(logits, k, mode=ROUTER_PHI_QUANT, quantum=1e-3, tie_eps=2e-2,

@@ -133,6 +133,48 @@ void orc_silu(const float* x, float* y, size_t n) {
         y[i] = x[i] / (1.0f + orc_accurate_exp(-x[i]));
 }
 
+/* tensor_ops::layer_norm (src/tensor.cu:175-189), the post-attention norm
+ * in front of the MoE block.  Per row: mean = (one float accumulator over
+ * j ascending) / h; var = (one float accumulator of d*d, d = x - mean) / h;
+ * inv = 1 / sqrt(var + eps); y = (x - mean) * inv * weight + bias, left to
+ * right.  `contract` decides whether the two `a*b + c` sites (var += d*d and
+ * ... * weight + bias) are fused, as for the gate (an FMA host build of the
+ * reference contracts them, its no-FMA Xeon build does not).  The
+ * reference's GPU form keeps the same chains (src/model.cu:720-846; the
+ * epilogue's four ops at :235-246).  y, row_mean and row_inv may each be
+ * NULL.
+ * Pinned by: closed forms (constant rows give y = bias exactly; small
+ * integer rows give exact mean and variance), float64 within rounding, and
+ * cases that fail the plausible slips -- a double or compensated
+ * accumulator, variance as E[x^2] - mean^2, eps outside the sqrt, the bias
+ * scaled by the weight (tests/test_oracle.py). */
+int orc_layer_norm(const float* x, const float* weight, const float* bias,
+                   float eps, size_t rows, size_t h, int contract, float* y,
+                   float* row_mean, float* row_inv) {
+    if (rows && (!x || h == 0 || !weight || !bias)) return 1;
+#pragma omp parallel for schedule(static)
+    for (long long r = 0; r < (long long)rows; ++r) {
+        float mean = 0.0f;
+        for (size_t j = 0; j < h; ++j) mean += x[orc_at(rows, h, (size_t)r, j)];
+        mean /= (float)h;
+        float var = 0.0f;
+        for (size_t j = 0; j < h; ++j) {
+            const float dv = x[orc_at(rows, h, (size_t)r, j)] - mean;
+            var = orc_mac(var, dv, dv, contract);
+        }
+        const float inv = 1.0f / sqrtf(var / (float)h + eps);
+        if (row_mean) row_mean[r] = mean;
+        if (row_inv) row_inv[r] = inv;
+        if (!y) continue;
+        for (size_t j = 0; j < h; ++j) {
+            const size_t o = orc_at(rows, h, (size_t)r, j);
+            const float scaled = (x[o] - mean) * inv;
+            y[o] = contract ? fmaf(scaled, weight[j], bias[j]) : scaled * weight[j] + bias[j];
+        }
+    }
+    return 0;
+}
+
 /* c = a * b elementwise (src/tensor.cu:163-167). Pinned by direct products. */
 void orc_mul(const float* a, const float* b, float* c, size_t n) {
 #pragma omp parallel for schedule(static)

@@ -49,6 +49,9 @@ int orc_matmul_nn(const float* a, const float* b, float* c,
                   size_t m, size_t n, size_t k, int contract);
 void orc_silu(const float* x, float* y, size_t n);
 void orc_mul(const float* a, const float* b, float* c, size_t n);
+int orc_layer_norm(const float* x, const float* weight, const float* bias,
+                   float eps, size_t rows, size_t h, int contract, float* y,
+                   float* row_mean, float* row_inv);
 
 int orc_route(const float* logits, const float* expert_bias,
               size_t T, size_t E, size_t k, int mode,

@@ -160,8 +160,25 @@ int shim_silu_mul(const float* x, const float* u, int64_t n, float* s, float* p)
 
 int shim_outside_op() {
     return guarded([] {
-        Tensor x({2, 4}), w({4}), b({4}), y({2, 4});
+        Tensor q({2, 8}), k({2, 8});
+        tensor_ops::apply_rope(q, k, 2, 1, 1, 8, 10000.0f);
+    });
+}
+
+int shim_layer_norm_bad_shape() {
+    return guarded([] {
+        Tensor x({2, 4}), w({3}), b({4}), y({2, 4});
         tensor_ops::layer_norm(x, w, b, 1e-5f, y);
+    });
+}
+
+int shim_layer_norm(const float* x, int64_t rows, int64_t h, const float* w, const float* b,
+                    float eps, float* y) {
+    return guarded([&] {
+        Tensor X = make(x, {size_t(rows), size_t(h)}), W = make(w, {size_t(h)}),
+               B = make(b, {size_t(h)}), Y({size_t(rows), size_t(h)});
+        tensor_ops::layer_norm(X, W, B, eps, Y);
+        std::memcpy(y, Y.data(), rows * h * sizeof(float));
     });
 }
 

@@ -111,12 +111,30 @@ def test_shape_errors_before_any_device_work(shim):
     assert err(shim) == "matmul_transposed shape"
     assert shim.shim_outside_op() == LOGIC
     assert "outside the MoE hot path" in err(shim)
+    assert shim.shim_layer_norm_bad_shape() == INVALID
+    assert err(shim) == "layer norm shape"
 
 
 # ---------------------------------------------------------------- GPU side
 @pytest.mark.gpu
 def test_tensor_pinned(shim):
     assert shim.shim_tensor_semantics(1) == 0, err(shim)
+
+
+@pytest.mark.gpu
+def test_layer_norm_bit_exact(shim, orc):
+    rng = np.random.default_rng(8)
+    rows, h = 45, 300
+    x = (1 + 3 * rng.normal(size=(rows, h))).astype(np.float32)
+    w = rng.normal(size=h).astype(np.float32)
+    b = rng.normal(size=h).astype(np.float32)
+    y = np.empty_like(x)
+    I = ctypes.c_int64
+    rc = shim.shim_layer_norm(fptr(x), I(rows), I(h), fptr(w), fptr(b), ctypes.c_float(1e-5),
+                              fptr(y))
+    assert rc == 0, err(shim)
+    want, _, _ = orc.layer_norm(x, w, b, 1e-5, orc.CONTRACT_FMA)
+    assert np.array_equal(y, want)
 
 
 @pytest.mark.gpu

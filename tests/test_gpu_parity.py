@@ -421,6 +421,117 @@ def test_layer_skewed_config4_full_size(ctx, pkg, torch, orc):
     assert counts.max() > 4 * counts.mean()  # heavily imbalanced loads
 
 
+# ------------------------------------------------------------- layer norm
+@pytest.mark.parametrize("contract", [0, 1])
+@pytest.mark.parametrize("rows,h", [(1, 1), (3, 5), (64, 64), (65, 4096), (200, 1000),
+                                    (130, 33), (4096, 1024)])
+def test_layer_norm_bit_exact(ctx, torch, orc, contract, rows, h):
+    print(f"layer_norm {rows}x{h} contract={contract}", flush=True)
+    rng = np.random.default_rng(rows * 7 + h + contract)
+    x = (2 + 3 * rng.normal(size=(rows, h))).astype(np.float32)
+    w = rng.normal(size=h).astype(np.float32)
+    b = rng.normal(size=h).astype(np.float32)
+    ry, rm, ri = orc.layer_norm(x, w, b, 1e-5, contract)
+    y = torch.empty((rows, h), device="cuda")
+    mean = torch.empty(rows, device="cuda")
+    inv = torch.empty(rows, device="cuda")
+    ctx.layer_norm(dev(torch, x), dev(torch, w), dev(torch, b), y, 1e-5, contract, mean, inv)
+    assert np.array_equal(host(mean), rm) and np.array_equal(host(inv), ri)
+    assert np.array_equal(host(y), ry)
+    # statistics only; and y alone (statistics in the workspace), in place
+    mean.zero_()
+    ctx.layer_norm(dev(torch, x), None, None, None, 1e-5, contract, mean, inv)
+    assert np.array_equal(host(mean), rm)
+    xd = dev(torch, x)
+    ctx.layer_norm(xd, dev(torch, w), dev(torch, b), xd, 1e-5, contract)
+    assert np.array_equal(host(xd), ry)
+
+
+def _norm_block(ctx, pkg, torch, x, gw, w1, w3, w2, nw, nb, k, act, mode, contract,
+                residual=True, bias=None):
+    T, d = x.shape
+    E, d_ff, _ = w1.shape
+    desc = pkg.make_desc(T, d, E, k, d_ff, act=act, router=mode, contract=contract,
+                         norm=pkg.NORM_LAYER, norm_eps=1e-5, residual=residual)
+    y = torch.empty((T, d), device="cuda")
+    idx = torch.empty((T, k), dtype=torch.int32, device="cuda")
+    w = torch.empty((T, k), device="cuda")
+    weights = {"gate_w": gw, "w1": w1, "w3": w3, "w2": w2, "expert_bias": bias,
+               "norm_w": nw, "norm_b": nb}
+    ctx.layer_forward(desc, weights, x, y, idx, w)
+    return y, idx, w
+
+
+def _norm_block_oracle(orc, x, gw, w1, w3, w2, nw, nb, k, act, mode, contract, residual,
+                       bias=None):
+    xn, _, _ = orc.layer_norm(x, nw, nb, 1e-5, contract)
+    y, idx, w = orc.moe_forward(xn, gw, w1, w3, w2, k, act=act, router_mode=mode,
+                                contract=contract, expert_bias=bias)
+    return (y + x if residual else y), idx, w
+
+
+# d = 256: normalised inside the gate and the w1/w3 GEMM; d = 200: the
+# normalised copy path (d % 16 != 0)
+@pytest.mark.parametrize("d", [256, 200])
+@pytest.mark.parametrize("mode,contract,act", [(0, 0, 0), (0, 1, 0), (1, 1, 0), (1, 0, 1)])
+def test_layer_norm_block_vs_oracle(ctx, pkg, torch, orc, d, mode, contract, act):
+    """The MoE block of the reference's decoder: y = x + MoE(layer_norm(x))
+    (src/model.cu:1968-2021); routing bit-exact, y within the 1e-4 rule."""
+    print(f"norm block d={d} mode={mode} contract={contract} act={act}", flush=True)
+    rng = np.random.default_rng(d + 10 * mode + 100 * contract + act)
+    T, E, k, d_ff = 300, 8, 2, 192
+    x = (0.5 + 2 * rng.normal(size=(T, d))).astype(np.float32)
+    gw = normal(rng, (E, d), 0.05)
+    w1 = normal(rng, (E, d_ff, d), 0.05)
+    w3 = normal(rng, (E, d_ff, d), 0.05) if act == 0 else None
+    w2 = normal(rng, (E, d, d_ff), 0.05)
+    nw = (1 + 0.1 * rng.normal(size=d)).astype(np.float32)
+    nb = (0.1 * rng.normal(size=d)).astype(np.float32)
+    y, idx, w = _norm_block(ctx, pkg, torch, dev(torch, x), dev(torch, gw), dev(torch, w1),
+                            None if w3 is None else dev(torch, w3), dev(torch, w2),
+                            dev(torch, nw), dev(torch, nb), k, act, mode, contract)
+    ry, ridx, rw = _norm_block_oracle(orc, x, gw, w1, w3, w2, nw, nb, k, act, mode, contract,
+                                      residual=True)
+    assert np.array_equal(host(idx), ridx)
+    assert np.max(np.abs(host(w).view(np.int32).astype(np.int64) - rw.view(np.int32))) <= 1
+    assert_close(host(y), ry, what="norm block y")
+
+
+def test_layer_norm_block_without_residual(ctx, pkg, torch, orc):
+    rng = np.random.default_rng(77)
+    T, d, E, k, d_ff = 130, 128, 4, 2, 96
+    x = normal(rng, (T, d))
+    gw, w1, w3 = normal(rng, (E, d), 0.05), normal(rng, (E, d_ff, d), 0.05), normal(rng, (E, d_ff, d), 0.05)
+    w2 = normal(rng, (E, d, d_ff), 0.05)
+    nw, nb = normal(rng, (d,)), normal(rng, (d,), 0.1)
+    y, idx, _ = _norm_block(ctx, pkg, torch, *[dev(torch, a) for a in (x, gw, w1, w3, w2, nw, nb)],
+                            k, 0, 1, 1, residual=False)
+    ry, ridx, _ = _norm_block_oracle(orc, x, gw, w1, w3, w2, nw, nb, k, 0, 1, 1, residual=False)
+    assert np.array_equal(host(idx), ridx)
+    assert_close(host(y), ry, what="norm block, no residual")
+
+
+def test_layer_norm_block_config5_moe_ffn(ctx, pkg, torch, orc):
+    """Config 5's MoE block at full size (8 x 512 tokens, d 1024, E=8, top-2,
+    SwiGLU 2816) behind its post-attention norm, with the residual; the oracle
+    recomputes 32 tokens (every step is per token)."""
+    T, d, E, k, d_ff = 4096, 1024, 8, 2, 2816
+    g = torch.Generator(device="cuda").manual_seed(5)
+    x = torch.randn((T, d), device="cuda", generator=g) * 2 + 0.5
+    gw = torch.randn((E, d), device="cuda", generator=g) * 0.02
+    w1 = torch.randn((E, d_ff, d), device="cuda", generator=g) * 0.02
+    w3 = torch.randn((E, d_ff, d), device="cuda", generator=g) * 0.02
+    w2 = torch.randn((E, d, d_ff), device="cuda", generator=g) * 0.02
+    nw = 1 + 0.1 * torch.randn(d, device="cuda", generator=g)
+    nb = 0.1 * torch.randn(d, device="cuda", generator=g)
+    y, idx, w = _norm_block(ctx, pkg, torch, x, gw, w1, w3, w2, nw, nb, k, 0, 1, 1)
+    s = 32
+    ry, ridx, rw = _norm_block_oracle(orc, host(x)[:s], host(gw), host(w1), host(w3), host(w2),
+                                      host(nw), host(nb), k, 0, 1, 1, residual=True)
+    assert np.array_equal(host(idx)[:s], ridx)
+    assert_close(host(y)[:s], ry, what="config5 block sample")
+
+
 # ------------------------------------------------------------------ errors
 def test_errors_are_reported(ctx, pkg, torch):
     c = torch.empty((4, 4), device="cuda")

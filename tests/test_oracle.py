@@ -109,6 +109,86 @@ def test_mul(orc):
     assert orc.mul(a, b).tolist() == [3.0, -0.5, -3.0]
 
 
+# ---------------------------------------------------------------- layer norm
+@pytest.mark.parametrize("contract", [0, 1])
+def test_layer_norm_closed_forms(orc, contract):
+    eps = F32(1e-5)
+    w = np.array([2.0, -3.0, 0.5, 4.0], F32)
+    b = np.array([0.25, -1.0, 7.0, 0.0], F32)
+    # a constant row: mean exact, var 0, inv = 1/sqrt(eps), y = bias exactly
+    # (eps outside the sqrt, or a bias scaled by the weight, fail here)
+    y, mean, inv = orc.layer_norm(np.full((1, 4), 3.0, F32), w, b, eps, contract)
+    assert mean[0] == 3.0 and inv[0] == F32(1) / np.sqrt(eps)
+    assert np.array_equal(y[0], b)
+    # 1, 2, 3, 4: mean 2.5 and var 1.25 are exact in float
+    x = np.array([[1, 2, 3, 4]], F32)
+    y, mean, inv = orc.layer_norm(x, w, b, eps, contract)
+    want_inv = F32(1) / np.sqrt(F32(1.25) + eps)
+    assert mean[0] == 2.5 and inv[0] == want_inv
+    scaled = (x[0] - F32(2.5)) * want_inv
+    assert np.allclose(y[0], scaled * w + b, rtol=2e-7, atol=1e-7)
+
+
+def test_layer_norm_single_float_accumulator(orc):
+    # 1e8 absorbs each later 1 in a float accumulator, so the ascending float
+    # sum is exactly 0; a double or compensated accumulator gives 16.
+    row = np.array([[1e8] + [1.0] * 16 + [-1e8]], F32)
+    one, zero = np.ones(18, F32), np.zeros(18, F32)
+    _, mean, _ = orc.layer_norm(row, one, zero, 1e-5)
+    assert mean[0] == 0.0
+
+
+def test_layer_norm_two_pass_variance(orc):
+    # mean 10002 is exact; the two-pass variance is (1 + 0 + 1) / 3.  The
+    # one-pass E[x^2] - mean^2 loses it to cancellation (x^2 ~ 1e8).
+    x = np.array([[10001.0, 10002.0, 10003.0]], F32)
+    eps = F32(1e-5)
+    _, mean, inv = orc.layer_norm(x, np.ones(3, F32), np.zeros(3, F32), eps)
+    assert mean[0] == 10002.0
+    assert inv[0] == F32(1) / np.sqrt(F32(2) / F32(3) + eps)
+
+
+@pytest.mark.parametrize("contract", [0, 1])
+def test_layer_norm_vs_float64(orc, contract):
+    rng = np.random.default_rng(31 + contract)
+    x = (3 + 2 * rng.normal(size=(20, 300))).astype(F32)
+    w = rng.normal(size=300).astype(F32)
+    b = rng.normal(size=300).astype(F32)
+    y, mean, inv = orc.layer_norm(x, w, b, 1e-5, contract)
+    x64 = x.astype(np.float64)
+    m64 = x64.mean(axis=1)
+    v64 = ((x64 - m64[:, None]) ** 2).mean(axis=1)
+    i64 = 1 / np.sqrt(v64 + 1e-5)
+    assert np.allclose(mean, m64, rtol=1e-5, atol=1e-6)
+    assert np.allclose(inv, i64, rtol=1e-5)
+    ref = (x64 - m64[:, None]) * i64[:, None] * w + b
+    assert np.max(np.abs(y - ref)) <= 1e-5 * np.max(np.abs(ref))
+
+
+def test_layer_norm_contraction_differs(orc):
+    # The FMA build fuses var += d*d and the weight/bias step; on random rows
+    # that changes some outputs, and the unfused build is the float32 chain.
+    rng = np.random.default_rng(5)
+    x = rng.normal(size=(64, 257)).astype(F32)
+    w = rng.normal(size=257).astype(F32)
+    b = rng.normal(size=257).astype(F32)
+    y1, _, _ = orc.layer_norm(x, w, b, 1e-5, 1)
+    y0, m0, i0 = orc.layer_norm(x, w, b, 1e-5, 0)
+    assert not np.array_equal(y0, y1)
+    r = 3
+    acc = F32(0)
+    for v in x[r]:
+        acc = F32(acc + v)
+    mean = F32(acc / F32(257))
+    var = F32(0)
+    for v in x[r]:
+        dv = F32(v - mean)
+        var = F32(var + F32(dv * dv))
+    inv = F32(F32(1) / np.sqrt(F32(var / F32(257)) + F32(1e-5)))
+    assert m0[r] == mean and i0[r] == inv
+    assert np.array_equal(y0[r], ((x[r] - mean) * inv) * w + b)
+
+
 # ---------------------------------------------------------------- routing
 def _phi(orc, row, k=2):
     idx, w = orc.route(np.array([row], F32), k)
