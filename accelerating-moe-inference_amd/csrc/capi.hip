@@ -265,7 +265,7 @@ void expert_ffn(moe_ctx* ctx, const float* x, const int32_t* perm,
                 const int32_t* offsets, const float* w1, const float* w3,
                 const float* w2, int act, int64_t T, int64_t k, int64_t d,
                 int64_t d_ff, int64_t E, float* h, float* out_rows, hipStream_t s,
-                int w2_splits = 1, const moe::RowNorm* norm = nullptr, int norm_contract = 0) {
+                int w2_splits = 1) {
     const int64_t pairs = T * k;
     if (pairs == 0 || d == 0) return;
     const bool swiglu = act == MOE_ACT_SWIGLU;
@@ -289,10 +289,6 @@ void expert_ffn(moe_ctx* ctx, const float* x, const int32_t* perm,
         a.E = static_cast<int32_t>(E);
         a.m_tiles = static_cast<int32_t>(grouped_m_tiles(pairs, E, tile.bm));
         a.n_tiles = static_cast<int32_t>(moe::ceil_div(d_ff, tile.bn));
-        if (norm != nullptr) {
-            a.norm = *norm;
-            a.norm_contract = norm_contract;
-        }
         moe::require(int64_t(a.m_tiles) * a.n_tiles <= INT32_MAX, "w13 grid too large");
         const bool vec = d % 4 == 0 && aligned16(x) && aligned16(w1) && (!swiglu || aligned16(w3));
         ctx->launch(swiglu ? "expert_w13_swiglu" : "expert_w1_silu", s, [&] {
@@ -341,11 +337,6 @@ void check_desc(const moe_layer_desc* desc) {
     moe::require(desc->residual == 0 || desc->residual == 1, "residual must be 0 or 1");
 }
 
-// The layer normalises x inside the gate and the w1/w3 GEMM when that GEMM
-// takes the direct-load path (d % 16 == 0, 16-byte aligned operands); other
-// shapes normalise x into the workspace first.
-bool fused_norm(const moe_layer_desc& d) { return d.d % 16 == 0; }
-
 // Workspace layout of moe_layer_forward; with base == nullptr it only sizes.
 struct LayerWs {
     float* logits;
@@ -359,12 +350,11 @@ struct LayerWs {
     float* out_rows;
     float* norm_mean;  // MOE_NORM_LAYER: per-token statistics
     float* norm_inv;
-    float* xnorm;      // MOE_NORM_LAYER without the fused path: normalised x
+    float* xnorm;      // MOE_NORM_LAYER: the normalised x [T, d] the experts read
     size_t bytes;
 };
 
-// `materialise`: room for the normalised x ([T, d]).
-LayerWs carve_layer(void* base, const moe_layer_desc& d, bool materialise) {
+LayerWs carve_layer(void* base, const moe_layer_desc& d) {
     Carve c(base);
     LayerWs w{};
     const int64_t pairs = d.T * d.k;
@@ -381,7 +371,7 @@ LayerWs carve_layer(void* base, const moe_layer_desc& d, bool materialise) {
     if (d.norm == MOE_NORM_LAYER) {
         w.norm_mean = c.take<float>(d.T);
         w.norm_inv = c.take<float>(d.T);
-        if (materialise) w.xnorm = c.take<float>(d.T * d.d);
+        w.xnorm = c.take<float>(d.T * d.d);
     }
     w.bytes = c.off + 256;
     return w;
@@ -463,7 +453,7 @@ int moe_ctx_reserve(moe_ctx* ctx, const moe_layer_desc* desc) {
         check_ctx(ctx);
         check_desc(desc);
         DeviceScope dev(ctx->device);
-        ctx->workspace(carve_layer(nullptr, *desc, !fused_norm(*desc)).bytes);
+        ctx->workspace(carve_layer(nullptr, *desc).bytes);
     });
 }
 
@@ -561,7 +551,7 @@ int moe_gate_logits(moe_ctx* ctx, const float* x, const float* gate_w, float* lo
         DeviceScope dev(ctx->device);
         hipStream_t s = as_stream(stream);
         ctx->launch("gate_logits", s, [&] {
-            moe::launch_gate_logits(x, gate_w, logits, T, d, E, contract, nullptr, s);
+            moe::launch_gate_logits(x, gate_w, logits, T, d, E, contract, s);
         });
     });
 }
@@ -590,14 +580,10 @@ int moe_layer_norm(moe_ctx* ctx, const float* x, const float* weight, const floa
             if (row_mean == nullptr) row_mean = c.take<float>(rows);
             if (row_inv == nullptr) row_inv = c.take<float>(rows);
         }
-        ctx->launch("norm_stats", s, [&] {
-            moe::launch_norm_stats(x, rows, h, eps, contract, row_mean, row_inv, s);
+        ctx->launch("layer_norm", s, [&] {
+            moe::launch_layer_norm(x, weight, bias, rows, h, eps, contract, row_mean, row_inv, y,
+                                   ctx->cus, s);
         });
-        if (y != nullptr)
-            ctx->launch("norm_apply", s, [&] {
-                moe::launch_norm_apply(x, weight, bias, row_mean, row_inv, rows, h, contract, y,
-                                       s);
-            });
     });
 }
 
@@ -726,42 +712,27 @@ int moe_layer_forward(moe_ctx* ctx, const moe_layer_desc* desc,
             check_ptr(weights->norm_w, "norm_w");
             check_ptr(weights->norm_b, "norm_b");
         }
-        // the w1/w3 GEMM normalises its A rows itself on the direct-load path
-        const bool fused = norm && fused_norm(D) && aligned16(weights->norm_w) &&
-                           aligned16(weights->norm_b) && aligned16(weights->w1) &&
-                           (D.act != MOE_ACT_SWIGLU || aligned16(weights->w3));
         DeviceScope dev(ctx->device);
         hipStream_t s = as_stream(stream);
-        LayerWs ws = carve_layer(ctx->workspace(carve_layer(nullptr, D, norm && !fused).bytes), D,
-                                 norm && !fused);
+        LayerWs ws = carve_layer(ctx->workspace(carve_layer(nullptr, D).bytes), D);
         int32_t* idx = topk_idx_out != nullptr ? topk_idx_out : ws.idx;
         float* w = topk_w_out != nullptr ? topk_w_out : ws.w;
         const int64_t nb = moe::ceil_div(D.T, moe::kPermTokens);
 
-        // The experts' input: x itself, x normalised on the fly (`rn`), or
-        // the normalised copy in the workspace.
+        // The experts' input: x, or its normalised copy (written once, read
+        // by the gate and the w1/w3 GEMM; the residual stays x).
         const float* xin = x;
-        moe::RowNorm rn{ws.norm_mean, ws.norm_inv, weights->norm_w, weights->norm_b};
-        const moe::RowNorm* rnp = nullptr;
         if (norm) {
-            ctx->launch("norm_stats", s, [&] {
-                moe::launch_norm_stats(x, D.T, D.d, D.norm_eps, D.contract, ws.norm_mean,
-                                       ws.norm_inv, s);
+            ctx->launch("layer_norm", s, [&] {
+                moe::launch_layer_norm(x, weights->norm_w, weights->norm_b, D.T, D.d, D.norm_eps,
+                                       D.contract, ws.norm_mean, ws.norm_inv, ws.xnorm, ctx->cus,
+                                       s);
             });
-            if (fused) {
-                rnp = &rn;
-            } else {
-                ctx->launch("norm_apply", s, [&] {
-                    moe::launch_norm_apply(x, weights->norm_w, weights->norm_b, ws.norm_mean,
-                                           ws.norm_inv, D.T, D.d, D.contract, ws.xnorm, s);
-                });
-                xin = ws.xnorm;
-            }
+            xin = ws.xnorm;
         }
 
         ctx->launch("gate_logits", s, [&] {
-            moe::launch_gate_logits(xin, weights->gate_w, ws.logits, D.T, D.d, D.E, D.contract,
-                                    rnp, s);
+            moe::launch_gate_logits(xin, weights->gate_w, ws.logits, D.T, D.d, D.E, D.contract, s);
         });
         ctx->launch(D.router == MOE_ROUTER_PHI_QUANT ? "route_phi" : "route_softmax", s, [&] {
             moe::launch_route(ws.logits, weights->expert_bias, D.T, D.E, D.k, D.router, D.quantum,
@@ -776,7 +747,7 @@ int moe_layer_forward(moe_ctx* ctx, const moe_layer_desc* desc,
         });
         const int splits = choose_w2_splits(ctx, D.T * D.k, D.d, D.d_ff, D.E);
         expert_ffn(ctx, xin, ws.perm, ws.offsets, weights->w1, weights->w3, weights->w2, D.act,
-                   D.T, D.k, D.d, D.d_ff, D.E, ws.h, ws.out_rows, s, splits, rnp, D.contract);
+                   D.T, D.k, D.d, D.d_ff, D.E, ws.h, ws.out_rows, s, splits);
         ctx->launch("combine", s, [&] {
             moe::launch_combine(ws.out_rows, idx, w, ws.inv, D.residual ? x : nullptr, y, D.T,
                                 D.k, D.d, D.T * D.k, D.contract, splits, D.T * D.k * D.d, s);

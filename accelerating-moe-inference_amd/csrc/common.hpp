@@ -65,16 +65,6 @@ constexpr int kMaxTopK = 32;
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-// Post-attention layer norm folded into a consumer of x (the gate, the
-// w1/w3 GEMM): per-row statistics from launch_norm_stats and the norm's
-// weight and bias, [d] each.
-struct RowNorm {
-    const float* mean;
-    const float* inv;
-    const float* w;
-    const float* b;
-};
-
 // Kernel launch arguments of the GEMM engine (one struct, passed by value).
 struct GemmArgs {
     const float* A;          // [rows, K] row-major, leading dim lda
@@ -99,8 +89,6 @@ struct GemmArgs {
     int64_t k_split_len;     // K per split (a multiple of 16)
     int64_t c_split_stride;  // elements between the outputs of consecutive splits
     int32_t tile;            // dense: tile shape (kDenseTiles)
-    RowNorm norm;            // grouped w1/w3: A rows normalised as read (norm.mean != nullptr)
-    int32_t norm_contract;   // MOE_CONTRACT_* of the norm's last step
 };
 
 enum Epilogue : int { EPI_STORE = 0, EPI_BIAS = 1, EPI_SILU = 2, EPI_SWIGLU = 3 };
@@ -108,10 +96,9 @@ enum Epilogue : int { EPI_STORE = 0, EPI_BIAS = 1, EPI_SILU = 2, EPI_SWIGLU = 3 
 // Launchers implemented in the .hip files.
 void launch_gemm(const GemmArgs& a, bool nn, bool grouped, int epi, bool vec,
                  hipStream_t s);
-// norm: x rows are normalised as they are read, or nullptr.
 void launch_gate_logits(const float* x, const float* w, float* logits,
                         int64_t T, int64_t d, int64_t E, int contract,
-                        const RowNorm* norm, hipStream_t s);
+                        hipStream_t s);
 void launch_route(const float* logits, const float* bias, int64_t T, int64_t E,
                   int64_t k, int mode, float quantum, float tie_eps,
                   int32_t* idx, float* w, hipStream_t s);
@@ -128,25 +115,12 @@ void launch_mul(const float* a, const float* b, float* c, int64_t n, hipStream_t
 // in order, + bias[cols] (nullable).
 void launch_split_sum(const float* parts, int splits, int64_t part_stride, const float* bias,
                       float* c, int64_t rows, int64_t cols, hipStream_t s);
-// Layer norm: per-row mean and 1/sqrt(var + eps) with the CPU loop's
-// sequential chains; y = normalised rows (the standalone op).
-void launch_norm_stats(const float* x, int64_t rows, int64_t h, float eps, int contract,
-                       float* row_mean, float* row_inv, hipStream_t s);
-void launch_norm_apply(const float* x, const float* w, const float* b, const float* row_mean,
-                       const float* row_inv, int64_t rows, int64_t h, int contract, float* y,
-                       hipStream_t s);
-
-// The last line of tensor_ops::layer_norm (src/tensor.cu:187), shared by every
-// kernel that normalises x as it reads it: (x - mean) * inv * w + b, left to
-// right, the final `* w + b` fused under MOE_CONTRACT_FMA.
-template <int CONTRACT>
-__device__ __forceinline__ float layer_norm_value(float x, float mean, float inv, float w,
-                                                  float b) {
-    const float scaled = (x - mean) * inv;
-    if (CONTRACT == MOE_CONTRACT_FMA) return __builtin_fmaf(scaled, w, b);
-    const float prod = scaled * w;
-    return prod + b;
-}
+// Layer norm over rows of h: per-row mean and 1/sqrt(var + eps) from the CPU
+// loop's sequential chains, and (y != nullptr) the normalised rows.
+// row_mean / row_inv must be valid [rows] buffers; cus sizes the grid.
+void launch_layer_norm(const float* x, const float* w, const float* b, int64_t rows, int64_t h,
+                       float eps, int contract, float* row_mean, float* row_inv, float* y,
+                       int cus, hipStream_t s);
 
 // out_rows holds `parts` partial row buffers of rows_total x d, part_stride
 // elements apart; a row's value is their sum in part order.

@@ -424,12 +424,7 @@ struct NnB {
     }
 };
 
-// ANORM (grouped w1/w3): the A rows are the un-normalised residual stream,
-// normalised after the fragment read with their token's statistics and the
-// norm's weight/bias (the post-attention layer norm folded into the GEMM, as
-// the reference's AGATHER + NORM staging does, src/model.cu:225-246).  The
-// weight/bias values of a K step are fetched with the step's loads.
-template <class C, int SCHED, bool NN, bool GROUPED, int NB, int EPI, bool ANORM = false>
+template <class C, int SCHED, bool NN, bool GROUPED, int NB, int EPI>
 __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmArgs p) {
     constexpr int BM = C::BM, BN = C::BN, BK = C::BK;
     constexpr int FM = C::FM, FN = C::FN;
@@ -559,36 +554,9 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
     const int live_rows = rows - arow0;
     const int live = live_rows <= 0 ? 0 : (live_rows >= FM * 32 ? FM : (live_rows + 31) / 32);
 
-    // ANORM: the statistics of each fragment row's token, and the norm's
-    // weight / bias at this lane's K columns k0 + 8 lh + 4 q + s, fetched
-    // with the stage's loads (a step ahead of their use).
-    float nmean[FM], ninv[FM];
-    f32x4 ngam[2], nbet[2], ngam_next[2], nbet_next[2];
-    if constexpr (ANORM) {
-#pragma unroll
-        for (int bi = 0; bi < FM; ++bi) {
-            int r = arow0 + bi * 32 + lr;
-            r = r < rows ? r : rows - 1;
-            int64_t tok = p.gather != nullptr ? p.gather[row0 + r] : row0 + r;
-            tok = tok < 0 ? 0 : (tok >= p.gather_rows ? p.gather_rows - 1 : tok);
-            nmean[bi] = p.norm.mean[tok];
-            ninv[bi] = p.norm.inv[tok];
-        }
-    }
-    auto norm_fetch = [&](int64_t k0) {
-        if constexpr (ANORM) {
-#pragma unroll
-            for (int q = 0; q < 2; ++q) {
-                ngam_next[q] = *reinterpret_cast<const f32x4*>(p.norm.w + k0 + 8 * lh + 4 * q);
-                nbet_next[q] = *reinterpret_cast<const f32x4*>(p.norm.b + k0 + 8 * lh + 4 * q);
-            }
-        }
-    };
-
     const int64_t nk = (K - kbeg) / BK;
     if (nk > 0) {
         issue(0, kbeg);
-        norm_fetch(kbeg);
         __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0): this wave's loads landed
         __syncthreads();                      // ... and every other wave's
     }
@@ -603,27 +571,6 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
             const float* base = &As[cur][r * BK];
             a[bi][0] = *reinterpret_cast<const f32x4*>(base + 4 * ((2 * lh) ^ swz(r)));
             a[bi][1] = *reinterpret_cast<const f32x4*>(base + 4 * ((2 * lh + 1) ^ swz(r)));
-        }
-        if constexpr (ANORM) {
-#pragma unroll
-            for (int q = 0; q < 2; ++q) {
-                ngam[q] = ngam_next[q];
-                nbet[q] = nbet_next[q];
-            }
-            const bool fma = p.norm_contract == MOE_CONTRACT_FMA;
-#pragma unroll
-            for (int bi = 0; bi < FM; ++bi)
-#pragma unroll
-                for (int q = 0; q < 2; ++q)
-#pragma unroll
-                    for (int s = 0; s < 4; ++s)
-                        a[bi][q][s] =
-                            fma ? layer_norm_value<MOE_CONTRACT_FMA>(a[bi][q][s], nmean[bi],
-                                                                     ninv[bi], ngam[q][s],
-                                                                     nbet[q][s])
-                                : layer_norm_value<MOE_CONTRACT_NONE>(a[bi][q][s], nmean[bi],
-                                                                      ninv[bi], ngam[q][s],
-                                                                      nbet[q][s]);
         }
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
@@ -644,10 +591,7 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
                         *reinterpret_cast<const f32x4*>(base + 4 * ((2 * lh + 1) ^ swz(r)));
                 }
             }
-        if (kt + 1 < nk) {
-            issue(cur ^ 1, kbeg + (kt + 1) * BK);
-            norm_fetch(kbeg + (kt + 1) * BK);
-        }
+        if (kt + 1 < nk) issue(cur ^ 1, kbeg + (kt + 1) * BK);
         if (SCHED & SCHED_PRIO) __builtin_amdgcn_s_setprio(1);
         // the burst over the first NBLK 32-row blocks of this wave
         auto burst = [&](auto nblk) {
@@ -697,28 +641,23 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
             }
 }
 
-template <class C, int SCHED, bool NN, bool GROUPED, int NB, int EPI, bool ANORM = false>
+template <class C, int SCHED, bool NN, bool GROUPED, int NB, int EPI>
 void launch_cfg(const GemmArgs& a, bool vec, hipStream_t s) {
     // direct global->LDS path: 16-byte aligned rows, K a multiple of 16 (NN:
-    // B's rows, of N floats, 16-byte aligned too; ANORM: the norm's weight
-    // and bias 16-byte aligned)
+    // B's rows, of N floats, 16-byte aligned too)
     if constexpr ((SCHED & SCHED_DIRECT) != 0 && C::BK == 16) {
         const bool b_ok = !NN || (a.ldb % 4 == 0 && a.N % 4 == 0 &&
                                   reinterpret_cast<uintptr_t>(a.B0) % 16 == 0);
-        const bool n_ok = !ANORM || (reinterpret_cast<uintptr_t>(a.norm.w) % 16 == 0 &&
-                                     reinterpret_cast<uintptr_t>(a.norm.b) % 16 == 0);
-        if (vec && b_ok && n_ok && a.K % 16 == 0 && a.k_split_len % 16 == 0) {
+        if (vec && b_ok && a.K % 16 == 0 && a.k_split_len % 16 == 0) {
             hipLaunchKernelGGL(
-                (gemm_direct_kernel<C, SCHED, NN, GROUPED, NB, EPI, ANORM>),
+                (gemm_direct_kernel<C, SCHED, NN, GROUPED, NB, EPI>),
                 dim3(static_cast<unsigned>(a.m_tiles) * static_cast<unsigned>(a.n_tiles) *
                      static_cast<unsigned>(a.k_splits)),
                 dim3(C::THREADS), 0, s, a);
             return;
         }
     }
-    if constexpr (ANORM) {
-        throw Unsupported("normalising GEMM needs aligned rows and K % 16 == 0");
-    } else if constexpr (C::STAGED) {
+    if constexpr (C::STAGED) {
         const dim3 grid(static_cast<unsigned>(a.m_tiles) * static_cast<unsigned>(a.n_tiles) *
                         static_cast<unsigned>(a.k_splits));
         if (vec)
@@ -848,18 +787,9 @@ void launch_gemm(const GemmArgs& args, bool nn, bool grouped, int epi, bool vec,
         return;
     }
     if (nn) throw Unsupported("grouped NN GEMM");
-    const bool anorm = a.norm.mean != nullptr;
-    if (anorm && epi != EPI_SWIGLU && epi != EPI_SILU)
-        throw Unsupported("normalised A rows: w1/w3 GEMMs only");
     switch (epi) {
-        case EPI_SWIGLU:
-            if (anorm) launch_cfg<W13Cfg, MOE_W13_SCHED, false, true, 2, EPI_SWIGLU, true>(a, vec, s);
-            else launch_cfg<W13Cfg, MOE_W13_SCHED, false, true, 2, EPI_SWIGLU>(a, vec, s);
-            break;
-        case EPI_SILU:
-            if (anorm) launch_cfg<W13Cfg, MOE_W13_SCHED, false, true, 1, EPI_SILU, true>(a, vec, s);
-            else launch_cfg<W13Cfg, MOE_W13_SCHED, false, true, 1, EPI_SILU>(a, vec, s);
-            break;
+        case EPI_SWIGLU: launch_cfg<W13Cfg, MOE_W13_SCHED, false, true, 2, EPI_SWIGLU>(a, vec, s); break;
+        case EPI_SILU: launch_cfg<W13Cfg, MOE_W13_SCHED, false, true, 1, EPI_SILU>(a, vec, s); break;
         case EPI_STORE: launch_cfg<W2Cfg, MOE_W2_SCHED, false, true, 1, EPI_STORE>(a, vec, s); break;
         default: throw Unsupported("grouped GEMM epilogue");
     }

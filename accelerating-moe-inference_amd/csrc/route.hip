@@ -13,7 +13,6 @@
 
 #include <climits>
 #include <cmath>
-#include <type_traits>
 
 namespace moe {
 namespace {
@@ -37,14 +36,10 @@ __device__ __forceinline__ float mac(float acc, float a, float b) {
     return acc + prod;
 }
 
-// With NORM, x rows are normalised as they are staged (the post-attention
-// layer norm folded into the gate, as the reference's gemm_gate<NORM> does,
-// src/model.cu:505-616): each staged value is bit-identical to what
-// tensor_ops::layer_norm would have stored, so the logits are too.
-template <int CONTRACT, int EB, bool NORM>
+template <int CONTRACT, int EB>
 __global__ __launch_bounds__(256) void gate_logits_kernel(
         const float* __restrict__ x, const float* __restrict__ w,
-        float* __restrict__ logits, int64_t T, int64_t d, int64_t E, const RowNorm norm) {
+        float* __restrict__ logits, int64_t T, int64_t d, int64_t E) {
     constexpr int R = 256 / EB;               // token rows per workgroup
     constexpr int ROWS = R + EB;              // staged rows: x rows, then w rows
     constexpr int PER = ROWS * GATE_KC / 256; // staged floats per thread
@@ -60,21 +55,14 @@ __global__ __launch_bounds__(256) void gate_logits_kernel(
     // wave read 64 consecutive floats of one row (256 contiguous bytes).
     const float* src[PER];
     bool ok[PER];
-    float nmean[PER], ninv[PER];  // NORM: the staged x row's statistics
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
         const int idx = i * 256 + tid;
         const int row = idx / GATE_KC, col = idx % GATE_KC;
-        nmean[i] = 0.0f;
-        ninv[i] = 0.0f;
         if (row < R) {
             const int64_t t = t0 + row;
             ok[i] = t < T;
             src[i] = x + (ok[i] ? t : 0) * d + col;
-            if (NORM && ok[i]) {
-                nmean[i] = norm.mean[t];
-                ninv[i] = norm.inv[t];
-            }
         } else {
             const int64_t e = e0 + (row - R);
             ok[i] = e < E;
@@ -86,12 +74,8 @@ __global__ __launch_bounds__(256) void gate_logits_kernel(
         const int64_t kn = d - k0;
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
-            const int idx = i * 256 + tid;
-            const int col = idx % GATE_KC;
+            const int col = (i * 256 + tid) % GATE_KC;
             stage[i] = (ok[i] && col < kn) ? src[i][k0] : 0.0f;
-            if (NORM && idx / GATE_KC < R && ok[i] && col < kn)
-                stage[i] = layer_norm_value<CONTRACT>(stage[i], nmean[i], ninv[i],
-                                                      norm.w[k0 + col], norm.b[k0 + col]);
         }
     };
     auto lstore = [&](int buf) {
@@ -414,31 +398,25 @@ __global__ __launch_bounds__(256) void combine_kernel(
 
 void launch_gate_logits(const float* x, const float* w, float* logits,
                         int64_t T, int64_t d, int64_t E, int contract,
-                        const RowNorm* norm, hipStream_t s) {
+                        hipStream_t s) {
     if (T == 0 || E == 0) return;
     int eb = 8;
     while (eb < E && eb < 64) eb <<= 1;
     const dim3 grid(static_cast<unsigned>(ceil_div(T, 256 / eb)),
                     static_cast<unsigned>(ceil_div(E, eb)));
-    const RowNorm nrm = norm != nullptr ? *norm : RowNorm{};
-    auto go = [&](auto norm_tag) {
-        constexpr bool NORM = decltype(norm_tag)::value;
-        auto run = [&](auto kernel) {
-            hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, x, w, logits, T, d, E, nrm);
-        };
-        switch (eb * 2 + (contract ? 1 : 0)) {
-            case 16: run(gate_logits_kernel<0, 8, NORM>); break;
-            case 17: run(gate_logits_kernel<1, 8, NORM>); break;
-            case 32: run(gate_logits_kernel<0, 16, NORM>); break;
-            case 33: run(gate_logits_kernel<1, 16, NORM>); break;
-            case 64: run(gate_logits_kernel<0, 32, NORM>); break;
-            case 65: run(gate_logits_kernel<1, 32, NORM>); break;
-            case 128: run(gate_logits_kernel<0, 64, NORM>); break;
-            default: run(gate_logits_kernel<1, 64, NORM>); break;
-        }
+    auto go = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, x, w, logits, T, d, E);
     };
-    if (norm != nullptr) go(std::true_type{});
-    else go(std::false_type{});
+    switch (eb * 2 + (contract ? 1 : 0)) {
+        case 16: go(gate_logits_kernel<0, 8>); break;
+        case 17: go(gate_logits_kernel<1, 8>); break;
+        case 32: go(gate_logits_kernel<0, 16>); break;
+        case 33: go(gate_logits_kernel<1, 16>); break;
+        case 64: go(gate_logits_kernel<0, 32>); break;
+        case 65: go(gate_logits_kernel<1, 32>); break;
+        case 128: go(gate_logits_kernel<0, 64>); break;
+        default: go(gate_logits_kernel<1, 64>); break;
+    }
 }
 
 void launch_route(const float* logits, const float* bias, int64_t T, int64_t E,

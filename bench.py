@@ -28,6 +28,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 METRIC = "MoE layer tokens/sec + expert-GEMM TFLOP/s (% fp32 MFMA peak), 1 MI355X"
 FP32_MFMA_PEAK_TFLOPS = 157.3
 HBM_PEAK_GBS = 8000.0
+NORM_EPS = 1e-5
 
 CONFIGS = {
     # name: T, d, E, k, d_ff, router bias (Zipf s) or None
@@ -110,13 +111,19 @@ def cpu_baseline(x, weights, cfg, pkg_outputs, target_s):
     threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
     oracle.set_threads(threads)
     gw, w1, w3, w2, bias = (weights[n] for n in ("gate_w", "w1", "w3", "w2", "expert_bias"))
+    nw, nb = weights.get("norm_w"), weights.get("norm_b")
     k = cfg["k"]
 
     def run(n):
         t0 = time.perf_counter()
-        y, idx, w = oracle.moe_forward(x[:n], gw, w1, w3, w2, k, act=oracle.ACT_SWIGLU,
+        xin = x[:n]
+        if nw is not None:  # the decoder block: y = x + MoE(layer_norm(x))
+            xin, _, _ = oracle.layer_norm(xin, nw, nb, NORM_EPS, oracle.CONTRACT_FMA)
+        y, idx, w = oracle.moe_forward(xin, gw, w1, w3, w2, k, act=oracle.ACT_SWIGLU,
                                        router_mode=oracle.ROUTER_SOFTMAX_TOPK,
                                        expert_bias=bias)
+        if nw is not None:
+            y = y + x[:n]
         return time.perf_counter() - t0, y, idx
 
     # Grow the prefix until it takes about target_s: small prefixes leave
@@ -156,6 +163,8 @@ def main():
                     help="target CPU time of the cpu_baseline sample (0 = skip)")
     ap.add_argument("--sgemm", action="store_true",
                     help="config-2 SGEMM sweep instead of the layer (one JSON line per shape)")
+    ap.add_argument("--block", action="store_true",
+                    help="the layer as the decoder's MoE block: y = x + MoE(layer_norm(x))")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported "
@@ -184,11 +193,16 @@ def main():
     }
     if cfg["zipf"] is not None:
         weights["expert_bias"] = torch.from_numpy(zipf_bias(E, cfg["zipf"])).to(dev)
+    if args.block:
+        weights["norm_w"] = 1 + 0.1 * torch.randn(d, device=dev, generator=g)
+        weights["norm_b"] = 0.1 * torch.randn(d, device=dev, generator=g)
     y = torch.empty((T, d), device=dev)
     idx = torch.empty((T, k), dtype=torch.int32, device=dev)
     w = torch.empty((T, k), device=dev)
     desc = pkg.make_desc(T, d, E, k, d_ff, act=pkg.ACT_SWIGLU,
-                         router=pkg.ROUTER_SOFTMAX_TOPK, contract=pkg.CONTRACT_FMA)
+                         router=pkg.ROUTER_SOFTMAX_TOPK, contract=pkg.CONTRACT_FMA,
+                         norm=pkg.NORM_LAYER if args.block else pkg.NORM_NONE,
+                         norm_eps=NORM_EPS, residual=args.block)
     ctx = pkg.Context(0)
     ctx.reserve(desc)
 
@@ -247,7 +261,9 @@ def main():
         "config": {"workload": cfg["workload"], "tokens": T, "d_model": d, "experts": E,
                    "top_k": k, "d_ff": d_ff, "router": "softmax over selected top-k",
                    "expert": "SwiGLU", "router_bias": (f"zipf(s={cfg['zipf']})"
-                                                       if cfg["zipf"] else None)},
+                                                       if cfg["zipf"] else None),
+                   "block": ("y = x + MoE(layer_norm(x)), norm folded into gate and w1/w3"
+                             if args.block else None)},
         "expert_gemm_tflops": expert_tflops,
         "expert_gemm_frac_fp32_mfma_peak": expert_tflops / FP32_MFMA_PEAK_TFLOPS,
         "roofline": {

@@ -64,9 +64,9 @@ extern "C" {
 /* Norm in front of the experts (moe_layer_desc.norm).  NONE: gate and
  * experts read x.  LAYER: they read layer_norm(x, norm_w, norm_b, norm_eps),
  * the reference's post-attention norm (src/model.cu:1968-2002), computed
- * bit-identically to tensor_ops::layer_norm under desc.contract; the layer
- * keeps only its per-row statistics and normalises x where the gate and the
- * w1/w3 GEMM read it. */
+ * bit-identically to tensor_ops::layer_norm under desc.contract.  The layer
+ * writes the normalised rows once, into its workspace, and the gate and the
+ * w1/w3 GEMM read them there. */
 #define MOE_NORM_NONE 0
 #define MOE_NORM_LAYER 1
 
@@ -141,7 +141,7 @@ int moe_mul(moe_ctx* ctx, const float* a, const float* b, float* c, int64_t n,
  * tensor_ops::layer_norm under `contract`: row_mean[r] and row_inv[r] =
  * 1 / sqrt(var + eps) from the CPU loop's sequential sums, and
  * y = (x - mean) * inv * weight + bias.  y, row_mean and row_inv may each be
- * NULL (statistics only: y NULL; the statistics are then still computed). */
+ * NULL (y NULL: statistics only); y == x (in place) is allowed. */
 int moe_layer_norm(moe_ctx* ctx, const float* x, const float* weight,
                    const float* bias, float eps, int64_t rows, int64_t h,
                    int contract, float* y, float* row_mean, float* row_inv,
@@ -186,7 +186,7 @@ int moe_combine(moe_ctx* ctx, const float* out_rows, const int32_t* topk_idx,
                 float* y, int64_t T, int64_t k, int64_t d, int contract,
                 void* stream);
 
-/* ---- the whole MoE layer: [norm statistics ->] gate -> route -> permute ->
+/* ---- the whole MoE layer: [layer norm ->] gate -> route -> permute ->
  * expert FFN -> combine [+ x].  topk_idx_out [T,k] / topk_w_out [T,k] may be
  * NULL. */
 int moe_layer_forward(moe_ctx* ctx, const moe_layer_desc* desc,

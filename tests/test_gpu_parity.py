@@ -423,8 +423,11 @@ def test_layer_skewed_config4_full_size(ctx, pkg, torch, orc):
 
 # ------------------------------------------------------------- layer norm
 @pytest.mark.parametrize("contract", [0, 1])
+# rows held in LDS (whole rows per workgroup, 16-byte and scalar paths; h =
+# 20220 is the widest row that fits) and, for h = 30000, the streaming
+# kernels for rows too wide for LDS
 @pytest.mark.parametrize("rows,h", [(1, 1), (3, 5), (64, 64), (65, 4096), (200, 1000),
-                                    (130, 33), (4096, 1024)])
+                                    (130, 33), (4096, 1024), (70, 20220), (3, 30000)])
 def test_layer_norm_bit_exact(ctx, torch, orc, contract, rows, h):
     print(f"layer_norm {rows}x{h} contract={contract}", flush=True)
     rng = np.random.default_rng(rows * 7 + h + contract)
@@ -470,9 +473,8 @@ def _norm_block_oracle(orc, x, gw, w1, w3, w2, nw, nb, k, act, mode, contract, r
     return (y + x if residual else y), idx, w
 
 
-# d = 256: normalised inside the gate and the w1/w3 GEMM; d = 200: the
-# normalised copy path (d % 16 != 0)
-@pytest.mark.parametrize("d", [256, 200])
+# d = 256: 16-byte paths throughout; d = 198: scalar norm and GEMM loads
+@pytest.mark.parametrize("d", [256, 198])
 @pytest.mark.parametrize("mode,contract,act", [(0, 0, 0), (0, 1, 0), (1, 1, 0), (1, 0, 1)])
 def test_layer_norm_block_vs_oracle(ctx, pkg, torch, orc, d, mode, contract, act):
     """The MoE block of the reference's decoder: y = x + MoE(layer_norm(x))
