@@ -88,8 +88,8 @@ int env_int(const char* name, int fallback) {
 
 // Tile shape and K splits of a dense SGEMM, from a cost model fitted to a
 // tile x split sweep of the SGEMM shapes on MI355X (every choice it makes
-// there is within 10 % of the best measured one, about twice the sweep's
-// run-to-run spread).  Per CU, the workgroups
+// there is within 8 % of the best measured one; the sweep's run-to-run
+// spread is about 5 %).  Per CU, the workgroups
 // dealt to it run `occupancy` at a time; each K step of the resident ones
 // costs the larger of their matrix-core time (the rows a wave really
 // computes: 32-row blocks past M are skipped) and the latency of one load
