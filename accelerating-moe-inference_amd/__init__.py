@@ -23,13 +23,13 @@ OK, ERR_INVALID, ERR_RUNTIME, ERR_UNSUPPORTED = 0, 1, 2, 3
 CONTRACT_NONE, CONTRACT_FMA = 0, 1
 ROUTER_PHI_QUANT, ROUTER_SOFTMAX_TOPK = 0, 1
 ACT_SWIGLU, ACT_SILU_MLP = 0, 1
-NORM_NONE, NORM_LAYER = 0, 1
+NORM_NONE, NORM_LAYER, NORM_RMS = 0, 1, 2
 
 EXPORTS = (
     "moe_ctx_create", "moe_ctx_destroy", "moe_ctx_reserve", "moe_ctx_set_timing",
     "moe_ctx_kernel_times", "moe_ctx_reset_timing", "moe_last_error",
     "moe_version", "moe_sgemm_nt", "moe_sgemm_nn", "moe_silu", "moe_mul",
-    "moe_layer_norm", "moe_gate_logits",
+    "moe_layer_norm", "moe_rms_norm", "moe_gate_logits",
     "moe_route", "moe_permute", "moe_expert_ffn_grouped", "moe_combine",
     "moe_layer_forward",
 )
@@ -91,6 +91,7 @@ def load_library(path: str = LIB_PATH):
         "moe_silu": ([P, P, P, I64, P], I),
         "moe_mul": ([P, P, P, P, I64, P], I),
         "moe_layer_norm": ([P, P, P, P, F, I64, I64, I, P, P, P, P], I),
+        "moe_rms_norm": ([P, P, P, F, I64, I64, I, P, P, P], I),
         "moe_gate_logits": ([P, P, P, P, I64, I64, I64, I, P], I),
         "moe_route": ([P, P, P, I64, I64, I64, I, F, F, P, P, P], I),
         "moe_permute": ([P, P, I64, I64, I64, P, P, P, P], I),
@@ -224,6 +225,14 @@ class Context:
                                    _f32(bias, "bias"), eps, rows, h, contract,
                                    _f32(y, "y"), _f32(row_mean, "row_mean"),
                                    _f32(row_inv, "row_inv"), _stream()))
+        return y
+
+    def rms_norm(self, x, weight, y=None, eps=1e-5, contract=CONTRACT_FMA, row_inv=None):
+        """RMS norm over the last axis; y / row_inv may be None."""
+        h = x.shape[-1]
+        rows = x.numel() // h if h else 0
+        _check(_lib.moe_rms_norm(self.handle, _f32(x, "x"), _f32(weight, "weight"), eps, rows,
+                                 h, contract, _f32(y, "y"), _f32(row_inv, "row_inv"), _stream()))
         return y
 
     def gate_logits(self, x, gate_w, logits, contract=CONTRACT_FMA):

@@ -333,7 +333,9 @@ void check_desc(const moe_layer_desc* desc) {
                  "unknown router mode");
     moe::require(desc->contract == MOE_CONTRACT_NONE || desc->contract == MOE_CONTRACT_FMA,
                  "unknown contract mode");
-    moe::require(desc->norm == MOE_NORM_NONE || desc->norm == MOE_NORM_LAYER, "unknown norm");
+    moe::require(desc->norm == MOE_NORM_NONE || desc->norm == MOE_NORM_LAYER ||
+                     desc->norm == MOE_NORM_RMS,
+                 "unknown norm");
     moe::require(desc->residual == 0 || desc->residual == 1, "residual must be 0 or 1");
 }
 
@@ -348,9 +350,9 @@ struct LayerWs {
     int32_t* inv;
     float* h;
     float* out_rows;
-    float* norm_mean;  // MOE_NORM_LAYER: per-token statistics
+    float* norm_mean;  // MOE_NORM_LAYER / RMS: per-token statistics
     float* norm_inv;
-    float* xnorm;      // MOE_NORM_LAYER: the normalised x [T, d] the experts read
+    float* xnorm;      // MOE_NORM_LAYER / RMS: the normalised x [T, d] the experts read
     size_t bytes;
 };
 
@@ -368,7 +370,7 @@ LayerWs carve_layer(void* base, const moe_layer_desc& d) {
     w.inv = c.take<int32_t>(pairs);
     w.h = c.take<float>(pairs * d.d_ff);
     w.out_rows = c.take<float>(pairs * d.d * moe::kMaxW2Splits);
-    if (d.norm == MOE_NORM_LAYER) {
+    if (d.norm != MOE_NORM_NONE) {
         w.norm_mean = c.take<float>(d.T);
         w.norm_inv = c.take<float>(d.T);
         w.xnorm = c.take<float>(d.T * d.d);
@@ -581,8 +583,33 @@ int moe_layer_norm(moe_ctx* ctx, const float* x, const float* weight, const floa
             if (row_inv == nullptr) row_inv = c.take<float>(rows);
         }
         ctx->launch("layer_norm", s, [&] {
-            moe::launch_layer_norm(x, weight, bias, rows, h, eps, contract, row_mean, row_inv, y,
-                                   ctx->cus, s);
+            moe::launch_layer_norm(x, weight, bias, rows, h, eps, contract, false, row_mean,
+                                   row_inv, y, ctx->cus, s);
+        });
+    });
+}
+
+int moe_rms_norm(moe_ctx* ctx, const float* x, const float* weight, float eps, int64_t rows,
+                 int64_t h, int contract, float* y, float* row_inv, void* stream) {
+    return guarded([&] {
+        check_ctx(ctx);
+        check_dims(rows, "rows");
+        check_dims(h, "h");
+        moe::require(contract == MOE_CONTRACT_NONE || contract == MOE_CONTRACT_FMA,
+                     "unknown contract mode");
+        if (rows == 0) return;
+        moe::require(h > 0, "rms norm: h must be > 0");
+        check_ptr(x, "x");
+        if (y != nullptr) check_ptr(weight, "weight");
+        DeviceScope dev(ctx->device);
+        hipStream_t s = as_stream(stream);
+        if (row_inv == nullptr) {
+            Carve c(ctx->workspace(size_t(rows) * sizeof(float) + 256));
+            row_inv = c.take<float>(rows);
+        }
+        ctx->launch("rms_norm", s, [&] {
+            moe::launch_layer_norm(x, weight, nullptr, rows, h, eps, contract, true, nullptr,
+                                   row_inv, y, ctx->cus, s);
         });
     });
 }
@@ -706,11 +733,11 @@ int moe_layer_forward(moe_ctx* ctx, const moe_layer_desc* desc,
         }
         moe::require(D.d % 4 != 0 || (aligned16(x) && aligned16(y)),
                      "layer: x and y must be 16-byte aligned");
-        const bool norm = D.norm == MOE_NORM_LAYER;
+        const bool norm = D.norm != MOE_NORM_NONE, rms = D.norm == MOE_NORM_RMS;
         if (norm) {
-            moe::require(D.d > 0, "layer norm: d must be > 0");
+            moe::require(D.d > 0, "norm: d must be > 0");
             check_ptr(weights->norm_w, "norm_w");
-            check_ptr(weights->norm_b, "norm_b");
+            if (!rms) check_ptr(weights->norm_b, "norm_b");
         }
         DeviceScope dev(ctx->device);
         hipStream_t s = as_stream(stream);
@@ -723,10 +750,10 @@ int moe_layer_forward(moe_ctx* ctx, const moe_layer_desc* desc,
         // by the gate and the w1/w3 GEMM; the residual stays x).
         const float* xin = x;
         if (norm) {
-            ctx->launch("layer_norm", s, [&] {
-                moe::launch_layer_norm(x, weights->norm_w, weights->norm_b, D.T, D.d, D.norm_eps,
-                                       D.contract, ws.norm_mean, ws.norm_inv, ws.xnorm, ctx->cus,
-                                       s);
+            ctx->launch(rms ? "rms_norm" : "layer_norm", s, [&] {
+                moe::launch_layer_norm(x, weights->norm_w, rms ? nullptr : weights->norm_b, D.T,
+                                       D.d, D.norm_eps, D.contract, rms, ws.norm_mean,
+                                       ws.norm_inv, ws.xnorm, ctx->cus, s);
             });
             xin = ws.xnorm;
         }

@@ -115,12 +115,13 @@ void launch_mul(const float* a, const float* b, float* c, int64_t n, hipStream_t
 // in order, + bias[cols] (nullable).
 void launch_split_sum(const float* parts, int splits, int64_t part_stride, const float* bias,
                       float* c, int64_t rows, int64_t cols, hipStream_t s);
-// Layer norm over rows of h: per-row mean and 1/sqrt(var + eps) from the CPU
-// loop's sequential chains, and (y != nullptr) the normalised rows.
-// row_mean / row_inv must be valid [rows] buffers; cus sizes the grid.
+// Layer norm (rms: RMS norm, no mean, no bias) over rows of h: per-row mean
+// and 1/sqrt(var + eps) from the CPU loop's sequential chains, and
+// (y != nullptr) the normalised rows.  row_inv (and row_mean for the layer
+// norm) must be valid [rows] buffers; cus sizes the grid.
 void launch_layer_norm(const float* x, const float* w, const float* b, int64_t rows, int64_t h,
-                       float eps, int contract, float* row_mean, float* row_inv, float* y,
-                       int cus, hipStream_t s);
+                       float eps, int contract, bool rms, float* row_mean, float* row_inv,
+                       float* y, int cus, hipStream_t s);
 
 // out_rows holds `parts` partial row buffers of rows_total x d, part_stride
 // elements apart; a row's value is their sum in part order.

@@ -7,6 +7,9 @@
 //   inv  = 1 / sqrt(var + eps)
 //   y    = (x - mean) * inv * w + b
 //
+// and the RMS norm config 5's decoder names (no reference code; defined in
+// the same style): inv = 1 / sqrt(sum of x*x / h + eps), y = x * inv * w.
+//
 // The two sums are sequential chains, so one lane owns one row's chain; the
 // work is feeding those chains.  Main kernel: a workgroup stages R whole
 // rows in LDS with every thread loading (all of the rows' bytes in flight at
@@ -42,9 +45,10 @@ __device__ __forceinline__ float mac(float acc, float a, float b) {
 }
 
 // The last line of the CPU loop: (x - mean) * inv * w + b, left to right,
-// the final `* w + b` fused under MOE_CONTRACT_FMA.
-template <int CONTRACT>
+// the final `* w + b` fused under MOE_CONTRACT_FMA.  RMS: x * inv * w.
+template <int CONTRACT, bool RMS>
 __device__ __forceinline__ float normalise(float x, float mean, float inv, float w, float b) {
+    if (RMS) return (x * inv) * w;
     const float scaled = (x - mean) * inv;
     if (CONTRACT == MOE_CONTRACT_FMA) return __builtin_fmaf(scaled, w, b);
     const float prod = scaled * w;
@@ -52,7 +56,8 @@ __device__ __forceinline__ float normalise(float x, float mean, float inv, float
 }
 
 // VEC4: h % 4 == 0 and 16-byte aligned x / y / w / b (16-byte accesses).
-template <int CONTRACT, bool VEC4>
+// RMS: no mean (the second chain sums x*x itself), no bias; row_mean unused.
+template <int CONTRACT, bool VEC4, bool RMS>
 __global__ __launch_bounds__(256) void norm_rows_kernel(
         const float* __restrict__ x, const float* __restrict__ w, const float* __restrict__ b,
         int64_t rows, int64_t h, int R, float eps, float* __restrict__ row_mean,
@@ -85,7 +90,7 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(
         constexpr int kAhead = 32;
         const float* row = &buf[tid * hs];
         float sum = 0.0f;
-        int64_t j = 0;
+        int64_t j = RMS ? h : 0;  // RMS: no mean chain
         if (VEC4)
             for (; j + kAhead <= h; j += kAhead) {
                 f32x4 v[kAhead / 4];
@@ -99,7 +104,7 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(
             }
 #pragma unroll 16
         for (; j < h; ++j) sum = sum + row[j];
-        const float mean = sum / static_cast<float>(h);
+        const float mean = RMS ? 0.0f : sum / static_cast<float>(h);
         float var = 0.0f;
         j = 0;
         if (VEC4)
@@ -112,19 +117,19 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(
                 for (int u = 0; u < kAhead / 4; ++u)
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
-                        const float dv = v[u][q] - mean;
+                        const float dv = RMS ? v[u][q] : v[u][q] - mean;
                         var = mac<CONTRACT>(var, dv, dv);
                     }
             }
 #pragma unroll 16
         for (; j < h; ++j) {
-            const float dv = row[j] - mean;
+            const float dv = RMS ? row[j] : row[j] - mean;
             var = mac<CONTRACT>(var, dv, dv);
         }
         const float inv = 1.0f / sqrtf(var / static_cast<float>(h) + eps);
         smean[tid] = mean;
         sinv[tid] = inv;
-        row_mean[r0 + tid] = mean;
+        if (!RMS) row_mean[r0 + tid] = mean;
         row_inv[r0 + tid] = inv;
     }
     __syncthreads();
@@ -136,16 +141,18 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(
             const int64_t r = i / h, j = i - r * h;
             const f32x4 v = *reinterpret_cast<const f32x4*>(&buf[r * hs + j]);
             const f32x4 wv = *reinterpret_cast<const f32x4*>(w + j);
-            const f32x4 bv = *reinterpret_cast<const f32x4*>(b + j);
+            const f32x4 bv = RMS ? wv : *reinterpret_cast<const f32x4*>(b + j);
             f32x4 o;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) o[q] = normalise<CONTRACT>(v[q], smean[r], sinv[r], wv[q], bv[q]);
+            for (int q = 0; q < 4; ++q)
+                o[q] = normalise<CONTRACT, RMS>(v[q], smean[r], sinv[r], wv[q], bv[q]);
             *reinterpret_cast<f32x4*>(dst + i) = o;
         }
     } else {
         for (int64_t i = tid; i < n; i += 256) {
             const int64_t r = i / h, j = i - r * h;
-            dst[i] = normalise<CONTRACT>(buf[r * hs + j], smean[r], sinv[r], w[j], b[j]);
+            dst[i] = normalise<CONTRACT, RMS>(buf[r * hs + j], smean[r], sinv[r], w[j],
+                                              RMS ? 0.0f : b[j]);
         }
     }
 }
@@ -159,7 +166,7 @@ constexpr int kStreamChunk = 32;
 constexpr int kStreamWaves = 4;
 constexpr int kStreamStride = kStreamRows + 1;
 
-template <int CONTRACT>
+template <int CONTRACT, bool RMS>
 __global__ __launch_bounds__(64 * kStreamWaves) void norm_stats_stream_kernel(
         const float* __restrict__ x, int64_t rows, int64_t h, float eps,
         float* __restrict__ row_mean, float* __restrict__ row_inv) {
@@ -194,28 +201,29 @@ __global__ __launch_bounds__(64 * kStreamWaves) void norm_stats_stream_kernel(
     };
 
     float sum = 0.0f;
-    for (int64_t j0 = 0; j0 < h; j0 += kStreamChunk) {
+    for (int64_t j0 = 0; !RMS && j0 < h; j0 += kStreamChunk) {
         const int64_t cols = stage(j0);
         for (int c = 0; c < cols; ++c) sum = sum + s[c * kStreamStride + lane];
         __builtin_amdgcn_wave_barrier();
     }
-    const float mean = sum / static_cast<float>(h);
+    const float mean = RMS ? 0.0f : sum / static_cast<float>(h);
     float var = 0.0f;
     for (int64_t j0 = 0; j0 < h; j0 += kStreamChunk) {
         const int64_t cols = stage(j0);
         for (int c = 0; c < cols; ++c) {
-            const float dv = s[c * kStreamStride + lane] - mean;
+            const float v = s[c * kStreamStride + lane];
+            const float dv = RMS ? v : v - mean;
             var = mac<CONTRACT>(var, dv, dv);
         }
         __builtin_amdgcn_wave_barrier();
     }
     if (lane < here) {
-        row_mean[row0 + lane] = mean;
+        if (!RMS) row_mean[row0 + lane] = mean;
         row_inv[row0 + lane] = 1.0f / sqrtf(var / static_cast<float>(h) + eps);
     }
 }
 
-template <int CONTRACT>
+template <int CONTRACT, bool RMS>
 __global__ __launch_bounds__(256) void norm_apply_kernel(
         const float* __restrict__ x, const float* __restrict__ w, const float* __restrict__ b,
         const float* __restrict__ row_mean, const float* __restrict__ row_inv, int64_t rows,
@@ -225,13 +233,14 @@ __global__ __launch_bounds__(256) void norm_apply_kernel(
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
          i += stride) {
         const int64_t r = i / h, j = i - r * h;
-        y[i] = normalise<CONTRACT>(x[i], row_mean[r], row_inv[r], w[j], b[j]);
+        y[i] = RMS ? normalise<CONTRACT, true>(x[i], 0.0f, row_inv[r], w[j], 0.0f)
+                   : normalise<CONTRACT, false>(x[i], row_mean[r], row_inv[r], w[j], b[j]);
     }
 }
 
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
-template <int CONTRACT>
+template <int CONTRACT, bool RMS>
 void launch(const float* x, const float* w, const float* b, int64_t rows, int64_t h, float eps,
             float* row_mean, float* row_inv, float* y, int cus, hipStream_t s) {
     const int64_t hs = h + kRowPad;
@@ -245,22 +254,22 @@ void launch(const float* x, const float* w, const float* b, int64_t rows, int64_
         R = R < kMaxResidentRows ? R : kMaxResidentRows;
         const dim3 grid(static_cast<unsigned>(ceil_div(rows, R)));
         const bool vec4 = h % 4 == 0 && aligned16(x) && (y == nullptr || aligned16(y)) &&
-                          (y == nullptr || (aligned16(w) && aligned16(b)));
+                          (y == nullptr || (aligned16(w) && (RMS || aligned16(b))));
         if (vec4)
-            hipLaunchKernelGGL((norm_rows_kernel<CONTRACT, true>), grid, dim3(256), 0, s, x, w, b,
-                               rows, h, static_cast<int>(R), eps, row_mean, row_inv, y);
+            hipLaunchKernelGGL((norm_rows_kernel<CONTRACT, true, RMS>), grid, dim3(256), 0, s, x,
+                               w, b, rows, h, static_cast<int>(R), eps, row_mean, row_inv, y);
         else
-            hipLaunchKernelGGL((norm_rows_kernel<CONTRACT, false>), grid, dim3(256), 0, s, x, w,
-                               b, rows, h, static_cast<int>(R), eps, row_mean, row_inv, y);
+            hipLaunchKernelGGL((norm_rows_kernel<CONTRACT, false, RMS>), grid, dim3(256), 0, s,
+                               x, w, b, rows, h, static_cast<int>(R), eps, row_mean, row_inv, y);
         return;
     }
     const unsigned blocks =
         static_cast<unsigned>(ceil_div(ceil_div(rows, kStreamRows), kStreamWaves));
-    hipLaunchKernelGGL(norm_stats_stream_kernel<CONTRACT>, dim3(blocks), dim3(64 * kStreamWaves),
-                       0, s, x, rows, h, eps, row_mean, row_inv);
+    hipLaunchKernelGGL((norm_stats_stream_kernel<CONTRACT, RMS>), dim3(blocks),
+                       dim3(64 * kStreamWaves), 0, s, x, rows, h, eps, row_mean, row_inv);
     if (y == nullptr) return;
     const int64_t nblk = ceil_div(rows * h, 256);
-    hipLaunchKernelGGL(norm_apply_kernel<CONTRACT>,
+    hipLaunchKernelGGL((norm_apply_kernel<CONTRACT, RMS>),
                        dim3(static_cast<unsigned>(nblk < 65536 ? nblk : 65536)), dim3(256), 0, s,
                        x, w, b, row_mean, row_inv, rows, h, y);
 }
@@ -268,13 +277,16 @@ void launch(const float* x, const float* w, const float* b, int64_t rows, int64_
 }  // namespace
 
 void launch_layer_norm(const float* x, const float* w, const float* b, int64_t rows, int64_t h,
-                       float eps, int contract, float* row_mean, float* row_inv, float* y,
-                       int cus, hipStream_t s) {
+                       float eps, int contract, bool rms, float* row_mean, float* row_inv,
+                       float* y, int cus, hipStream_t s) {
     if (rows <= 0 || h <= 0) return;
-    if (contract == MOE_CONTRACT_FMA)
-        launch<MOE_CONTRACT_FMA>(x, w, b, rows, h, eps, row_mean, row_inv, y, cus, s);
-    else
-        launch<MOE_CONTRACT_NONE>(x, w, b, rows, h, eps, row_mean, row_inv, y, cus, s);
+    if (contract == MOE_CONTRACT_FMA) {
+        if (rms) launch<MOE_CONTRACT_FMA, true>(x, w, b, rows, h, eps, row_mean, row_inv, y, cus, s);
+        else launch<MOE_CONTRACT_FMA, false>(x, w, b, rows, h, eps, row_mean, row_inv, y, cus, s);
+    } else {
+        if (rms) launch<MOE_CONTRACT_NONE, true>(x, w, b, rows, h, eps, row_mean, row_inv, y, cus, s);
+        else launch<MOE_CONTRACT_NONE, false>(x, w, b, rows, h, eps, row_mean, row_inv, y, cus, s);
+    }
 }
 
 }  // namespace moe

@@ -32,12 +32,12 @@ NORM_EPS = 1e-5
 
 CONFIGS = {
     # name: T, d, E, k, d_ff, router bias (Zipf s) or None
-    "c3": dict(T=4096, d=4096, E=8, k=2, d_ff=14336, zipf=None,
+    "c3": dict(T=4096, d=4096, E=8, k=2, d_ff=14336, zipf=None, norm="layer",
                workload="mixtral_moe_layer_fp32"),
-    "c4": dict(T=16384, d=2048, E=64, k=8, d_ff=1408, zipf=1.2,
+    "c4": dict(T=16384, d=2048, E=64, k=8, d_ff=1408, zipf=1.2, norm="layer",
                workload="fine_grained_zipf_moe_layer_fp32"),
     # the MoE FFN of config 5's decoder (batch 8 x seq 512 tokens, d 1024)
-    "c5": dict(T=4096, d=1024, E=8, k=2, d_ff=2816, zipf=None,
+    "c5": dict(T=4096, d=1024, E=8, k=2, d_ff=2816, zipf=None, norm="rms",
                workload="decoder_prefill_moe_ffn_fp32"),
 }
 
@@ -117,8 +117,11 @@ def cpu_baseline(x, weights, cfg, pkg_outputs, target_s):
     def run(n):
         t0 = time.perf_counter()
         xin = x[:n]
-        if nw is not None:  # the decoder block: y = x + MoE(layer_norm(x))
-            xin, _, _ = oracle.layer_norm(xin, nw, nb, NORM_EPS, oracle.CONTRACT_FMA)
+        if nw is not None:  # the decoder block: y = x + MoE(norm(x))
+            if nb is None:
+                xin, _ = oracle.rms_norm(xin, nw, NORM_EPS, oracle.CONTRACT_FMA)
+            else:
+                xin, _, _ = oracle.layer_norm(xin, nw, nb, NORM_EPS, oracle.CONTRACT_FMA)
         y, idx, w = oracle.moe_forward(xin, gw, w1, w3, w2, k, act=oracle.ACT_SWIGLU,
                                        router_mode=oracle.ROUTER_SOFTMAX_TOPK,
                                        expert_bias=bias)
@@ -193,15 +196,17 @@ def main():
     }
     if cfg["zipf"] is not None:
         weights["expert_bias"] = torch.from_numpy(zipf_bias(E, cfg["zipf"])).to(dev)
+    rms = cfg["norm"] == "rms"
     if args.block:
         weights["norm_w"] = 1 + 0.1 * torch.randn(d, device=dev, generator=g)
-        weights["norm_b"] = 0.1 * torch.randn(d, device=dev, generator=g)
+        weights["norm_b"] = None if rms else 0.1 * torch.randn(d, device=dev, generator=g)
     y = torch.empty((T, d), device=dev)
     idx = torch.empty((T, k), dtype=torch.int32, device=dev)
     w = torch.empty((T, k), device=dev)
     desc = pkg.make_desc(T, d, E, k, d_ff, act=pkg.ACT_SWIGLU,
                          router=pkg.ROUTER_SOFTMAX_TOPK, contract=pkg.CONTRACT_FMA,
-                         norm=pkg.NORM_LAYER if args.block else pkg.NORM_NONE,
+                         norm=(pkg.NORM_RMS if rms else pkg.NORM_LAYER) if args.block
+                         else pkg.NORM_NONE,
                          norm_eps=NORM_EPS, residual=args.block)
     ctx = pkg.Context(0)
     ctx.reserve(desc)
@@ -262,7 +267,7 @@ def main():
                    "top_k": k, "d_ff": d_ff, "router": "softmax over selected top-k",
                    "expert": "SwiGLU", "router_bias": (f"zipf(s={cfg['zipf']})"
                                                        if cfg["zipf"] else None),
-                   "block": ("y = x + MoE(layer_norm(x)), norm folded into gate and w1/w3"
+                   "block": (f"y = x + MoE({'rms_norm' if rms else 'layer_norm'}(x))"
                              if args.block else None)},
         "expert_gemm_tflops": expert_tflops,
         "expert_gemm_frac_fp32_mfma_peak": expert_tflops / FP32_MFMA_PEAK_TFLOPS,

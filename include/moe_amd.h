@@ -25,6 +25,7 @@
  *                       gemm_grouped_combine epilogue      src/model.cu:436-447
  *   moe_layer_norm      tensor_ops::layer_norm             src/tensor.cu:175-189,
  *                       layer_norm_rows / forward_stats    src/model.cu:720-846,1440-1480
+ *   moe_rms_norm        (no counterpart: the RMSNorm config 5's decoder names)
  *   moe_layer_forward   PhiMoE::forward                    src/layer.cu:80-103,
  *                       the MoE block of generate()        src/model.cu:1968-2021
  *   moe_ctx_*           DeviceBuffer / Scratch workspace   src/model.cu:45-68,1294-1324
@@ -69,6 +70,10 @@ extern "C" {
  * w1/w3 GEMM read them there. */
 #define MOE_NORM_NONE 0
 #define MOE_NORM_LAYER 1
+/* RMS: the RMSNorm config 5's decoder names, which the reference does not
+ * have; defined like tensor_ops::layer_norm without the mean and the bias
+ * (see moe_rms_norm).  weights.norm_b is ignored. */
+#define MOE_NORM_RMS 2
 
 typedef struct moe_ctx moe_ctx;
 
@@ -84,7 +89,7 @@ typedef struct moe_layer_desc {
     float tie_eps;    /* PHI_QUANT tie margin (2e-2 in the reference)      */
     int32_t contract; /* MOE_CONTRACT_* for the norm, gate logits, combine   */
     int32_t norm;     /* MOE_NORM_*                                         */
-    float norm_eps;   /* layer norm epsilon (MOE_NORM_LAYER)                */
+    float norm_eps;   /* norm epsilon (MOE_NORM_LAYER, MOE_NORM_RMS)        */
     int32_t residual; /* 1: y = x + MoE(...), x un-normalised (the block's
                          residual, src/model.cu:2009-2012); 0: y = MoE(...) */
 } moe_layer_desc;
@@ -95,8 +100,8 @@ typedef struct moe_layer_weights {
     const float* w1;          /* [E, d_ff, d]                   */
     const float* w3;          /* [E, d_ff, d]; NULL for SILU_MLP */
     const float* w2;          /* [E, d, d_ff]                   */
-    const float* norm_w;      /* [d] layer norm weight (MOE_NORM_LAYER) */
-    const float* norm_b;      /* [d] layer norm bias   (MOE_NORM_LAYER) */
+    const float* norm_w;      /* [d] norm weight (MOE_NORM_LAYER / RMS) */
+    const float* norm_b;      /* [d] layer norm bias (MOE_NORM_LAYER)  */
 } moe_layer_weights;
 
 /* ---- context: device binding, grow-only workspace, optional kernel timing.
@@ -146,6 +151,16 @@ int moe_layer_norm(moe_ctx* ctx, const float* x, const float* weight,
                    const float* bias, float eps, int64_t rows, int64_t h,
                    int contract, float* y, float* row_mean, float* row_inv,
                    void* stream);
+
+/* ---- RMS norm over the last axis of x[rows, h]: row_inv[r] =
+ * 1 / sqrt(ss / h + eps), ss = one float accumulator of x*x over the row in
+ * order (fused multiply-add under MOE_CONTRACT_FMA), and
+ * y = x * inv * weight.  y and row_inv may each be NULL; y == x is allowed.
+ * No reference counterpart (config 5 names RMSNorm; the reference's norm is
+ * tensor_ops::layer_norm). */
+int moe_rms_norm(moe_ctx* ctx, const float* x, const float* weight, float eps,
+                 int64_t rows, int64_t h, int contract, float* y,
+                 float* row_inv, void* stream);
 
 /* ---- router gate logits[T,E] = x[T,d] Wg[E,d]^T with one k-ascending fp32
  * accumulator per output: bit-identical to the CPU path under `contract`. */

@@ -56,6 +56,8 @@ def lib():
         L.orc_mul.restype = None
         L.orc_layer_norm.argtypes = [P, P, P, F, S, S, I, P, P, P]
         L.orc_layer_norm.restype = I
+        L.orc_rms_norm.argtypes = [P, P, F, S, S, I, P, P]
+        L.orc_rms_norm.restype = I
         L.orc_route.argtypes = [P, P, S, S, S, I, F, F, P, P]
         L.orc_route.restype = I
         L.orc_permute.argtypes = [P, S, S, S, P, P, P]
@@ -152,6 +154,19 @@ def layer_norm(x, weight, bias, eps=1e-5, contract=CONTRACT_FMA):
     _check(lib().orc_layer_norm(_p(x), _p(weight), _p(bias), float(eps), rows, h,
                                 int(contract), _p(y), _p(mean), _p(inv)), "layer_norm")
     return y, mean, inv
+
+
+def rms_norm(x, weight, eps=1e-5, contract=CONTRACT_FMA):
+    """RMS norm over the last axis; returns (y, row_inv)."""
+    x, weight = _f32(x), _f32(weight)
+    h = x.shape[-1]
+    rows = x.size // h if h else 0
+    assert weight.size == h
+    y = np.empty_like(x)
+    inv = np.empty(rows, np.float32)
+    _check(lib().orc_rms_norm(_p(x), _p(weight), float(eps), rows, h, int(contract), _p(y),
+                              _p(inv)), "rms_norm")
+    return y, inv
 
 
 def route(logits, k, mode=ROUTER_PHI_QUANT, quantum=1e-3, tie_eps=2e-2,

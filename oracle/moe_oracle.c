@@ -175,6 +175,35 @@ int orc_layer_norm(const float* x, const float* weight, const float* bias,
     return 0;
 }
 
+/* RMS norm (config 5's decoder names RMSNorm; the reference has none -- its
+ * norm is layer_norm above).  Defined in the same style as tensor_ops::
+ * layer_norm: ss = one float accumulator of x*x over j ascending (fused under
+ * `contract`), inv = 1 / sqrt(ss / h + eps), y = x * inv * weight, left to
+ * right.  y and row_inv may be NULL.
+ * Pinned by: closed forms (a constant row c gives inv = 1/sqrt(c*c + eps);
+ * 3, 4 gives ss = 25 exactly), float64 within rounding, and a row whose
+ * single-float sum of squares differs from a double one (tests/test_oracle.py). */
+int orc_rms_norm(const float* x, const float* weight, float eps, size_t rows,
+                 size_t h, int contract, float* y, float* row_inv) {
+    if (rows && (!x || h == 0 || !weight)) return 1;
+#pragma omp parallel for schedule(static)
+    for (long long r = 0; r < (long long)rows; ++r) {
+        float ss = 0.0f;
+        for (size_t j = 0; j < h; ++j) {
+            const float v = x[orc_at(rows, h, (size_t)r, j)];
+            ss = orc_mac(ss, v, v, contract);
+        }
+        const float inv = 1.0f / sqrtf(ss / (float)h + eps);
+        if (row_inv) row_inv[r] = inv;
+        if (!y) continue;
+        for (size_t j = 0; j < h; ++j) {
+            const size_t o = orc_at(rows, h, (size_t)r, j);
+            y[o] = (x[o] * inv) * weight[j];
+        }
+    }
+    return 0;
+}
+
 /* c = a * b elementwise (src/tensor.cu:163-167). Pinned by direct products. */
 void orc_mul(const float* a, const float* b, float* c, size_t n) {
 #pragma omp parallel for schedule(static)

@@ -52,6 +52,8 @@ void orc_mul(const float* a, const float* b, float* c, size_t n);
 int orc_layer_norm(const float* x, const float* weight, const float* bias,
                    float eps, size_t rows, size_t h, int contract, float* y,
                    float* row_mean, float* row_inv);
+int orc_rms_norm(const float* x, const float* weight, float eps, size_t rows,
+                 size_t h, int contract, float* y, float* row_inv);
 
 int orc_route(const float* logits, const float* expert_bias,
               size_t T, size_t E, size_t k, int mode,

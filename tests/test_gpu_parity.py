@@ -450,12 +450,31 @@ def test_layer_norm_bit_exact(ctx, torch, orc, contract, rows, h):
     assert np.array_equal(host(xd), ry)
 
 
+@pytest.mark.parametrize("contract", [0, 1])
+@pytest.mark.parametrize("rows,h", [(1, 1), (3, 5), (65, 4096), (130, 33), (4096, 1024),
+                                    (3, 30000)])
+def test_rms_norm_bit_exact(ctx, torch, orc, contract, rows, h):
+    print(f"rms_norm {rows}x{h} contract={contract}", flush=True)
+    rng = np.random.default_rng(rows * 3 + h + contract)
+    x = (1 + 3 * rng.normal(size=(rows, h))).astype(np.float32)
+    w = rng.normal(size=h).astype(np.float32)
+    ry, ri = orc.rms_norm(x, w, 1e-5, contract)
+    y = torch.empty((rows, h), device="cuda")
+    inv = torch.empty(rows, device="cuda")
+    ctx.rms_norm(dev(torch, x), dev(torch, w), y, 1e-5, contract, inv)
+    assert np.array_equal(host(inv), ri) and np.array_equal(host(y), ry)
+    xd = dev(torch, x)
+    ctx.rms_norm(xd, dev(torch, w), xd, 1e-5, contract)  # in place, statistics in the workspace
+    assert np.array_equal(host(xd), ry)
+
+
 def _norm_block(ctx, pkg, torch, x, gw, w1, w3, w2, nw, nb, k, act, mode, contract,
-                residual=True, bias=None):
+                residual=True, bias=None, norm=None):
     T, d = x.shape
     E, d_ff, _ = w1.shape
     desc = pkg.make_desc(T, d, E, k, d_ff, act=act, router=mode, contract=contract,
-                         norm=pkg.NORM_LAYER, norm_eps=1e-5, residual=residual)
+                         norm=pkg.NORM_LAYER if norm is None else norm, norm_eps=1e-5,
+                         residual=residual)
     y = torch.empty((T, d), device="cuda")
     idx = torch.empty((T, k), dtype=torch.int32, device="cuda")
     w = torch.empty((T, k), device="cuda")
@@ -466,8 +485,11 @@ def _norm_block(ctx, pkg, torch, x, gw, w1, w3, w2, nw, nb, k, act, mode, contra
 
 
 def _norm_block_oracle(orc, x, gw, w1, w3, w2, nw, nb, k, act, mode, contract, residual,
-                       bias=None):
-    xn, _, _ = orc.layer_norm(x, nw, nb, 1e-5, contract)
+                       bias=None, rms=False):
+    if rms:
+        xn, _ = orc.rms_norm(x, nw, 1e-5, contract)
+    else:
+        xn, _, _ = orc.layer_norm(x, nw, nb, 1e-5, contract)
     y, idx, w = orc.moe_forward(xn, gw, w1, w3, w2, k, act=act, router_mode=mode,
                                 contract=contract, expert_bias=bias)
     return (y + x if residual else y), idx, w
@@ -475,11 +497,13 @@ def _norm_block_oracle(orc, x, gw, w1, w3, w2, nw, nb, k, act, mode, contract, r
 
 # d = 256: 16-byte paths throughout; d = 198: scalar norm and GEMM loads
 @pytest.mark.parametrize("d", [256, 198])
-@pytest.mark.parametrize("mode,contract,act", [(0, 0, 0), (0, 1, 0), (1, 1, 0), (1, 0, 1)])
-def test_layer_norm_block_vs_oracle(ctx, pkg, torch, orc, d, mode, contract, act):
+@pytest.mark.parametrize("mode,contract,act,rms", [(0, 0, 0, False), (0, 1, 0, False),
+                                                   (1, 1, 0, False), (1, 0, 1, False),
+                                                   (1, 1, 0, True), (0, 0, 1, True)])
+def test_layer_norm_block_vs_oracle(ctx, pkg, torch, orc, d, mode, contract, act, rms):
     """The MoE block of the reference's decoder: y = x + MoE(layer_norm(x))
     (src/model.cu:1968-2021); routing bit-exact, y within the 1e-4 rule."""
-    print(f"norm block d={d} mode={mode} contract={contract} act={act}", flush=True)
+    print(f"norm block d={d} mode={mode} contract={contract} act={act} rms={rms}", flush=True)
     rng = np.random.default_rng(d + 10 * mode + 100 * contract + act)
     T, E, k, d_ff = 300, 8, 2, 192
     x = (0.5 + 2 * rng.normal(size=(T, d))).astype(np.float32)
@@ -491,9 +515,10 @@ def test_layer_norm_block_vs_oracle(ctx, pkg, torch, orc, d, mode, contract, act
     nb = (0.1 * rng.normal(size=d)).astype(np.float32)
     y, idx, w = _norm_block(ctx, pkg, torch, dev(torch, x), dev(torch, gw), dev(torch, w1),
                             None if w3 is None else dev(torch, w3), dev(torch, w2),
-                            dev(torch, nw), dev(torch, nb), k, act, mode, contract)
+                            dev(torch, nw), None if rms else dev(torch, nb), k, act, mode,
+                            contract, norm=pkg.NORM_RMS if rms else pkg.NORM_LAYER)
     ry, ridx, rw = _norm_block_oracle(orc, x, gw, w1, w3, w2, nw, nb, k, act, mode, contract,
-                                      residual=True)
+                                      residual=True, rms=rms)
     assert np.array_equal(host(idx), ridx)
     assert np.max(np.abs(host(w).view(np.int32).astype(np.int64) - rw.view(np.int32))) <= 1
     assert_close(host(y), ry, what="norm block y")
@@ -513,10 +538,14 @@ def test_layer_norm_block_without_residual(ctx, pkg, torch, orc):
     assert_close(host(y), ry, what="norm block, no residual")
 
 
-def test_layer_norm_block_config5_moe_ffn(ctx, pkg, torch, orc):
+@pytest.mark.parametrize("norm", ["layer", "rms"])
+def test_layer_norm_block_config5_moe_ffn(ctx, pkg, torch, orc, norm):
     """Config 5's MoE block at full size (8 x 512 tokens, d 1024, E=8, top-2,
-    SwiGLU 2816) behind its post-attention norm, with the residual; the oracle
-    recomputes 32 tokens (every step is per token)."""
+    SwiGLU 2816) behind its norm (the RMSNorm config 5 names, and the
+    reference's layer norm), with the residual; the oracle recomputes 32
+    tokens (every step is per token)."""
+    print(f"config5 block norm={norm}", flush=True)
+    rms = norm == "rms"
     T, d, E, k, d_ff = 4096, 1024, 8, 2, 2816
     g = torch.Generator(device="cuda").manual_seed(5)
     x = torch.randn((T, d), device="cuda", generator=g) * 2 + 0.5
@@ -526,10 +555,11 @@ def test_layer_norm_block_config5_moe_ffn(ctx, pkg, torch, orc):
     w2 = torch.randn((E, d, d_ff), device="cuda", generator=g) * 0.02
     nw = 1 + 0.1 * torch.randn(d, device="cuda", generator=g)
     nb = 0.1 * torch.randn(d, device="cuda", generator=g)
-    y, idx, w = _norm_block(ctx, pkg, torch, x, gw, w1, w3, w2, nw, nb, k, 0, 1, 1)
+    y, idx, w = _norm_block(ctx, pkg, torch, x, gw, w1, w3, w2, nw, None if rms else nb, k, 0,
+                            1, 1, norm=pkg.NORM_RMS if rms else pkg.NORM_LAYER)
     s = 32
     ry, ridx, rw = _norm_block_oracle(orc, host(x)[:s], host(gw), host(w1), host(w3), host(w2),
-                                      host(nw), host(nb), k, 0, 1, 1, residual=True)
+                                      host(nw), host(nb), k, 0, 1, 1, residual=True, rms=rms)
     assert np.array_equal(host(idx)[:s], ridx)
     assert_close(host(y)[:s], ry, what="config5 block sample")
 

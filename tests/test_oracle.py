@@ -165,6 +165,44 @@ def test_layer_norm_vs_float64(orc, contract):
     assert np.max(np.abs(y - ref)) <= 1e-5 * np.max(np.abs(ref))
 
 
+@pytest.mark.parametrize("contract", [0, 1])
+def test_rms_norm_closed_forms(orc, contract):
+    eps = F32(1e-5)
+    w = np.array([2.0, -0.5, 3.0], F32)
+    # constant row c: ss = 3 c^2 exactly (c = 2), inv = 1 / sqrt(c^2 + eps)
+    y, inv = orc.rms_norm(np.full((1, 3), 2.0, F32), w, eps, contract)
+    want_inv = F32(1) / np.sqrt(F32(4) + eps)
+    assert inv[0] == want_inv
+    assert np.array_equal(y[0], (F32(2) * want_inv) * w)
+    # 3, 4: ss = 25, ss / 2 = 12.5 exact; a mean subtracted (layer norm's
+    # slip) would give 0.25
+    y, inv = orc.rms_norm(np.array([[3.0, 4.0]], F32), np.ones(2, F32), eps, contract)
+    assert inv[0] == F32(1) / np.sqrt(F32(12.5) + eps)
+
+
+def test_rms_norm_single_float_accumulator(orc):
+    # 4096 squares of 1 after one 2^24: each 1 is absorbed in a float sum
+    row = np.array([[4096.0] + [1.0] * 4096], F32)  # 4096^2 = 2^24
+    _, inv = orc.rms_norm(row, np.ones(row.shape[1], F32), 0.0, 0)
+    ss = F32(2 ** 24)  # the float chain: 2^24 + 1 rounds back to 2^24 every time
+    assert inv[0] == F32(1) / np.sqrt(ss / F32(row.shape[1]))
+    exact = F32(1) / np.sqrt(F32((2 ** 24 + 4096) / row.shape[1]))
+    assert inv[0] != exact  # what a double accumulator would give
+
+
+@pytest.mark.parametrize("contract", [0, 1])
+def test_rms_norm_vs_float64(orc, contract):
+    rng = np.random.default_rng(41 + contract)
+    x = (1 + 2 * rng.normal(size=(17, 300))).astype(F32)
+    w = rng.normal(size=300).astype(F32)
+    y, inv = orc.rms_norm(x, w, 1e-5, contract)
+    x64 = x.astype(np.float64)
+    i64 = 1 / np.sqrt((x64 ** 2).mean(axis=1) + 1e-5)
+    assert np.allclose(inv, i64, rtol=1e-5)
+    ref = x64 * i64[:, None] * w
+    assert np.max(np.abs(y - ref)) <= 1e-5 * np.max(np.abs(ref))
+
+
 def test_layer_norm_contraction_differs(orc):
     # The FMA build fuses var += d*d and the weight/bias step; on random rows
     # that changes some outputs, and the unfused build is the float32 chain.
