@@ -31,7 +31,7 @@ EXPORTS = (
     "moe_version", "moe_sgemm_nt", "moe_sgemm_nn", "moe_silu", "moe_mul",
     "moe_layer_norm", "moe_rms_norm", "moe_gate_logits",
     "moe_route", "moe_permute", "moe_expert_ffn_grouped", "moe_combine",
-    "moe_layer_forward",
+    "moe_layer_forward", "moe_layer_w2_splits",
 )
 
 
@@ -100,6 +100,8 @@ def load_library(path: str = LIB_PATH):
         "moe_combine": ([P, P, P, P, P, P, P, I64, I64, I64, I, P], I),
         "moe_layer_forward": ([P, ctypes.POINTER(LayerDesc),
                                ctypes.POINTER(LayerWeights), P, P, P, P, P], I),
+        "moe_layer_w2_splits": ([P, ctypes.POINTER(LayerDesc), ctypes.POINTER(ctypes.c_int32)],
+                                I),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -296,6 +298,12 @@ class Context:
                                       _f32(y, "y"), _i32(topk_idx, "topk_idx"),
                                       _f32(topk_w, "topk_w"), _stream()))
         return y
+
+    def w2_splits(self, desc: LayerDesc) -> int:
+        """K splits layer_forward(desc) uses for w2 on this context's GPU."""
+        out = ctypes.c_int32(0)
+        _check(_lib.moe_layer_w2_splits(self.handle, ctypes.byref(desc), ctypes.byref(out)))
+        return out.value
 
 
 def make_desc(T, d, E, k, d_ff, act=ACT_SWIGLU, router=ROUTER_PHI_QUANT,

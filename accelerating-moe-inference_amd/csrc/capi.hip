@@ -782,4 +782,14 @@ int moe_layer_forward(moe_ctx* ctx, const moe_layer_desc* desc,
     });
 }
 
+int moe_layer_w2_splits(moe_ctx* ctx, const moe_layer_desc* desc, int32_t* splits) {
+    return guarded([&] {
+        check_ctx(ctx);
+        check_desc(desc);
+        check_ptr(splits, "splits");
+        DeviceScope dev(ctx->device);
+        *splits = choose_w2_splits(ctx, desc->T * desc->k, desc->d, desc->d_ff, desc->E);
+    });
+}
+
 }  // extern "C"

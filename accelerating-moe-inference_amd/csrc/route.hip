@@ -20,12 +20,15 @@ namespace {
 // ---------------------------------------------------------------- gate
 // The gate is a row-times-[E, d] product whose every output must be the
 // CPU's sequential k-ascending chain, so its parallelism is the T*E outputs:
-// one thread per output.  A workgroup covers R = 256/EB token rows x EB
+// one thread per output, or per TB outputs of one expert (TB tokens' chains
+// advanced together: the expert's 16-byte LDS read then feeds TB tokens, the
+// cut in LDS traffic that large E needs -- at E = 64 one read per output made
+// the kernel LDS-bound).  A workgroup covers R = TB * 256/EB token rows x EB
 // experts (EB = E rounded up to a power of two, 8..64); in a wave the lanes
-// sharing a row (or an expert) read the same LDS word, so both operand reads
-// are broadcasts.  K streams through a double-buffered LDS tile of R + EB
-// rows x 64 columns; the next chunk's coalesced global loads are in flight
-// while the current one is consumed, 4 columns per 16-byte LDS read.
+// sharing a row read the same LDS word (a broadcast).  K streams through a
+// double-buffered LDS tile of R + EB rows x 64 columns; the next chunk's
+// coalesced global loads are in flight while the current one is consumed, 4
+// columns per 16-byte LDS read.
 constexpr int GATE_KC = 64;
 constexpr int GATE_LDS = GATE_KC + 4;  // 16-byte aligned, conflict-free rows
 
@@ -36,11 +39,11 @@ __device__ __forceinline__ float mac(float acc, float a, float b) {
     return acc + prod;
 }
 
-template <int CONTRACT, int EB>
+template <int CONTRACT, int EB, int TB>
 __global__ __launch_bounds__(256) void gate_logits_kernel(
         const float* __restrict__ x, const float* __restrict__ w,
         float* __restrict__ logits, int64_t T, int64_t d, int64_t E) {
-    constexpr int R = 256 / EB;               // token rows per workgroup
+    constexpr int R = TB * (256 / EB);        // token rows per workgroup
     constexpr int ROWS = R + EB;              // staged rows: x rows, then w rows
     constexpr int PER = ROWS * GATE_KC / 256; // staged floats per thread
     typedef float f4 __attribute__((ext_vector_type(4)));
@@ -86,7 +89,9 @@ __global__ __launch_bounds__(256) void gate_logits_kernel(
         }
     };
 
-    float acc = 0.0f;
+    float acc[TB];
+#pragma unroll
+    for (int u = 0; u < TB; ++u) acc[u] = 0.0f;
     const int64_t nchunks = (d + GATE_KC - 1) / GATE_KC;
     if (nchunks > 0) {
         gload(0);
@@ -100,23 +105,32 @@ __global__ __launch_bounds__(256) void gate_logits_kernel(
         // Only the kn real columns enter the sum: the chain is exactly the
         // CPU's, with no padding term.
         const int kn = static_cast<int>(d - k0 < GATE_KC ? d - k0 : GATE_KC);
-        const float* xr = &tile[buf][r * GATE_LDS];
+        const float* xr = &tile[buf][r * TB * GATE_LDS];  // this thread's TB rows
         const float* wr = &tile[buf][(R + el) * GATE_LDS];
         int kk = 0;
         for (; kk + 4 <= kn; kk += 4) {
-            const f4 xv = *reinterpret_cast<const f4*>(xr + kk);
             const f4 wv = *reinterpret_cast<const f4*>(wr + kk);
-            acc = mac<CONTRACT>(acc, xv[0], wv[0]);
-            acc = mac<CONTRACT>(acc, xv[1], wv[1]);
-            acc = mac<CONTRACT>(acc, xv[2], wv[2]);
-            acc = mac<CONTRACT>(acc, xv[3], wv[3]);
+#pragma unroll
+            for (int u = 0; u < TB; ++u) {
+                const f4 xv = *reinterpret_cast<const f4*>(xr + u * GATE_LDS + kk);
+                acc[u] = mac<CONTRACT>(acc[u], xv[0], wv[0]);
+                acc[u] = mac<CONTRACT>(acc[u], xv[1], wv[1]);
+                acc[u] = mac<CONTRACT>(acc[u], xv[2], wv[2]);
+                acc[u] = mac<CONTRACT>(acc[u], xv[3], wv[3]);
+            }
         }
-        for (; kk < kn; ++kk) acc = mac<CONTRACT>(acc, xr[kk], wr[kk]);
+        for (; kk < kn; ++kk)
+#pragma unroll
+            for (int u = 0; u < TB; ++u) acc[u] = mac<CONTRACT>(acc[u], xr[u * GATE_LDS + kk], wr[kk]);
         if (c + 1 < nchunks) lstore(buf ^ 1);
         __syncthreads();
     }
-    const int64_t t = t0 + r, e = e0 + el;
-    if (t < T && e < E) logits[t * E + e] = acc;
+    const int64_t e = e0 + el;
+#pragma unroll
+    for (int u = 0; u < TB; ++u) {
+        const int64_t t = t0 + r * TB + u;
+        if (t < T && e < E) logits[t * E + e] = acc[u];
+    }
 }
 
 // -------------------------------------------------------------- routers
@@ -402,20 +416,23 @@ void launch_gate_logits(const float* x, const float* w, float* logits,
     if (T == 0 || E == 0) return;
     int eb = 8;
     while (eb < E && eb < 64) eb <<= 1;
-    const dim3 grid(static_cast<unsigned>(ceil_div(T, 256 / eb)),
+    // 4 tokens per thread from 32 experts up (small E keeps one output per
+    // thread: its rows per workgroup are already many, and the grid stays wide)
+    const int tb = eb >= 32 ? 4 : 1;
+    const dim3 grid(static_cast<unsigned>(ceil_div(T, tb * (256 / eb))),
                     static_cast<unsigned>(ceil_div(E, eb)));
     auto go = [&](auto kernel) {
         hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, x, w, logits, T, d, E);
     };
     switch (eb * 2 + (contract ? 1 : 0)) {
-        case 16: go(gate_logits_kernel<0, 8>); break;
-        case 17: go(gate_logits_kernel<1, 8>); break;
-        case 32: go(gate_logits_kernel<0, 16>); break;
-        case 33: go(gate_logits_kernel<1, 16>); break;
-        case 64: go(gate_logits_kernel<0, 32>); break;
-        case 65: go(gate_logits_kernel<1, 32>); break;
-        case 128: go(gate_logits_kernel<0, 64>); break;
-        default: go(gate_logits_kernel<1, 64>); break;
+        case 16: go(gate_logits_kernel<0, 8, 1>); break;
+        case 17: go(gate_logits_kernel<1, 8, 1>); break;
+        case 32: go(gate_logits_kernel<0, 16, 1>); break;
+        case 33: go(gate_logits_kernel<1, 16, 1>); break;
+        case 64: go(gate_logits_kernel<0, 32, 4>); break;
+        case 65: go(gate_logits_kernel<1, 32, 4>); break;
+        case 128: go(gate_logits_kernel<0, 64, 4>); break;
+        default: go(gate_logits_kernel<1, 64, 4>); break;
     }
 }
 

@@ -100,6 +100,38 @@ def zipf_bias(E, s):
     return np.log(p).astype(np.float32)
 
 
+def hbm_kernel_rates(avg, T, d, E, k, block, w2_splits):
+    """Achieved HBM rate of the routing, permutation, combine and norm kernels
+    against the 8 TB/s peak: algorithmic bytes (each operand read once, each
+    result written once) over the kernel's HIP-event time.  The combine reads
+    the w2_splits K-split partial row buffers the layer's w2 wrote."""
+    nb = -(-T // 256)
+    pairs = T * k
+    algo = {
+        "gate_logits": 4 * (T * d + E * d + T * E),
+        "route_softmax": 4 * (T * E + E) + 8 * pairs,
+        "route_phi": 4 * (T * E + E) + 8 * pairs,
+        "perm_count": 4 * pairs + 4 * E * nb,
+        "perm_scan": 8 * E * nb + 4 * (E + 1),
+        "perm_place": 4 * pairs + 4 * E * nb + 8 * pairs,
+        "layer_norm": 8 * T * d + 8 * T,
+        "rms_norm": 8 * T * d + 4 * T,
+    }
+    out = {}
+    for name, b in algo.items():
+        if name in avg:
+            gbs = b / (avg[name] * 1e-3) / 1e9
+            out[name] = {"bytes": b, "ms": round(avg[name], 5), "GB/s": round(gbs, 1),
+                         "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    if "combine" in avg:
+        S = w2_splits
+        b = 4 * S * pairs * d + 12 * pairs + 4 * T * d * (2 if block else 1)
+        gbs = b / (avg["combine"] * 1e-3) / 1e9
+        out["combine"] = {"bytes": b, "ms": round(avg["combine"], 5), "GB/s": round(gbs, 1),
+                          "frac": round(gbs / HBM_PEAK_GBS, 4), "w2_splits": S}
+    return out
+
+
 def cpu_baseline(x, weights, cfg, pkg_outputs, target_s):
     """The oracle's PhiMoE::forward restatement on a prefix of the tokens,
     sized to about target_s seconds of CPU work.  Test infrastructure: timed
@@ -232,6 +264,7 @@ def main():
     flops_w13 = 2.0 * pairs * d * d_ff * 2
     flops_w2 = 2.0 * pairs * d_ff * d
     avg = {name: ms / n for name, (ms, n) in kt.items()}
+    hbm = hbm_kernel_rates(avg, T, d, E, k, args.block, ctx.w2_splits(desc))
     w13_ms = avg["expert_w13_swiglu"]
     w2_ms = avg["expert_w2"]
     w13_tflops = flops_w13 / (w13_ms * 1e-3) / 1e12
@@ -282,6 +315,7 @@ def main():
             "flops_per_launch": flops_w13,
         },
         "kernel_avg_ms": {n: round(v, 5) for n, v in sorted(avg.items())},
+        "hbm_kernels": hbm,
         "expert_rows": counts.tolist(),
         "cpu_baseline": cpu,
         "cpu_sample_parity": parity,

@@ -209,6 +209,12 @@ int moe_layer_forward(moe_ctx* ctx, const moe_layer_desc* desc,
                       float* y, int32_t* topk_idx_out, float* topk_w_out,
                       void* stream);
 
+/* ---- the number of K splits moe_layer_forward(desc) runs its w2 GEMM with
+ * on this context's device (its combine then reads that many partial row
+ * buffers).  No reference counterpart: an introspection query for
+ * measurement tools. */
+int moe_layer_w2_splits(moe_ctx* ctx, const moe_layer_desc* desc, int32_t* splits);
+
 #ifdef __cplusplus
 }
 #endif
