@@ -29,7 +29,8 @@ EXPORTS = (
     "moe_ctx_create", "moe_ctx_destroy", "moe_ctx_reserve", "moe_ctx_set_timing",
     "moe_ctx_kernel_times", "moe_ctx_reset_timing", "moe_last_error",
     "moe_version", "moe_sgemm_nt", "moe_sgemm_nn", "moe_silu", "moe_mul",
-    "moe_layer_norm", "moe_rms_norm", "moe_gate_logits",
+    "moe_layer_norm", "moe_rms_norm", "moe_rope_table", "moe_rope", "moe_attention", "moe_add",
+    "moe_add_bias", "moe_embed", "moe_gate_logits",
     "moe_route", "moe_permute", "moe_expert_ffn_grouped", "moe_combine",
     "moe_layer_forward", "moe_layer_w2_splits",
 )
@@ -92,6 +93,12 @@ def load_library(path: str = LIB_PATH):
         "moe_mul": ([P, P, P, P, I64, P], I),
         "moe_layer_norm": ([P, P, P, P, F, I64, I64, I, P, P, P, P], I),
         "moe_rms_norm": ([P, P, P, F, I64, I64, I, P, P, P], I),
+        "moe_rope_table": ([F, I64, I64, P], I),
+        "moe_rope": ([P, P, P, P, I64, I64, I64, I64, I64, I64, P], I),
+        "moe_attention": ([P, P, P, P, P, I64, I64, I64, I64, I64, I64, P], I),
+        "moe_add": ([P, P, P, I64, P], I),
+        "moe_add_bias": ([P, P, P, I64, I64, P], I),
+        "moe_embed": ([P, P, P, I64, I64, I64, P, P], I),
         "moe_gate_logits": ([P, P, P, P, I64, I64, I64, I, P], I),
         "moe_route": ([P, P, P, I64, I64, I64, I, F, F, P, P, P], I),
         "moe_permute": ([P, P, I64, I64, I64, P, P, P, P], I),
@@ -158,6 +165,7 @@ class Context:
         _check(L.moe_ctx_create(device, ctypes.byref(h)))
         self.handle = h
         self.device = device
+        self._rope_tables = {}
 
     def close(self):
         if self.handle:
@@ -236,6 +244,57 @@ class Context:
         _check(_lib.moe_rms_norm(self.handle, _f32(x, "x"), _f32(weight, "weight"), eps, rows,
                                  h, contract, _f32(y, "y"), _f32(row_inv, "row_inv"), _stream()))
         return y
+
+    def rope_table(self, theta, head_dim, positions):
+        """The cos/sin table [positions, head_dim/2, 2] on this context's
+        device, built on the host by moe_rope_table (cached per shape)."""
+        import numpy as np
+        import torch
+        key = (float(theta), int(head_dim), int(positions))
+        t = self._rope_tables.get(key)
+        if t is None:
+            host = np.empty(max(positions * head_dim, 1), np.float32)
+            _check(_lib.moe_rope_table(float(theta), head_dim, positions,
+                                       host.ctypes.data_as(ctypes.c_void_p)))
+            t = torch.from_numpy(host).to(f"cuda:{self.device}")
+            self._rope_tables[key] = t
+        return t
+
+    def rope(self, q, k, batch, seq_len, q_heads, kv_heads, head_dim, theta=10000.0,
+             table=None):
+        """RoPE in place on q [B*S, Hq*hd] and k [B*S, Hkv*hd]."""
+        if table is None:
+            table = self.rope_table(theta, head_dim, seq_len)
+        positions = table.numel() // head_dim if head_dim else 0
+        _check(_lib.moe_rope(self.handle, _f32(q, "q"), _f32(k, "k"), _f32(table, "table"),
+                             positions, batch, seq_len, q_heads, kv_heads, head_dim,
+                             _stream()))
+
+    def attention(self, q, k, v, out, batch, seq_len, q_heads, kv_heads, head_dim, window=0):
+        """Causal attention per sequence and head; window 0 = unlimited."""
+        _check(_lib.moe_attention(self.handle, _f32(q, "q"), _f32(k, "k"), _f32(v, "v"),
+                                  _f32(out, "out"), batch, seq_len, q_heads, kv_heads,
+                                  head_dim, window, _stream()))
+        return out
+
+    def add(self, a, b):
+        """a += b."""
+        _check(_lib.moe_add(self.handle, _f32(a, "a"), _f32(b, "b"), a.numel(), _stream()))
+        return a
+
+    def add_bias(self, a, bias):
+        """a[r, c] += bias[c]."""
+        cols = bias.numel()
+        _check(_lib.moe_add_bias(self.handle, _f32(a, "a"), _f32(bias, "bias"),
+                                 a.numel() // cols if cols else 0, cols, _stream()))
+        return a
+
+    def embed(self, table, tokens, out):
+        """out[i] = table[tokens[i]]."""
+        vocab, d = table.shape
+        _check(_lib.moe_embed(self.handle, _f32(table, "table"), _i32(tokens, "tokens"),
+                              tokens.numel(), d, vocab, _f32(out, "out"), _stream()))
+        return out
 
     def gate_logits(self, x, gate_w, logits, contract=CONTRACT_FMA):
         T, d = x.shape

@@ -18,7 +18,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libmoe_amd.so")
-HIP_SOURCES = ["gemm.hip", "route.hip", "elementwise.hip", "norm.hip", "capi.hip"]
+HIP_SOURCES = ["gemm.hip", "route.hip", "elementwise.hip", "norm.hip", "attention.hip",
+               "capi.hip"]
 DROPIN_LIB = os.path.join(HERE, "libmoe_dropin.so")
 DROPIN_SOURCES = ["device.cpp", "tensor.cpp", "model_loader.cpp", "layer.cpp"]
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")

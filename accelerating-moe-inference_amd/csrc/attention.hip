@@ -1,0 +1,150 @@
+// The decoder pieces around the MoE block (config 5's prefill): rotary
+// position embedding, the masked softmax of causal attention, the residual
+// and bias adds, and the embedding gather.  The attention's two products
+// (Q K^T and P V) run on the GEMM engine as batched launches over
+// (sequence, head); this file holds the elementwise and row-wise steps.
+#include "common.hpp"
+
+#include <cmath>
+
+namespace moe {
+namespace {
+
+// tensor_ops::apply_rope (src/tensor.cu:191-210) with the cos/sin of every
+// (position, pair) read from a table built on the host by libm (as the
+// reference's GPU path does, src/model.cu:1784-1798 and rope_rows
+// :1046-1083): pair (j, j + half) of every head becomes (x0 c - x1 s,
+// x1 c + x0 s), each product rounded on its own (this file is built without
+// contraction).  One thread per pair; row r is at position r % seq_len.
+__global__ __launch_bounds__(256) void rope_kernel(float* __restrict__ q, float* __restrict__ k,
+                                                   const float* __restrict__ table, int64_t rows,
+                                                   int64_t seq_len, int64_t q_heads,
+                                                   int64_t kv_heads, int64_t head_dim) {
+    const int64_t half = head_dim / 2, heads = q_heads + kv_heads;
+    const int64_t n = rows * heads * half;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += stride) {
+        const int64_t j = i % half, hh = (i / half) % heads, r = i / (half * heads);
+        float* x = hh < q_heads ? q + r * q_heads * head_dim + hh * head_dim
+                                : k + r * kv_heads * head_dim + (hh - q_heads) * head_dim;
+        const float* trig = table + ((r % seq_len) * half + j) * 2;
+        const float c = trig[0], sn = trig[1];
+        const float x0 = x[j], x1 = x[j + half];
+        x[j] = x0 * c - x1 * sn;
+        x[j + half] = x1 * c + x0 * sn;
+    }
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// The softmax of PhiAttention::forward (src/layer.cu:118-140) on one score
+// row per wave: scaled = score / sqrt(head_dim) over the visible keys
+// (ki <= qi, qi - ki < window), m = max, p = exp(scaled - m) / sum, with the
+// reference's accurate_exp (double exp, one rounding); invisible keys get 0.
+// The row's score entries past the diagonal were never written (the score
+// GEMM skips those tiles) and are not read.
+__global__ __launch_bounds__(256) void attn_softmax_kernel(float* __restrict__ scores,
+                                                           int64_t rows_total, int64_t S,
+                                                           float scale, int64_t window) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (row >= rows_total) return;  // wave-uniform
+    const int64_t qi = row % S;
+    const int64_t lo = window > 0 && qi - window + 1 > 0 ? qi - window + 1 : 0;
+    float* p = scores + row * S;
+    float m = -INFINITY;
+    for (int64_t ki = lo + lane; ki <= qi; ki += 64) m = fmaxf(m, p[ki] / scale);
+    m = wave_max(m);
+    float den = 0.0f;
+    for (int64_t ki = lo + lane; ki <= qi; ki += 64)
+        den += static_cast<float>(exp(static_cast<double>(p[ki] / scale - m)));
+    den = wave_sum(den);
+    for (int64_t ki = lane; ki < S; ki += 64) {
+        const bool vis = ki >= lo && ki <= qi;
+        p[ki] = vis ? static_cast<float>(exp(static_cast<double>(p[ki] / scale - m))) / den : 0.0f;
+    }
+}
+
+__global__ __launch_bounds__(256) void add_kernel(float* __restrict__ a, const float* __restrict__ b,
+                                                  int64_t n) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += stride)
+        a[i] = a[i] + b[i];
+}
+
+__global__ __launch_bounds__(256) void add_bias_kernel(float* __restrict__ a,
+                                                       const float* __restrict__ bias,
+                                                       int64_t n, int64_t cols) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += stride)
+        a[i] = a[i] + bias[i % cols];
+}
+
+// out[i, :] = table[tokens[i], :]; a token outside [0, vocab) gives a zero row.
+__global__ __launch_bounds__(256) void embed_kernel(const float* __restrict__ table,
+                                                    const int32_t* __restrict__ tokens,
+                                                    int64_t n, int64_t d, int64_t vocab,
+                                                    float* __restrict__ out) {
+    const int64_t total = n * d;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+         i += stride) {
+        const int64_t r = i / d, c = i - r * d;
+        const int64_t t = tokens[r];
+        out[i] = t >= 0 && t < vocab ? table[t * d + c] : 0.0f;
+    }
+}
+
+unsigned grid_for(int64_t n) {
+    const int64_t blocks = ceil_div(n, 256);
+    return static_cast<unsigned>(blocks < 65536 ? blocks : 65536);
+}
+
+}  // namespace
+
+void launch_rope(float* q, float* k, const float* table, int64_t rows, int64_t seq_len,
+                 int64_t q_heads, int64_t kv_heads, int64_t head_dim, hipStream_t s) {
+    const int64_t n = rows * (q_heads + kv_heads) * (head_dim / 2);
+    if (n <= 0) return;
+    hipLaunchKernelGGL(rope_kernel, dim3(grid_for(n)), dim3(256), 0, s, q, k, table, rows,
+                       seq_len, q_heads, kv_heads, head_dim);
+}
+
+void launch_attn_softmax(float* scores, int64_t batches, int64_t seq_len, int64_t head_dim,
+                         int64_t window, hipStream_t s) {
+    const int64_t rows = batches * seq_len;
+    if (rows <= 0) return;
+    const float scale = sqrtf(static_cast<float>(head_dim));
+    hipLaunchKernelGGL(attn_softmax_kernel, dim3(static_cast<unsigned>(ceil_div(rows, 4))),
+                       dim3(256), 0, s, scores, rows, seq_len, scale, window);
+}
+
+void launch_add(float* a, const float* b, int64_t n, hipStream_t s) {
+    if (n <= 0) return;
+    hipLaunchKernelGGL(add_kernel, dim3(grid_for(n)), dim3(256), 0, s, a, b, n);
+}
+
+void launch_add_bias(float* a, const float* bias, int64_t rows, int64_t cols, hipStream_t s) {
+    const int64_t n = rows * cols;
+    if (n <= 0) return;
+    hipLaunchKernelGGL(add_bias_kernel, dim3(grid_for(n)), dim3(256), 0, s, a, bias, n, cols);
+}
+
+void launch_embed(const float* table, const int32_t* tokens, int64_t n, int64_t d, int64_t vocab,
+                  float* out, hipStream_t s) {
+    if (n <= 0 || d <= 0) return;
+    hipLaunchKernelGGL(embed_kernel, dim3(grid_for(n * d)), dim3(256), 0, s, table, tokens, n,
+                       d, vocab, out);
+}
+
+}  // namespace moe

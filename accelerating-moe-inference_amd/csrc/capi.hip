@@ -589,6 +589,170 @@ int moe_layer_norm(moe_ctx* ctx, const float* x, const float* weight, const floa
     });
 }
 
+int moe_rope_table(float theta, int64_t head_dim, int64_t positions, float* table) {
+    return guarded([&] {
+        moe::require(head_dim > 0 && head_dim % 2 == 0, "head_dim must be even and > 0");
+        check_dims(positions, "positions");
+        if (positions == 0) return;
+        check_ptr(table, "table");
+        // the libm calls of the reference's host-built table, in float
+        const int64_t half = head_dim / 2;
+        for (int64_t si = 0; si < positions; ++si)
+            for (int64_t j = 0; j < half; ++j) {
+                const float inv = powf(theta, -2.0f * static_cast<float>(j) /
+                                                  static_cast<float>(head_dim));
+                table[(si * half + j) * 2] = cosf(static_cast<float>(si) * inv);
+                table[(si * half + j) * 2 + 1] = sinf(static_cast<float>(si) * inv);
+            }
+    });
+}
+
+int moe_rope(moe_ctx* ctx, float* q, float* k, const float* table, int64_t table_positions,
+             int64_t batch, int64_t seq_len, int64_t q_heads, int64_t kv_heads,
+             int64_t head_dim, void* stream) {
+    return guarded([&] {
+        check_ctx(ctx);
+        check_dims(batch, "batch");
+        check_dims(seq_len, "seq_len");
+        moe::require(q_heads >= 0 && kv_heads >= 0, "heads must be >= 0");
+        moe::require(head_dim > 0 && head_dim % 2 == 0, "head_dim must be even and > 0");
+        const int64_t rows = batch * seq_len;
+        if (rows == 0 || q_heads + kv_heads == 0) return;
+        moe::require(table_positions >= seq_len, "the rope table needs seq_len positions");
+        check_ptr(table, "table");
+        if (q_heads > 0) check_ptr(q, "q");
+        if (kv_heads > 0) check_ptr(k, "k");
+        DeviceScope dev(ctx->device);
+        hipStream_t s = as_stream(stream);
+        ctx->launch("rope", s, [&] {
+            moe::launch_rope(q, k, table, rows, seq_len, q_heads, kv_heads, head_dim, s);
+        });
+    });
+}
+
+int moe_attention(moe_ctx* ctx, const float* q, const float* k, const float* v, float* out,
+                  int64_t batch, int64_t seq_len, int64_t q_heads, int64_t kv_heads,
+                  int64_t head_dim, int64_t window, void* stream) {
+    return guarded([&] {
+        check_ctx(ctx);
+        check_dims(batch, "batch");
+        check_dims(seq_len, "seq_len");
+        moe::require(kv_heads >= 1 && q_heads >= kv_heads && q_heads % kv_heads == 0,
+                     "q_heads must be a positive multiple of kv_heads");
+        moe::require(head_dim > 0, "head_dim must be > 0");
+        moe::require(window >= 0, "window must be >= 0 (0 = unlimited)");
+        if (batch == 0 || seq_len == 0) return;
+        check_ptr(q, "q");
+        check_ptr(k, "k");
+        check_ptr(v, "v");
+        check_ptr(out, "out");
+        if (head_dim % 16 != 0 || seq_len % 16 != 0 || !aligned16(q) || !aligned16(k) ||
+            !aligned16(v) || !aligned16(out))
+            throw moe::Unsupported(
+                "attention needs head_dim and seq_len multiples of 16 and 16-byte aligned q/k/v/out");
+        const int64_t w = window >= seq_len ? 0 : window;
+        const int64_t zb = batch * q_heads;
+        moe::require(zb <= 65535, "attention: batch * q_heads exceeds the grid's y range");
+        DeviceScope dev(ctx->device);
+        hipStream_t s = as_stream(stream);
+        const int64_t S = seq_len, qw = q_heads * head_dim, kw = kv_heads * head_dim;
+        float* scores = static_cast<float*>(ctx->workspace(size_t(zb) * S * S * sizeof(float)));
+        // scores[b, h] = Q[b, :, h] K[b, :, h / group]^T   (queries x keys)
+        moe::GemmArgs a{};
+        a.A = q;
+        a.lda = qw;
+        a.B0 = a.B1 = k;
+        a.ldb = kw;
+        a.C = scores;
+        a.ldc = S;
+        a.M = S;
+        a.N = S;
+        a.K = head_dim;
+        a.batch_inner = static_cast<int32_t>(q_heads);
+        a.b_group = static_cast<int32_t>(q_heads / kv_heads);
+        a.a_so = S * qw;
+        a.a_si = head_dim;
+        a.b_so = S * kw;
+        a.b_si = head_dim;
+        a.c_so = q_heads * S * S;
+        a.c_si = S * S;
+        a.causal = moe::CAUSAL_SCORES;
+        a.window = static_cast<int32_t>(w);
+        ctx->launch("attn_scores", s,
+                    [&] { moe::launch_gemm_batched(a, false, static_cast<int>(zb), s); });
+        ctx->launch("attn_softmax", s,
+                    [&] { moe::launch_attn_softmax(scores, zb, S, head_dim, w, s); });
+        // out[b, :, h] = P[b, h] V[b, :, h / group]   (queries x head_dim)
+        moe::GemmArgs b{};
+        b.A = scores;
+        b.lda = S;
+        b.B0 = b.B1 = v;
+        b.ldb = kw;
+        b.C = out;
+        b.ldc = qw;
+        b.M = S;
+        b.N = head_dim;
+        b.K = S;
+        b.batch_inner = static_cast<int32_t>(q_heads);
+        b.b_group = static_cast<int32_t>(q_heads / kv_heads);
+        b.a_so = q_heads * S * S;
+        b.a_si = S * S;
+        b.b_so = S * kw;
+        b.b_si = head_dim;
+        b.c_so = S * qw;
+        b.c_si = head_dim;
+        b.causal = moe::CAUSAL_PV;
+        b.window = static_cast<int32_t>(w);
+        ctx->launch("attn_pv", s,
+                    [&] { moe::launch_gemm_batched(b, true, static_cast<int>(zb), s); });
+    });
+}
+
+int moe_add(moe_ctx* ctx, float* a, const float* b, int64_t n, void* stream) {
+    return guarded([&] {
+        check_ctx(ctx);
+        moe::require(n >= 0, "n must be >= 0");
+        if (n == 0) return;
+        check_ptr(a, "a");
+        check_ptr(b, "b");
+        DeviceScope dev(ctx->device);
+        hipStream_t s = as_stream(stream);
+        ctx->launch("add", s, [&] { moe::launch_add(a, b, n, s); });
+    });
+}
+
+int moe_add_bias(moe_ctx* ctx, float* a, const float* bias, int64_t rows, int64_t cols,
+                 void* stream) {
+    return guarded([&] {
+        check_ctx(ctx);
+        check_dims(rows, "rows");
+        check_dims(cols, "cols");
+        if (rows == 0 || cols == 0) return;
+        check_ptr(a, "a");
+        check_ptr(bias, "bias");
+        DeviceScope dev(ctx->device);
+        hipStream_t s = as_stream(stream);
+        ctx->launch("add_bias", s, [&] { moe::launch_add_bias(a, bias, rows, cols, s); });
+    });
+}
+
+int moe_embed(moe_ctx* ctx, const float* table, const int32_t* tokens, int64_t n, int64_t d,
+              int64_t vocab, float* out, void* stream) {
+    return guarded([&] {
+        check_ctx(ctx);
+        check_dims(n, "n");
+        check_dims(d, "d");
+        check_dims(vocab, "vocab");
+        if (n == 0 || d == 0) return;
+        check_ptr(table, "table");
+        check_ptr(tokens, "tokens");
+        check_ptr(out, "out");
+        DeviceScope dev(ctx->device);
+        hipStream_t s = as_stream(stream);
+        ctx->launch("embed", s, [&] { moe::launch_embed(table, tokens, n, d, vocab, out, s); });
+    });
+}
+
 int moe_rms_norm(moe_ctx* ctx, const float* x, const float* weight, float eps, int64_t rows,
                  int64_t h, int contract, float* y, float* row_inv, void* stream) {
     return guarded([&] {

@@ -89,13 +89,43 @@ struct GemmArgs {
     int64_t k_split_len;     // K per split (a multiple of 16)
     int64_t c_split_stride;  // elements between the outputs of consecutive splits
     int32_t tile;            // dense: tile shape (kDenseTiles)
+    // Batched dense GEMMs (attention; grid.y = batches): batch z splits into
+    // zo = z / batch_inner, zi = z % batch_inner, and the operands start at
+    // A + zo*a_so + zi*a_si, B + zo*b_so + (zi / b_group)*b_si,
+    // C + zo*c_so + zi*c_si.  Zero-initialised arguments mean one batch.
+    int32_t batch_inner, b_group;
+    int64_t a_so, a_si, b_so, b_si, c_so, c_si;
+    // Causal attention (rows are query positions): CAUSAL_SCORES skips tiles
+    // whose keys (columns) all lie after every query row or, with window > 0,
+    // all before it; CAUSAL_PV limits K (keys) to the causal window of the
+    // tile's rows -- the probabilities outside it are zero.
+    int32_t causal;
+    int32_t window;
 };
+
+enum Causal : int { CAUSAL_NONE = 0, CAUSAL_SCORES = 1, CAUSAL_PV = 2 };
 
 enum Epilogue : int { EPI_STORE = 0, EPI_BIAS = 1, EPI_SILU = 2, EPI_SWIGLU = 3 };
 
 // Launchers implemented in the .hip files.
 void launch_gemm(const GemmArgs& a, bool nn, bool grouped, int epi, bool vec,
                  hipStream_t s);
+// Dense batched GEMM over grid.y (the batch fields of GemmArgs; M, N, K,
+// lda/ldb/ldc, causal, window as for one batch; direct-load path only).
+void launch_gemm_batched(const GemmArgs& a, bool nn, int batches, hipStream_t s);
+// Attention pieces: RoPE in place on q [rows, q_heads*hd] and k [rows,
+// kv_heads*hd] (row r at position r % seq_len, cos/sin from table[pos][hd/2][2]);
+// the masked softmax of a [batches, S, S] score block in place (scores scaled
+// by 1/sqrt(hd), keys ki <= qi and qi - ki < window visible, the rest set to 0).
+void launch_rope(float* q, float* k, const float* table, int64_t rows, int64_t seq_len,
+                 int64_t q_heads, int64_t kv_heads, int64_t head_dim, hipStream_t s);
+void launch_attn_softmax(float* scores, int64_t batches, int64_t seq_len, int64_t head_dim,
+                         int64_t window, hipStream_t s);
+// a[i] += b[i];  a[r, c] += bias[c];  out[i, :] = table[tokens[i], :]
+void launch_add(float* a, const float* b, int64_t n, hipStream_t s);
+void launch_add_bias(float* a, const float* bias, int64_t rows, int64_t cols, hipStream_t s);
+void launch_embed(const float* table, const int32_t* tokens, int64_t n, int64_t d,
+                  int64_t vocab, float* out, hipStream_t s);
 void launch_gate_logits(const float* x, const float* w, float* logits,
                         int64_t T, int64_t d, int64_t E, int contract,
                         hipStream_t s);

@@ -454,6 +454,8 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
     int64_t row0;
     int rows;
     const float* B[NB];
+    const float* Ab = p.A;
+    float* Cb = p.C;
     if (GROUPED) {
         int e, first;
         if (!find_expert<BM>(p.offsets, p.E, mt, e, first)) return;  // surplus tile
@@ -467,14 +469,37 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
     } else {
         row0 = static_cast<int64_t>(mt) * BM;
         rows = static_cast<int>(p.M - row0 < BM ? p.M - row0 : BM);
-        B[0] = p.B0;
-        if (NB == 2) B[NB - 1] = p.B1;
+        // batch of a batched launch (grid.y); one batch otherwise
+        const int64_t z = blockIdx.y;
+        const int64_t inner = p.batch_inner > 0 ? p.batch_inner : 1;
+        const int64_t zo = z / inner, zi = z % inner;
+        const int64_t bz = zi / (p.b_group > 0 ? p.b_group : 1);
+        Ab = p.A + zo * p.a_so + zi * p.a_si;
+        Cb = p.C + zo * p.c_so + zi * p.c_si;
+        B[0] = p.B0 + zo * p.b_so + bz * p.b_si;
+        if (NB == 2) B[NB - 1] = p.B1 + zo * p.b_so + bz * p.b_si;
     }
     const int64_t n0 = static_cast<int64_t>(nt) * BN;
     const int64_t N = p.N;
     // K columns [kbeg, K) of this split; loads are bounded by K
-    const int64_t kbeg = split * p.k_split_len;
-    const int64_t K = p.K - kbeg < p.k_split_len ? p.K : kbeg + p.k_split_len;
+    int64_t kbeg = split * p.k_split_len;
+    int64_t K = p.K - kbeg < p.k_split_len ? p.K : kbeg + p.k_split_len;
+    if (!GROUPED && p.causal == CAUSAL_SCORES) {
+        // keys n0.. all after the last query row, or (window) all too old for
+        // the first: nothing of this tile is ever read
+        if (n0 > row0 + rows - 1) return;
+        if (p.window > 0 && n0 + BN - 1 < row0 - (p.window - 1)) return;
+    } else if (!GROUPED && p.causal == CAUSAL_PV) {
+        // probabilities of keys past the last row (or before the first row's
+        // window) are zero: leave them out of the K loop (multiples of 16)
+        const int64_t hi = ((row0 + rows + 15) / 16) * 16;
+        K = K < hi ? K : hi;
+        if (p.window > 0) {
+            int64_t lo = row0 - (p.window - 1);
+            lo = lo > 0 ? (lo / 16) * 16 : 0;
+            kbeg = kbeg > lo ? kbeg : lo;
+        }
+    }
 
     // Per-lane source of each load instruction: instruction j of this wave
     // fills rows 16*J .. 16*J+15 (J = wave*INS + j); lane L writes slot L%4
@@ -492,7 +517,7 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
             tok = tok < 0 ? 0 : (tok >= p.gather_rows ? p.gather_rows - 1 : tok);
             src = tok;
         }
-        asrc[j] = p.A + src * p.lda + 4 * (lslot ^ swz(r));
+        asrc[j] = Ab + src * p.lda + 4 * (lslot ^ swz(r));
     }
     // B: NT rows n like A's rows.  NN: instruction J's lane L holds floats
     // 256 J + 4 L .. +3 of the k-major tile, i.e. k-row (256 J + 4 L) / BN,
@@ -636,7 +661,7 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
                     } else if (EPI == EPI_SWIGLU) {
                         v = silu_ref(v) * acc[NB - 1][bi][bj][r];
                     }
-                    p.C[split * p.c_split_stride + (row0 + i) * p.ldc + n] = v;
+                    Cb[split * p.c_split_stride + (row0 + i) * p.ldc + n] = v;
                 }
             }
 }
@@ -696,6 +721,41 @@ int dense_occupancy(bool nn) {
 }
 
 }  // namespace
+
+namespace {
+template <class C, bool NN>
+void launch_batched_cfg(const GemmArgs& args, int batches, hipStream_t s) {
+    GemmArgs a = args;
+    a.m_tiles = static_cast<int32_t>(ceil_div(a.M, C::BM));
+    a.n_tiles = static_cast<int32_t>(ceil_div(a.N, C::BN));
+    a.group_m = a.m_tiles;
+    a.k_splits = 1;
+    a.k_split_len = a.K;
+    a.c_split_stride = 0;
+    constexpr int SCHED = MOE_DENSE_SCHED | SCHED_DIRECT;
+    hipLaunchKernelGGL((gemm_direct_kernel<C, SCHED, NN, false, 1, EPI_BIAS>),
+                       dim3(static_cast<unsigned>(a.m_tiles) * static_cast<unsigned>(a.n_tiles),
+                            static_cast<unsigned>(batches)),
+                       dim3(C::THREADS), 0, s, a);
+}
+}  // namespace
+
+void launch_gemm_batched(const GemmArgs& a, bool nn, int batches, hipStream_t s) {
+    if (batches <= 0 || a.M <= 0 || a.N <= 0) return;
+    auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    const bool ok = a.K % 16 == 0 && a.lda % 4 == 0 && a.ldb % 4 == 0 && al(a.A) && al(a.B0) &&
+                    (!nn || a.N % 4 == 0) && a.a_so % 4 == 0 && a.a_si % 4 == 0 &&
+                    a.b_so % 4 == 0 && a.b_si % 4 == 0;
+    if (!ok) throw Unsupported("batched GEMM needs 16-byte aligned rows and K % 16 == 0");
+    // narrow outputs (an attention head's 64 values) take the 128 x 64 tile
+    if (a.N <= 64) {
+        if (nn) launch_batched_cfg<CfgOf<3>::T, true>(a, batches, s);
+        else launch_batched_cfg<CfgOf<3>::T, false>(a, batches, s);
+    } else {
+        if (nn) launch_batched_cfg<DenseCfg, true>(a, batches, s);
+        else launch_batched_cfg<DenseCfg, false>(a, batches, s);
+    }
+}
 
 GemmTile dense_tile(int tile) {
     switch (tile) {

@@ -26,6 +26,14 @@
  *   moe_layer_norm      tensor_ops::layer_norm             src/tensor.cu:175-189,
  *                       layer_norm_rows / forward_stats    src/model.cu:720-846,1440-1480
  *   moe_rms_norm        (no counterpart: the RMSNorm config 5's decoder names)
+ *   moe_rope_table      the host-built cos/sin table       src/model.cu:1784-1798
+ *   moe_rope            tensor_ops::apply_rope             src/tensor.cu:191-210,
+ *                       rope_rows                          src/model.cu:1046-1083
+ *   moe_attention       PhiAttention::forward, after the projections  src/layer.cu:111-143;
+ *                       attention_heads                    src/model.cu:1161-1283
+ *   moe_add             tensor_ops::add_inplace            src/tensor.cu:150-154
+ *   moe_add_bias        tensor_ops::add_bias_inplace       src/tensor.cu:156-161
+ *   moe_embed           embedding row gather (gather_rows) src/model.cu:674-693,1878-1885
  *   moe_layer_forward   PhiMoE::forward                    src/layer.cu:80-103,
  *                       the MoE block of generate()        src/model.cu:1968-2021
  *   moe_ctx_*           DeviceBuffer / Scratch workspace   src/model.cu:45-68,1294-1324
@@ -161,6 +169,42 @@ int moe_layer_norm(moe_ctx* ctx, const float* x, const float* weight,
 int moe_rms_norm(moe_ctx* ctx, const float* x, const float* weight, float eps,
                  int64_t rows, int64_t h, int contract, float* y,
                  float* row_inv, void* stream);
+
+/* ---- decoder pieces around the MoE block (config 5's prefill).
+ * moe_rope_table: host function, no device work: table[pos][j] = (cosf(pos *
+ *   inv_j), sinf(pos * inv_j)), inv_j = powf(theta, -2j/head_dim), for pos <
+ *   positions and j < head_dim/2 -- the libm calls of the reference's
+ *   host-built table (src/model.cu:1784-1798); `table` is host memory of
+ *   positions * head_dim floats.  Copy it to the device for moe_rope.
+ * moe_rope: RoPE in place on q [batch*seq_len, q_heads*head_dim] and k
+ *   [batch*seq_len, kv_heads*head_dim] with a device copy of that table
+ *   (table_positions >= seq_len rows); row r is at position r % seq_len;
+ *   pair (x0, x1) = (x[j], x[j + head_dim/2]) of each head becomes
+ *   (x0*c - x1*s, x1*c + x0*s), each product rounded on its own:
+ *   bit-identical to tensor_ops::apply_rope and rope_rows
+ *   (src/model.cu:1046-1083) given the table.
+ * moe_attention: out = softmax(q k^T / sqrt(head_dim), causal, keys within
+ *   `window` positions (0 = unlimited)) v per sequence and head; q and out
+ *   [batch*seq_len, q_heads*head_dim], k and v [batch*seq_len,
+ *   kv_heads*head_dim], query head h reads key head h / (q_heads/kv_heads).
+ *   Needs head_dim and seq_len multiples of 16 and 16-byte aligned buffers
+ *   (MOE_ERR_UNSUPPORTED otherwise); uses batch*q_heads*seq_len^2 floats of
+ *   workspace.
+ * moe_add: a += b elementwise.  moe_add_bias: a[r, c] += bias[c].
+ * moe_embed: out[i, :] = table[tokens[i], :] (table [vocab, d]); a token
+ *   outside [0, vocab) gives a zero row. */
+int moe_rope_table(float theta, int64_t head_dim, int64_t positions, float* table);
+int moe_rope(moe_ctx* ctx, float* q, float* k, const float* table,
+             int64_t table_positions, int64_t batch, int64_t seq_len,
+             int64_t q_heads, int64_t kv_heads, int64_t head_dim, void* stream);
+int moe_attention(moe_ctx* ctx, const float* q, const float* k, const float* v,
+                  float* out, int64_t batch, int64_t seq_len, int64_t q_heads,
+                  int64_t kv_heads, int64_t head_dim, int64_t window, void* stream);
+int moe_add(moe_ctx* ctx, float* a, const float* b, int64_t n, void* stream);
+int moe_add_bias(moe_ctx* ctx, float* a, const float* bias, int64_t rows,
+                 int64_t cols, void* stream);
+int moe_embed(moe_ctx* ctx, const float* table, const int32_t* tokens, int64_t n,
+              int64_t d, int64_t vocab, float* out, void* stream);
 
 /* ---- router gate logits[T,E] = x[T,d] Wg[E,d]^T with one k-ascending fp32
  * accumulator per output: bit-identical to the CPU path under `contract`. */

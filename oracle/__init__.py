@@ -58,6 +58,12 @@ def lib():
         L.orc_layer_norm.restype = I
         L.orc_rms_norm.argtypes = [P, P, F, S, S, I, P, P]
         L.orc_rms_norm.restype = I
+        L.orc_rope_table.argtypes = [F, S, S, P]
+        L.orc_rope_table.restype = I
+        L.orc_rope.argtypes = [P, P, P, S, S, S, S, S]
+        L.orc_rope.restype = I
+        L.orc_attention.argtypes = [P, P, P, P, S, S, S, S, S, S]
+        L.orc_attention.restype = I
         L.orc_route.argtypes = [P, P, S, S, S, I, F, F, P, P]
         L.orc_route.restype = I
         L.orc_permute.argtypes = [P, S, S, S, P, P, P]
@@ -154,6 +160,33 @@ def layer_norm(x, weight, bias, eps=1e-5, contract=CONTRACT_FMA):
     _check(lib().orc_layer_norm(_p(x), _p(weight), _p(bias), float(eps), rows, h,
                                 int(contract), _p(y), _p(mean), _p(inv)), "layer_norm")
     return y, mean, inv
+
+
+def rope(q, k, batch, seq_len, q_heads, kv_heads, head_dim, theta=10000.0, table=None):
+    """tensor_ops::apply_rope on copies of q [B*S, Hq*hd] and k [B*S, Hkv*hd]
+    (table: rope_table(theta, head_dim, seq_len) unless given)."""
+    q, k = _f32(q).copy(), _f32(k).copy()
+    t = rope_table(theta, head_dim, seq_len) if table is None else _f32(table)
+    _check(lib().orc_rope(_p(q), _p(k), _p(t), batch, seq_len, q_heads, kv_heads,
+                          head_dim), "rope")
+    return q, k
+
+
+def rope_table(theta, head_dim, positions):
+    """cos/sin of RoPE, [positions, head_dim/2, 2] (float libm calls)."""
+    t = np.empty((positions, head_dim // 2, 2), np.float32)
+    _check(lib().orc_rope_table(float(theta), head_dim, positions, _p(t)), "rope_table")
+    return t
+
+
+def attention(q, k, v, batch, seq_len, q_heads, kv_heads, head_dim, window=None):
+    """PhiAttention's core (after the projections and RoPE): [B*S, Hq*hd]."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    out = np.empty(q.shape, np.float32)
+    w = seq_len if window is None else window
+    _check(lib().orc_attention(_p(q), _p(k), _p(v), _p(out), batch, seq_len, q_heads,
+                               kv_heads, head_dim, w), "attention")
+    return out
 
 
 def rms_norm(x, weight, eps=1e-5, contract=CONTRACT_FMA):

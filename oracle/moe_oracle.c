@@ -204,6 +204,114 @@ int orc_rms_norm(const float* x, const float* weight, float eps, size_t rows,
     return 0;
 }
 
+/* The cos/sin of RoPE for positions [0, positions) and pairs j < head_dim/2:
+ * inv = powf(theta, -2j/head_dim), table[(pos*half + j)*2 + {0,1}] =
+ * {cosf, sinf}(pos * inv) -- the float libm calls of tensor_ops::apply_rope
+ * (src/tensor.cu:196-197) and of the reference's host-built GPU table
+ * (src/model.cu:1791-1797).
+ * Pinned by: angles against float64 (tests/test_oracle.py); libm's
+ * powf/cosf/sinf last ulp: parity unpinned, as for exp. */
+int orc_rope_table(float theta, size_t head_dim, size_t positions, float* table) {
+    if (head_dim % 2 || (positions > 0 && !table)) return 1;
+    const size_t half = head_dim / 2;
+    for (size_t s = 0; s < positions; ++s)
+        for (size_t j = 0; j < half; ++j) {
+            const float inv = powf(theta, -2.0f * (float)j / (float)head_dim);
+            table[(s * half + j) * 2] = cosf((float)s * inv);
+            table[(s * half + j) * 2 + 1] = sinf((float)s * inv);
+        }
+    return 0;
+}
+
+/* tensor_ops::apply_rope (src/tensor.cu:191-210) over `batch` sequences of
+ * seq_len rows (row r sits at position r % seq_len), cos/sin from
+ * orc_rope_table's layout: (x0, x1) = (x[j], x[j + half]) -> (x0 c - x1 s,
+ * x1 c + x0 s), each product rounded on its own (this file is built with
+ * -ffp-contract=off), as rope_rows does on the GPU (src/model.cu:1066-1081,
+ * __fmul_rn / __fsub_rn / __fadd_rn); q has q_heads heads, k kv_heads, rows
+ * of heads * head_dim.
+ * Pinned by: position 0 is the identity exactly; each (x0, x1) pair keeps its
+ * length; a pair at the angles of a 90-degree table turns exactly
+ * (tests/test_oracle.py). */
+int orc_rope(float* q, float* k, const float* table, size_t batch, size_t seq_len,
+             size_t q_heads, size_t kv_heads, size_t head_dim) {
+    if (head_dim % 2 || (batch * seq_len > 0 && (!q || !k || !table))) return 1;
+    const size_t half = head_dim / 2, rows = batch * seq_len;
+#pragma omp parallel for schedule(static)
+    for (long long r = 0; r < (long long)rows; ++r) {
+        const size_t s = (size_t)r % seq_len;
+        for (int which = 0; which < 2; ++which) {
+            float* x = which == 0 ? q : k;
+            const size_t heads = which == 0 ? q_heads : kv_heads;
+            for (size_t h = 0; h < heads; ++h)
+                for (size_t j = 0; j < half; ++j) {
+                    const float c = table[(s * half + j) * 2], sn = table[(s * half + j) * 2 + 1];
+                    const size_t o = orc_at(rows, heads * head_dim, (size_t)r, h * head_dim + j);
+                    const float x0 = x[o], x1 = x[o + half];
+                    x[o] = x0 * c - x1 * sn;
+                    x[o + half] = x1 * c + x0 * sn;
+                }
+        }
+    }
+    return 0;
+}
+
+/* The attention core of PhiAttention::forward (src/layer.cu:111-143) over
+ * `batch` sequences of seq_len rows: for query row qi and head qh (key head
+ * qh / (q_heads / kv_heads)), keys ki <= qi with qi - ki < window;
+ * score = sum_d q*k (one float accumulator, d ascending), scaled =
+ * score / sqrt(head_dim); m = max scaled; denom = sum accurate_exp(scaled - m)
+ * over ki ascending; out[qi, qh, d] = sum over ki ascending of
+ * accurate_exp(scaled - m) / denom * v[ki, kh, d].  The reference recomputes
+ * each score three times; it is computed once here (the same value).
+ * Pinned by: one visible key gives out = v exactly; window 1 gives
+ * out = v[qi]; identical keys give the mean of the visible values; float64
+ * brute force (tests/test_oracle.py). */
+int orc_attention(const float* q, const float* k, const float* v, float* out,
+                  size_t batch, size_t seq_len, size_t q_heads, size_t kv_heads,
+                  size_t head_dim, size_t window) {
+    if (!kv_heads || q_heads % kv_heads || window == 0) return 1;
+    if (batch * seq_len > 0 && (!q || !k || !v || !out)) return 1;
+    const size_t group = q_heads / kv_heads, rows = batch * seq_len;
+    const size_t qw = q_heads * head_dim, kw = kv_heads * head_dim;
+    const float scale = sqrtf((float)head_dim);
+#pragma omp parallel for schedule(dynamic, 4)
+    for (long long r = 0; r < (long long)rows; ++r) {
+        const size_t b = (size_t)r / seq_len, qi = (size_t)r % seq_len;
+        float* scaled = (float*)malloc((seq_len + 1) * sizeof(float));
+        float* wts = (float*)malloc((seq_len + 1) * sizeof(float));
+        for (size_t qh = 0; qh < q_heads; ++qh) {
+            const size_t kh = qh / group;
+            float maxv = -INFINITY;
+            for (size_t ki = 0; ki <= qi; ++ki) {
+                if (qi - ki >= window) continue;
+                float score = 0.0f;
+                for (size_t d = 0; d < head_dim; ++d)
+                    score += q[orc_at(rows, qw, (size_t)r, qh * head_dim + d)] *
+                             k[orc_at(rows, kw, b * seq_len + ki, kh * head_dim + d)];
+                scaled[ki] = score / scale;
+                maxv = fmaxf(maxv, scaled[ki]);
+            }
+            float denom = 0.0f;
+            for (size_t ki = 0; ki <= qi; ++ki)
+                if (qi - ki < window) {
+                    wts[ki] = orc_accurate_exp(scaled[ki] - maxv);
+                    denom += wts[ki];
+                }
+            for (size_t d = 0; d < head_dim; ++d) {
+                float value = 0.0f;
+                for (size_t ki = 0; ki <= qi; ++ki)
+                    if (qi - ki < window)
+                        value += wts[ki] / denom * v[orc_at(rows, kw, b * seq_len + ki, kh * head_dim + d)];
+                out[orc_at(rows, qw, (size_t)r, qh * head_dim + d)] = value;
+            }
+        }
+        free(scaled);
+        free(wts);
+    }
+    return 0;
+}
+
 /* c = a * b elementwise (src/tensor.cu:163-167). Pinned by direct products. */
 void orc_mul(const float* a, const float* b, float* c, size_t n) {
 #pragma omp parallel for schedule(static)

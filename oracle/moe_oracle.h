@@ -54,6 +54,12 @@ int orc_layer_norm(const float* x, const float* weight, const float* bias,
                    float* row_mean, float* row_inv);
 int orc_rms_norm(const float* x, const float* weight, float eps, size_t rows,
                  size_t h, int contract, float* y, float* row_inv);
+int orc_rope_table(float theta, size_t head_dim, size_t positions, float* table);
+int orc_rope(float* q, float* k, const float* table, size_t batch, size_t seq_len,
+             size_t q_heads, size_t kv_heads, size_t head_dim);
+int orc_attention(const float* q, const float* k, const float* v, float* out,
+                  size_t batch, size_t seq_len, size_t q_heads, size_t kv_heads,
+                  size_t head_dim, size_t window);
 
 int orc_route(const float* logits, const float* expert_bias,
               size_t T, size_t E, size_t k, int mode,

@@ -58,3 +58,17 @@ def test_errors_without_context(lib_path):
     assert "moe_ctx" in lib.moe_last_error().decode()
     rc = lib.moe_route(None, None, None, 4, 8, 2, 0, 1e-3, 2e-2, None, None, None)
     assert rc == pkg.ERR_INVALID
+
+
+def test_rope_table_is_the_oracles_libm_table(lib_path, orc):
+    # moe_rope_table is host code (no device work): its float libm calls must
+    # give the oracle's table bit for bit, since RoPE's parity rests on it
+    import numpy as np
+    lib = load_pkg().load_library()
+    for theta, hd, pos in ((10000.0, 64, 513), (500000.0, 128, 40), (10000.0, 2, 7)):
+        t = np.empty((pos, hd // 2, 2), np.float32)
+        assert lib.moe_rope_table(theta, hd, pos, t.ctypes.data_as(ctypes.c_void_p)) == 0
+        assert np.array_equal(t, orc.rope_table(theta, hd, pos))
+    t = np.empty(4, np.float32)
+    assert lib.moe_rope_table(10000.0, 3, 1, t.ctypes.data_as(ctypes.c_void_p)) == \
+        load_pkg().ERR_INVALID

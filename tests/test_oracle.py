@@ -203,6 +203,123 @@ def test_rms_norm_vs_float64(orc, contract):
     assert np.max(np.abs(y - ref)) <= 1e-5 * np.max(np.abs(ref))
 
 
+# ---------------------------------------------------------------- RoPE
+def test_rope_position_zero_is_identity_and_pairs_keep_length(orc):
+    rng = np.random.default_rng(3)
+    B, S, H, KVH, hd = 2, 9, 4, 2, 16
+    q = rng.normal(size=(B * S, H * hd)).astype(F32)
+    k = rng.normal(size=(B * S, KVH * hd)).astype(F32)
+    rq, rk = orc.rope(q, k, B, S, H, KVH, hd)
+    for b in range(B):  # position 0 of every sequence: cos 0 = 1, sin 0 = 0
+        assert np.array_equal(rq[b * S], q[b * S]) and np.array_equal(rk[b * S], k[b * S])
+    half = hd // 2
+    for x, y in ((q, rq), (k, rk)):
+        x3 = x.reshape(B * S, -1, hd).astype(np.float64)
+        y3 = y.reshape(B * S, -1, hd).astype(np.float64)
+        n0 = x3[..., :half] ** 2 + x3[..., half:] ** 2
+        n1 = y3[..., :half] ** 2 + y3[..., half:] ** 2
+        assert np.allclose(n0, n1, rtol=1e-5, atol=1e-6)
+
+
+def test_rope_angles_vs_float64(orc):
+    # one head, x = (1 on the first half, 0 on the second): pair j at position
+    # s becomes (cos a, sin a) with a = s * theta^(-2j/hd)
+    S, hd, theta = 40, 8, 10000.0
+    q = np.zeros((S, hd), F32)
+    q[:, : hd // 2] = 1.0
+    rq, _ = orc.rope(q, q.copy(), 1, S, 1, 1, hd, theta)
+    s = np.arange(S)[:, None].astype(np.float64)
+    j = np.arange(hd // 2)[None, :].astype(np.float64)
+    a = s * theta ** (-2 * j / hd)
+    assert np.allclose(rq[:, : hd // 2], np.cos(a), atol=2e-6)
+    assert np.allclose(rq[:, hd // 2:], np.sin(a), atol=2e-6)
+    # the reference's frequency of pair j = hd/4: theta^(-1/2) = 0.01 at theta 1e4
+    assert np.isclose(rq[1, hd // 4], np.cos(0.01), atol=1e-7)
+    t = orc.rope_table(theta, hd, S)
+    assert t.shape == (S, hd // 2, 2)
+    assert np.allclose(t[..., 0], np.cos(a), atol=2e-6) and np.allclose(t[..., 1], np.sin(a),
+                                                                        atol=2e-6)
+
+
+def test_rope_quarter_turn_table_and_uncontracted_products(orc):
+    rng = np.random.default_rng(5)
+    S, H, hd = 3, 2, 8
+    q = rng.normal(size=(S, H * hd)).astype(F32)
+    k = rng.normal(size=(S, hd)).astype(F32)
+    # cos 0 / sin 1 everywhere: (x0, x1) -> (-x1, x0) exactly
+    t = np.zeros((S, hd // 2, 2), F32)
+    t[..., 1] = 1.0
+    rq, rk = orc.rope(q, k, 1, S, H, 1, hd, table=t)
+    for x, y in ((q, rq), (k, rk)):
+        x3, y3 = x.reshape(S, -1, hd), y.reshape(S, -1, hd)
+        assert np.array_equal(y3[..., : hd // 2], -x3[..., hd // 2:])
+        assert np.array_equal(y3[..., hd // 2:], x3[..., : hd // 2])
+    # a generic table: each product rounds to float on its own (no FMA), the
+    # rounding the reference's rope_rows spells out with __fmul_rn/__fsub_rn
+    t = rng.uniform(-1, 1, (S, hd // 2, 2)).astype(F32)
+    rq, _ = orc.rope(q, k, 1, S, H, 1, hd, table=t)
+    q3 = q.reshape(S, H, hd)
+    c, s = t[:, None, :, 0], t[:, None, :, 1]
+    x0, x1 = q3[..., : hd // 2], q3[..., hd // 2:]
+    exp0 = (x0 * c).astype(F32) - (x1 * s).astype(F32)
+    exp1 = (x1 * c).astype(F32) + (x0 * s).astype(F32)
+    assert np.array_equal(rq.reshape(S, H, hd), np.concatenate([exp0, exp1], axis=-1))
+    fused = (x0.astype(np.float64) * c - (x1 * s).astype(F32)).astype(F32)
+    assert not np.array_equal(fused, exp0)  # the inputs tell the two roundings apart
+
+
+# ------------------------------------------------------------ attention
+def test_attention_closed_forms(orc):
+    rng = np.random.default_rng(8)
+    B, S, H, KVH, hd = 2, 7, 4, 2, 8
+    q = rng.normal(size=(B * S, H * hd)).astype(F32)
+    k = rng.normal(size=(B * S, KVH * hd)).astype(F32)
+    v = rng.normal(size=(B * S, KVH * hd)).astype(F32)
+    out = orc.attention(q, k, v, B, S, H, KVH, hd)
+    group = H // KVH
+    for b in range(B):  # the first token of a sequence sees only itself: out = v
+        for h in range(H):
+            kh = h // group
+            assert np.array_equal(out[b * S, h * hd:(h + 1) * hd], v[b * S, kh * hd:(kh + 1) * hd])
+    # window 1: every token sees only itself
+    out1 = orc.attention(q, k, v, B, S, H, KVH, hd, window=1)
+    for h in range(H):
+        kh = h // group
+        assert np.array_equal(out1[:, h * hd:(h + 1) * hd], v[:, kh * hd:(kh + 1) * hd])
+    # identical keys: uniform weights over the visible keys -> running mean of v
+    kk = np.tile(k[:1], (B * S, 1))
+    outu = orc.attention(q, kk, v, B, S, H, KVH, hd)
+    for b in range(B):
+        for qi in range(S):
+            mean = v[b * S:b * S + qi + 1].astype(np.float64).mean(axis=0)
+            assert np.allclose(outu[b * S + qi, :hd], mean[:hd], atol=1e-6)
+
+
+@pytest.mark.parametrize("H,KVH,window", [(4, 4, None), (4, 2, None), (6, 3, 5)])
+def test_attention_vs_float64(orc, H, KVH, window):
+    rng = np.random.default_rng(H * 10 + KVH)
+    B, S, hd = 2, 23, 16
+    q = rng.normal(size=(B * S, H * hd)).astype(F32)
+    k = rng.normal(size=(B * S, KVH * hd)).astype(F32)
+    v = rng.normal(size=(B * S, KVH * hd)).astype(F32)
+    out = orc.attention(q, k, v, B, S, H, KVH, hd, window=window)
+    w = S if window is None else window
+    ref = np.zeros_like(out, dtype=np.float64)
+    for b in range(B):
+        for h in range(H):
+            kh = h // (H // KVH)
+            Q = q[b * S:(b + 1) * S, h * hd:(h + 1) * hd].astype(np.float64)
+            K = k[b * S:(b + 1) * S, kh * hd:(kh + 1) * hd].astype(np.float64)
+            V = v[b * S:(b + 1) * S, kh * hd:(kh + 1) * hd].astype(np.float64)
+            sc = Q @ K.T / np.sqrt(hd)
+            i, j = np.indices((S, S))
+            sc[(j > i) | (i - j >= w)] = -np.inf
+            p = np.exp(sc - sc.max(axis=1, keepdims=True))
+            p /= p.sum(axis=1, keepdims=True)
+            ref[b * S:(b + 1) * S, h * hd:(h + 1) * hd] = p @ V
+    assert np.max(np.abs(out - ref)) <= 1e-5 * np.max(np.abs(ref))
+
+
 def test_layer_norm_contraction_differs(orc):
     # The FMA build fuses var += d*d and the weight/bias step; on random rows
     # that changes some outputs, and the unfused build is the float32 chain.
