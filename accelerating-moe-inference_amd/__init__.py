@@ -6,10 +6,15 @@ PhiMoE::route, PhiMoE::forward ...).  Arguments are torch tensors on the GPU;
 work is enqueued on torch's current stream.  There is no fallback: if the
 HIP library is missing or fails to load, every call raises.
 
-Load it by path (the directory name is not a Python identifier):
+Load it by path, as a package (the directory name is not a Python
+identifier; decoder.py beside this file is its submodule):
 
     spec = importlib.util.spec_from_file_location(
-        "moe_amd", "accelerating-moe-inference_amd/__init__.py")
+        "moe_amd", "accelerating-moe-inference_amd/__init__.py",
+        submodule_search_locations=["accelerating-moe-inference_amd"])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["moe_amd"] = mod
+    spec.loader.exec_module(mod)
 """
 from __future__ import annotations
 
@@ -371,3 +376,6 @@ def make_desc(T, d, E, k, d_ff, act=ACT_SWIGLU, router=ROUTER_PHI_QUANT,
     return LayerDesc(T=T, d=d, E=E, k=k, d_ff=d_ff, act=act, router=router,
                      quantum=quantum, tie_eps=tie_eps, contract=contract, norm=norm,
                      norm_eps=norm_eps, residual=int(bool(residual)))
+
+
+from .decoder import DecoderConfig, DecoderModel, random_weights  # noqa: E402

@@ -1,0 +1,208 @@
+"""Decoder prefill on the library's kernels: config 5's 4-layer MoE decoder.
+
+The layer is PhiDecoderLayer::forward (src/layer.cu:152-162) with the
+projections of PhiAttention::forward (src/layer.cu:111-143):
+
+    h = x + o_proj(attention(rope(q_proj(n1(x)), k_proj(n1(x))), v_proj(n1(x))))
+    y = h + MoE(n2(h))
+
+and the model is PhiTinyMoEModel::generate (src/model.cu:1575-2059) without
+its prefix trie: embedding gather, the layers over all batch * seq_len rows,
+then the final norm and lm_head on the last row of every sequence only
+(the rows whose logits the model returns).  Every step is one call of the C
+ABI on the current torch stream; nothing here computes on the host.
+
+Norms are RMS norms by default, as config 5 names (n1, n2 and the final
+norm; "layer" selects the reference's layer norm with bias).  The MoE block
+is one moe_layer_forward with the post-attention norm and the residual
+folded in (norm = n2, residual = 1).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+from . import (ACT_SWIGLU, CONTRACT_FMA, NORM_LAYER, NORM_RMS, ROUTER_SOFTMAX_TOPK,
+               make_desc)
+
+
+@dataclass
+class DecoderConfig:
+    """Shape of the decoder; the defaults are config 5."""
+    layers: int = 4
+    d: int = 1024
+    heads: int = 16
+    kv_heads: int = 16
+    head_dim: int = 64
+    experts: int = 8
+    top_k: int = 2
+    d_ff: int = 2816
+    vocab: int = 32000
+    norm: str = "rms"            # "rms" or "layer" (with bias)
+    norm_eps: float = 1e-5
+    rope_theta: float = 10000.0
+    window: int = 0              # sliding window of attention, 0 = unlimited
+    router: int = ROUTER_SOFTMAX_TOPK
+    contract: int = CONTRACT_FMA
+
+    def __post_init__(self):
+        if self.norm not in ("rms", "layer"):
+            raise ValueError(f"norm must be 'rms' or 'layer', not {self.norm!r}")
+        if self.heads * self.head_dim != self.d:
+            raise ValueError("heads * head_dim must equal d")
+        if self.kv_heads < 1 or self.heads % self.kv_heads:
+            raise ValueError("heads must be a multiple of kv_heads")
+
+
+def random_weights(cfg: DecoderConfig, device, seed: int = 0, std: float = 0.02):
+    """Seeded random-init weights of the decoder's shapes (there is no
+    checkpoint): embedding N(0, 1), projections, router, experts and lm_head
+    N(0, std), biases N(0, std), norm weights 1 + N(0, 0.1), norm biases
+    N(0, 0.1).  Names follow the reference's model.bin tensors."""
+    import torch
+    g = torch.Generator(device=device).manual_seed(seed)
+
+    def rn(*shape, scale=std):
+        return torch.randn(shape, device=device, generator=g) * scale
+
+    layer_norm = cfg.norm == "layer"
+    qw, kw = cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
+
+    def norm_params():
+        return 1 + rn(cfg.d, scale=0.1), (rn(cfg.d, scale=0.1) if layer_norm else None)
+
+    W = {"embed": rn(cfg.vocab, cfg.d, scale=1.0), "layers": []}
+    for _ in range(cfg.layers):
+        n1w, n1b = norm_params()
+        n2w, n2b = norm_params()
+        W["layers"].append({
+            "input_norm_w": n1w, "input_norm_b": n1b,
+            "q_w": rn(qw, cfg.d), "q_b": rn(qw),
+            "k_w": rn(kw, cfg.d), "k_b": rn(kw),
+            "v_w": rn(kw, cfg.d), "v_b": rn(kw),
+            "o_w": rn(cfg.d, qw), "o_b": rn(cfg.d),
+            "post_norm_w": n2w, "post_norm_b": n2b,
+            "gate_w": rn(cfg.experts, cfg.d),
+            "w1": rn(cfg.experts, cfg.d_ff, cfg.d),
+            "w3": rn(cfg.experts, cfg.d_ff, cfg.d),
+            "w2": rn(cfg.experts, cfg.d, cfg.d_ff),
+        })
+    W["final_norm_w"], W["final_norm_b"] = norm_params()
+    W["lm_head_w"] = rn(cfg.vocab, cfg.d)
+    W["lm_head_b"] = rn(cfg.vocab)
+    return W
+
+
+class DecoderModel:
+    """The decoder on one Context.  Activation buffers are grow-only and
+    owned here, so repeated calls allocate nothing once warmed up."""
+
+    def __init__(self, ctx, cfg: DecoderConfig, weights: dict):
+        self.ctx, self.cfg, self.W = ctx, cfg, weights
+        self._bufs = {}
+        self._shape = None
+
+    # ---- buffers
+    def _buf(self, name, shape, dtype=None):
+        import torch
+        dtype = dtype or torch.float32
+        n = 1
+        for s in shape:
+            n *= s
+        t = self._bufs.get(name)
+        if t is None or t.numel() < n or t.dtype != dtype:
+            t = torch.empty(max(n, 1), dtype=dtype, device=f"cuda:{self.ctx.device}")
+            self._bufs[name] = t
+        return t[:n].view(*shape)
+
+    def moe_desc(self, rows):
+        c = self.cfg
+        return make_desc(rows, c.d, c.experts, c.top_k, c.d_ff, act=ACT_SWIGLU, router=c.router,
+                         contract=c.contract,
+                         norm=NORM_RMS if c.norm == "rms" else NORM_LAYER,
+                         norm_eps=c.norm_eps, residual=True)
+
+    def reserve(self, batch, seq_len):
+        """Sizes every buffer and the context's workspace for batch x seq_len."""
+        c, T = self.cfg, batch * seq_len
+        for name in ("xa", "xb", "xn", "h"):
+            self._buf(name, (T, c.d))
+        self._buf("q", (T, c.heads * c.head_dim))
+        self._buf("attn", (T, c.heads * c.head_dim))
+        self._buf("k", (T, c.kv_heads * c.head_dim))
+        self._buf("v", (T, c.kv_heads * c.head_dim))
+        self.ctx.reserve(self.moe_desc(T))
+        self.ctx.rope_table(c.rope_theta, c.head_dim, seq_len)
+
+    def _norm(self, x, w, b, y):
+        c = self.cfg
+        if c.norm == "rms":
+            self.ctx.rms_norm(x, w, y=y, eps=c.norm_eps, contract=c.contract)
+        else:
+            self.ctx.layer_norm(x, w, b, y=y, eps=c.norm_eps, contract=c.contract)
+        return y
+
+    # ---- one layer
+    def layer_forward(self, li, x, y, batch, seq_len, topk_idx=None, topk_w=None):
+        """y = decoder layer li applied to x [batch*seq_len, d]."""
+        c, ctx, L = self.cfg, self.ctx, self.W["layers"][li]
+        T = batch * seq_len
+        xn, h = self._buf("xn", (T, c.d)), self._buf("h", (T, c.d))
+        q = self._buf("q", (T, c.heads * c.head_dim))
+        k = self._buf("k", (T, c.kv_heads * c.head_dim))
+        v = self._buf("v", (T, c.kv_heads * c.head_dim))
+        attn = self._buf("attn", (T, c.heads * c.head_dim))
+        self._norm(x, L["input_norm_w"], L["input_norm_b"], xn)
+        ctx.sgemm_nt(xn, L["q_w"], q, bias=L["q_b"])
+        ctx.sgemm_nt(xn, L["k_w"], k, bias=L["k_b"])
+        ctx.sgemm_nt(xn, L["v_w"], v, bias=L["v_b"])
+        ctx.rope(q, k, batch, seq_len, c.heads, c.kv_heads, c.head_dim, c.rope_theta,
+                 table=ctx.rope_table(c.rope_theta, c.head_dim, seq_len))
+        ctx.attention(q, k, v, attn, batch, seq_len, c.heads, c.kv_heads, c.head_dim,
+                      c.window)
+        ctx.sgemm_nt(attn, L["o_w"], h, bias=L["o_b"])
+        ctx.add(h, x)  # h = o_proj(attn) + x, the reference's add_inplace(attn, x)
+        moe = {"gate_w": L["gate_w"], "w1": L["w1"], "w3": L["w3"], "w2": L["w2"],
+               "norm_w": L["post_norm_w"], "norm_b": L["post_norm_b"]}
+        ctx.layer_forward(self.moe_desc(T), moe, h, y, topk_idx, topk_w)
+        return y
+
+    # ---- the model
+    def hidden(self, tokens, routing=None):
+        """The residual stream after the last layer, [batch*seq_len, d].
+        routing: a list that receives each layer's top-k experts [T, k]."""
+        import torch
+        batch, seq_len = tokens.shape
+        T = batch * seq_len
+        tok = tokens.reshape(-1)
+        if tok.dtype != torch.int32 or not tok.is_contiguous():
+            tok = tok.to(torch.int32).contiguous()
+        x, y = self._buf("xa", (T, self.cfg.d)), self._buf("xb", (T, self.cfg.d))
+        self.ctx.embed(self.W["embed"], tok, x)
+        for li in range(self.cfg.layers):
+            idx = None
+            if routing is not None:
+                idx = torch.empty((T, self.cfg.top_k), dtype=torch.int32, device=x.device)
+                routing.append(idx)
+            self.layer_forward(li, x, y, batch, seq_len, topk_idx=idx)
+            x, y = y, x
+        return x
+
+    def generate(self, tokens, logits=None, routing=None):
+        """Logits [batch, vocab] of the last position of every sequence of
+        tokens [batch, seq_len] (int32, on the device)."""
+        import torch
+        batch, seq_len = tokens.shape
+        c = self.cfg
+        x = self.hidden(tokens, routing)
+        last = self._buf("last_idx", (batch,), torch.int32)
+        if self._shape != (batch, seq_len):  # row b * seq_len + seq_len - 1 of each sequence
+            last.copy_(torch.arange(1, batch + 1, dtype=torch.int32) * seq_len - 1)
+            self._shape = (batch, seq_len)
+        xl = self._buf("xl", (batch, c.d))
+        xln = self._buf("xln", (batch, c.d))
+        self.ctx.embed(x, last, xl)  # row gather: the last row of each sequence
+        self._norm(xl, self.W["final_norm_w"], self.W["final_norm_b"], xln)
+        if logits is None:
+            logits = torch.empty((batch, c.vocab), device=x.device)
+        self.ctx.sgemm_nt(xln, self.W["lm_head_w"], logits, bias=self.W["lm_head_b"])
+        return logits

@@ -1,6 +1,9 @@
 """Benchmark of the MoE layer forward on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--config c3|c4] [--cpu-seconds S]
+    python bench.py [--steps K] [--warmup W] [--config c3|c4|c5] [--block]
+                    [--cpu-seconds S]
+    python bench.py --sgemm        (config 2: the SGEMM sweep, a line per shape)
+    python bench.py --decoder      (config 5: the whole 4-layer decoder prefill)
 
 A step is one moe_layer_forward (gate -> route -> permute -> grouped expert
 FFN -> combine) over one batch of synthetic tokens whose inputs and weights
@@ -86,9 +89,11 @@ def sgemm_sweep(args):
 
 
 def load_pkg():
+    pkg_dir = os.path.join(ROOT, "accelerating-moe-inference_amd")
     spec = importlib.util.spec_from_file_location(
-        "moe_amd", os.path.join(ROOT, "accelerating-moe-inference_amd", "__init__.py"))
+        "moe_amd", os.path.join(pkg_dir, "__init__.py"), submodule_search_locations=[pkg_dir])
     mod = importlib.util.module_from_spec(spec)
+    sys.modules["moe_amd"] = mod
     spec.loader.exec_module(mod)
     return mod
 
@@ -188,6 +193,138 @@ def cpu_baseline(x, weights, cfg, pkg_outputs, target_s):
     }, parity
 
 
+def decoder_cpu_baseline(tokens, W, cfg, gpu_hidden, target_s):
+    """The oracle decoder (oracle/decoder.py) on a sample of the batch sized
+    to about target_s seconds of CPU work: a prefix of sequence 0 while one
+    sequence is more than enough, else the first m whole sequences.
+    Attention is causal and sequences are independent, so the sample's rows
+    are exactly those rows of the full prefill."""
+    import numpy as np
+    sys.path.insert(0, ROOT)
+    import oracle
+    from oracle import decoder as od
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
+    oracle.set_threads(threads)
+    B, S = tokens.shape
+    m, n = 1, 16
+    while True:
+        t0 = time.perf_counter()
+        _, x, _ = od.generate(tokens[:m, :n], W, cfg)
+        dt = time.perf_counter() - t0
+        if dt >= 0.5 * target_s or m >= B:
+            break
+        if n < S:
+            n = int(min(S, max(2 * n, 16 * round(0.9 * n * target_s / max(dt, 1e-9) / 16))))
+        else:
+            m = int(min(B, max(m + 1, round(0.9 * m * target_s / max(dt, 1e-9)))))
+    ref = gpu_hidden.reshape(B, S, -1)[:m, :n].reshape(m * n, -1)
+    parity = {"tokens": m * n,
+              "hidden_max_rel_err": float(np.max(np.abs(ref - x)) / (np.max(np.abs(x)) or 1.0))}
+    what = (f"first {n} positions of sequence 0" if m == 1 and n < S
+            else f"the first {m} whole sequences")
+    return {
+        "value": m * n / dt,
+        "unit": "tokens/s",
+        "cores": oracle.get_threads(),
+        "kind": "port",
+        "sample": (f"{what} of {B} x {S} (all {cfg.layers} layers, same weights; causal "
+                   f"attention, so these rows are those of the full prefill), {dt:.1f} s on "
+                   f"{oracle.get_threads()} threads"),
+    }, parity
+
+
+def decoder_bench(args, pkg):
+    """Config 5 as a whole: the 4-layer decoder prefill of 8 x 512 tokens
+    (embedding, per layer RMS norm, q/k/v projections, RoPE, causal
+    attention, o projection + residual, the MoE block with its norm and
+    residual; final norm and lm_head on the last row of every sequence)."""
+    import numpy as np
+    import torch
+
+    B, S = 8, 512
+    cfg = pkg.DecoderConfig()
+    dev = torch.device("cuda:0")
+    W = pkg.random_weights(cfg, dev, seed=0)
+    g = torch.Generator(device="cpu").manual_seed(1)
+    tokens = torch.randint(0, cfg.vocab, (B, S), generator=g, dtype=torch.int32).to(dev)
+    ctx = pkg.Context(0)
+    model = pkg.DecoderModel(ctx, cfg, W)
+    model.reserve(B, S)
+    logits = torch.empty((B, cfg.vocab), device=dev)
+    for _ in range(args.warmup):
+        model.generate(tokens, logits)
+    torch.cuda.synchronize()
+    ctx.reset_timing()
+    ctx.set_timing(True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        model.generate(tokens, logits)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ctx.set_timing(False)
+    kt = ctx.kernel_times()
+    T = B * S
+    per_step = {n: ms / args.steps for n, (ms, _) in kt.items()}
+    avg = {n: ms / c for n, (ms, c) in kt.items()}
+    pairs = T * cfg.top_k
+    flops_w13 = 2.0 * pairs * cfg.d * cfg.d_ff * 2
+    w13_tflops = flops_w13 / (avg["expert_w13_swiglu"] * 1e-3) / 1e12
+    qw, kw = cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
+    proj_flops = cfg.layers * 2.0 * T * cfg.d * (qw + 2 * kw + qw) + 2.0 * B * cfg.d * cfg.vocab
+    # causal attention: S(S+1)/2 (query, key) pairs per sequence and head, 2 products
+    attn_flops = cfg.layers * B * cfg.heads * 2 * (2.0 * cfg.head_dim * S * (S + 1) / 2)
+    moe_flops = cfg.layers * 2.0 * pairs * cfg.d * cfg.d_ff * 3
+    cpu = parity = None
+    if args.cpu_seconds > 0:
+        hidden = model.hidden(tokens).cpu().numpy()
+        Wh = {k: (None if v is None else v.cpu().numpy()) for k, v in W.items() if k != "layers"}
+        Wh["layers"] = [{k: (None if v is None else v.cpu().numpy()) for k, v in L.items()}
+                        for L in W["layers"]]
+        cpu, parity = decoder_cpu_baseline(tokens.cpu().numpy(), Wh, cfg, hidden,
+                                           args.cpu_seconds)
+    ms_per_step = 1e3 * elapsed / args.steps
+    out = {
+        "metric": "decoder prefill tokens/sec (config 5), 1 MI355X",
+        "value": T * args.steps / elapsed,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": ("synthetic (seeded: token ids uniform over the vocabulary, embedding "
+                 "N(0,1), weights N(0,0.02), norm weights 1 + N(0,0.1))"),
+        "config": {"workload": "decoder_prefill_fp32", "batch": B, "seq_len": S,
+                   "layers": cfg.layers, "d_model": cfg.d, "heads": cfg.heads,
+                   "kv_heads": cfg.kv_heads, "experts": cfg.experts, "top_k": cfg.top_k,
+                   "d_ff": cfg.d_ff, "vocab": cfg.vocab, "norm": "rms", "rope_theta":
+                   cfg.rope_theta, "router": "softmax over selected top-k",
+                   "lm_head": "last position of each sequence"},
+        "model_tflops": (proj_flops + attn_flops + moe_flops) / (ms_per_step * 1e-3) / 1e12,
+        "roofline": {
+            "kernel": "expert_w13_swiglu",
+            "bound": "mfma",
+            "achieved": w13_tflops,
+            "peak": FP32_MFMA_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": w13_tflops / FP32_MFMA_PEAK_TFLOPS,
+            "traffic": None,
+            "flops_per_launch": flops_w13,
+        },
+        "kernel_ms_per_step": {n: round(v, 4) for n, v in sorted(per_step.items())},
+        "kernel_avg_ms": {n: round(v, 5) for n, v in sorted(avg.items())},
+        "cpu_baseline": cpu,
+        "cpu_sample_parity": parity,
+    }
+    ctx.close()
+    print(json.dumps(out))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -200,6 +337,8 @@ def main():
                     help="config-2 SGEMM sweep instead of the layer (one JSON line per shape)")
     ap.add_argument("--block", action="store_true",
                     help="the layer as the decoder's MoE block: y = x + MoE(layer_norm(x))")
+    ap.add_argument("--decoder", action="store_true",
+                    help="config 5's whole decoder prefill (8 x 512 tokens, 4 layers)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported "
@@ -208,6 +347,9 @@ def main():
         sys.exit(2)
     if args.sgemm:
         sgemm_sweep(args)
+        return
+    if args.decoder:
+        decoder_bench(args, load_pkg())
         return
 
     import numpy as np

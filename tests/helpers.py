@@ -3,6 +3,7 @@ tolerance rule of the activations."""
 import importlib.util
 import os
 import re
+import sys
 
 import numpy as np
 
@@ -24,8 +25,10 @@ def load_pkg():
     global _pkg
     if _pkg is None:
         spec = importlib.util.spec_from_file_location(
-            "moe_amd", os.path.join(PKG_DIR, "__init__.py"))
+            "moe_amd", os.path.join(PKG_DIR, "__init__.py"),
+            submodule_search_locations=[PKG_DIR])
         mod = importlib.util.module_from_spec(spec)
+        sys.modules["moe_amd"] = mod
         spec.loader.exec_module(mod)
         _pkg = mod
     return _pkg

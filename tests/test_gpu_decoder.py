@@ -146,3 +146,90 @@ def test_embed_gathers_rows_and_zeroes_out_of_range_tokens(ctx, torch):
     ref = table[np.clip(tokens, 0, vocab - 1)]
     ref[[3, 10]] = 0.0
     assert np.array_equal(host(out), ref)
+
+
+# ------------------------------------------------------- the decoder model
+def _host_weights(W):
+    np_ = lambda t: None if t is None else t.detach().cpu().numpy()
+    out = {k: np_(v) for k, v in W.items() if k != "layers"}
+    out["layers"] = [{k: np_(v) for k, v in L.items()} for L in W["layers"]]
+    return out
+
+
+def _topk_margin(orc, h, L, cfg):
+    """The oracle's gate logits of the MoE input h: the gap between the k-th
+    and (k+1)-th largest logit of every row (a near tie flips on 1e-7 noise)."""
+    from oracle import decoder as od
+    logits = orc.matmul_nt(od.norm(h, L["post_norm_w"], L["post_norm_b"], cfg), L["gate_w"],
+                           cfg.contract)
+    s = -np.sort(-logits, axis=1)
+    k = cfg.top_k
+    return (s[:, k - 1] - s[:, k]) if k < s.shape[1] else np.full(len(s), np.inf)
+
+
+def _per_layer_check(ctx, pkg, torch, orc, model, cfg, Wh, trace, x_last, batch, seq_len):
+    """Multi-layer drift: each GPU layer runs on the oracle's input of that
+    layer; routing must match except on rows whose oracle top-k margin is
+    within float noise, and the output within REL_TOL elsewhere."""
+    T = batch * seq_len
+    flips = 0
+    for li, (x, h, idx_ref) in enumerate(trace):
+        y_ref = trace[li + 1][0] if li + 1 < len(trace) else x_last
+        y = torch.empty((T, cfg.d), device="cuda")
+        idx = torch.empty((T, cfg.top_k), dtype=torch.int32, device="cuda")
+        model.layer_forward(li, dev(torch, x), y, batch, seq_len, topk_idx=idx)
+        idx = host(idx)
+        bad = np.any(idx != idx_ref, axis=1)
+        if bad.any():
+            margin = _topk_margin(orc, h, Wh["layers"][li], cfg)
+            scale = float(np.max(np.abs(h)))
+            assert np.all(margin[bad] <= 1e-5 * max(scale, 1.0)), \
+                f"layer {li}: routing differs on rows with clear margins"
+            flips += int(bad.sum())
+        assert_close(host(y)[~bad], y_ref[~bad], what=f"layer {li}")
+    return flips
+
+
+def test_decoder_small_end_to_end_and_per_layer(ctx, pkg, torch, orc):
+    from oracle import decoder as od
+    cfg = pkg.DecoderConfig(layers=2, d=64, heads=4, kv_heads=2, head_dim=16, experts=4,
+                            top_k=2, d_ff=96, vocab=300)
+    W = pkg.random_weights(cfg, "cuda", seed=3)
+    model = pkg.DecoderModel(ctx, cfg, W)
+    B, S = 2, 48
+    tokens = np.random.default_rng(2).integers(0, cfg.vocab, (B, S)).astype(np.int32)
+    model.reserve(B, S)
+    routing = []
+    logits = model.generate(dev(torch, tokens), routing=routing)
+    Wh = _host_weights(W)
+    ref, x_last, trace = od.generate(tokens, Wh, cfg)
+    for li, (_, _, idx_ref) in enumerate(trace):
+        assert np.array_equal(host(routing[li]), idx_ref), f"routing of layer {li}"
+    assert_close(host(logits), ref, what="logits")
+    assert _per_layer_check(ctx, pkg, torch, orc, model, cfg, Wh, trace, x_last, B, S) == 0
+    # a second call on the warmed-up buffers gives the same logits bit for bit
+    again = model.generate(dev(torch, tokens))
+    assert np.array_equal(host(again), host(logits))
+
+
+def test_decoder_config5_one_sequence(ctx, pkg, torch, orc):
+    # config 5's shapes (4 layers, d 1024, 16 heads, 8 SwiGLU experts d_ff
+    # 2816 top-2, vocab 32000) on one of its 8 sequences of 512 tokens: the
+    # oracle covers every layer in seconds
+    from oracle import decoder as od
+    print("decoder config 5, 1 x 512", flush=True)
+    cfg = pkg.DecoderConfig()
+    W = pkg.random_weights(cfg, "cuda", seed=0)
+    model = pkg.DecoderModel(ctx, cfg, W)
+    B, S = 1, 512
+    tokens = np.random.default_rng(5).integers(0, cfg.vocab, (B, S)).astype(np.int32)
+    model.reserve(B, S)
+    routing = []
+    logits = host(model.generate(dev(torch, tokens), routing=routing))
+    Wh = _host_weights(W)
+    ref, x_last, trace = od.generate(tokens, Wh, cfg)
+    flips = _per_layer_check(ctx, pkg, torch, orc, model, cfg, Wh, trace, x_last, B, S)
+    e2e = sum(int(np.any(host(r) != t[2], axis=1).sum()) for r, t in zip(routing, trace))
+    print(f"per-layer flips {flips}, end-to-end routing rows differing {e2e}", flush=True)
+    if e2e == 0:
+        assert_close(logits, ref, what="logits")

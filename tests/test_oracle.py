@@ -503,3 +503,53 @@ def test_moe_forward_vs_float64(orc, act, mode):
     assert np.array_equal(idx, ridx) and np.array_equal(w, rw)
     ref = _f64_layer(x, gw, w1, w3, w2, idx, w, act)
     assert np.max(np.abs(y - ref)) <= 1e-5 * np.max(np.abs(ref))
+
+
+# ---------------------------------------------------- decoder composition
+def _small_decoder(layers=2, seed=0):
+    import torch
+    from helpers import load_pkg
+    pkg = load_pkg()
+    cfg = pkg.DecoderConfig(layers=layers, d=32, heads=4, kv_heads=2, head_dim=8, experts=4,
+                            top_k=2, d_ff=48, vocab=50)
+    W = pkg.random_weights(cfg, "cpu", seed=seed)
+    np_ = lambda t: None if t is None else t.numpy().copy()
+    Wn = {k: np_(v) for k, v in W.items() if k != "layers"}
+    Wn["layers"] = [{k: np_(v) for k, v in L.items()} for L in W["layers"]]
+    return cfg, Wn
+
+
+def test_decoder_layers_are_identities_when_their_weights_are_zero(orc):
+    from oracle import decoder as od
+    cfg, W = _small_decoder()
+    for L in W["layers"]:
+        for name in ("q_w", "k_w", "v_w", "o_w", "q_b", "k_b", "v_b", "o_b", "w1", "w3", "w2"):
+            L[name][...] = 0.0
+    tokens = np.random.default_rng(0).integers(0, cfg.vocab, (2, 5))
+    logits, x, _ = od.generate(tokens, W, cfg)
+    assert np.array_equal(x, W["embed"][tokens.reshape(-1)])
+    last = W["embed"][tokens[:, -1]]
+    ref = od.linear(od.norm(last, W["final_norm_w"], W["final_norm_b"], cfg), W["lm_head_w"],
+                    W["lm_head_b"], cfg.contract)
+    assert np.array_equal(logits, ref)
+    # only o_proj's bias left: every layer adds it once to every row
+    for L in W["layers"]:
+        L["o_b"][...] = 0.25
+    _, x2, _ = od.generate(tokens, W, cfg)
+    assert np.allclose(x2, W["embed"][tokens.reshape(-1)] + 0.25 * cfg.layers, atol=1e-6)
+
+
+def test_decoder_is_causal_and_sequences_are_independent(orc):
+    from oracle import decoder as od
+    cfg, W = _small_decoder()
+    rng = np.random.default_rng(1)
+    B, S = 3, 7
+    tokens = rng.integers(0, cfg.vocab, (B, S))
+    _, x, _ = od.generate(tokens, W, cfg)
+    t2 = tokens.copy()
+    t2[1, 4] = (t2[1, 4] + 1) % cfg.vocab  # sequence 1, position 4
+    _, x2, _ = od.generate(t2, W, cfg)
+    x3, x23 = x.reshape(B, S, -1), x2.reshape(B, S, -1)
+    assert np.array_equal(x3[[0, 2]], x23[[0, 2]])       # other sequences untouched
+    assert np.array_equal(x3[1, :4], x23[1, :4])         # earlier positions untouched
+    assert not np.array_equal(x3[1, 4:], x23[1, 4:])     # the rest sees the change
