@@ -206,3 +206,46 @@ class DecoderModel:
             logits = torch.empty((batch, c.vocab), device=x.device)
         self.ctx.sgemm_nt(xln, self.W["lm_head_w"], logits, bias=self.W["lm_head_b"])
         return logits
+
+
+class CapturedPrefill:
+    """One generate() of a fixed (batch, seq_len) captured in a HIP graph:
+    replay() reruns every kernel of the prefill on `tokens` (update it in
+    place) into `logits` with one launch from the host.
+
+    The capture runs on a Context of its own, so no other call can grow
+    (and free) the workspace the graph's kernels address, and the graph
+    keeps its activation buffers alive.  The library records no memset and
+    makes no host synchronisation inside a step once its workspace is sized
+    (one eager warm-up call does that here)."""
+
+    def __init__(self, model: DecoderModel, batch: int, seq_len: int, warmup: int = 1):
+        import torch
+        from . import Context
+        self.ctx = Context(model.ctx.device)
+        self.model = DecoderModel(self.ctx, model.cfg, model.W)
+        self.model.reserve(batch, seq_len)
+        dev = f"cuda:{model.ctx.device}"
+        self.tokens = torch.zeros((batch, seq_len), dtype=torch.int32, device=dev)
+        self.logits = torch.empty((batch, model.cfg.vocab), device=dev)
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(max(warmup, 1)):
+                self.model.generate(self.tokens, self.logits)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.model.generate(self.tokens, self.logits)
+        torch.cuda.synchronize()
+
+    def replay(self, tokens=None):
+        if tokens is not None:
+            self.tokens.copy_(tokens)
+        self.graph.replay()
+        return self.logits
+
+    def close(self):
+        self.graph = None
+        self.ctx.close()

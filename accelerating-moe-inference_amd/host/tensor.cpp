@@ -165,11 +165,6 @@ void gemm(bool nn, const Tensor& a, const Tensor& b, Tensor& c, const char* what
     dc.download(c.data(), m * n * sizeof(float));
 }
 
-[[noreturn]] void outside(const char* op) {
-    throw std::logic_error(std::string("tensor_ops::") + op +
-                           " is outside the MoE hot path this library implements");
-}
-
 }  // namespace
 
 void matmul(const Tensor& a, const Tensor& b, Tensor& c) { gemm(true, a, b, c, "matmul shape"); }
@@ -194,9 +189,33 @@ void silu(const Tensor& x, Tensor& y) {
     dx.download(y.data(), y.size() * sizeof(float));
 }
 
-void add_inplace(Tensor&, const Tensor&) { outside("add_inplace"); }
-void add_bias_inplace(Tensor&, const Tensor&) { outside("add_bias_inplace"); }
-void softmax_last_dim(const Tensor&, Tensor&) { outside("softmax_last_dim"); }
+// a[i] += b[i] (src/tensor.cu:150-154).
+void add_inplace(Tensor& a, const Tensor& b) {
+    if (a.size() != b.size()) throw std::invalid_argument("add shape");
+    if (a.size() == 0) return;
+    DeviceBuffer da = to_device(a), db = to_device(b);
+    check(moe_add(moe_dropin::context(), da.as<float>(), db.as<float>(),
+                  static_cast<int64_t>(a.size()), nullptr));
+    da.download(a.data(), a.size() * sizeof(float));
+}
+
+// a[i] += bias[i % h] with h = the last dimension (src/tensor.cu:156-161).
+void add_bias_inplace(Tensor& a, const Tensor& bias) {
+    if (bias.ndim() != 1 || a.ndim() == 0 || a.size(a.ndim() - 1) != bias.size(0))
+        throw std::invalid_argument("bias shape");
+    const std::size_t h = bias.size(0);
+    if (a.size() == 0) return;
+    DeviceBuffer da = to_device(a), db = to_device(bias);
+    check(moe_add_bias(moe_dropin::context(), da.as<float>(), db.as<float>(),
+                       static_cast<int64_t>(a.size() / h), static_cast<int64_t>(h), nullptr));
+    da.download(a.data(), a.size() * sizeof(float));
+}
+
+// include/tensor.h:67 of the reference declares it; no source defines it.
+void softmax_last_dim(const Tensor&, Tensor&) {
+    throw std::logic_error(
+        "tensor_ops::softmax_last_dim is declared by the reference but never defined");
+}
 // The post-attention norm in front of the MoE block (src/tensor.cu:175-189):
 // bit-identical to the CPU loop built with FMA contraction, the drop-in's
 // default (PhiMoE's `contract`).
@@ -211,8 +230,30 @@ void layer_norm(const Tensor& x, const Tensor& weight, const Tensor& bias, float
                          MOE_CONTRACT_FMA, dx.as<float>(), nullptr, nullptr, nullptr));
     dx.download(y.data(), y.size() * sizeof(float));
 }
-void apply_rope(Tensor&, Tensor&, std::size_t, std::size_t, std::size_t, std::size_t, float) {
-    outside("apply_rope");
+// src/tensor.cu:191-210 on the GPU: the cos/sin table comes from the same
+// float libm calls (moe_rope_table, on the host), the rotation rounds each
+// product on its own, as the reference's loop does.
+void apply_rope(Tensor& q, Tensor& k, std::size_t seq_len, std::size_t q_heads,
+                std::size_t kv_heads, std::size_t head_dim, float theta) {
+    if (q.ndim() != 2 || k.ndim() != 2) throw std::invalid_argument("apply_rope rank");
+    if (head_dim % 2 != 0 || q.size(1) != q_heads * head_dim ||
+        k.size(1) != kv_heads * head_dim)
+        throw std::invalid_argument("apply_rope shape");
+    if (seq_len == 0 || head_dim == 0) return;
+    if ((q_heads > 0 && seq_len > q.size(0)) || (kv_heads > 0 && seq_len > k.size(0)))
+        throw std::out_of_range("Tensor index");
+    std::vector<float> table(seq_len * head_dim);
+    check(moe_rope_table(theta, static_cast<int64_t>(head_dim), static_cast<int64_t>(seq_len),
+                         table.data()));
+    DeviceBuffer dt(table.size() * sizeof(float));
+    dt.upload(table.data(), table.size() * sizeof(float));
+    DeviceBuffer dq = to_device(q), dk = to_device(k);
+    check(moe_rope(moe_dropin::context(), dq.as<float>(), dk.as<float>(), dt.as<float>(),
+                   static_cast<int64_t>(seq_len), 1, static_cast<int64_t>(seq_len),
+                   static_cast<int64_t>(q_heads), static_cast<int64_t>(kv_heads),
+                   static_cast<int64_t>(head_dim), nullptr));
+    dq.download(q.data(), q.size() * sizeof(float));
+    dk.download(k.data(), k.size() * sizeof(float));
 }
 
 }  // namespace tensor_ops

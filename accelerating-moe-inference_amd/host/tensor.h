@@ -74,11 +74,18 @@ void silu(const Tensor& x, Tensor& y);
 // bit-identical to the reference's CPU loop under FMA contraction.
 void layer_norm(const Tensor& x, const Tensor& weight, const Tensor& bias,
                 float eps, Tensor& y);
-// Outside the MoE hot path this library accelerates: declared for source
-// compatibility with the reference header, they throw std::logic_error.
+// GPU residual and bias adds, bit-identical to the reference's loops.
 void add_inplace(Tensor& a, const Tensor& b);
 void add_bias_inplace(Tensor& a, const Tensor& bias);
+// Declared by the reference's header but never defined there: throws
+// std::logic_error.
 void softmax_last_dim(const Tensor& x, Tensor& y);
+// GPU RoPE on the first seq_len rows of q [rows, q_heads*head_dim] and k
+// [rows, kv_heads*head_dim], cos/sin from the same float libm calls as the
+// reference: bit-identical to its loop (each product rounded on its own).
+// Rows must be exactly heads*head_dim wide and head_dim even
+// (std::invalid_argument otherwise); seq_len past the rows throws
+// std::out_of_range, as the reference's at() does.
 void apply_rope(Tensor& q, Tensor& k, std::size_t seq_len,
                 std::size_t q_heads, std::size_t kv_heads, std::size_t head_dim,
                 float theta);

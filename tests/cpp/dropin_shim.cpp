@@ -158,10 +158,54 @@ int shim_silu_mul(const float* x, const float* u, int64_t n, float* s, float* p)
     });
 }
 
+// Declared by the reference's header, defined nowhere: logic_error.
 int shim_outside_op() {
     return guarded([] {
-        Tensor q({2, 8}), k({2, 8});
-        tensor_ops::apply_rope(q, k, 2, 1, 1, 8, 10000.0f);
+        Tensor x({2, 8}), y({2, 8});
+        tensor_ops::softmax_last_dim(x, y);
+    });
+}
+
+// Shape errors of the adds and RoPE, raised before any device work:
+// 1 add, 2 bias rank, 3 bias width, 4 rope width, 5 rope odd head_dim,
+// 6 rope seq_len past the rows (out_of_range).
+int shim_elementwise_bad_shape(int which) {
+    return guarded([&] {
+        Tensor a({2, 4}), b({3, 4}), bias2({1, 4}), bias3({3});
+        Tensor q({4, 16}), k({4, 8});
+        switch (which) {
+            case 1: tensor_ops::add_inplace(a, b); break;
+            case 2: tensor_ops::add_bias_inplace(a, bias2); break;
+            case 3: tensor_ops::add_bias_inplace(a, bias3); break;
+            case 4: tensor_ops::apply_rope(q, k, 4, 2, 2, 8, 1e4f); break;
+            case 5: tensor_ops::apply_rope(q, k, 4, 2, 1, 8 + 1, 1e4f); break;
+            case 6: tensor_ops::apply_rope(q, k, 5, 2, 1, 8, 1e4f); break;
+        }
+    });
+}
+
+// a += b, then a += bias (rows x cols), through tensor_ops.
+int shim_add_and_bias(const float* a, const float* b, const float* bias, int64_t rows,
+                      int64_t cols, float* out) {
+    return guarded([&] {
+        Tensor A = make(a, {size_t(rows), size_t(cols)}), B = make(b, {size_t(rows), size_t(cols)}),
+               Bias = make(bias, {size_t(cols)});
+        tensor_ops::add_inplace(A, B);
+        tensor_ops::add_bias_inplace(A, Bias);
+        std::memcpy(out, A.data(), rows * cols * sizeof(float));
+    });
+}
+
+// tensor_ops::apply_rope on q [rows, q_heads*hd], k [rows, kv_heads*hd].
+int shim_rope(float* q, float* k, int64_t rows, int64_t seq_len, int64_t q_heads,
+              int64_t kv_heads, int64_t hd, float theta) {
+    return guarded([&] {
+        Tensor Q = make(q, {size_t(rows), size_t(q_heads * hd)}),
+               K = make(k, {size_t(rows), size_t(kv_heads * hd)});
+        tensor_ops::apply_rope(Q, K, size_t(seq_len), size_t(q_heads), size_t(kv_heads),
+                               size_t(hd), theta);
+        std::memcpy(q, Q.data(), Q.size() * sizeof(float));
+        std::memcpy(k, K.data(), K.size() * sizeof(float));
     });
 }
 

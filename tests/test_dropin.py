@@ -110,7 +110,13 @@ def test_shape_errors_before_any_device_work(shim):
     assert shim.shim_matmul_bad_shape() == INVALID
     assert err(shim) == "matmul_transposed shape"
     assert shim.shim_outside_op() == LOGIC
-    assert "outside the MoE hot path" in err(shim)
+    assert "never defined" in err(shim)
+    want = {1: (INVALID, "add shape"), 2: (INVALID, "bias shape"), 3: (INVALID, "bias shape"),
+            4: (INVALID, "apply_rope shape"), 5: (INVALID, "apply_rope shape"),
+            6: (OUT_OF_RANGE, "Tensor index")}
+    for which, (code, msg) in want.items():
+        assert shim.shim_elementwise_bad_shape(which) == code, which
+        assert err(shim) == msg
     assert shim.shim_layer_norm_bad_shape() == INVALID
     assert err(shim) == "layer norm shape"
 
@@ -217,3 +223,25 @@ def test_moe_missing_expert_raises(shim, tmp_path):
     I = ctypes.c_int64
     rc = shim.shim_moe(path.encode(), I(0), 1, fptr(x), I(4), I(8), fptr(y), fptr(topk))
     assert rc == RUNTIME and err(shim) == f"missing tensor: {base}.experts.1.w1.weight"
+
+
+@pytest.mark.gpu
+def test_add_bias_and_rope_bit_exact(shim, orc):
+    rng = np.random.default_rng(6)
+    I = ctypes.c_int64
+    rows, cols = 33, 40
+    a, b = normal(rng, (rows, cols)), normal(rng, (rows, cols))
+    bias = normal(rng, (cols,))
+    out = np.empty_like(a)
+    assert shim.shim_add_and_bias(fptr(a), fptr(b), fptr(bias), I(rows), I(cols),
+                                  fptr(out)) == 0, err(shim)
+    assert np.array_equal(out, (a + b) + bias[None, :])
+    # rows past seq_len stay as they are, as in the reference's loop over s < seq_len
+    rows, S, H, KVH, hd = 12, 9, 4, 2, 16
+    q, k = normal(rng, (rows, H * hd)), normal(rng, (rows, KVH * hd))
+    gq, gk = q.copy(), k.copy()
+    assert shim.shim_rope(fptr(gq), fptr(gk), I(rows), I(S), I(H), I(KVH), I(hd),
+                          ctypes.c_float(10000.0)) == 0, err(shim)
+    rq, rk = orc.rope(q[:S], k[:S], 1, S, H, KVH, hd)
+    assert np.array_equal(gq[:S], rq) and np.array_equal(gk[:S], rk)
+    assert np.array_equal(gq[S:], q[S:]) and np.array_equal(gk[S:], k[S:])

@@ -233,3 +233,29 @@ def test_decoder_config5_one_sequence(ctx, pkg, torch, orc):
     print(f"per-layer flips {flips}, end-to-end routing rows differing {e2e}", flush=True)
     if e2e == 0:
         assert_close(logits, ref, what="logits")
+
+
+def test_captured_prefill_replays_match_eager(ctx, pkg, torch):
+    # several replays with eager work and synchronisations between them,
+    # each against the eager result; new tokens written in place between
+    cfg = pkg.DecoderConfig(layers=2, d=64, heads=4, kv_heads=4, head_dim=16, experts=4,
+                            top_k=2, d_ff=96, vocab=300)
+    W = pkg.random_weights(cfg, "cuda", seed=8)
+    model = pkg.DecoderModel(ctx, cfg, W)
+    B, S = 2, 32
+    rng = np.random.default_rng(9)
+    toks = [dev(torch, rng.integers(0, cfg.vocab, (B, S)).astype(np.int32)) for _ in range(3)]
+    eager = [host(model.generate(t)) for t in toks]
+    from moe_amd.decoder import CapturedPrefill
+    cap = CapturedPrefill(model, B, S)
+    try:
+        for rep in range(6):
+            i = rep % 3
+            got = host(cap.replay(toks[i]))
+            assert np.array_equal(got, eager[i]), f"replay {rep}"
+            # eager work on the shared model's context between replays
+            other = host(model.generate(toks[(i + 1) % 3]))
+            assert np.array_equal(other, eager[(i + 1) % 3])
+            torch.cuda.synchronize()
+    finally:
+        cap.close()
