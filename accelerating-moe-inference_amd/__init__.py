@@ -34,7 +34,8 @@ EXPORTS = (
     "moe_ctx_create", "moe_ctx_destroy", "moe_ctx_reserve", "moe_ctx_set_timing",
     "moe_ctx_kernel_times", "moe_ctx_reset_timing", "moe_last_error",
     "moe_version", "moe_sgemm_nt", "moe_sgemm_nn", "moe_silu", "moe_mul",
-    "moe_layer_norm", "moe_rms_norm", "moe_rope_table", "moe_rope", "moe_attention", "moe_add",
+    "moe_layer_norm", "moe_rms_norm", "moe_rope_table", "moe_rope", "moe_attention",
+    "moe_attention_last", "moe_add",
     "moe_add_bias", "moe_embed", "moe_gate_logits",
     "moe_route", "moe_permute", "moe_expert_ffn_grouped", "moe_combine",
     "moe_layer_forward", "moe_layer_w2_splits",
@@ -99,7 +100,8 @@ def load_library(path: str = LIB_PATH):
         "moe_layer_norm": ([P, P, P, P, F, I64, I64, I, P, P, P, P], I),
         "moe_rms_norm": ([P, P, P, F, I64, I64, I, P, P, P], I),
         "moe_rope_table": ([F, I64, I64, P], I),
-        "moe_rope": ([P, P, P, P, I64, I64, I64, I64, I64, I64, P], I),
+        "moe_rope": ([P, P, P, P, I64, I64, I64, I64, I64, I64, I64, P], I),
+        "moe_attention_last": ([P, P, P, P, P, I64, I64, I64, I64, I64, I64, P], I),
         "moe_attention": ([P, P, P, P, P, I64, I64, I64, I64, I64, I64, P], I),
         "moe_add": ([P, P, P, I64, P], I),
         "moe_add_bias": ([P, P, P, I64, I64, P], I),
@@ -266,13 +268,14 @@ class Context:
         return t
 
     def rope(self, q, k, batch, seq_len, q_heads, kv_heads, head_dim, theta=10000.0,
-             table=None):
-        """RoPE in place on q [B*S, Hq*hd] and k [B*S, Hkv*hd]."""
+             table=None, first_pos=0):
+        """RoPE in place on q [B*S, Hq*hd] and k [B*S, Hkv*hd]; row r at
+        position first_pos + r % seq_len."""
         if table is None:
-            table = self.rope_table(theta, head_dim, seq_len)
+            table = self.rope_table(theta, head_dim, first_pos + seq_len)
         positions = table.numel() // head_dim if head_dim else 0
         _check(_lib.moe_rope(self.handle, _f32(q, "q"), _f32(k, "k"), _f32(table, "table"),
-                             positions, batch, seq_len, q_heads, kv_heads, head_dim,
+                             positions, batch, seq_len, first_pos, q_heads, kv_heads, head_dim,
                              _stream()))
 
     def attention(self, q, k, v, out, batch, seq_len, q_heads, kv_heads, head_dim, window=0):
@@ -280,6 +283,15 @@ class Context:
         _check(_lib.moe_attention(self.handle, _f32(q, "q"), _f32(k, "k"), _f32(v, "v"),
                                   _f32(out, "out"), batch, seq_len, q_heads, kv_heads,
                                   head_dim, window, _stream()))
+        return out
+
+    def attention_last(self, q, k, v, out, batch, seq_len, q_heads, kv_heads, head_dim,
+                       window=0):
+        """Attention of the last position of each sequence: q and out
+        [batch, Hq*hd], k and v [batch*seq_len, Hkv*hd]."""
+        _check(_lib.moe_attention_last(self.handle, _f32(q, "q"), _f32(k, "k"), _f32(v, "v"),
+                                       _f32(out, "out"), batch, seq_len, q_heads, kv_heads,
+                                       head_dim, window, _stream()))
         return out
 
     def add(self, a, b):

@@ -15,11 +15,13 @@ namespace {
 // reference's GPU path does, src/model.cu:1784-1798 and rope_rows
 // :1046-1083): pair (j, j + half) of every head becomes (x0 c - x1 s,
 // x1 c + x0 s), each product rounded on its own (this file is built without
-// contraction).  One thread per pair; row r is at position r % seq_len.
+// contraction).  One thread per pair; row r is at position
+// first_pos + r % seq_len.
 __global__ __launch_bounds__(256) void rope_kernel(float* __restrict__ q, float* __restrict__ k,
                                                    const float* __restrict__ table, int64_t rows,
-                                                   int64_t seq_len, int64_t q_heads,
-                                                   int64_t kv_heads, int64_t head_dim) {
+                                                   int64_t seq_len, int64_t first_pos,
+                                                   int64_t q_heads, int64_t kv_heads,
+                                                   int64_t head_dim) {
     const int64_t half = head_dim / 2, heads = q_heads + kv_heads;
     const int64_t n = rows * heads * half;
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
@@ -28,7 +30,7 @@ __global__ __launch_bounds__(256) void rope_kernel(float* __restrict__ q, float*
         const int64_t j = i % half, hh = (i / half) % heads, r = i / (half * heads);
         float* x = hh < q_heads ? q + r * q_heads * head_dim + hh * head_dim
                                 : k + r * kv_heads * head_dim + (hh - q_heads) * head_dim;
-        const float* trig = table + ((r % seq_len) * half + j) * 2;
+        const float* trig = table + ((first_pos + r % seq_len) * half + j) * 2;
         const float c = trig[0], sn = trig[1];
         const float x0 = x[j], x1 = x[j + half];
         x[j] = x0 * c - x1 * sn;
@@ -73,6 +75,75 @@ __global__ __launch_bounds__(256) void attn_softmax_kernel(float* __restrict__ s
     }
 }
 
+// Attention of the last position of every sequence (the rows the model's
+// logits read): one workgroup per (sequence b, query head h), q row b of
+// [batch, q_heads*hd] against keys [lo, S) of sequence b, lo = S - window
+// (window > 0) or 0.  Every sum runs in the oracle's order -- the score's
+// d-ascending chain per thread, the denominator ki-ascending on one thread,
+// each output value ki-ascending on its own thread -- so given the same
+// inputs the result is bit-identical to the reference's loop
+// (src/layer.cu:117-140).  The row's scores live in LDS when they fit
+// (LDS_ROW: S <= kAttnLastLds), else in `scores` (batch*q_heads*S floats).
+constexpr int kAttnLastLds = 8192;
+template <bool VEC4, bool LDS_ROW>
+__global__ __launch_bounds__(256) void attn_last_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    float* __restrict__ out, float* __restrict__ scores, int64_t S, int64_t H, int64_t KVH,
+    int64_t hd, int64_t window, float scale) {
+    __shared__ float red[4];
+    __shared__ float row[LDS_ROW ? kAttnLastLds : 1];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t b = blockIdx.x / H, h = blockIdx.x % H, kh = h / (H / KVH);
+    const int64_t kw = KVH * hd;
+    const float* qr = q + b * H * hd + h * hd;
+    const float* kb = k + b * S * kw + kh * hd;
+    const float* vb = v + b * S * kw + kh * hd;
+    float* sc = LDS_ROW ? row : scores + static_cast<int64_t>(blockIdx.x) * S;
+    const int64_t lo = window > 0 && S > window ? S - window : 0;
+    float m = -INFINITY;
+    for (int64_t ki = lo + tid; ki < S; ki += blockDim.x) {
+        const float* kr = kb + ki * kw;
+        float acc = 0.0f;
+        if (VEC4) {
+            for (int64_t d = 0; d < hd; d += 4) {
+                const float4 a = *reinterpret_cast<const float4*>(qr + d);
+                const float4 c = *reinterpret_cast<const float4*>(kr + d);
+                acc += a.x * c.x;
+                acc += a.y * c.y;
+                acc += a.z * c.z;
+                acc += a.w * c.w;
+            }
+        } else {
+            for (int64_t d = 0; d < hd; ++d) acc += qr[d] * kr[d];
+        }
+        const float sv = acc / scale;
+        sc[ki] = sv;
+        m = fmaxf(m, sv);
+    }
+    m = wave_max(m);
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (int64_t ki = lo + tid; ki < S; ki += blockDim.x)
+        sc[ki] = static_cast<float>(exp(static_cast<double>(sc[ki] - m)));
+    __syncthreads();  // the weights of every thread, before the ordered sum
+    if (tid == 0) {
+        float den = 0.0f;
+#pragma unroll 8
+        for (int64_t ki = lo; ki < S; ++ki) den += sc[ki];
+        red[0] = den;
+    }
+    __syncthreads();
+    const float den = red[0];
+    float* o = out + b * H * hd + h * hd;
+    for (int64_t d = tid; d < hd; d += blockDim.x) {
+        float value = 0.0f;
+#pragma unroll 8
+        for (int64_t ki = lo; ki < S; ++ki) value += sc[ki] / den * vb[ki * kw + d];
+        o[d] = value;
+    }
+}
+
 __global__ __launch_bounds__(256) void add_kernel(float* __restrict__ a, const float* __restrict__ b,
                                                   int64_t n) {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
@@ -113,11 +184,31 @@ unsigned grid_for(int64_t n) {
 }  // namespace
 
 void launch_rope(float* q, float* k, const float* table, int64_t rows, int64_t seq_len,
-                 int64_t q_heads, int64_t kv_heads, int64_t head_dim, hipStream_t s) {
+                 int64_t first_pos, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                 hipStream_t s) {
     const int64_t n = rows * (q_heads + kv_heads) * (head_dim / 2);
     if (n <= 0) return;
     hipLaunchKernelGGL(rope_kernel, dim3(grid_for(n)), dim3(256), 0, s, q, k, table, rows,
-                       seq_len, q_heads, kv_heads, head_dim);
+                       seq_len, first_pos, q_heads, kv_heads, head_dim);
+}
+
+void launch_attn_last(const float* q, const float* k, const float* v, float* out, float* scores,
+                      int64_t batch, int64_t seq_len, int64_t q_heads, int64_t kv_heads,
+                      int64_t head_dim, int64_t window, hipStream_t s) {
+    const int64_t blocks = batch * q_heads;
+    if (blocks <= 0 || seq_len <= 0) return;
+    const float scale = sqrtf(static_cast<float>(head_dim));
+    const bool vec4 = head_dim % 4 == 0 && reinterpret_cast<uintptr_t>(q) % 16 == 0 &&
+                      reinterpret_cast<uintptr_t>(k) % 16 == 0;
+    auto go = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, q, k, v,
+                           out, scores, seq_len, q_heads, kv_heads, head_dim, window, scale);
+    };
+    const bool lds = seq_len <= kAttnLastLds;
+    if (vec4 && lds) go(attn_last_kernel<true, true>);
+    else if (vec4) go(attn_last_kernel<true, false>);
+    else if (lds) go(attn_last_kernel<false, true>);
+    else go(attn_last_kernel<false, false>);
 }
 
 void launch_attn_softmax(float* scores, int64_t batches, int64_t seq_len, int64_t head_dim,

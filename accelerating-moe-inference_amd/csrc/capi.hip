@@ -608,8 +608,8 @@ int moe_rope_table(float theta, int64_t head_dim, int64_t positions, float* tabl
 }
 
 int moe_rope(moe_ctx* ctx, float* q, float* k, const float* table, int64_t table_positions,
-             int64_t batch, int64_t seq_len, int64_t q_heads, int64_t kv_heads,
-             int64_t head_dim, void* stream) {
+             int64_t batch, int64_t seq_len, int64_t first_pos, int64_t q_heads,
+             int64_t kv_heads, int64_t head_dim, void* stream) {
     return guarded([&] {
         check_ctx(ctx);
         check_dims(batch, "batch");
@@ -618,14 +618,17 @@ int moe_rope(moe_ctx* ctx, float* q, float* k, const float* table, int64_t table
         moe::require(head_dim > 0 && head_dim % 2 == 0, "head_dim must be even and > 0");
         const int64_t rows = batch * seq_len;
         if (rows == 0 || q_heads + kv_heads == 0) return;
-        moe::require(table_positions >= seq_len, "the rope table needs seq_len positions");
+        moe::require(first_pos >= 0, "first_pos must be >= 0");
+        moe::require(table_positions >= first_pos + seq_len,
+                     "the rope table needs first_pos + seq_len positions");
         check_ptr(table, "table");
         if (q_heads > 0) check_ptr(q, "q");
         if (kv_heads > 0) check_ptr(k, "k");
         DeviceScope dev(ctx->device);
         hipStream_t s = as_stream(stream);
         ctx->launch("rope", s, [&] {
-            moe::launch_rope(q, k, table, rows, seq_len, q_heads, kv_heads, head_dim, s);
+            moe::launch_rope(q, k, table, rows, seq_len, first_pos, q_heads, kv_heads, head_dim,
+                             s);
         });
     });
 }
@@ -705,6 +708,33 @@ int moe_attention(moe_ctx* ctx, const float* q, const float* k, const float* v, 
         b.window = static_cast<int32_t>(w);
         ctx->launch("attn_pv", s,
                     [&] { moe::launch_gemm_batched(b, true, static_cast<int>(zb), s); });
+    });
+}
+
+int moe_attention_last(moe_ctx* ctx, const float* q, const float* k, const float* v, float* out,
+                       int64_t batch, int64_t seq_len, int64_t q_heads, int64_t kv_heads,
+                       int64_t head_dim, int64_t window, void* stream) {
+    return guarded([&] {
+        check_ctx(ctx);
+        check_dims(batch, "batch");
+        check_dims(seq_len, "seq_len");
+        moe::require(kv_heads >= 1 && q_heads >= kv_heads && q_heads % kv_heads == 0,
+                     "q_heads must be a positive multiple of kv_heads");
+        moe::require(head_dim > 0, "head_dim must be > 0");
+        moe::require(window >= 0, "window must be >= 0 (0 = unlimited)");
+        if (batch == 0 || seq_len == 0) return;
+        check_ptr(q, "q");
+        check_ptr(k, "k");
+        check_ptr(v, "v");
+        check_ptr(out, "out");
+        DeviceScope dev(ctx->device);
+        hipStream_t s = as_stream(stream);
+        float* scores =
+            static_cast<float*>(ctx->workspace(size_t(batch * q_heads * seq_len) * sizeof(float)));
+        ctx->launch("attn_last", s, [&] {
+            moe::launch_attn_last(q, k, v, out, scores, batch, seq_len, q_heads, kv_heads,
+                                  head_dim, window, s);
+        });
     });
 }
 

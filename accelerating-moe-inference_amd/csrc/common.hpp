@@ -118,7 +118,14 @@ void launch_gemm_batched(const GemmArgs& a, bool nn, int batches, hipStream_t s)
 // the masked softmax of a [batches, S, S] score block in place (scores scaled
 // by 1/sqrt(hd), keys ki <= qi and qi - ki < window visible, the rest set to 0).
 void launch_rope(float* q, float* k, const float* table, int64_t rows, int64_t seq_len,
-                 int64_t q_heads, int64_t kv_heads, int64_t head_dim, hipStream_t s);
+                 int64_t first_pos, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                 hipStream_t s);
+// Attention of the last position of each sequence: q [batch, q_heads*hd]
+// (one row per sequence) against k, v [batch*seq_len, kv_heads*hd];
+// scores: batch*q_heads*seq_len floats of workspace.
+void launch_attn_last(const float* q, const float* k, const float* v, float* out, float* scores,
+                      int64_t batch, int64_t seq_len, int64_t q_heads, int64_t kv_heads,
+                      int64_t head_dim, int64_t window, hipStream_t s);
 void launch_attn_softmax(float* scores, int64_t batches, int64_t seq_len, int64_t head_dim,
                          int64_t window, hipStream_t s);
 // a[i] += b[i];  a[r, c] += bias[c];  out[i, :] = table[tokens[i], :]

@@ -94,10 +94,16 @@ def random_weights(cfg: DecoderConfig, device, seed: int = 0, std: float = 0.02)
 
 class DecoderModel:
     """The decoder on one Context.  Activation buffers are grow-only and
-    owned here, so repeated calls allocate nothing once warmed up."""
+    owned here, so repeated calls allocate nothing once warmed up.
 
-    def __init__(self, ctx, cfg: DecoderConfig, weights: dict):
+    prune_last: generate() runs the last layer's q projection, attention,
+    o projection and MoE block on the last row of every sequence only --
+    the rows the logits read -- while its norm, k and v still cover every
+    row (the reference's last-layer pruning, src/model.cu:1889-1960)."""
+
+    def __init__(self, ctx, cfg: DecoderConfig, weights: dict, prune_last: bool = True):
         self.ctx, self.cfg, self.W = ctx, cfg, weights
+        self.prune_last = prune_last
         self._bufs = {}
         self._shape = None
 
@@ -132,6 +138,7 @@ class DecoderModel:
         self._buf("v", (T, c.kv_heads * c.head_dim))
         self.ctx.reserve(self.moe_desc(T))
         self.ctx.rope_table(c.rope_theta, c.head_dim, seq_len)
+        self._last_rows(batch, seq_len)
 
     def _norm(self, x, w, b, y):
         c = self.cfg
@@ -166,10 +173,51 @@ class DecoderModel:
         ctx.layer_forward(self.moe_desc(T), moe, h, y, topk_idx, topk_w)
         return y
 
+    def _last_rows(self, batch, seq_len):
+        """Row indices b * seq_len + seq_len - 1 of the last position of every
+        sequence, on the device (rebuilt when the shape changes)."""
+        import torch
+        last = self._buf("last_idx", (batch,), torch.int32)
+        if self._shape != (batch, seq_len):
+            last.copy_(torch.arange(1, batch + 1, dtype=torch.int32) * seq_len - 1)
+            self._shape = (batch, seq_len)
+        return last
+
+    def last_layer_tail(self, li, x, y_last, batch, seq_len, topk_idx=None):
+        """Layer li on the last rows only: y_last [batch, d] = the layer's
+        output rows b * seq_len + seq_len - 1 of x [batch*seq_len, d]."""
+        c, ctx, L = self.cfg, self.ctx, self.W["layers"][li]
+        T = batch * seq_len
+        qw, kw = c.heads * c.head_dim, c.kv_heads * c.head_dim
+        xn = self._buf("xn", (T, c.d))
+        k, v = self._buf("k", (T, kw)), self._buf("v", (T, kw))
+        last = self._last_rows(batch, seq_len)
+        xn_l, x_l = self._buf("tail_xn", (batch, c.d)), self._buf("tail_x", (batch, c.d))
+        q_l, a_l = self._buf("tail_q", (batch, qw)), self._buf("tail_attn", (batch, qw))
+        h_l = self._buf("tail_h", (batch, c.d))
+        self._norm(x, L["input_norm_w"], L["input_norm_b"], xn)
+        ctx.sgemm_nt(xn, L["k_w"], k, bias=L["k_b"])
+        ctx.sgemm_nt(xn, L["v_w"], v, bias=L["v_b"])
+        ctx.embed(xn, last, xn_l)  # row gathers of the last rows
+        ctx.embed(x, last, x_l)
+        ctx.sgemm_nt(xn_l, L["q_w"], q_l, bias=L["q_b"])
+        table = ctx.rope_table(c.rope_theta, c.head_dim, seq_len)
+        ctx.rope(None, k, batch, seq_len, 0, c.kv_heads, c.head_dim, table=table)
+        ctx.rope(q_l, None, batch, 1, c.heads, 0, c.head_dim, table=table, first_pos=seq_len - 1)
+        ctx.attention_last(q_l, k, v, a_l, batch, seq_len, c.heads, c.kv_heads, c.head_dim,
+                           c.window)
+        ctx.sgemm_nt(a_l, L["o_w"], h_l, bias=L["o_b"])
+        ctx.add(h_l, x_l)
+        moe = {"gate_w": L["gate_w"], "w1": L["w1"], "w3": L["w3"], "w2": L["w2"],
+               "norm_w": L["post_norm_w"], "norm_b": L["post_norm_b"]}
+        ctx.layer_forward(self.moe_desc(batch), moe, h_l, y_last, topk_idx)
+        return y_last
+
     # ---- the model
-    def hidden(self, tokens, routing=None):
-        """The residual stream after the last layer, [batch*seq_len, d].
-        routing: a list that receives each layer's top-k experts [T, k]."""
+    def hidden(self, tokens, routing=None, layers=None):
+        """The residual stream after the first `layers` layers (all by
+        default), [batch*seq_len, d].  routing: a list that receives each
+        layer's top-k experts [T, k]."""
         import torch
         batch, seq_len = tokens.shape
         T = batch * seq_len
@@ -178,7 +226,7 @@ class DecoderModel:
             tok = tok.to(torch.int32).contiguous()
         x, y = self._buf("xa", (T, self.cfg.d)), self._buf("xb", (T, self.cfg.d))
         self.ctx.embed(self.W["embed"], tok, x)
-        for li in range(self.cfg.layers):
+        for li in range(self.cfg.layers if layers is None else layers):
             idx = None
             if routing is not None:
                 idx = torch.empty((T, self.cfg.top_k), dtype=torch.int32, device=x.device)
@@ -189,18 +237,23 @@ class DecoderModel:
 
     def generate(self, tokens, logits=None, routing=None):
         """Logits [batch, vocab] of the last position of every sequence of
-        tokens [batch, seq_len] (int32, on the device)."""
+        tokens [batch, seq_len] (int32, on the device).  routing receives
+        each layer's top-k experts (the pruned last layer's: [batch, k])."""
         import torch
         batch, seq_len = tokens.shape
         c = self.cfg
-        x = self.hidden(tokens, routing)
-        last = self._buf("last_idx", (batch,), torch.int32)
-        if self._shape != (batch, seq_len):  # row b * seq_len + seq_len - 1 of each sequence
-            last.copy_(torch.arange(1, batch + 1, dtype=torch.int32) * seq_len - 1)
-            self._shape = (batch, seq_len)
         xl = self._buf("xl", (batch, c.d))
         xln = self._buf("xln", (batch, c.d))
-        self.ctx.embed(x, last, xl)  # row gather: the last row of each sequence
+        if self.prune_last and c.layers > 0:
+            x = self.hidden(tokens, routing, layers=c.layers - 1)
+            idx = None
+            if routing is not None:
+                idx = torch.empty((batch, c.top_k), dtype=torch.int32, device=x.device)
+                routing.append(idx)
+            self.last_layer_tail(c.layers - 1, x, xl, batch, seq_len, topk_idx=idx)
+        else:
+            x = self.hidden(tokens, routing)
+            self.ctx.embed(x, self._last_rows(batch, seq_len), xl)  # the last rows
         self._norm(xl, self.W["final_norm_w"], self.W["final_norm_b"], xln)
         if logits is None:
             logits = torch.empty((batch, c.vocab), device=x.device)
@@ -223,7 +276,7 @@ class CapturedPrefill:
         import torch
         from . import Context
         self.ctx = Context(model.ctx.device)
-        self.model = DecoderModel(self.ctx, model.cfg, model.W)
+        self.model = DecoderModel(self.ctx, model.cfg, model.W, prune_last=model.prune_last)
         self.model.reserve(batch, seq_len)
         dev = f"cuda:{model.ctx.device}"
         self.tokens = torch.zeros((batch, seq_len), dtype=torch.int32, device=dev)

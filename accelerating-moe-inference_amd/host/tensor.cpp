@@ -249,7 +249,7 @@ void apply_rope(Tensor& q, Tensor& k, std::size_t seq_len, std::size_t q_heads,
     dt.upload(table.data(), table.size() * sizeof(float));
     DeviceBuffer dq = to_device(q), dk = to_device(k);
     check(moe_rope(moe_dropin::context(), dq.as<float>(), dk.as<float>(), dt.as<float>(),
-                   static_cast<int64_t>(seq_len), 1, static_cast<int64_t>(seq_len),
+                   static_cast<int64_t>(seq_len), 1, static_cast<int64_t>(seq_len), 0,
                    static_cast<int64_t>(q_heads), static_cast<int64_t>(kv_heads),
                    static_cast<int64_t>(head_dim), nullptr));
     dq.download(q.data(), q.size() * sizeof(float));

@@ -31,6 +31,7 @@
  *                       rope_rows                          src/model.cu:1046-1083
  *   moe_attention       PhiAttention::forward, after the projections  src/layer.cu:111-143;
  *                       attention_heads                    src/model.cu:1161-1283
+ *   moe_attention_last  attention_heads<true> of the pruned last layer  src/model.cu:1889-1960
  *   moe_add             tensor_ops::add_inplace            src/tensor.cu:150-154
  *   moe_add_bias        tensor_ops::add_bias_inplace       src/tensor.cu:156-161
  *   moe_embed           embedding row gather (gather_rows) src/model.cu:674-693,1878-1885
@@ -178,7 +179,9 @@ int moe_rms_norm(moe_ctx* ctx, const float* x, const float* weight, float eps,
  *   positions * head_dim floats.  Copy it to the device for moe_rope.
  * moe_rope: RoPE in place on q [batch*seq_len, q_heads*head_dim] and k
  *   [batch*seq_len, kv_heads*head_dim] with a device copy of that table
- *   (table_positions >= seq_len rows); row r is at position r % seq_len;
+ *   (table_positions >= first_pos + seq_len rows); row r is at position
+ *   first_pos + r % seq_len (first_pos = seq_len - 1 with seq_len 1 rotates
+ *   one row per sequence at its last position, as rope_rows<2> does);
  *   pair (x0, x1) = (x[j], x[j + head_dim/2]) of each head becomes
  *   (x0*c - x1*s, x1*c + x0*s), each product rounded on its own:
  *   bit-identical to tensor_ops::apply_rope and rope_rows
@@ -190,16 +193,27 @@ int moe_rms_norm(moe_ctx* ctx, const float* x, const float* weight, float eps,
  *   Needs head_dim and seq_len multiples of 16 and 16-byte aligned buffers
  *   (MOE_ERR_UNSUPPORTED otherwise); uses batch*q_heads*seq_len^2 floats of
  *   workspace.
+ * moe_attention_last: the same attention for the last position of every
+ *   sequence only (the rows the model's logits read): q [batch,
+ *   q_heads*head_dim], one row per sequence, against k, v [batch*seq_len,
+ *   kv_heads*head_dim]; out [batch, q_heads*head_dim].  Every sum runs in
+ *   the reference loop's order, so it is bit-identical to that loop given
+ *   the same q, k, v.  Any head_dim and seq_len; batch*q_heads*seq_len
+ *   floats of workspace.
  * moe_add: a += b elementwise.  moe_add_bias: a[r, c] += bias[c].
  * moe_embed: out[i, :] = table[tokens[i], :] (table [vocab, d]); a token
  *   outside [0, vocab) gives a zero row. */
 int moe_rope_table(float theta, int64_t head_dim, int64_t positions, float* table);
 int moe_rope(moe_ctx* ctx, float* q, float* k, const float* table,
              int64_t table_positions, int64_t batch, int64_t seq_len,
-             int64_t q_heads, int64_t kv_heads, int64_t head_dim, void* stream);
+             int64_t first_pos, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+             void* stream);
 int moe_attention(moe_ctx* ctx, const float* q, const float* k, const float* v,
                   float* out, int64_t batch, int64_t seq_len, int64_t q_heads,
                   int64_t kv_heads, int64_t head_dim, int64_t window, void* stream);
+int moe_attention_last(moe_ctx* ctx, const float* q, const float* k, const float* v,
+                       float* out, int64_t batch, int64_t seq_len, int64_t q_heads,
+                       int64_t kv_heads, int64_t head_dim, int64_t window, void* stream);
 int moe_add(moe_ctx* ctx, float* a, const float* b, int64_t n, void* stream);
 int moe_add_bias(moe_ctx* ctx, float* a, const float* bias, int64_t rows,
                  int64_t cols, void* stream);
