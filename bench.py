@@ -294,13 +294,21 @@ def decoder_bench(args, pkg):
     per_step = {n: ms / args.steps for n, (ms, _) in kt.items()}
     avg = {n: ms / c for n, (ms, c) in kt.items()}
     pairs = T * cfg.top_k
-    flops_w13 = 2.0 * pairs * cfg.d * cfg.d_ff * 2
-    w13_tflops = flops_w13 / (avg["expert_w13_swiglu"] * 1e-3) / 1e12
+    # w13 launches differ in size (the pruned last layer has B*k pairs), so
+    # the roofline is the step's w13 FLOPs over the step's w13 time
+    full = cfg.layers - 1 if model.prune_last else cfg.layers
+    tail_pairs = B * cfg.top_k if model.prune_last else 0
+    flops_w13 = 2.0 * (full * pairs + tail_pairs) * cfg.d * cfg.d_ff * 2
+    w13_tflops = flops_w13 / (per_step["expert_w13_swiglu"] * 1e-3) / 1e12
     qw, kw = cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
-    proj_flops = cfg.layers * 2.0 * T * cfg.d * (qw + 2 * kw + qw) + 2.0 * B * cfg.d * cfg.vocab
-    # causal attention: S(S+1)/2 (query, key) pairs per sequence and head, 2 products
-    attn_flops = cfg.layers * B * cfg.heads * 2 * (2.0 * cfg.head_dim * S * (S + 1) / 2)
-    moe_flops = cfg.layers * 2.0 * pairs * cfg.d * cfg.d_ff * 3
+    tail_rows = B if model.prune_last else 0
+    proj_flops = (2.0 * full * T * cfg.d * (qw + 2 * kw + qw) + 2.0 * tail_rows * cfg.d * (qw + qw)
+                  + 2.0 * (cfg.layers - full) * T * cfg.d * 2 * kw + 2.0 * B * cfg.d * cfg.vocab)
+    # causal attention: S(S+1)/2 (query, key) pairs per sequence and head, 2 products;
+    # the pruned layer's last rows see S keys each
+    attn_flops = (full * B * cfg.heads * 2 * (2.0 * cfg.head_dim * S * (S + 1) / 2)
+                  + tail_rows * cfg.heads * 2 * (2.0 * cfg.head_dim * S))
+    moe_flops = 2.0 * (full * pairs + tail_pairs) * cfg.d * cfg.d_ff * 3
     cpu = parity = None
     if args.cpu_seconds > 0:
         hidden = model.hidden(tokens).cpu().numpy()
@@ -339,7 +347,10 @@ def decoder_bench(args, pkg):
             "unit": "TFLOP/s",
             "frac": w13_tflops / FP32_MFMA_PEAK_TFLOPS,
             "traffic": None,
-            "flops_per_launch": flops_w13,
+            "flops_per_step": flops_w13,
+            "launches_per_step": cfg.layers,
+            "note": (f"achieved = the step's w13 FLOPs ({full} layers x {pairs} pairs + "
+                     f"{tail_pairs} pairs of the pruned layer) over the step's w13 HIP-event time"),
         },
         "kernel_ms_per_step": {n: round(v, 4) for n, v in sorted(per_step.items())},
         "kernel_avg_ms": {n: round(v, 5) for n, v in sorted(avg.items())},
