@@ -83,6 +83,10 @@ void DeviceBuffer::upload(const void* src, std::size_t bytes, std::size_t offset
         "hipMemcpy H2D");
 }
 
+void DeviceBuffer::zero() {
+    if (n_ != 0) hip(hipMemset(p_, 0, n_), "hipMemset");
+}
+
 void DeviceBuffer::download(void* dst, std::size_t bytes) const {
     if (bytes == 0) return;
     if (bytes > n_) throw std::invalid_argument("device download out of range");

@@ -35,6 +35,7 @@ public:
     template <class T>
     T* as() const { return static_cast<T*>(p_); }
     void upload(const void* src, std::size_t bytes, std::size_t offset = 0);
+    void zero();  // every byte 0 (synchronous)
     void download(void* dst, std::size_t bytes) const;
 
 private:

@@ -1,5 +1,6 @@
 #include "layer.h"
 
+#include <mutex>
 #include <numeric>
 #include <stdexcept>
 
@@ -27,6 +28,33 @@ std::shared_ptr<const DeviceBuffer> upload_stacked(const std::vector<Tensor>& ts
 void require_2d(const Tensor& t, std::size_t rows, std::size_t cols, const std::string& what) {
     if (t.ndim() != 2 || t.size(0) != rows || t.size(1) != cols)
         throw std::invalid_argument(what + ": unexpected weight shape");
+}
+
+// The RoPE cos/sin of `positions` positions (host libm, moe_rope_table) on
+// the device.
+std::shared_ptr<const DeviceBuffer> rope_table(std::size_t positions) {
+    std::vector<float> t(positions * apss26::HEAD_DIM);
+    check(moe_rope_table(apss26::ROPE_THETA, static_cast<int64_t>(apss26::HEAD_DIM),
+                         static_cast<int64_t>(positions), t.data()));
+    auto b = std::make_shared<DeviceBuffer>(t.size() * sizeof(float));
+    b->upload(t.data(), t.size() * sizeof(float));
+    return b;
+}
+
+// One table of MAX_POSITION_EMBEDDINGS positions shared by every layer.
+std::shared_ptr<const DeviceBuffer> shared_rope_table() {
+    static std::mutex mu;
+    static std::shared_ptr<const DeviceBuffer> table;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!table) table = rope_table(apss26::MAX_POSITION_EMBEDDINGS);
+    return table;
+}
+
+void sgemm_nt(const float* a, const DeviceBuffer& w, const std::shared_ptr<const DeviceBuffer>& b,
+              float* c, std::size_t m, std::size_t n, std::size_t k) {
+    check(moe_sgemm_nt(moe_dropin::context(), a, w.as<float>(), b ? b->as<float>() : nullptr, c,
+                       static_cast<int64_t>(m), static_cast<int64_t>(n), static_cast<int64_t>(k),
+                       nullptr));
 }
 
 }  // namespace
@@ -133,6 +161,23 @@ void PhiMoE::forward(const Tensor& x, Tensor& y, std::vector<int32_t>* topk_idx)
     const std::size_t rows = x.size(0), h = x.size(1);
     if (h != hidden_) throw std::invalid_argument("matmul_transposed shape");
     const std::size_t k = apss26::TOP_K < experts_ ? apss26::TOP_K : experts_;
+    DeviceBuffer dx(x.size() * sizeof(float)), dy(rows * hidden_ * sizeof(float)),
+        didx(rows * k * sizeof(int32_t));
+    dx.upload(x.data(), x.size() * sizeof(float));
+    forward_device(dx.as<float>(), dy.as<float>(), rows, MOE_NORM_NONE, nullptr, nullptr, 0,
+                   didx.as<int32_t>());
+    y = Tensor({rows, h});
+    dy.download(y.data(), rows * h * sizeof(float));
+    if (topk_idx != nullptr) {
+        topk_idx->resize(rows * k);
+        didx.download(topk_idx->data(), rows * k * sizeof(int32_t));
+    }
+}
+
+void PhiMoE::forward_device(const float* dx, float* dy, std::size_t rows, int norm,
+                            const float* norm_w, const float* norm_b, int residual,
+                            int32_t* topk_idx) const {
+    const std::size_t k = apss26::TOP_K < experts_ ? apss26::TOP_K : experts_;
     moe_layer_desc desc{};
     desc.T = static_cast<int64_t>(rows);
     desc.d = static_cast<int64_t>(hidden_);
@@ -144,20 +189,127 @@ void PhiMoE::forward(const Tensor& x, Tensor& y, std::vector<int32_t>* topk_idx)
     desc.quantum = apss26::ROUTER_SCORE_QUANTUM;
     desc.tie_eps = apss26::ROUTER_TIE_EPS;
     desc.contract = contract_;
+    desc.norm = norm;
+    desc.norm_eps = apss26::NORM_EPS;
+    desc.residual = residual;
     moe_layer_weights w{};
     w.gate_w = gate_->as<float>();
     w.w1 = w1_->as<float>();
     w.w3 = w3_->as<float>();
     w.w2 = w2_->as<float>();
-    DeviceBuffer dx(x.size() * sizeof(float)), dy(rows * hidden_ * sizeof(float)),
-        didx(rows * k * sizeof(int32_t));
-    dx.upload(x.data(), x.size() * sizeof(float));
-    check(moe_layer_forward(moe_dropin::context(), &desc, &w, dx.as<float>(), dy.as<float>(),
-                            didx.as<int32_t>(), nullptr, nullptr));
-    y = Tensor({rows, h});
-    dy.download(y.data(), rows * h * sizeof(float));
-    if (topk_idx != nullptr) {
-        topk_idx->resize(rows * k);
-        didx.download(topk_idx->data(), rows * k * sizeof(int32_t));
+    w.norm_w = norm_w;
+    w.norm_b = norm_b;
+    check(moe_layer_forward(moe_dropin::context(), &desc, &w, dx, dy, topk_idx, nullptr, nullptr));
+}
+
+// ------------------------------------------------------------ PhiAttention
+// src/layer.cu:105-143: projections with bias, RoPE over the sequence's s
+// positions, causal attention within SLIDING_WINDOW, o projection.
+PhiAttention::PhiAttention(const ModelLoader& loader, std::size_t layer_idx) {
+    const std::string base = "model.layers." + std::to_string(layer_idx) + ".self_attn.";
+    const std::size_t qw = apss26::NUM_ATTENTION_HEADS * apss26::HEAD_DIM;
+    const std::size_t kw = apss26::NUM_KV_HEADS * apss26::HEAD_DIM;
+    const Tensor q = loader.load(base + "q_proj.weight");
+    if (q.ndim() != 2) throw std::invalid_argument(base + "q_proj.weight: weight must be 2-D");
+    hidden_ = q.size(1);
+    auto proj = [&](const std::string& name, std::size_t out, std::size_t in,
+                    std::shared_ptr<const DeviceBuffer>& w, std::shared_ptr<const DeviceBuffer>& b) {
+        const Tensor wt = name == "q_proj" ? q : loader.load(base + name + ".weight");
+        require_2d(wt, out, in, base + name + ".weight");
+        w = upload(wt);
+        if (loader.has(base + name + ".bias")) {
+            const Tensor bt = loader.load(base + name + ".bias");
+            if (bt.size() != out) throw std::invalid_argument(base + name + ".bias: bias shape");
+            b = upload(bt);
+        }
+    };
+    proj("q_proj", qw, hidden_, wq_, bq_);
+    proj("k_proj", kw, hidden_, wk_, bk_);
+    proj("v_proj", kw, hidden_, wv_, bv_);
+    proj("o_proj", hidden_, qw, wo_, bo_);
+    rope_ = shared_rope_table();
+    rope_positions_ = apss26::MAX_POSITION_EMBEDDINGS;
+}
+
+void PhiAttention::forward_device(const float* dx, float* dy, std::size_t s) const {
+    const std::size_t sp = padded_rows(s);
+    const std::size_t H = apss26::NUM_ATTENTION_HEADS, KVH = apss26::NUM_KV_HEADS,
+                      hd = apss26::HEAD_DIM;
+    DeviceBuffer q(sp * H * hd * sizeof(float)), k(sp * KVH * hd * sizeof(float)),
+        v(sp * KVH * hd * sizeof(float)), a(sp * H * hd * sizeof(float));
+    sgemm_nt(dx, *wq_, bq_, q.as<float>(), sp, H * hd, hidden_);
+    sgemm_nt(dx, *wk_, bk_, k.as<float>(), sp, KVH * hd, hidden_);
+    sgemm_nt(dx, *wv_, bv_, v.as<float>(), sp, KVH * hd, hidden_);
+    std::shared_ptr<const DeviceBuffer> table = rope_;
+    std::size_t positions = rope_positions_;
+    if (s > positions) {
+        table = rope_table(s);
+        positions = s;
     }
+    moe_ctx* ctx = moe_dropin::context();
+    // Rows past s come from finite padding rows and sit after every real
+    // query, so the causal mask hides them: the padded attention is exact
+    // for the rows < s.
+    check(moe_rope(ctx, q.as<float>(), k.as<float>(), table->as<float>(),
+                   static_cast<int64_t>(positions), 1, static_cast<int64_t>(s), 0,
+                   static_cast<int64_t>(H), static_cast<int64_t>(KVH), static_cast<int64_t>(hd),
+                   nullptr));
+    check(moe_attention(ctx, q.as<float>(), k.as<float>(), v.as<float>(), a.as<float>(), 1,
+                        static_cast<int64_t>(sp), static_cast<int64_t>(H),
+                        static_cast<int64_t>(KVH), static_cast<int64_t>(hd),
+                        static_cast<int64_t>(apss26::SLIDING_WINDOW), nullptr));
+    sgemm_nt(a.as<float>(), *wo_, bo_, dy, sp, hidden_, H * hd);
+}
+
+void PhiAttention::forward(const Tensor& x, Tensor& y) const {
+    if (x.ndim() != 2 || x.size(1) != hidden_) throw std::invalid_argument("matmul_transposed shape");
+    const std::size_t s = x.size(0), sp = padded_rows(s);
+    y = Tensor({s, hidden_});
+    if (s == 0) return;
+    DeviceBuffer dx(sp * hidden_ * sizeof(float)), dy(sp * hidden_ * sizeof(float));
+    dx.zero();
+    dx.upload(x.data(), x.size() * sizeof(float));
+    forward_device(dx.as<float>(), dy.as<float>(), s);
+    dy.download(y.data(), s * hidden_ * sizeof(float));
+}
+
+// --------------------------------------------------------- PhiDecoderLayer
+// src/layer.cu:145-162: h = x + attention(layer_norm(x)), y = h +
+// moe(layer_norm(h)); the second norm and both residual adds of the MoE
+// block run inside moe_layer_forward (norm = MOE_NORM_LAYER, residual = 1).
+PhiDecoderLayer::PhiDecoderLayer(const ModelLoader& loader, std::size_t layer_idx)
+    : attention_(loader, layer_idx), moe_(loader, layer_idx) {
+    const std::string base = "model.layers." + std::to_string(layer_idx) + ".";
+    const std::size_t h = attention_.hidden();
+    if (moe_.hidden() != h) throw std::invalid_argument(base + "block_sparse_moe: width differs");
+    auto vec = [&](const std::string& name) {
+        const Tensor t = loader.load(base + name);
+        if (t.size() != h) throw std::invalid_argument(base + name + ": unexpected weight shape");
+        return upload(t);
+    };
+    in_w_ = vec("input_layernorm.weight");
+    in_b_ = vec("input_layernorm.bias");
+    post_w_ = vec("post_attention_layernorm.weight");
+    post_b_ = vec("post_attention_layernorm.bias");
+}
+
+void PhiDecoderLayer::forward(const Tensor& x, Tensor& y) const {
+    const std::size_t h = attention_.hidden();
+    if (x.ndim() != 2 || x.size(1) != h) throw std::invalid_argument("layer norm shape");
+    const std::size_t s = x.size(0), sp = PhiAttention::padded_rows(s);
+    y = Tensor({s, h});
+    if (s == 0) return;
+    DeviceBuffer dx(sp * h * sizeof(float)), dn(sp * h * sizeof(float)),
+        da(sp * h * sizeof(float)), dy(s * h * sizeof(float));
+    dx.zero();
+    dx.upload(x.data(), x.size() * sizeof(float));
+    moe_ctx* ctx = moe_dropin::context();
+    check(moe_layer_norm(ctx, dx.as<float>(), in_w_->as<float>(), in_b_->as<float>(),
+                         apss26::NORM_EPS, static_cast<int64_t>(sp), static_cast<int64_t>(h),
+                         MOE_CONTRACT_FMA, dn.as<float>(), nullptr, nullptr, nullptr));
+    attention_.forward_device(dn.as<float>(), da.as<float>(), s);
+    check(moe_add(ctx, da.as<float>(), dx.as<float>(), static_cast<int64_t>(s * h), nullptr));
+    moe_.forward_device(da.as<float>(), dy.as<float>(), s, MOE_NORM_LAYER, post_w_->as<float>(),
+                        post_b_->as<float>(), 1, nullptr);
+    dy.download(y.data(), s * h * sizeof(float));
 }

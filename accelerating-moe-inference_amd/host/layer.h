@@ -5,8 +5,10 @@
 // the same, src/model.cu:1491-1513); forward() copies the input in, runs the
 // HIP path and copies the result out.
 //
-// PhiAttention / PhiDecoderLayer (include/layer.h:39-56) are outside the MoE
-// hot path and are not provided.
+// PhiAttention and PhiDecoderLayer (include/layer.h:39-56) keep the
+// reference's constructors, weight names and forward(x, y) on one sequence
+// x [s, hidden]; a decoder layer runs on the device from one upload of x to
+// one download of y.
 #pragma once
 
 #include <cstdint>
@@ -61,9 +63,52 @@ public:
     void forward(const Tensor& x, Tensor& y, std::vector<int32_t>* topk_idx) const;
 
     std::size_t num_experts() const { return experts_; }
+    std::size_t hidden() const { return hidden_; }
+
+    // The MoE block on device rows (an extension PhiDecoderLayer uses):
+    // dy[rows, h] = (residual ? dx : 0) + MoE(norm(dx)), norm a MOE_NORM_*
+    // with its [h] weight and bias; topk_idx (device, rows x top_k) may be null.
+    void forward_device(const float* dx, float* dy, std::size_t rows, int norm,
+                        const float* norm_w, const float* norm_b, int residual,
+                        int32_t* topk_idx) const;
 
 private:
     std::shared_ptr<const moe_dropin::DeviceBuffer> gate_, w1_, w3_, w2_;
     std::size_t experts_ = 0, hidden_ = 0, ff_ = 0;
     int contract_ = MOE_CONTRACT_FMA;
+};
+
+class PhiAttention {
+public:
+    // Loads model.layers.{layer_idx}.self_attn.{q,k,v,o}_proj.{weight,bias}
+    // (a bias is optional, as in Linear); heads, key heads, head_dim, RoPE
+    // theta and the sliding window are the apss26 constants.
+    PhiAttention(const ModelLoader& loader, std::size_t layer_idx);
+    // y[s, hidden] = o_proj(attention(rope(q_proj(x), k_proj(x)), v_proj(x)))
+    // over one sequence x[s, hidden]; y is reassigned.
+    void forward(const Tensor& x, Tensor& y) const;
+    // Device rows (an extension): dx holds padded_rows(s) rows, those past s
+    // zero; dy receives as many (rows past s are scratch).
+    void forward_device(const float* dx, float* dy, std::size_t s) const;
+    // s rounded up to the attention kernels' 16-row granule.
+    static std::size_t padded_rows(std::size_t s) { return (s + 15) / 16 * 16; }
+    std::size_t hidden() const { return hidden_; }
+
+private:
+    std::shared_ptr<const moe_dropin::DeviceBuffer> wq_, bq_, wk_, bk_, wv_, bv_, wo_, bo_, rope_;
+    std::size_t hidden_ = 0, rope_positions_ = 0;
+};
+
+class PhiDecoderLayer {
+public:
+    // Loads model.layers.{layer_idx}.{input_layernorm,post_attention_layernorm}
+    // .{weight,bias}, the attention and the MoE block of the layer.
+    PhiDecoderLayer(const ModelLoader& loader, std::size_t layer_idx);
+    // y = h + MoE(layer_norm(h)), h = x + attention(layer_norm(x)); y is reassigned.
+    void forward(const Tensor& x, Tensor& y) const;
+
+private:
+    std::shared_ptr<const moe_dropin::DeviceBuffer> in_w_, in_b_, post_w_, post_b_;
+    PhiAttention attention_;
+    PhiMoE moe_;
 };

@@ -264,4 +264,29 @@ int shim_moe(const char* path, int64_t layer, int contract, const float* x, int6
     });
 }
 
+// PhiAttention / PhiDecoderLayer of layer `layer` on one sequence x [s, h].
+int shim_attention(const char* path, int64_t layer, const float* x, int64_t s, int64_t h,
+                   float* y) {
+    return guarded([&] {
+        ModelLoader l(path);
+        PhiAttention att(l, size_t(layer));
+        Tensor X = make(x, {size_t(s), size_t(h)}), Y;
+        att.forward(X, Y);
+        expect(Y.ndim() == 2 && Y.size(0) == size_t(s) && Y.size(1) == size_t(h), "y shape");
+        std::memcpy(y, Y.data(), Y.size() * sizeof(float));
+    });
+}
+
+int shim_decoder_layer(const char* path, int64_t layer, const float* x, int64_t s, int64_t h,
+                       float* y) {
+    return guarded([&] {
+        ModelLoader l(path);
+        PhiDecoderLayer dec(l, size_t(layer));
+        Tensor X = make(x, {size_t(s), size_t(h)}), Y;
+        dec.forward(X, Y);
+        expect(Y.ndim() == 2 && Y.size(0) == size_t(s) && Y.size(1) == size_t(h), "y shape");
+        std::memcpy(y, Y.data(), Y.size() * sizeof(float));
+    });
+}
+
 }  // extern "C"

@@ -245,3 +245,70 @@ def test_add_bias_and_rope_bit_exact(shim, orc):
     rq, rk = orc.rope(q[:S], k[:S], 1, S, H, KVH, hd)
     assert np.array_equal(gq[:S], rq) and np.array_equal(gk[:S], rk)
     assert np.array_equal(gq[S:], q[S:]) and np.array_equal(gk[S:], k[S:])
+
+
+def _decoder_layer_tensors(rng, li, h, E, ff):
+    """Weights of decoder layer li in the reference's names; the apss26
+    attention shape: 16 query heads, 4 key heads, head_dim 128."""
+    qw, kw = 16 * 128, 4 * 128
+    p = f"model.layers.{li}"
+    t = {f"{p}.input_layernorm.weight": 1 + normal(rng, (h,), 0.1),
+         f"{p}.input_layernorm.bias": normal(rng, (h,), 0.1),
+         f"{p}.post_attention_layernorm.weight": 1 + normal(rng, (h,), 0.1),
+         f"{p}.post_attention_layernorm.bias": normal(rng, (h,), 0.1),
+         f"{p}.block_sparse_moe.gate.weight": normal(rng, (E, h), 0.02)}
+    for name, out, inp in (("q_proj", qw, h), ("k_proj", kw, h), ("v_proj", kw, h),
+                           ("o_proj", h, qw)):
+        t[f"{p}.self_attn.{name}.weight"] = normal(rng, (out, inp), 0.02)
+        t[f"{p}.self_attn.{name}.bias"] = normal(rng, (out,), 0.02)
+    for e in range(E):
+        t[f"{p}.block_sparse_moe.experts.{e}.w1.weight"] = normal(rng, (ff, h), 0.02)
+        t[f"{p}.block_sparse_moe.experts.{e}.w3.weight"] = normal(rng, (ff, h), 0.02)
+        t[f"{p}.block_sparse_moe.experts.{e}.w2.weight"] = normal(rng, (h, ff), 0.02)
+    return t
+
+
+def _oracle_layer(t, li, E):
+    """The names of oracle/decoder.py for the reference's layer li."""
+    p = f"model.layers.{li}"
+    L = {"input_norm_w": t[f"{p}.input_layernorm.weight"],
+         "input_norm_b": t[f"{p}.input_layernorm.bias"],
+         "post_norm_w": t[f"{p}.post_attention_layernorm.weight"],
+         "post_norm_b": t[f"{p}.post_attention_layernorm.bias"],
+         "gate_w": t[f"{p}.block_sparse_moe.gate.weight"]}
+    for n in ("q", "k", "v", "o"):
+        L[f"{n}_w"] = t[f"{p}.self_attn.{n}_proj.weight"]
+        L[f"{n}_b"] = t[f"{p}.self_attn.{n}_proj.bias"]
+    for n in ("w1", "w3", "w2"):
+        L[n] = np.stack([t[f"{p}.block_sparse_moe.experts.{e}.{n}.weight"] for e in range(E)])
+    return L
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("s", [37, 64])
+def test_attention_and_decoder_layer_vs_oracle(shim, orc, tmp_path, s):
+    # s = 37 is not a multiple of the attention kernels' 16-row granule: the
+    # drop-in pads the sequence at its end, which the causal mask leaves exact
+    import types
+    from oracle import decoder as od
+    rng = np.random.default_rng(40 + s)
+    h, E, ff, li = 256, 16, 64, 2
+    t = _decoder_layer_tensors(rng, li, h, E, ff)
+    path = str(tmp_path / "model.bin")
+    write_model_bin(path, t)
+    cfg = types.SimpleNamespace(norm="layer", norm_eps=1e-5, heads=16, kv_heads=4, head_dim=128,
+                                rope_theta=10000.0, window=2047, top_k=2,
+                                router=orc.ROUTER_PHI_QUANT, contract=orc.CONTRACT_FMA)
+    L = _oracle_layer(t, li, E)
+    x = normal(rng, (s, h))
+    I = ctypes.c_int64
+    y = np.empty((s, h), np.float32)
+    assert shim.shim_attention(path.encode(), I(li), fptr(x), I(s), I(h), fptr(y)) == 0, err(shim)
+    q, k, v = (od.linear(x, L[f"{n}_w"], L[f"{n}_b"], cfg.contract) for n in "qkv")
+    q, k = orc.rope(q, k, 1, s, 16, 4, 128)
+    a = orc.attention(q, k, v, 1, s, 16, 4, 128, window=2047)
+    assert_close(y, od.linear(a, L["o_w"], L["o_b"], cfg.contract), what="PhiAttention")
+    assert shim.shim_decoder_layer(path.encode(), I(li), fptr(x), I(s), I(h), fptr(y)) == 0, \
+        err(shim)
+    ref, _, _ = od.layer_forward(x, L, cfg, 1, s)
+    assert_close(y, ref, what="PhiDecoderLayer")
