@@ -35,7 +35,7 @@ EXPORTS = (
     "moe_ctx_kernel_times", "moe_ctx_reset_timing", "moe_last_error",
     "moe_version", "moe_sgemm_nt", "moe_sgemm_nn", "moe_silu", "moe_mul",
     "moe_layer_norm", "moe_rms_norm", "moe_rope_table", "moe_rope", "moe_attention",
-    "moe_attention_last", "moe_add",
+    "moe_attention_last", "moe_rope_rows", "moe_attention_paths", "moe_add",
     "moe_add_bias", "moe_embed", "moe_gate_logits",
     "moe_route", "moe_permute", "moe_expert_ffn_grouped", "moe_combine",
     "moe_layer_forward", "moe_layer_w2_splits",
@@ -102,6 +102,9 @@ def load_library(path: str = LIB_PATH):
         "moe_rope_table": ([F, I64, I64, P], I),
         "moe_rope": ([P, P, P, P, I64, I64, I64, I64, I64, I64, I64, P], I),
         "moe_attention_last": ([P, P, P, P, P, I64, I64, I64, I64, I64, I64, P], I),
+        "moe_rope_rows": ([P, P, P, P, I64, P, I64, I64, I64, I64, P], I),
+        "moe_attention_paths": ([P, P, P, P, P, I64, I64, P, P, P, I64, I64, I64, I64, I64,
+                                 I64, P], I),
         "moe_attention": ([P, P, P, P, P, I64, I64, I64, I64, I64, I64, P], I),
         "moe_add": ([P, P, P, I64, P], I),
         "moe_add_bias": ([P, P, P, I64, I64, P], I),
@@ -292,6 +295,23 @@ class Context:
         _check(_lib.moe_attention_last(self.handle, _f32(q, "q"), _f32(k, "k"), _f32(v, "v"),
                                        _f32(out, "out"), batch, seq_len, q_heads, kv_heads,
                                        head_dim, window, _stream()))
+        return out
+
+    def rope_rows(self, q, k, table, positions, rows, q_heads, kv_heads, head_dim):
+        """RoPE with row r at positions[r] (int32, on the device)."""
+        _check(_lib.moe_rope_rows(self.handle, _f32(q, "q"), _f32(k, "k"), _f32(table, "table"),
+                                  table.numel() // head_dim, _i32(positions, "positions"), rows,
+                                  q_heads, kv_heads, head_dim, _stream()))
+
+    def attention_paths(self, q, k, v, out, key_rows, key_beg, key_end, max_len, q_heads,
+                        kv_heads, head_dim, window=0):
+        """Attention of q's rows over explicit key lists (int32 device arrays)."""
+        nq = key_beg.numel()
+        _check(_lib.moe_attention_paths(
+            self.handle, _f32(q, "q"), _f32(k, "k"), _f32(v, "v"), _f32(out, "out"), nq,
+            k.shape[0], _i32(key_rows, "key_rows"), _i32(key_beg, "key_beg"),
+            _i32(key_end, "key_end"), max_len, key_rows.numel(), q_heads, kv_heads, head_dim,
+            window, _stream()))
         return out
 
     def add(self, a, b):

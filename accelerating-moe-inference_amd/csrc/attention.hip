@@ -144,6 +144,123 @@ __global__ __launch_bounds__(256) void attn_last_kernel(
     }
 }
 
+// RoPE with an explicit position per row (the depth of a prefix-trie node,
+// src/model.cu:1046-1083 with `pos`): row r at positions[r], clamped into
+// the table so that a bad position cannot read past it.
+__global__ __launch_bounds__(256) void rope_rows_kernel(float* __restrict__ q,
+                                                        float* __restrict__ k,
+                                                        const float* __restrict__ table,
+                                                        int64_t table_positions,
+                                                        const int32_t* __restrict__ positions,
+                                                        int64_t rows, int64_t q_heads,
+                                                        int64_t kv_heads, int64_t head_dim) {
+    const int64_t half = head_dim / 2, heads = q_heads + kv_heads;
+    const int64_t n = rows * heads * half;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += stride) {
+        const int64_t j = i % half, hh = (i / half) % heads, r = i / (half * heads);
+        float* x = hh < q_heads ? q + r * q_heads * head_dim + hh * head_dim
+                                : k + r * kv_heads * head_dim + (hh - q_heads) * head_dim;
+        int64_t pos = positions[r];
+        pos = pos < 0 ? 0 : (pos >= table_positions ? table_positions - 1 : pos);
+        const float* trig = table + (pos * half + j) * 2;
+        const float c = trig[0], sn = trig[1];
+        const float x0 = x[j], x1 = x[j + half];
+        x[j] = x0 * c - x1 * sn;
+        x[j + half] = x1 * c + x0 * sn;
+    }
+}
+
+// Attention of query row i over an explicit key list: key rows
+// key_rows[key_beg[i] .. key_end[i]) of k and v, ascending positions ending
+// at the query's own (a prefix-trie node's root path, src/model.cu:1667-1680;
+// attention_heads :1161-1283), of which the last `window` are visible
+// (window > 0).  One workgroup per (query, head); every sum in the
+// reference loop's order, as attn_last_kernel: bit-identical to it given the
+// same inputs.  Key indices are clamped into [0, kv_rows).  The scores live
+// in LDS when the list fits (LDS_ROW), else in `scores` at key_beg[i] * H +
+// h * len.
+template <bool VEC4, bool LDS_ROW>
+__global__ __launch_bounds__(256) void attn_paths_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    float* __restrict__ out, float* __restrict__ scores, const int32_t* __restrict__ key_rows,
+    const int32_t* __restrict__ key_beg, const int32_t* __restrict__ key_end, int64_t kv_rows,
+    int64_t key_total, int64_t scores_floats, int64_t H, int64_t KVH, int64_t hd, int64_t window,
+    float scale) {
+    __shared__ float red[4];
+    __shared__ float row[LDS_ROW ? kAttnLastLds : 1];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t i = blockIdx.x / H, h = blockIdx.x % H, kh = h / (H / KVH);
+    const int64_t kw = KVH * hd;
+    const float* qr = q + i * H * hd + h * hd;
+    int64_t beg = key_beg[i];
+    const int64_t end = key_end[i];
+    if (window > 0 && end - beg > window) beg = end - window;
+    const int64_t len = end > beg ? end - beg : 0;
+    float* sc = LDS_ROW ? row : scores + static_cast<int64_t>(key_beg[i]) * H + h * len;
+    float* o = out + i * H * hd + h * hd;
+    if (len == 0) {  // an empty key list (not a trie path): zeros
+        for (int64_t d = tid; d < hd; d += blockDim.x) o[d] = 0.0f;
+        return;
+    }
+    // a list outside key_rows, or longer than the caller's bound (it would
+    // overrun the score row): NaN output instead (block-uniform)
+    const bool fits = key_beg[i] >= 0 && end <= key_total &&
+                      (LDS_ROW ? len <= kAttnLastLds
+                               : static_cast<int64_t>(key_beg[i]) * H + (h + 1) * len <=
+                                     scores_floats);
+    if (!fits) {
+        for (int64_t d = tid; d < hd; d += blockDim.x) o[d] = NAN;
+        return;
+    }
+    auto key_row = [&](int64_t t) {
+        int64_t r = key_rows[beg + t];
+        return r < 0 ? 0 : (r >= kv_rows ? kv_rows - 1 : r);
+    };
+    float m = -INFINITY;
+    for (int64_t t = tid; t < len; t += blockDim.x) {
+        const float* kr = k + key_row(t) * kw + kh * hd;
+        float acc = 0.0f;
+        if (VEC4) {
+            for (int64_t d = 0; d < hd; d += 4) {
+                const float4 a = *reinterpret_cast<const float4*>(qr + d);
+                const float4 c = *reinterpret_cast<const float4*>(kr + d);
+                acc += a.x * c.x;
+                acc += a.y * c.y;
+                acc += a.z * c.z;
+                acc += a.w * c.w;
+            }
+        } else {
+            for (int64_t d = 0; d < hd; ++d) acc += qr[d] * kr[d];
+        }
+        const float sv = acc / scale;
+        sc[t] = sv;
+        m = fmaxf(m, sv);
+    }
+    m = wave_max(m);
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (int64_t t = tid; t < len; t += blockDim.x)
+        sc[t] = static_cast<float>(exp(static_cast<double>(sc[t] - m)));
+    __syncthreads();
+    if (tid == 0) {
+        float den = 0.0f;
+#pragma unroll 8
+        for (int64_t t = 0; t < len; ++t) den += sc[t];
+        red[0] = den;
+    }
+    __syncthreads();
+    const float den = red[0];
+    for (int64_t d = tid; d < hd; d += blockDim.x) {
+        float value = 0.0f;
+#pragma unroll 8
+        for (int64_t t = 0; t < len; ++t) value += sc[t] / den * v[key_row(t) * kw + kh * hd + d];
+        o[d] = value;
+    }
+}
+
 __global__ __launch_bounds__(256) void add_kernel(float* __restrict__ a, const float* __restrict__ b,
                                                   int64_t n) {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
@@ -218,6 +335,37 @@ void launch_attn_softmax(float* scores, int64_t batches, int64_t seq_len, int64_
     const float scale = sqrtf(static_cast<float>(head_dim));
     hipLaunchKernelGGL(attn_softmax_kernel, dim3(static_cast<unsigned>(ceil_div(rows, 4))),
                        dim3(256), 0, s, scores, rows, seq_len, scale, window);
+}
+
+void launch_rope_rows(float* q, float* k, const float* table, int64_t table_positions,
+                      const int32_t* positions, int64_t rows, int64_t q_heads, int64_t kv_heads,
+                      int64_t head_dim, hipStream_t s) {
+    const int64_t n = rows * (q_heads + kv_heads) * (head_dim / 2);
+    if (n <= 0) return;
+    hipLaunchKernelGGL(rope_rows_kernel, dim3(grid_for(n)), dim3(256), 0, s, q, k, table,
+                       table_positions, positions, rows, q_heads, kv_heads, head_dim);
+}
+
+void launch_attn_paths(const float* q, const float* k, const float* v, float* out,
+                       float* scores, const int32_t* key_rows, const int32_t* key_beg,
+                       const int32_t* key_end, int64_t nq, int64_t kv_rows, int64_t max_len,
+                       int64_t key_total, int64_t scores_floats, int64_t q_heads,
+                       int64_t kv_heads, int64_t head_dim, int64_t window, hipStream_t s) {
+    const int64_t blocks = nq * q_heads;
+    if (blocks <= 0) return;
+    const float scale = sqrtf(static_cast<float>(head_dim));
+    const bool vec4 = head_dim % 4 == 0 && reinterpret_cast<uintptr_t>(q) % 16 == 0 &&
+                      reinterpret_cast<uintptr_t>(k) % 16 == 0;
+    auto go = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, q, k, v,
+                           out, scores, key_rows, key_beg, key_end, kv_rows, key_total,
+                           scores_floats, q_heads, kv_heads, head_dim, window, scale);
+    };
+    const bool lds = max_len <= kAttnLastLds;
+    if (vec4 && lds) go(attn_paths_kernel<true, true>);
+    else if (vec4) go(attn_paths_kernel<true, false>);
+    else if (lds) go(attn_paths_kernel<false, true>);
+    else go(attn_paths_kernel<false, false>);
 }
 
 void launch_add(float* a, const float* b, int64_t n, hipStream_t s) {

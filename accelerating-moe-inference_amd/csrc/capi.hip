@@ -738,6 +738,68 @@ int moe_attention_last(moe_ctx* ctx, const float* q, const float* k, const float
     });
 }
 
+int moe_rope_rows(moe_ctx* ctx, float* q, float* k, const float* table, int64_t table_positions,
+                  const int32_t* positions, int64_t rows, int64_t q_heads, int64_t kv_heads,
+                  int64_t head_dim, void* stream) {
+    return guarded([&] {
+        check_ctx(ctx);
+        check_dims(rows, "rows");
+        moe::require(q_heads >= 0 && kv_heads >= 0, "heads must be >= 0");
+        moe::require(head_dim > 0 && head_dim % 2 == 0, "head_dim must be even and > 0");
+        if (rows == 0 || q_heads + kv_heads == 0) return;
+        moe::require(table_positions >= 1, "the rope table needs at least one position");
+        check_ptr(table, "table");
+        check_ptr(positions, "positions");
+        if (q_heads > 0) check_ptr(q, "q");
+        if (kv_heads > 0) check_ptr(k, "k");
+        DeviceScope dev(ctx->device);
+        hipStream_t s = as_stream(stream);
+        ctx->launch("rope", s, [&] {
+            moe::launch_rope_rows(q, k, table, table_positions, positions, rows, q_heads,
+                                  kv_heads, head_dim, s);
+        });
+    });
+}
+
+int moe_attention_paths(moe_ctx* ctx, const float* q, const float* k, const float* v, float* out,
+                        int64_t nq, int64_t kv_rows, const int32_t* key_rows,
+                        const int32_t* key_beg, const int32_t* key_end, int64_t max_len,
+                        int64_t key_total, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                        int64_t window, void* stream) {
+    return guarded([&] {
+        check_ctx(ctx);
+        check_dims(nq, "nq");
+        check_dims(kv_rows, "kv_rows");
+        moe::require(kv_heads >= 1 && q_heads >= kv_heads && q_heads % kv_heads == 0,
+                     "q_heads must be a positive multiple of kv_heads");
+        moe::require(head_dim > 0, "head_dim must be > 0");
+        moe::require(window >= 0, "window must be >= 0 (0 = unlimited)");
+        moe::require(max_len >= 0 && key_total >= 0, "max_len and key_total must be >= 0");
+        if (nq == 0) return;
+        moe::require(kv_rows >= 1, "kv_rows must be >= 1");
+        check_ptr(q, "q");
+        check_ptr(k, "k");
+        check_ptr(v, "v");
+        check_ptr(out, "out");
+        check_ptr(key_rows, "key_rows");
+        check_ptr(key_beg, "key_beg");
+        check_ptr(key_end, "key_end");
+        DeviceScope dev(ctx->device);
+        hipStream_t s = as_stream(stream);
+        float* scores = nullptr;
+        int64_t scores_floats = 0;
+        if (max_len > 8192) {
+            scores_floats = std::max<int64_t>(key_total, 1) * q_heads;
+            scores = static_cast<float*>(ctx->workspace(size_t(scores_floats) * sizeof(float)));
+        }
+        ctx->launch("attn_paths", s, [&] {
+            moe::launch_attn_paths(q, k, v, out, scores, key_rows, key_beg, key_end, nq, kv_rows,
+                                   max_len, key_total, scores_floats, q_heads, kv_heads,
+                                   head_dim, window, s);
+        });
+    });
+}
+
 int moe_add(moe_ctx* ctx, float* a, const float* b, int64_t n, void* stream) {
     return guarded([&] {
         check_ctx(ctx);

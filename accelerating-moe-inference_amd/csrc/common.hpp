@@ -126,6 +126,17 @@ void launch_rope(float* q, float* k, const float* table, int64_t rows, int64_t s
 void launch_attn_last(const float* q, const float* k, const float* v, float* out, float* scores,
                       int64_t batch, int64_t seq_len, int64_t q_heads, int64_t kv_heads,
                       int64_t head_dim, int64_t window, hipStream_t s);
+// RoPE with row r at positions[r]; attention of nq query rows over explicit
+// key lists key_rows[key_beg[i] .. key_end[i]) (max_len: the longest list;
+// scores: workspace of (last key_end) * q_heads floats when a list exceeds LDS).
+void launch_rope_rows(float* q, float* k, const float* table, int64_t table_positions,
+                      const int32_t* positions, int64_t rows, int64_t q_heads, int64_t kv_heads,
+                      int64_t head_dim, hipStream_t s);
+void launch_attn_paths(const float* q, const float* k, const float* v, float* out,
+                       float* scores, const int32_t* key_rows, const int32_t* key_beg,
+                       const int32_t* key_end, int64_t nq, int64_t kv_rows, int64_t max_len,
+                       int64_t key_total, int64_t scores_floats, int64_t q_heads,
+                       int64_t kv_heads, int64_t head_dim, int64_t window, hipStream_t s);
 void launch_attn_softmax(float* scores, int64_t batches, int64_t seq_len, int64_t head_dim,
                          int64_t window, hipStream_t s);
 // a[i] += b[i];  a[r, c] += bias[c];  out[i, :] = table[tokens[i], :]

@@ -32,6 +32,8 @@
  *   moe_attention       PhiAttention::forward, after the projections  src/layer.cu:111-143;
  *                       attention_heads                    src/model.cu:1161-1283
  *   moe_attention_last  attention_heads<true> of the pruned last layer  src/model.cu:1889-1960
+ *   moe_rope_rows       rope_rows with per-node positions  src/model.cu:1046-1083
+ *   moe_attention_paths attention_heads over trie root paths  src/model.cu:1161-1283,1667-1680
  *   moe_add             tensor_ops::add_inplace            src/tensor.cu:150-154
  *   moe_add_bias        tensor_ops::add_bias_inplace       src/tensor.cu:156-161
  *   moe_embed           embedding row gather (gather_rows) src/model.cu:674-693,1878-1885
@@ -200,6 +202,21 @@ int moe_rms_norm(moe_ctx* ctx, const float* x, const float* weight, float eps,
  *   the reference loop's order, so it is bit-identical to that loop given
  *   the same q, k, v.  Any head_dim and seq_len; batch*q_heads*seq_len
  *   floats of workspace.
+ * moe_rope_rows: moe_rope with row r at positions[r] (device int32 [rows],
+ *   e.g. the depths of prefix-trie nodes); positions outside [0,
+ *   table_positions) are clamped into the table.
+ * moe_attention_paths: query row i of q [nq, q_heads*head_dim] attends over
+ *   the key rows key_rows[key_beg[i] .. key_end[i]) of k, v [kv_rows,
+ *   kv_heads*head_dim], listed by ascending position and ending at the
+ *   query's own (a prefix-trie node's root path); the last `window` of them
+ *   are visible (0 = all).  out [nq, q_heads*head_dim].  Every sum runs in
+ *   the reference loop's order: bit-identical to it given the same q, k, v.
+ *   max_len bounds every list length; key_total is the length of key_rows
+ *   (every list must lie inside it).  Lists
+ *   up to 8192 keys use no workspace; longer ones use key_total*q_heads
+ *   floats and must not overlap each other in key_rows.  Key indices are
+ *   clamped into [0, kv_rows); a list outside key_rows or longer than max_len
+ *   allows gives NaN rows instead of reading or writing out of bounds.
  * moe_add: a += b elementwise.  moe_add_bias: a[r, c] += bias[c].
  * moe_embed: out[i, :] = table[tokens[i], :] (table [vocab, d]); a token
  *   outside [0, vocab) gives a zero row. */
@@ -214,6 +231,14 @@ int moe_attention(moe_ctx* ctx, const float* q, const float* k, const float* v,
 int moe_attention_last(moe_ctx* ctx, const float* q, const float* k, const float* v,
                        float* out, int64_t batch, int64_t seq_len, int64_t q_heads,
                        int64_t kv_heads, int64_t head_dim, int64_t window, void* stream);
+int moe_rope_rows(moe_ctx* ctx, float* q, float* k, const float* table,
+                  int64_t table_positions, const int32_t* positions, int64_t rows,
+                  int64_t q_heads, int64_t kv_heads, int64_t head_dim, void* stream);
+int moe_attention_paths(moe_ctx* ctx, const float* q, const float* k, const float* v,
+                        float* out, int64_t nq, int64_t kv_rows, const int32_t* key_rows,
+                        const int32_t* key_beg, const int32_t* key_end, int64_t max_len,
+                        int64_t key_total, int64_t q_heads, int64_t kv_heads,
+                        int64_t head_dim, int64_t window, void* stream);
 int moe_add(moe_ctx* ctx, float* a, const float* b, int64_t n, void* stream);
 int moe_add_bias(moe_ctx* ctx, float* a, const float* bias, int64_t rows,
                  int64_t cols, void* stream);

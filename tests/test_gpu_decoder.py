@@ -303,3 +303,94 @@ def test_rope_first_pos_rotates_rows_at_their_position(ctx, pkg, torch, orc):
     assert np.array_equal(host(ql), rq[last])
     with pytest.raises(pkg.MoeInvalidArgument):  # the table has no position S
         ctx.rope(ql, None, B, 1, H, 0, hd, first_pos=S, table=ctx.rope_table(1e4, hd, S))
+
+
+# ------------------------------------------- prefix-trie rows (key lists)
+def _trie(seqs):
+    """One node per distinct prefix, in order of first appearance, as the
+    reference builds it (src/model.cu:1624-1680): node tokens, depths,
+    root paths flattened (CSR), the last node of every sequence."""
+    child, tok, depth, parent, last = {}, [], [], [], []
+    for seq in seqs:
+        p = -1
+        for pos, t in enumerate(seq):
+            key = (p, int(t))
+            if key not in child:
+                child[key] = len(tok)
+                tok.append(int(t))
+                depth.append(pos)
+                parent.append(p)
+            p = child[key]
+        last.append(p)
+    off, anc = [0], []
+    for n in range(len(tok)):
+        path = (anc[off[parent[n]]:off[parent[n] + 1]] if parent[n] >= 0 else []) + [n]
+        anc += path
+        off.append(len(anc))
+    return (np.array(tok, np.int32), np.array(depth, np.int32), np.array(anc, np.int32),
+            np.array(off, np.int32), np.array(last, np.int32))
+
+
+def test_rope_rows_at_explicit_positions(ctx, torch, orc):
+    rng = np.random.default_rng(31)
+    rows, H, KVH, hd = 50, 3, 1, 16
+    pos = rng.integers(0, 200, rows).astype(np.int32)
+    q, k = normal(rng, (rows, H * hd)), normal(rng, (rows, KVH * hd))
+    qd, kd = dev(torch, q), dev(torch, k)
+    ctx.rope_rows(qd, kd, ctx.rope_table(1e4, hd, 200), dev(torch, pos), rows, H, KVH, hd)
+    # the oracle with a table whose row r is the position of row r
+    t = orc.rope_table(1e4, hd, 200)[pos]
+    rq, rk = orc.rope(q, k, 1, rows, H, KVH, hd, table=t)
+    assert np.array_equal(host(qd), rq) and np.array_equal(host(kd), rk)
+
+
+@pytest.mark.parametrize("window", [None, 4])
+def test_attention_paths_over_a_trie_bit_exact(ctx, torch, orc, window):
+    # sequences with shared prefixes (and one that is a prefix of another):
+    # every node's result equals the oracle's attention over its sequence
+    rng = np.random.default_rng(32)
+    H, KVH, hd = 4, 2, 32
+    base = rng.integers(0, 50, 30)
+    seqs = [base[:30], base[:12], np.concatenate([base[:12], [7, 8, 9]]), base[:5],
+            rng.integers(0, 50, 21), np.concatenate([base[:20], rng.integers(0, 50, 9)])]
+    tok, depth, anc, off, last = _trie(seqs)
+    n = len(tok)
+    assert n < sum(len(s) for s in seqs)  # prefixes are shared
+    q = normal(rng, (n, H * hd))
+    k, v = normal(rng, (n, KVH * hd)), normal(rng, (n, KVH * hd))
+    out = torch.full((n, H * hd), float("nan"), device="cuda")
+    offd = dev(torch, off)
+    ctx.attention_paths(dev(torch, q), dev(torch, k), dev(torch, v), out, dev(torch, anc),
+                        offd[:-1], offd[1:], int(np.max(np.diff(off))), H, KVH, hd,
+                        window or 0)
+    got = host(out)
+    for b, seq in enumerate(seqs):
+        path = anc[off[last[b]]:off[last[b] + 1]]  # the sequence's nodes, by position
+        ref = orc.attention(q[path], k[path], v[path], 1, len(seq), H, KVH, hd, window)
+        assert np.array_equal(got[path], ref), f"sequence {b}"
+    # the last rows alone (the pruned layer's queries), key lists by begin/end
+    beg, end = off[last], off[last + 1]
+    out_l = torch.empty((len(seqs), H * hd), device="cuda")
+    ctx.attention_paths(dev(torch, q[last]), dev(torch, k), dev(torch, v), out_l,
+                        dev(torch, anc), dev(torch, beg), dev(torch, end),
+                        int(np.max(end - beg)), H, KVH, hd, window or 0)
+    assert np.array_equal(host(out_l), got[last])
+
+
+def test_attention_paths_refuses_lists_past_its_bounds(ctx, torch):
+    # a list longer than the stated max_len, or past key_rows: NaN rows, no
+    # access outside the buffers
+    H, hd = 2, 16
+    q = torch.ones((2, H * hd), device="cuda")
+    kv = torch.ones((40, H * hd), device="cuda")
+    rows = torch.arange(40, dtype=torch.int32, device="cuda")
+    beg = torch.tensor([0, 5], dtype=torch.int32, device="cuda")  # disjoint lists
+    end = torch.tensor([5, 40], dtype=torch.int32, device="cuda")
+    out = torch.zeros((2, H * hd), device="cuda")
+    ctx.attention_paths(q, kv, kv, out, rows, beg, end, 8200, H, H, hd)  # global-score path
+    got = host(out)
+    assert np.all(np.isfinite(got))
+    end2 = torch.tensor([5, 41], dtype=torch.int32, device="cuda")  # past key_rows
+    ctx.attention_paths(q, kv, kv, out, rows, beg, end2, 64, H, H, hd)
+    got = host(out)
+    assert np.all(np.isfinite(got[0])) and np.all(np.isnan(got[1]))
