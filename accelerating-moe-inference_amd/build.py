@@ -21,7 +21,8 @@ LIB = os.path.join(HERE, "libmoe_amd.so")
 HIP_SOURCES = ["gemm.hip", "route.hip", "elementwise.hip", "norm.hip", "attention.hip",
                "capi.hip"]
 DROPIN_LIB = os.path.join(HERE, "libmoe_dropin.so")
-DROPIN_SOURCES = ["device.cpp", "tensor.cpp", "model_loader.cpp", "layer.cpp"]
+DROPIN_SOURCES = ["device.cpp", "tensor.cpp", "model_loader.cpp", "layer.cpp", "model.cpp",
+                  "driver.cpp"]
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"

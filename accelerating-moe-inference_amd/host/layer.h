@@ -78,6 +78,23 @@ private:
     int contract_ = MOE_CONTRACT_FMA;
 };
 
+// Rows of a packed batch on the device (an extension the model uses): the
+// nodes of a prefix trie over the batch's sequences (src/model.cu:1624-1680),
+// one row per distinct prefix.  A node's keys are its root path.
+struct NodeRows {
+    std::size_t rows = 0;
+    const int32_t* positions = nullptr;  // [rows] depth of each node
+    const int32_t* key_rows = nullptr;   // root paths, flattened, ascending depth
+    const int32_t* key_off = nullptr;    // [rows + 1] offsets into key_rows
+    std::size_t key_total = 0, max_len = 0;
+    // The pruned last layer's rows: the last node of every sequence.
+    std::size_t tail_rows = 0;
+    const int32_t* tail_nodes = nullptr;      // [tail_rows]
+    const int32_t* tail_positions = nullptr;  // [tail_rows]
+    const int32_t* tail_key_beg = nullptr;    // [tail_rows] their root paths in key_rows
+    const int32_t* tail_key_end = nullptr;
+};
+
 class PhiAttention {
 public:
     // Loads model.layers.{layer_idx}.self_attn.{q,k,v,o}_proj.{weight,bias}
@@ -92,6 +109,9 @@ public:
     void forward_device(const float* dx, float* dy, std::size_t s) const;
     // s rounded up to the attention kernels' 16-row granule.
     static std::size_t padded_rows(std::size_t s) { return (s + 15) / 16 * 16; }
+    // Trie rows (an extension): dn [rows, hidden] normalised input; dy gets
+    // o_proj(attention) for every node, or (tail) for the tail rows only.
+    void forward_nodes(const float* dn, float* dy, const NodeRows& nb, bool tail) const;
     std::size_t hidden() const { return hidden_; }
 
 private:
@@ -106,6 +126,9 @@ public:
     PhiDecoderLayer(const ModelLoader& loader, std::size_t layer_idx);
     // y = h + MoE(layer_norm(h)), h = x + attention(layer_norm(x)); y is reassigned.
     void forward(const Tensor& x, Tensor& y) const;
+    // Trie rows (an extension): dx [rows, hidden] -> dy [rows, hidden], or
+    // (tail) dy [tail_rows, hidden] for the last node of every sequence.
+    void forward_nodes(const float* dx, float* dy, const NodeRows& nb, bool tail) const;
 
 private:
     std::shared_ptr<const moe_dropin::DeviceBuffer> in_w_, in_b_, post_w_, post_b_;

@@ -3,13 +3,16 @@
 // scenario as an extern "C" function for tests/test_dropin.py (ctypes).
 // Exceptions come back as codes: 1 invalid_argument, 2 runtime_error,
 // 3 logic_error, 4 out_of_range, 5 other; shim_error() holds the message.
+#include <cmath>
 #include <cstdint>
 #include <cstring>
 #include <stdexcept>
 #include <string>
 #include <vector>
 
+#include "driver.h"
 #include "layer.h"
+#include "model.h"
 #include "model_loader.h"
 #include "tensor.h"
 
@@ -286,6 +289,126 @@ int shim_decoder_layer(const char* path, int64_t layer, const float* x, int64_t 
         dec.forward(X, Y);
         expect(Y.ndim() == 2 && Y.size(0) == size_t(s) && Y.size(1) == size_t(h), "y shape");
         std::memcpy(y, Y.data(), Y.size() * sizeof(float));
+    });
+}
+
+// ---- PhiTinyMoEModel: sequences as lengths + concatenated ids.
+namespace {
+std::vector<std::vector<int>> unpack(const int32_t* lens, const int32_t* ids, int64_t batch) {
+    std::vector<std::vector<int>> seqs(static_cast<std::size_t>(batch));
+    std::size_t at = 0;
+    for (int64_t b = 0; b < batch; ++b) {
+        seqs[b].assign(ids + at, ids + at + lens[b]);
+        at += static_cast<std::size_t>(lens[b]);
+    }
+    return seqs;
+}
+}  // namespace
+
+int shim_model_generate(const char* path, const int32_t* lens, const int32_t* ids, int64_t batch,
+                        float* logits, int64_t vocab) {
+    return guarded([&] {
+        PhiTinyMoEModel m(path);
+        expect(m.vocab_size() == size_t(vocab), "vocab");
+        Tensor L;
+        m.generate(unpack(lens, ids, batch), L);
+        expect(L.ndim() == 2 && L.size(0) == size_t(batch) && L.size(1) == size_t(vocab), "shape");
+        std::memcpy(logits, L.data(), L.size() * sizeof(float));
+        // forward() of one sequence is generate() of a batch of one
+        Tensor one;
+        m.forward(unpack(lens, ids, 1)[0], one);
+        expect(one.ndim() == 2 && one.size(0) == 1, "forward shape");
+        for (std::size_t v = 0; v < size_t(vocab); ++v)
+            expect(std::fabs(one[v] - L[v]) <= 1e-4f * (1.0f + std::fabs(L[v])), "forward == row 0");
+    });
+}
+
+int shim_model_decode(const char* path, const int32_t* lens, const int32_t* ids, int64_t batch,
+                      int64_t max_new, float* logits, int32_t* gen_lens, int32_t* gen_ids) {
+    return guarded([&] {
+        PhiTinyMoEModel m(path);
+        Tensor L;
+        std::vector<std::vector<int>> gen;
+        m.generate_decode(unpack(lens, ids, batch), size_t(max_new), L, gen);
+        std::memcpy(logits, L.data(), L.size() * sizeof(float));
+        for (int64_t b = 0; b < batch; ++b) {
+            gen_lens[b] = static_cast<int32_t>(gen[b].size());
+            for (int64_t s = 0; s < max_new; ++s)
+                gen_ids[b * max_new + s] = s < int64_t(gen[b].size()) ? gen[b][s] : -1;
+        }
+    });
+}
+
+// Input errors of generate(): 1 empty batch, 2 empty sequence, 3 token past
+// the vocabulary, 4 sequence longer than MAX_POSITION_EMBEDDINGS.
+int shim_model_bad_input(const char* path, int which) {
+    return guarded([&] {
+        PhiTinyMoEModel m(path);
+        Tensor L;
+        std::vector<std::vector<int>> seqs;
+        if (which == 2) seqs = {{1, 2}, {}};
+        if (which == 3) seqs = {{1, int(m.vocab_size())}};
+        if (which == 4) seqs = {std::vector<int>(apss26::MAX_POSITION_EMBEDDINGS + 1, 1)};
+        m.generate(seqs, L);
+    });
+}
+
+// ---- driver formats
+int shim_read_inputs(const char* path, int64_t cap, int32_t* lens, int32_t* ids, int64_t* batch,
+                     int64_t* max_seq) {
+    return guarded([&] {
+        std::size_t ms = 0;
+        const auto seqs = moe_driver::read_inputs(path, ms);
+        *batch = int64_t(seqs.size());
+        *max_seq = int64_t(ms);
+        std::size_t at = 0;
+        for (std::size_t b = 0; b < seqs.size(); ++b) {
+            lens[b] = int32_t(seqs[b].size());
+            for (int t : seqs[b]) {
+                expect(int64_t(at) < cap, "capacity");
+                ids[at++] = t;
+            }
+        }
+    });
+}
+
+int shim_write_outputs(const char* path, const float* logits, int64_t batch, int64_t vocab) {
+    return guarded([&] {
+        moe_driver::write_outputs(path, make(logits, {size_t(batch), size_t(vocab)}));
+    });
+}
+
+// validate(output, read_answers(answer_path)); *passed = the verdict.
+int shim_validate(const char* answer_path, const float* output, int64_t batch, int64_t vocab,
+                  int* passed) {
+    return guarded([&] {
+        const Tensor ans = moe_driver::read_answers(answer_path, size_t(batch), size_t(vocab));
+        *passed = moe_driver::validate(make(output, {size_t(batch), size_t(vocab)}), ans) ? 1 : 0;
+    });
+}
+
+int shim_write_decode(const char* path, const float* logits, const int32_t* gen_lens,
+                      const int32_t* gen_ids, int64_t batch, int64_t steps, int64_t vocab) {
+    return guarded([&] {
+        std::vector<std::vector<int>> gen(static_cast<std::size_t>(batch));
+        for (int64_t b = 0; b < batch; ++b) gen[b].assign(gen_ids + b * steps, gen_ids + b * steps + gen_lens[b]);
+        moe_driver::write_decode_outputs(path, make(logits, {size_t(batch), size_t(steps), size_t(vocab)}), gen);
+    });
+}
+
+// validate_decode(output, ids, read_decode_answers(answer_path)).
+int shim_validate_decode(const char* answer_path, const float* logits, const int32_t* gen_lens,
+                         const int32_t* gen_ids, int64_t batch, int64_t steps, int64_t vocab,
+                         int* passed) {
+    return guarded([&] {
+        const auto ans = moe_driver::read_decode_answers(answer_path, size_t(batch), size_t(steps),
+                                                         size_t(vocab));
+        std::vector<std::vector<int>> gen(static_cast<std::size_t>(batch));
+        for (int64_t b = 0; b < batch; ++b) gen[b].assign(gen_ids + b * steps, gen_ids + b * steps + gen_lens[b]);
+        *passed = moe_driver::validate_decode(
+                      make(logits, {size_t(batch), size_t(steps), size_t(vocab)}), gen, ans)
+                      ? 1
+                      : 0;
     });
 }
 

@@ -312,3 +312,212 @@ def test_attention_and_decoder_layer_vs_oracle(shim, orc, tmp_path, s):
         err(shim)
     ref, _, _ = od.layer_forward(x, L, cfg, 1, s)
     assert_close(y, ref, what="PhiDecoderLayer")
+
+
+# ------------------------------------------------------ driver formats (CPU)
+def _write_inputs(path, seqs, batch=None, max_seq=None):
+    with open(path, "wb") as f:
+        f.write(struct.pack("<II", len(seqs) if batch is None else batch,
+                            max(len(s) for s in seqs) if max_seq is None else max_seq))
+        for s in seqs:
+            f.write(struct.pack("<I", len(s)) + np.asarray(s, np.int32).tobytes())
+
+
+def test_driver_read_inputs_and_its_errors(shim, tmp_path):
+    I = ctypes.c_int64
+    p = str(tmp_path / "inputs.bin")
+    seqs = [[5, 6, 7], list(range(10)), [31999]]
+    _write_inputs(p, seqs, max_seq=12)
+    lens, ids = np.zeros(8, np.int32), np.zeros(64, np.int32)
+    b, ms = I(), I()
+    assert shim.shim_read_inputs(p.encode(), I(64), fptr(lens), fptr(ids), ctypes.byref(b),
+                                 ctypes.byref(ms)) == 0, err(shim)
+    assert b.value == 3 and ms.value == 12 and lens[:3].tolist() == [3, 10, 1]
+    assert ids[:14].tolist() == sum(seqs, [])
+    cases = [(dict(batch=0), "invalid input header"), (dict(max_seq=4097), "invalid input header"),
+             (dict(max_seq=2), "invalid sequence length in input")]
+    for kw, msg in cases:
+        _write_inputs(p, seqs, **kw)
+        assert shim.shim_read_inputs(p.encode(), I(64), fptr(lens), fptr(ids), ctypes.byref(b),
+                                     ctypes.byref(ms)) == RUNTIME
+        assert err(shim) == msg
+    _write_inputs(p, [[1, 2], [3]])
+    raw = open(p, "rb").read()
+    open(p, "wb").write(raw[:-2])
+    assert shim.shim_read_inputs(p.encode(), I(64), fptr(lens), fptr(ids), ctypes.byref(b),
+                                 ctypes.byref(ms)) == RUNTIME and err(shim) == "truncated input"
+    missing = str(tmp_path / "none.bin")
+    assert shim.shim_read_inputs(missing.encode(), I(64), fptr(lens), fptr(ids), ctypes.byref(b),
+                                 ctypes.byref(ms)) == RUNTIME
+    assert err(shim) == "cannot open input: " + missing
+
+
+def test_driver_outputs_and_the_validation_rule(shim, tmp_path):
+    I = ctypes.c_int64
+    rng = np.random.default_rng(5)
+    out = normal(rng, (3, 7))
+    p = str(tmp_path / "outputs.bin")
+    assert shim.shim_write_outputs(p.encode(), fptr(out), I(3), I(7)) == 0, err(shim)
+    raw = open(p, "rb").read()
+    assert struct.unpack("<II", raw[:8]) == (3, 7)
+    assert np.array_equal(np.frombuffer(raw[8:], np.float32).reshape(3, 7), out)
+    ans = str(tmp_path / "answers.bin")
+
+    def verdict(answer, output):
+        answer.astype(np.float32).tofile(ans)
+        ok = ctypes.c_int(-1)
+        assert shim.shim_validate(ans.encode(), fptr(output), I(3), I(7), ctypes.byref(ok)) == 0
+        return ok.value
+
+    a = out.copy()
+    a[1, 2] = 1.0
+    assert verdict(a, a.copy()) == 1
+    o = a.copy(); o[1, 2] = 1.0025  # abs 2.5e-3 <= 3e-3
+    assert verdict(a, o) == 1
+    o = a.copy(); o[1, 2] = 1.01  # abs and rel 1e-2
+    assert verdict(a, o) == 0
+    a2 = a.copy(); a2[0, 0] = 1e-9  # near zero the rule is absolute
+    o = a2.copy(); o[0, 0] = 2e-3
+    assert verdict(a2, o) == 1
+    o[0, 0] = 1e-2
+    assert verdict(a2, o) == 0
+    big = a.copy(); big[2, 3] = 1000.0
+    o = big.copy(); o[2, 3] = 1002.0  # abs 2 but rel 2e-3
+    assert verdict(big, o) == 1
+    o = a.copy(); o[2, 6] = np.nan
+    assert verdict(a, o) == 0
+    a[:2].tofile(ans)  # too short
+    ok = ctypes.c_int(-1)
+    assert shim.shim_validate(ans.encode(), fptr(out), I(3), I(7), ctypes.byref(ok)) == RUNTIME
+    assert err(shim).startswith("invalid answer size: expected at least 84 bytes")
+
+
+def test_driver_decode_format_and_rule(shim, tmp_path):
+    I = ctypes.c_int64
+    rng = np.random.default_rng(6)
+    B, S, V = 2, 3, 50
+    logits = normal(rng, (B, S, V))
+    logits[1, 1:] = 0.0
+    lens = np.array([3, 1], np.int32)
+    gen = np.array([[4, 9, 2], [7, -1, -1]], np.int32)
+    p = str(tmp_path / "decode.bin")
+    assert shim.shim_write_decode(p.encode(), fptr(logits), fptr(lens), fptr(gen), I(B), I(S),
+                                  I(V)) == 0, err(shim)
+    raw = open(p, "rb").read()
+    assert struct.unpack("<III", raw[:12]) == (B, S, V)
+    assert np.frombuffer(raw[12:20], np.uint32).tolist() == [3, 1]
+    assert np.frombuffer(raw[20:44], np.int32).reshape(B, S).tolist() == gen.tolist()
+    assert np.array_equal(np.frombuffer(raw[44:], np.float32).reshape(B, S, V), logits)
+
+    def verdict(lg, ln, gn):
+        ok = ctypes.c_int(-1)
+        assert shim.shim_validate_decode(p.encode(), fptr(lg), fptr(ln), fptr(gn), I(B), I(S),
+                                         I(V), ctypes.byref(ok)) == 0, err(shim)
+        return ok.value
+
+    assert verdict(logits, lens, gen) == 1
+    g = gen.copy(); g[0, 1] = 5
+    assert verdict(logits, lens, g) == 0  # token
+    ln = lens.copy(); ln[1] = 2
+    g = gen.copy(); g[1, 1] = 3
+    assert verdict(logits, ln, g) == 0  # length
+    lg = logits.copy(); lg[0, 0, 3] += 0.05
+    assert verdict(lg, lens, gen) == 0  # step 0: the prefill rule
+    lg = logits.copy(); lg[0, 2] += 1e-3
+    assert verdict(lg, lens, gen) == 1  # later steps: vector statistics
+    lg = logits.copy(); lg[0, 2] += 0.5
+    assert verdict(lg, lens, gen) == 0
+    lg = logits.copy(); lg[0, 1, 0] = np.inf
+    assert verdict(lg, lens, gen) == 0
+    ok = ctypes.c_int(-1)
+    assert shim.shim_validate_decode(p.encode(), fptr(logits), fptr(lens), fptr(gen), I(B),
+                                     I(S + 1), I(V), ctypes.byref(ok)) == RUNTIME
+    assert err(shim) == "decode answer header mismatch"
+
+
+# ------------------------------------------------------ the model (GPU)
+def _model_tensors(rng, layers, h, E, ff, vocab):
+    t = {"model.embed_tokens.weight": normal(rng, (vocab, h)),
+         "model.norm.weight": 1 + normal(rng, (h,), 0.1), "model.norm.bias": normal(rng, (h,), 0.1),
+         "lm_head.weight": normal(rng, (vocab, h), 0.02), "lm_head.bias": normal(rng, (vocab,), 0.02)}
+    for li in range(layers):
+        t.update(_decoder_layer_tensors(rng, li, h, E, ff))
+    return t
+
+
+def _oracle_model(orc, t, layers, E):
+    import types
+    W = {"embed": t["model.embed_tokens.weight"], "final_norm_w": t["model.norm.weight"],
+         "final_norm_b": t["model.norm.bias"], "lm_head_w": t["lm_head.weight"],
+         "lm_head_b": t["lm_head.bias"], "layers": [_oracle_layer(t, li, E) for li in range(layers)]}
+    cfg = types.SimpleNamespace(norm="layer", norm_eps=1e-5, heads=16, kv_heads=4, head_dim=128,
+                                rope_theta=10000.0, window=2047, top_k=2,
+                                router=orc.ROUTER_PHI_QUANT, contract=orc.CONTRACT_FMA, layers=layers)
+    return W, cfg
+
+
+@pytest.mark.gpu
+def test_model_generate_and_decode_vs_oracle(shim, orc, tmp_path):
+    # a batch with shared prefixes, a duplicate and a sequence that is a
+    # prefix of another: the trie computes each prefix once; every sequence's
+    # logits must equal the oracle's run of that sequence alone
+    from oracle import decoder as od
+    rng = np.random.default_rng(50)
+    L, h, E, ff, V = 2, 256, 4, 64, 32064
+    t = _model_tensors(rng, L, h, E, ff, V)
+    path = str(tmp_path / "model.bin")
+    write_model_bin(path, t)
+    W, cfg = _oracle_model(orc, t, L, E)
+    base = rng.integers(0, 32000, 24)
+    seqs = [base[:24], base[:9], np.concatenate([base[:9], [11, 12]]), base[:24],
+            rng.integers(0, 32000, 17), base[:1]]
+    lens = np.array([len(s) for s in seqs], np.int32)
+    ids = np.concatenate(seqs).astype(np.int32)
+    I = ctypes.c_int64
+    got = np.empty((len(seqs), V), np.float32)
+    assert shim.shim_model_generate(path.encode(), fptr(lens), fptr(ids), I(len(seqs)), fptr(got),
+                                    I(V)) == 0, err(shim)
+    for b, s in enumerate(seqs):
+        ref, _, _ = od.generate(np.asarray(s)[None, :], W, cfg)
+        assert_close(got[b], ref[0], what=f"sequence {b}")
+    # greedy decode of 3 tokens: the oracle's loop over each sequence alone
+    steps = 3
+    dl = np.empty((len(seqs), steps, V), np.float32)
+    gl = np.empty(len(seqs), np.int32)
+    gi = np.empty((len(seqs), steps), np.int32)
+    assert shim.shim_model_decode(path.encode(), fptr(lens), fptr(ids), I(len(seqs)), I(steps),
+                                  fptr(dl), fptr(gl), fptr(gi)) == 0, err(shim)
+    for b, s in enumerate(seqs[:4]):
+        prefix = list(s)
+        for st in range(steps):
+            ref, _, _ = od.generate(np.asarray(prefix)[None, :], W, cfg)
+            nxt = int(np.argmax(ref[0]))
+            assert gi[b, st] == nxt, f"sequence {b} step {st}"
+            assert_close(dl[b, st], ref[0], what=f"decode logits {b},{st}")
+            prefix.append(nxt)
+        assert gl[b] == steps
+
+
+@pytest.mark.gpu
+def test_model_decode_stops_at_eos_and_rejects_bad_input(shim, orc, tmp_path):
+    rng = np.random.default_rng(51)
+    L, h, E, ff, V = 1, 256, 4, 64, 32064
+    t = _model_tensors(rng, L, h, E, ff, V)
+    t["lm_head.bias"][32000] = 100.0  # EOS wins every step
+    path = str(tmp_path / "model.bin")
+    write_model_bin(path, t)
+    I = ctypes.c_int64
+    lens = np.array([5, 3], np.int32)
+    ids = rng.integers(0, 32000, 8).astype(np.int32)
+    dl = np.full((2, 4, V), 7.0, np.float32)
+    gl = np.empty(2, np.int32)
+    gi = np.empty((2, 4), np.int32)
+    assert shim.shim_model_decode(path.encode(), fptr(lens), fptr(ids), I(2), I(4), fptr(dl),
+                                  fptr(gl), fptr(gi)) == 0, err(shim)
+    assert gl.tolist() == [1, 1] and gi[:, 0].tolist() == [32000, 32000]
+    assert np.all(gi[:, 1:] == -1) and np.all(dl[:, 1:] == 0.0) and np.all(dl[:, 0] != 0.0)
+    want = {1: (RUNTIME, "generate received an empty input batch"), 2: (INVALID, "empty input"),
+            3: (INVALID, "token out of vocabulary"), 4: (INVALID, "sequence is too long")}
+    for which, (code, msg) in want.items():
+        assert shim.shim_model_bad_input(path.encode(), which) == code, which
+        assert err(shim) == msg
