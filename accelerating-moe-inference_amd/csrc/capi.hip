@@ -233,17 +233,39 @@ int64_t grouped_m_tiles(int64_t pairs, int64_t E, int bm) {
 // slots.  The smallest S in {1, 2, 4} whose fill reaches 95 % is taken (else
 // the best); each split must be a multiple of 16 columns.  MOE_W2_SPLITS
 // overrides for tuning.
-int choose_w2_splits(moe_ctx* ctx, int64_t pairs, int64_t d, int64_t d_ff, int64_t E) {
+struct W2Plan {
+    int tile;    // GemmArgs::tile of the w2 launch: 0 wide (W2), 1 128x128 (W2Narrow)
+    int splits;  // K splits
+};
+
+int choose_w2_splits(moe_ctx* ctx, int64_t pairs, int64_t d, int64_t d_ff, int64_t E, int w2_tile);
+
+// The w2 plan of a layer: the tile and its K splits.  The wide tile (its
+// 256 columns halve the B traffic per MFMA) unless d gives it at most 4
+// n-tiles: then each expert's rows form so few tiles that the 128x128 tile's
+// extra parallelism wins (a tile x split sweep on MI355X: config 5, d = 1024,
+// 1.545 -> 1.488 ms per layer; configs 3 and 4, with 16 and 8 wide n-tiles,
+// 3-5 % slower on the narrow tile).  MOE_W2_TILE = 0 / 1 overrides.
+W2Plan choose_w2_plan(moe_ctx* ctx, int64_t pairs, int64_t d, int64_t d_ff, int64_t E) {
+    static const int env_tile = env_int("MOE_W2_TILE", -1);
+    int tile = moe::ceil_div(d, moe::gemm_tile(moe::GemmUse::W2).bn) <= 4 ? 1 : 0;
+    if (env_tile == 0 || env_tile == 1) tile = env_tile;
+    return {tile, choose_w2_splits(ctx, pairs, d, d_ff, E, tile)};
+}
+
+int choose_w2_splits(moe_ctx* ctx, int64_t pairs, int64_t d, int64_t d_ff, int64_t E, int w2_tile) {
     static const int env = [] {
         const char* v = std::getenv("MOE_W2_SPLITS");
         return v != nullptr ? std::atoi(v) : 0;
     }();
     auto allowed = [&](int S) { return S == 1 || (d_ff > 0 && d_ff % (16 * S) == 0); };
     if (env == 1 || env == 2 || env == 4) return allowed(env) ? env : 1;
-    if (ctx->w2_blocks_per_cu == 0) ctx->w2_blocks_per_cu = moe::gemm_blocks_per_cu(moe::GemmUse::W2);
-    const moe::GemmTile tile = moe::gemm_tile(moe::GemmUse::W2);
+    const moe::GemmUse use = w2_tile == 1 ? moe::GemmUse::W2Narrow : moe::GemmUse::W2;
+    int& occ = w2_tile == 1 ? ctx->w2n_blocks_per_cu : ctx->w2_blocks_per_cu;
+    if (occ == 0) occ = moe::gemm_blocks_per_cu(use);
+    const moe::GemmTile tile = moe::gemm_tile(use);
     const double tiles = double(grouped_m_tiles(pairs, E, tile.bm) * moe::ceil_div(d, tile.bn));
-    const double slots = double(int64_t(ctx->cus) * ctx->w2_blocks_per_cu);
+    const double slots = double(int64_t(ctx->cus) * occ);
     int best = 1;
     double best_fill = 0.0;
     for (int S : {1, 2, 4}) {
@@ -265,7 +287,7 @@ void expert_ffn(moe_ctx* ctx, const float* x, const int32_t* perm,
                 const int32_t* offsets, const float* w1, const float* w3,
                 const float* w2, int act, int64_t T, int64_t k, int64_t d,
                 int64_t d_ff, int64_t E, float* h, float* out_rows, hipStream_t s,
-                int w2_splits = 1) {
+                int w2_splits = 1, int w2_tile = 0) {
     const int64_t pairs = T * k;
     if (pairs == 0 || d == 0) return;
     const bool swiglu = act == MOE_ACT_SWIGLU;
@@ -295,8 +317,10 @@ void expert_ffn(moe_ctx* ctx, const float* x, const int32_t* perm,
             moe::launch_gemm(a, false, true, swiglu ? moe::EPI_SWIGLU : moe::EPI_SILU, vec, s);
         });
     }
-    const moe::GemmTile tile = moe::gemm_tile(moe::GemmUse::W2);
+    const moe::GemmTile tile =
+        moe::gemm_tile(w2_tile == 1 ? moe::GemmUse::W2Narrow : moe::GemmUse::W2);
     moe::GemmArgs b{};
+    b.tile = w2_tile;
     b.A = d_ff > 0 ? h : out_rows;
     b.lda = d_ff;
     b.B0 = d_ff > 0 ? w2 : out_rows;
@@ -1028,9 +1052,10 @@ int moe_layer_forward(moe_ctx* ctx, const moe_layer_desc* desc,
         ctx->launch("perm_place", s, [&] {
             moe::launch_perm_place(idx, D.T, D.k, D.E, ws.counts, ws.perm, ws.inv, s);
         });
-        const int splits = choose_w2_splits(ctx, D.T * D.k, D.d, D.d_ff, D.E);
+        const W2Plan plan = choose_w2_plan(ctx, D.T * D.k, D.d, D.d_ff, D.E);
+        const int splits = plan.splits;
         expert_ffn(ctx, xin, ws.perm, ws.offsets, weights->w1, weights->w3, weights->w2, D.act,
-                   D.T, D.k, D.d, D.d_ff, D.E, ws.h, ws.out_rows, s, splits);
+                   D.T, D.k, D.d, D.d_ff, D.E, ws.h, ws.out_rows, s, splits, plan.tile);
         ctx->launch("combine", s, [&] {
             moe::launch_combine(ws.out_rows, idx, w, ws.inv, D.residual ? x : nullptr, y, D.T,
                                 D.k, D.d, D.T * D.k, D.contract, splits, D.T * D.k * D.d, s);
@@ -1044,7 +1069,7 @@ int moe_layer_w2_splits(moe_ctx* ctx, const moe_layer_desc* desc, int32_t* split
         check_desc(desc);
         check_ptr(splits, "splits");
         DeviceScope dev(ctx->device);
-        *splits = choose_w2_splits(ctx, desc->T * desc->k, desc->d, desc->d_ff, desc->E);
+        *splits = choose_w2_plan(ctx, desc->T * desc->k, desc->d, desc->d_ff, desc->E).splits;
     });
 }
 

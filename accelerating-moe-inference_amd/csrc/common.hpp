@@ -40,7 +40,9 @@ constexpr int kNumXcd = 8;  // MI355X: 8 XCDs, workgroups dealt round-robin
 constexpr int kGemmGroupM = 0;
 
 // The GEMM uses whose tile shape the host needs for grid sizing.
-enum class GemmUse { Dense, W13, W2 };
+// W2Narrow: the w2 GEMM on the 128x128 tile (GemmArgs::tile = 1 on the
+// grouped EPI_STORE path), for widths d whose wide tile leaves few n-tiles.
+enum class GemmUse { Dense, W13, W2, W2Narrow };
 struct GemmTile {
     int bm, bn;
 };
@@ -88,7 +90,7 @@ struct GemmArgs {
     int32_t k_splits;        // K ranges computed by separate tiles (>= 1)
     int64_t k_split_len;     // K per split (a multiple of 16)
     int64_t c_split_stride;  // elements between the outputs of consecutive splits
-    int32_t tile;            // dense: tile shape (kDenseTiles)
+    int32_t tile;            // dense: tile shape (kDenseTiles); grouped w2: 1 = 128x128
     // Batched dense GEMMs (attention; grid.y = batches): batch z splits into
     // zo = z / batch_inner, zi = z % batch_inner, and the operands start at
     // A + zo*a_so + zi*a_si, B + zo*b_so + (zi / b_group)*b_si,
@@ -186,6 +188,7 @@ struct moe_ctx {
     int device = 0;
     int cus = 0;               // compute units of the device
     int w2_blocks_per_cu = 0;  // occupancy of the grouped w2 kernel (lazily queried)
+    int w2n_blocks_per_cu = 0;  // ... of its 128x128-tile variant
     int dense_blocks_per_cu[2][moe::kDenseTiles] = {};  // [nn][tile], lazily queried
     void* ws = nullptr;
     size_t ws_bytes = 0;

@@ -701,6 +701,7 @@ using DenseMidCfg = CfgOf<8>::T;
 using DenseSmallCfg = CfgOf<9>::T;
 using W13Cfg = CfgOf<MOE_W13_CFG>::T;
 using W2Cfg = CfgOf<MOE_W2_CFG>::T;
+using W2NarrowCfg = CfgOf<0>::T;  // w2 with d too narrow for the wide tile's n-tiles
 
 template <class C, bool NN>
 void launch_dense(const GemmArgs& a, bool vec, hipStream_t s) {
@@ -780,6 +781,11 @@ int gemm_blocks_per_cu(GemmUse use) {
         e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, 0);
     };
     switch (use) {
+        case GemmUse::W2Narrow:
+            query(gemm_direct_kernel<W2NarrowCfg, MOE_W2_SCHED | SCHED_DIRECT, false, true, 1,
+                                     EPI_STORE>,
+                  W2NarrowCfg::THREADS);
+            break;
         case GemmUse::W2:
             if constexpr ((MOE_W2_SCHED & SCHED_DIRECT) != 0 && W2Cfg::BK == 16)
                 query(gemm_direct_kernel<W2Cfg, MOE_W2_SCHED, false, true, 1, EPI_STORE>,
@@ -805,6 +811,7 @@ GemmTile gemm_tile(GemmUse use) {
     switch (use) {
         case GemmUse::Dense: return {DenseCfg::BM, DenseCfg::BN};
         case GemmUse::W13: return {W13Cfg::BM, W13Cfg::BN};
+        case GemmUse::W2Narrow: return {W2NarrowCfg::BM, W2NarrowCfg::BN};
         default: return {W2Cfg::BM, W2Cfg::BN};
     }
 }
@@ -850,7 +857,13 @@ void launch_gemm(const GemmArgs& args, bool nn, bool grouped, int epi, bool vec,
     switch (epi) {
         case EPI_SWIGLU: launch_cfg<W13Cfg, MOE_W13_SCHED, false, true, 2, EPI_SWIGLU>(a, vec, s); break;
         case EPI_SILU: launch_cfg<W13Cfg, MOE_W13_SCHED, false, true, 1, EPI_SILU>(a, vec, s); break;
-        case EPI_STORE: launch_cfg<W2Cfg, MOE_W2_SCHED, false, true, 1, EPI_STORE>(a, vec, s); break;
+        case EPI_STORE:
+            if (a.tile == 1)
+                launch_cfg<W2NarrowCfg, MOE_W2_SCHED | SCHED_DIRECT, false, true, 1, EPI_STORE>(
+                    a, vec, s);
+            else
+                launch_cfg<W2Cfg, MOE_W2_SCHED, false, true, 1, EPI_STORE>(a, vec, s);
+            break;
         default: throw Unsupported("grouped GEMM epilogue");
     }
 }
