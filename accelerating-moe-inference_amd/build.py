@@ -19,7 +19,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libmoe_amd.so")
 HIP_SOURCES = ["gemm.hip", "route.hip", "elementwise.hip", "norm.hip", "attention.hip",
-               "capi.hip"]
+               "flash.hip", "capi.hip"]
 DROPIN_LIB = os.path.join(HERE, "libmoe_dropin.so")
 DROPIN_SOURCES = ["device.cpp", "tensor.cpp", "model_loader.cpp", "layer.cpp", "model.cpp",
                   "driver.cpp"]

@@ -673,15 +673,26 @@ int moe_attention(moe_ctx* ctx, const float* q, const float* k, const float* v, 
         check_ptr(k, "k");
         check_ptr(v, "v");
         check_ptr(out, "out");
-        if (head_dim % 16 != 0 || seq_len % 16 != 0 || !aligned16(q) || !aligned16(k) ||
-            !aligned16(v) || !aligned16(out))
-            throw moe::Unsupported(
-                "attention needs head_dim and seq_len multiples of 16 and 16-byte aligned q/k/v/out");
         const int64_t w = window >= seq_len ? 0 : window;
         const int64_t zb = batch * q_heads;
         moe::require(zb <= 65535, "attention: batch * q_heads exceeds the grid's y range");
+        const bool aligned = aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out);
         DeviceScope dev(ctx->device);
         hipStream_t s = as_stream(stream);
+        // head_dim 64 / 128: one fused pass, any seq_len, no workspace
+        // (MOE_ATTN_FLASH=0 keeps the three-launch path, for comparison)
+        static const int flash = env_int("MOE_ATTN_FLASH", 1);
+        if (flash != 0 && aligned && (head_dim == 64 || head_dim == 128)) {
+            ctx->launch("attn_flash", s, [&] {
+                moe::launch_flash_attention(q, k, v, out, batch, seq_len, q_heads, kv_heads,
+                                            head_dim, w, s);
+            });
+            return;
+        }
+        if (head_dim % 16 != 0 || seq_len % 16 != 0 || !aligned)
+            throw moe::Unsupported(
+                "attention needs head_dim 64 or 128, or head_dim and seq_len multiples of 16, "
+                "and 16-byte aligned q/k/v/out");
         const int64_t S = seq_len, qw = q_heads * head_dim, kw = kv_heads * head_dim;
         float* scores = static_cast<float*>(ctx->workspace(size_t(zb) * S * S * sizeof(float)));
         // scores[b, h] = Q[b, :, h] K[b, :, h / group]^T   (queries x keys)

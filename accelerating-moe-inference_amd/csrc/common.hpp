@@ -139,6 +139,11 @@ void launch_attn_paths(const float* q, const float* k, const float* v, float* ou
                        const int32_t* key_end, int64_t nq, int64_t kv_rows, int64_t max_len,
                        int64_t key_total, int64_t scores_floats, int64_t q_heads,
                        int64_t kv_heads, int64_t head_dim, int64_t window, hipStream_t s);
+// Causal attention in one pass, scores on chip (head_dim 64 or 128; false:
+// another head_dim, nothing launched).  16-byte aligned q, k, v, out.
+bool launch_flash_attention(const float* q, const float* k, const float* v, float* out,
+                            int64_t batch, int64_t seq_len, int64_t q_heads, int64_t kv_heads,
+                            int64_t head_dim, int64_t window, hipStream_t s);
 void launch_attn_softmax(float* scores, int64_t batches, int64_t seq_len, int64_t head_dim,
                          int64_t window, hipStream_t s);
 // a[i] += b[i];  a[r, c] += bias[c];  out[i, :] = table[tokens[i], :]

@@ -76,10 +76,14 @@ def test_rope_longer_table_and_errors(ctx, pkg, torch, orc):
 # ------------------------------------------------------------- attention
 # (B, S, Hq, Hkv, hd, window): one tile; grouped query heads; a window inside
 # one tile and across tiles; several 128-row tiles of a 64-wide head; a
-# window of exactly S (unlimited); config 5's full prefill shape.
+# window of exactly S (unlimited); config 5's full prefill shape.  head_dim
+# 64 and 128 take the fused kernel (any S: 1, 37, 200, 300 below), the
+# others the batched-GEMM path.
 ATTN_CASES = [(1, 16, 1, 1, 16, None), (2, 48, 4, 2, 16, None), (2, 48, 4, 2, 16, 5),
               (1, 160, 2, 1, 64, None), (1, 160, 2, 1, 64, 130), (2, 272, 3, 3, 32, 20),
-              (1, 144, 4, 1, 48, 144), (8, 512, 16, 16, 64, None)]
+              (1, 144, 4, 1, 48, 144), (8, 512, 16, 16, 64, None), (3, 1, 2, 1, 64, None),
+              (2, 37, 4, 2, 64, None), (1, 300, 2, 2, 128, None), (2, 200, 4, 1, 128, 50),
+              (1, 129, 16, 4, 128, 33)]
 
 
 @pytest.mark.parametrize("B,S,H,KVH,hd,window", ATTN_CASES)
@@ -111,7 +115,7 @@ def test_attention_after_rope_matches_the_oracle_chain(ctx, torch, orc):
 
 def test_attention_unsupported_and_invalid_shapes(ctx, pkg, torch):
     z = torch.zeros(4096, device="cuda")
-    with pytest.raises(pkg.MoeRuntimeError):  # seq_len not a multiple of 16
+    with pytest.raises(pkg.MoeRuntimeError):  # seq_len not a multiple of 16 (head_dim 16)
         ctx.attention(z, z, z, z, 1, 20, 2, 2, 16)
     with pytest.raises(pkg.MoeRuntimeError):  # head_dim not a multiple of 16
         ctx.attention(z, z, z, z, 1, 16, 2, 2, 8)
