@@ -52,9 +52,19 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(const float* __restrict
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lq = lane & 31, half = lane >> 5;
-    const int64_t z = blockIdx.y, b = z / H, h = z % H, kh = h / (H / KVH);
+    // Causal work grows with the tile index (tile t walks 4t + 4 key blocks).
+    // Workgroups half a grid apart share a CU when the grid fills two per CU
+    // (the dispatcher deals ids round-robin over the XCDs and their CUs), so
+    // the order is tile-major with heavy and light tiles interleaved -- rank
+    // r < T/2 takes tile T-1-r, the rest tile r - T/2 -- and each CU gets a
+    // heavy and a light tile (measured: 0.41 -> 0.29 ms per config-5 prefill).
+    const int64_t T = gridDim.x, BH = gridDim.y;
+    const int64_t L = static_cast<int64_t>(blockIdx.y) * T + blockIdx.x;
+    const int64_t rank = L / BH, z = L % BH;
+    const int64_t tile = rank < (T + 1) / 2 ? T - 1 - rank : rank - (T + 1) / 2;
+    const int64_t b = z / H, h = z % H, kh = h / (H / KVH);
     const int64_t qw = H * HD, kw = KVH * HD;
-    const int64_t row0 = static_cast<int64_t>(blockIdx.x) * kQTile;
+    const int64_t row0 = tile * kQTile;
     const int64_t q0 = row0 + 32 * wave;              // this wave's first query
     const int64_t qi = q0 + lq;                       // this lane's query
     const bool wave_live = q0 < S;
