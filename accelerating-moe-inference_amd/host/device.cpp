@@ -2,6 +2,7 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <memory>
@@ -91,6 +92,27 @@ void DeviceBuffer::download(void* dst, std::size_t bytes) const {
     if (bytes == 0) return;
     if (bytes > n_) throw std::invalid_argument("device download out of range");
     hip(hipMemcpy(dst, p_, bytes, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+}
+
+void* Scratch::get(std::size_t slot, std::size_t bytes) {
+    if (slot >= bufs_.size()) bufs_.resize(slot + 1);
+    DeviceBuffer& b = bufs_[slot];
+    if (b.bytes() < bytes || b.get() == nullptr) {
+        const std::size_t grow = std::max(bytes, b.bytes() + b.bytes() / 2);
+        b = DeviceBuffer(std::max<std::size_t>(grow, 16));  // frees the old one (synchronising)
+    }
+    return b.get();
+}
+
+void Scratch::download(std::size_t slot, void* dst, std::size_t bytes) const {
+    if (slot >= bufs_.size()) throw std::invalid_argument("scratch slot never filled");
+    bufs_[slot].download(dst, bytes);
+}
+
+const int32_t* Scratch::upload(std::size_t slot, const int32_t* src, std::size_t count) {
+    int32_t* p = i32(slot, count);
+    bufs_[slot].upload(src, count * sizeof(int32_t));
+    return p;
 }
 
 }  // namespace moe_dropin

@@ -4,6 +4,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <vector>
 
 #include "../../include/moe_amd.h"
 
@@ -41,6 +42,28 @@ public:
 private:
     void* p_ = nullptr;
     std::size_t n_ = 0;
+};
+
+// Grow-only device scratch, one buffer per slot (the reference's Scratch,
+// src/model.cu:1294-1324): a slot reallocates only when a call asks for more
+// than it holds, so repeated calls of one shape allocate nothing.  Not safe
+// for concurrent use.
+class Scratch {
+public:
+    float* f32(std::size_t slot, std::size_t count) {
+        return static_cast<float*>(get(slot, count * sizeof(float)));
+    }
+    int32_t* i32(std::size_t slot, std::size_t count) {
+        return static_cast<int32_t*>(get(slot, count * sizeof(int32_t)));
+    }
+    // Copies count host values into the slot and returns its device copy.
+    const int32_t* upload(std::size_t slot, const int32_t* src, std::size_t count);
+    // Copies the slot's first `bytes` bytes to the host (synchronous).
+    void download(std::size_t slot, void* dst, std::size_t bytes) const;
+
+private:
+    std::vector<DeviceBuffer> bufs_;
+    void* get(std::size_t slot, std::size_t bytes);
 };
 
 }  // namespace moe_dropin

@@ -273,42 +273,42 @@ void PhiAttention::forward(const Tensor& x, Tensor& y) const {
     dy.download(y.data(), s * hidden_ * sizeof(float));
 }
 
-void PhiAttention::forward_nodes(const float* dn, float* dy, const NodeRows& nb,
-                                 bool tail) const {
+void PhiAttention::forward_nodes(const float* dn, float* dy, const NodeRows& nb, bool tail,
+                                 moe_dropin::Scratch& sc) const {
     const std::size_t H = apss26::NUM_ATTENTION_HEADS, KVH = apss26::NUM_KV_HEADS,
                       hd = apss26::HEAD_DIM;
     const std::size_t rows = nb.rows, nq = tail ? nb.tail_rows : rows;
     if (rows == 0 || nq == 0) return;
     moe_ctx* ctx = moe_dropin::context();
-    DeviceBuffer k(rows * KVH * hd * sizeof(float)), v(rows * KVH * hd * sizeof(float)),
-        q(nq * H * hd * sizeof(float)), a(nq * H * hd * sizeof(float));
-    sgemm_nt(dn, *wk_, bk_, k.as<float>(), rows, KVH * hd, hidden_);
-    sgemm_nt(dn, *wv_, bv_, v.as<float>(), rows, KVH * hd, hidden_);
+    float* k = sc.f32(kSlotK, rows * KVH * hd);
+    float* v = sc.f32(kSlotV, rows * KVH * hd);
+    float* q = sc.f32(kSlotQ, nq * H * hd);
+    float* a = sc.f32(kSlotAttn, nq * H * hd);
+    sgemm_nt(dn, *wk_, bk_, k, rows, KVH * hd, hidden_);
+    sgemm_nt(dn, *wv_, bv_, v, rows, KVH * hd, hidden_);
     if (tail) {  // q of the last node of every sequence only
-        DeviceBuffer dt(nq * hidden_ * sizeof(float));
+        float* dt = sc.f32(kSlotTailIn, nq * hidden_);
         check(moe_embed(ctx, dn, nb.tail_nodes, static_cast<int64_t>(nq),
-                        static_cast<int64_t>(hidden_), static_cast<int64_t>(rows),
-                        dt.as<float>(), nullptr));
-        sgemm_nt(dt.as<float>(), *wq_, bq_, q.as<float>(), nq, H * hd, hidden_);
+                        static_cast<int64_t>(hidden_), static_cast<int64_t>(rows), dt, nullptr));
+        sgemm_nt(dt, *wq_, bq_, q, nq, H * hd, hidden_);
     } else {
-        sgemm_nt(dn, *wq_, bq_, q.as<float>(), rows, H * hd, hidden_);
+        sgemm_nt(dn, *wq_, bq_, q, rows, H * hd, hidden_);
     }
     const auto P = static_cast<int64_t>(rope_positions_);
-    check(moe_rope_rows(ctx, nullptr, k.as<float>(), rope_->as<float>(), P, nb.positions,
+    check(moe_rope_rows(ctx, nullptr, k, rope_->as<float>(), P, nb.positions,
                         static_cast<int64_t>(rows), 0, static_cast<int64_t>(KVH),
                         static_cast<int64_t>(hd), nullptr));
-    check(moe_rope_rows(ctx, q.as<float>(), nullptr, rope_->as<float>(), P,
+    check(moe_rope_rows(ctx, q, nullptr, rope_->as<float>(), P,
                         tail ? nb.tail_positions : nb.positions, static_cast<int64_t>(nq),
                         static_cast<int64_t>(H), 0, static_cast<int64_t>(hd), nullptr));
-    check(moe_attention_paths(ctx, q.as<float>(), k.as<float>(), v.as<float>(), a.as<float>(),
-                              static_cast<int64_t>(nq), static_cast<int64_t>(rows), nb.key_rows,
+    check(moe_attention_paths(ctx, q, k, v, a, static_cast<int64_t>(nq), static_cast<int64_t>(rows), nb.key_rows,
                               tail ? nb.tail_key_beg : nb.key_off,
                               tail ? nb.tail_key_end : nb.key_off + 1,
                               static_cast<int64_t>(nb.max_len),
                               static_cast<int64_t>(nb.key_total), static_cast<int64_t>(H),
                               static_cast<int64_t>(KVH), static_cast<int64_t>(hd),
                               static_cast<int64_t>(apss26::SLIDING_WINDOW), nullptr));
-    sgemm_nt(a.as<float>(), *wo_, bo_, dy, nq, hidden_, H * hd);
+    sgemm_nt(a, *wo_, bo_, dy, nq, hidden_, H * hd);
 }
 
 // --------------------------------------------------------- PhiDecoderLayer
@@ -355,25 +355,26 @@ void PhiDecoderLayer::forward(const Tensor& x, Tensor& y) const {
 // The layer over trie rows; with `tail` (the reference's pruned last layer,
 // src/model.cu:1889-1960) the norm, k and v still cover every node, and the
 // rest runs on the last node of every sequence.
-void PhiDecoderLayer::forward_nodes(const float* dx, float* dy, const NodeRows& nb,
-                                    bool tail) const {
+void PhiDecoderLayer::forward_nodes(const float* dx, float* dy, const NodeRows& nb, bool tail,
+                                    moe_dropin::Scratch& sc) const {
     const std::size_t h = attention_.hidden(), rows = nb.rows;
     const std::size_t n = tail ? nb.tail_rows : rows;
     if (rows == 0 || n == 0) return;
     moe_ctx* ctx = moe_dropin::context();
-    DeviceBuffer dn(rows * h * sizeof(float)), da(n * h * sizeof(float));
+    float* dn = sc.f32(kSlotNorm, rows * h);
+    float* da = sc.f32(kSlotAttnOut, n * h);
     check(moe_layer_norm(ctx, dx, in_w_->as<float>(), in_b_->as<float>(), apss26::NORM_EPS,
-                         static_cast<int64_t>(rows), static_cast<int64_t>(h), MOE_CONTRACT_FMA,
-                         dn.as<float>(), nullptr, nullptr, nullptr));
-    attention_.forward_nodes(dn.as<float>(), da.as<float>(), nb, tail);
+                         static_cast<int64_t>(rows), static_cast<int64_t>(h), MOE_CONTRACT_FMA, dn,
+                         nullptr, nullptr, nullptr));
+    attention_.forward_nodes(dn, da, nb, tail, sc);
     if (tail) {
-        DeviceBuffer dr(n * h * sizeof(float));
+        float* dr = sc.f32(kSlotTailResid, n * h);
         check(moe_embed(ctx, dx, nb.tail_nodes, static_cast<int64_t>(n), static_cast<int64_t>(h),
-                        static_cast<int64_t>(rows), dr.as<float>(), nullptr));
-        check(moe_add(ctx, da.as<float>(), dr.as<float>(), static_cast<int64_t>(n * h), nullptr));
+                        static_cast<int64_t>(rows), dr, nullptr));
+        check(moe_add(ctx, da, dr, static_cast<int64_t>(n * h), nullptr));
     } else {
-        check(moe_add(ctx, da.as<float>(), dx, static_cast<int64_t>(n * h), nullptr));
+        check(moe_add(ctx, da, dx, static_cast<int64_t>(n * h), nullptr));
     }
-    moe_.forward_device(da.as<float>(), dy, n, MOE_NORM_LAYER, post_w_->as<float>(),
-                        post_b_->as<float>(), 1, nullptr);
+    moe_.forward_device(da, dy, n, MOE_NORM_LAYER, post_w_->as<float>(), post_b_->as<float>(), 1,
+                        nullptr);
 }

@@ -24,7 +24,14 @@
 
 namespace moe_dropin {
 class DeviceBuffer;
+class Scratch;
 }
+
+// Scratch slots of the trie-row path (the model's own start at kSlotModel).
+enum NodeSlot : std::size_t {
+    kSlotK, kSlotV, kSlotQ, kSlotAttn, kSlotTailIn, kSlotNorm, kSlotAttnOut, kSlotTailResid,
+    kSlotModel = 16
+};
 
 class Linear {
 public:
@@ -111,7 +118,8 @@ public:
     static std::size_t padded_rows(std::size_t s) { return (s + 15) / 16 * 16; }
     // Trie rows (an extension): dn [rows, hidden] normalised input; dy gets
     // o_proj(attention) for every node, or (tail) for the tail rows only.
-    void forward_nodes(const float* dn, float* dy, const NodeRows& nb, bool tail) const;
+    void forward_nodes(const float* dn, float* dy, const NodeRows& nb, bool tail,
+                       moe_dropin::Scratch& sc) const;
     std::size_t hidden() const { return hidden_; }
 
 private:
@@ -128,7 +136,8 @@ public:
     void forward(const Tensor& x, Tensor& y) const;
     // Trie rows (an extension): dx [rows, hidden] -> dy [rows, hidden], or
     // (tail) dy [tail_rows, hidden] for the last node of every sequence.
-    void forward_nodes(const float* dx, float* dy, const NodeRows& nb, bool tail) const;
+    void forward_nodes(const float* dx, float* dy, const NodeRows& nb, bool tail,
+                       moe_dropin::Scratch& sc) const;
 
 private:
     std::shared_ptr<const moe_dropin::DeviceBuffer> in_w_, in_b_, post_w_, post_b_;

@@ -19,12 +19,10 @@ std::shared_ptr<const DeviceBuffer> upload(const Tensor& t) {
     return b;
 }
 
-template <class T>
-DeviceBuffer upload_vec(const std::vector<T>& v) {
-    DeviceBuffer b(v.size() * sizeof(T));
-    b.upload(v.data(), v.size() * sizeof(T));
-    return b;
-}
+enum ModelSlot : std::size_t {
+    kX = kSlotModel, kY, kLast, kLastNorm, kLogits, kTok, kPos, kKeys, kOff, kLastIdx, kTailPos,
+    kTailBeg, kTailEnd
+};
 
 // The prefix trie of a batch (src/model.cu:1624-1680): one node per distinct
 // prefix in order of first appearance, with its token, depth and root path.
@@ -128,50 +126,47 @@ void PhiTinyMoEModel::generate(const std::vector<std::vector<int>>& input_ids,
         tail_beg[b] = t.key_off[t.last[b]];
         tail_end[b] = t.key_off[t.last[b] + 1];
     }
-    const DeviceBuffer d_tok = upload_vec(t.token), d_pos = upload_vec(t.depth),
-                       d_keys = upload_vec(t.key_rows), d_off = upload_vec(t.key_off),
-                       d_last = upload_vec(t.last), d_tpos = upload_vec(tail_pos),
-                       d_tbeg = upload_vec(tail_beg), d_tend = upload_vec(tail_end);
+    moe_dropin::Scratch& sc = scratch_;
+    const int32_t* d_tok = sc.upload(kTok, t.token.data(), rows);
+    const int32_t* d_last = sc.upload(kLastIdx, t.last.data(), batch);
     NodeRows nb;
     nb.rows = rows;
-    nb.positions = d_pos.as<int32_t>();
-    nb.key_rows = d_keys.as<int32_t>();
-    nb.key_off = d_off.as<int32_t>();
+    nb.positions = sc.upload(kPos, t.depth.data(), rows);
+    nb.key_rows = sc.upload(kKeys, t.key_rows.data(), t.key_rows.size());
+    nb.key_off = sc.upload(kOff, t.key_off.data(), t.key_off.size());
     nb.key_total = t.key_rows.size();
     nb.max_len = t.max_len;
     nb.tail_rows = batch;
-    nb.tail_nodes = d_last.as<int32_t>();
-    nb.tail_positions = d_tpos.as<int32_t>();
-    nb.tail_key_beg = d_tbeg.as<int32_t>();
-    nb.tail_key_end = d_tend.as<int32_t>();
+    nb.tail_nodes = d_last;
+    nb.tail_positions = sc.upload(kTailPos, tail_pos.data(), batch);
+    nb.tail_key_beg = sc.upload(kTailBeg, tail_beg.data(), batch);
+    nb.tail_key_end = sc.upload(kTailEnd, tail_end.data(), batch);
 
     moe_ctx* ctx = moe_dropin::context();
-    DeviceBuffer x(rows * h * sizeof(float)), y(rows * h * sizeof(float));
-    check(moe_embed(ctx, embed_->as<float>(), d_tok.as<int32_t>(), static_cast<int64_t>(rows),
-                    static_cast<int64_t>(h), static_cast<int64_t>(embed_rows_), x.as<float>(),
-                    nullptr));
-    DeviceBuffer last(batch * h * sizeof(float)), last_n(batch * h * sizeof(float));
+    float* x = sc.f32(kX, rows * h);
+    float* y = sc.f32(kY, rows * h);
+    float* last = sc.f32(kLast, batch * h);
+    float* last_n = sc.f32(kLastNorm, batch * h);
+    float* out = sc.f32(kLogits, batch * vocab_);
+    check(moe_embed(ctx, embed_->as<float>(), d_tok, static_cast<int64_t>(rows),
+                    static_cast<int64_t>(h), static_cast<int64_t>(embed_rows_), x, nullptr));
     if (layers_.empty()) {
-        check(moe_embed(ctx, x.as<float>(), d_last.as<int32_t>(), static_cast<int64_t>(batch),
-                        static_cast<int64_t>(h), static_cast<int64_t>(rows), last.as<float>(),
-                        nullptr));
+        check(moe_embed(ctx, x, d_last, static_cast<int64_t>(batch), static_cast<int64_t>(h),
+                        static_cast<int64_t>(rows), last, nullptr));
     }
     for (std::size_t l = 0; l < layers_.size(); ++l) {
         const bool tail = l + 1 == layers_.size();
-        layers_[l]->forward_nodes(x.as<float>(), tail ? last.as<float>() : y.as<float>(), nb,
-                                  tail);
+        layers_[l]->forward_nodes(x, tail ? last : y, nb, tail, sc);
         if (!tail) std::swap(x, y);
     }
-    check(moe_layer_norm(ctx, last.as<float>(), norm_w_->as<float>(), norm_b_->as<float>(),
-                         apss26::NORM_EPS, static_cast<int64_t>(batch), static_cast<int64_t>(h),
-                         MOE_CONTRACT_FMA, last_n.as<float>(), nullptr, nullptr, nullptr));
-    DeviceBuffer out(batch * vocab_ * sizeof(float));
-    check(moe_sgemm_nt(ctx, last_n.as<float>(), lm_w_->as<float>(),
-                       lm_b_ ? lm_b_->as<float>() : nullptr, out.as<float>(),
+    check(moe_layer_norm(ctx, last, norm_w_->as<float>(), norm_b_->as<float>(), apss26::NORM_EPS,
+                         static_cast<int64_t>(batch), static_cast<int64_t>(h), MOE_CONTRACT_FMA,
+                         last_n, nullptr, nullptr, nullptr));
+    check(moe_sgemm_nt(ctx, last_n, lm_w_->as<float>(), lm_b_ ? lm_b_->as<float>() : nullptr, out,
                        static_cast<int64_t>(batch), static_cast<int64_t>(vocab_),
                        static_cast<int64_t>(h), nullptr));
     logits = Tensor({batch, vocab_});
-    out.download(logits.data(), batch * vocab_ * sizeof(float));
+    sc.download(kLogits, logits.data(), batch * vocab_ * sizeof(float));
 }
 
 void PhiTinyMoEModel::generate_decode(const std::vector<std::vector<int>>& input_ids,

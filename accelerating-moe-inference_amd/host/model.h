@@ -15,6 +15,7 @@
 #include <string>
 #include <vector>
 
+#include "device.h"
 #include "layer.h"
 #include "model_loader.h"
 #include "tensor.h"
@@ -51,4 +52,8 @@ private:
     std::shared_ptr<const moe_dropin::DeviceBuffer> embed_, norm_w_, norm_b_, lm_w_, lm_b_;
     std::vector<std::unique_ptr<PhiDecoderLayer>> layers_;
     std::size_t hidden_ = 0, vocab_ = 0, embed_rows_ = 0;
+    // Activations and trie arrays, grow-only: generate() of a shape seen
+    // before allocates nothing (so, like the reference's generate(), a model
+    // is not safe for concurrent calls).
+    mutable moe_dropin::Scratch scratch_;
 };

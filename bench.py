@@ -137,6 +137,20 @@ def hbm_kernel_rates(avg, T, d, E, k, block, w2_splits):
     return out
 
 
+def host_cpu():
+    """The host's CPU model and logical core count (the CPU baseline's hardware)."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return f"{model}, {os.cpu_count()} logical cores on the host"
+
+
 def cpu_baseline(x, weights, cfg, pkg_outputs, target_s):
     """The oracle's PhiMoE::forward restatement on a prefix of the tokens,
     sized to about target_s seconds of CPU work.  Test infrastructure: timed
@@ -188,6 +202,7 @@ def cpu_baseline(x, weights, cfg, pkg_outputs, target_s):
         "unit": "tokens/s",
         "cores": oracle.get_threads(),
         "kind": "port",
+        "host": host_cpu(),
         "sample": (f"first {n} of {cfg['T']} tokens of the same layer (same weights; "
                    f"routing is per token), {dt:.1f} s on {oracle.get_threads()} threads"),
     }, parity
@@ -228,6 +243,7 @@ def decoder_cpu_baseline(tokens, W, cfg, gpu_hidden, target_s):
         "unit": "tokens/s",
         "cores": oracle.get_threads(),
         "kind": "port",
+        "host": host_cpu(),
         "sample": (f"{what} of {B} x {S} (all {cfg.layers} layers, same weights; causal "
                    f"attention, so these rows are those of the full prefill), {dt:.1f} s on "
                    f"{oracle.get_threads()} threads"),

@@ -314,6 +314,10 @@ int shim_model_generate(const char* path, const int32_t* lens, const int32_t* id
         m.generate(unpack(lens, ids, batch), L);
         expect(L.ndim() == 2 && L.size(0) == size_t(batch) && L.size(1) == size_t(vocab), "shape");
         std::memcpy(logits, L.data(), L.size() * sizeof(float));
+        // again, on the model's warmed-up scratch: the same bits
+        Tensor L2;
+        m.generate(unpack(lens, ids, batch), L2);
+        expect(std::memcmp(L.data(), L2.data(), L.size() * sizeof(float)) == 0, "repeat call");
         // forward() of one sequence is generate() of a batch of one
         Tensor one;
         m.forward(unpack(lens, ids, 1)[0], one);
