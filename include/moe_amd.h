@@ -192,8 +192,9 @@ int moe_rms_norm(moe_ctx* ctx, const float* x, const float* weight, float eps,
  *   `window` positions (0 = unlimited)) v per sequence and head; q and out
  *   [batch*seq_len, q_heads*head_dim], k and v [batch*seq_len,
  *   kv_heads*head_dim], query head h reads key head h / (q_heads/kv_heads).
- *   Needs head_dim and seq_len multiples of 16 and 16-byte aligned buffers
- *   (MOE_ERR_UNSUPPORTED otherwise); uses batch*q_heads*seq_len^2 floats of
+ *   16-byte aligned buffers.  head_dim 64 or 128: one fused pass, any
+ *   seq_len, no workspace.  Other head_dims: head_dim and seq_len multiples
+ *   of 16 (MOE_ERR_UNSUPPORTED otherwise), batch*q_heads*seq_len^2 floats of
  *   workspace.
  * moe_attention_last: the same attention for the last position of every
  *   sequence only (the rows the model's logits read): q [batch,
