@@ -1,6 +1,6 @@
 """Benchmark of the MoE layer forward on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--config c3|c4|c5] [--block]
+    python bench.py [--steps K] [--warmup W] [--config c3|c4|c5|ref] [--block]
                     [--cpu-seconds S]
     python bench.py --sgemm        (config 2: the SGEMM sweep, a line per shape)
     python bench.py --decoder      (config 5: the whole 4-layer decoder prefill)
@@ -42,7 +42,16 @@ CONFIGS = {
     # the MoE FFN of config 5's decoder (batch 8 x seq 512 tokens, d 1024)
     "c5": dict(T=4096, d=1024, E=8, k=2, d_ff=2816, zipf=None, norm="rms",
                workload="decoder_prefill_moe_ffn_fp32"),
+    # the reference's own MoE layer (Phi-tiny-MoE: d 4096, 16 experts of d_ff 448,
+    # its quantised top-2 router) at its contest input's 15,583 rows, the shape its
+    # per-layer expert GEMM times are quoted on (docs/lab-note.md:4294-4296)
+    "ref": dict(T=15583, d=4096, E=16, k=2, d_ff=448, zipf=None, norm="layer",
+                workload="phi_tiny_moe_layer_fp32", router="phi_quant"),
 }
+# The reference's grouped expert GEMM times per layer on its RTX 3090 (summed
+# over 32 layers in docs/lab-note.md:4294-4296: w13 363 ms, w2 191 ms), for
+# the "ref" workload only.
+REF_GEMM_MS = {"expert_w13_swiglu": 363.0 / 32, "expert_w2": 191.0 / 32}
 
 # Config 2: standalone SGEMM sweep (NN, row-major, A and B ~ U[-1, 1]).
 SGEMM_SHAPES = [(1024, 1024, 1024), (2048, 2048, 2048), (4096, 4096, 4096), (8192, 8192, 8192),
@@ -174,7 +183,9 @@ def cpu_baseline(x, weights, cfg, pkg_outputs, target_s):
             else:
                 xin, _, _ = oracle.layer_norm(xin, nw, nb, NORM_EPS, oracle.CONTRACT_FMA)
         y, idx, w = oracle.moe_forward(xin, gw, w1, w3, w2, k, act=oracle.ACT_SWIGLU,
-                                       router_mode=oracle.ROUTER_SOFTMAX_TOPK,
+                                       router_mode=(oracle.ROUTER_PHI_QUANT
+                                                    if cfg.get("router") == "phi_quant"
+                                                    else oracle.ROUTER_SOFTMAX_TOPK),
                                        expert_bias=bias)
         if nw is not None:
             y = y + x[:n]
@@ -434,7 +445,8 @@ def main():
     idx = torch.empty((T, k), dtype=torch.int32, device=dev)
     w = torch.empty((T, k), device=dev)
     desc = pkg.make_desc(T, d, E, k, d_ff, act=pkg.ACT_SWIGLU,
-                         router=pkg.ROUTER_SOFTMAX_TOPK, contract=pkg.CONTRACT_FMA,
+                         router=(pkg.ROUTER_PHI_QUANT if cfg.get("router") == "phi_quant"
+                                 else pkg.ROUTER_SOFTMAX_TOPK), contract=pkg.CONTRACT_FMA,
                          norm=(pkg.NORM_RMS if rms else pkg.NORM_LAYER) if args.block
                          else pkg.NORM_NONE,
                          norm_eps=NORM_EPS, residual=args.block)
@@ -495,7 +507,10 @@ def main():
         "dtype": "f32",
         "data": "synthetic (seeded torch.randn: x ~ N(0,1), weights ~ N(0,0.02))",
         "config": {"workload": cfg["workload"], "tokens": T, "d_model": d, "experts": E,
-                   "top_k": k, "d_ff": d_ff, "router": "softmax over selected top-k",
+                   "top_k": k, "d_ff": d_ff,
+                   "router": ("quantised top-2, weights 1/2 (PhiMoE::route)"
+                              if cfg.get("router") == "phi_quant"
+                              else "softmax over selected top-k"),
                    "expert": "SwiGLU", "router_bias": (f"zipf(s={cfg['zipf']})"
                                                        if cfg["zipf"] else None),
                    "block": (f"y = x + MoE({'rms_norm' if rms else 'layer_norm'}(x))"
@@ -518,6 +533,11 @@ def main():
         "cpu_baseline": cpu,
         "cpu_sample_parity": parity,
     }
+    if args.config == "ref":
+        # the reference's own per-layer expert GEMM times at this shape (RTX 3090)
+        out["reference_gpu_gemm_ms"] = {n: round(v, 3) for n, v in REF_GEMM_MS.items()}
+        out["speedup_vs_reference_gpu_gemms"] = {
+            n: round(REF_GEMM_MS[n] / avg[n], 2) for n in REF_GEMM_MS if n in avg}
     ctx.close()
     print(json.dumps(out))
 
