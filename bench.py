@@ -409,7 +409,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported "
-              "(this build targets a single MI355X; see DESIGN.md for sharding)",
+              "(this build targets a single MI355X: one GPU's share of the expert "
+              "GEMMs is what it times)",
               file=sys.stderr)
         sys.exit(2)
     if args.sgemm:
