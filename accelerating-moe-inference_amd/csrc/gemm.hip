@@ -45,16 +45,17 @@
 #define MOE_DENSE_CFG 0
 #endif
 // Main-loop schedule per use, a bit mask of SCHED_* (below).  Defaults are
-// the measured best on MI355X: direct loads for both expert GEMMs, raised
-// priority for w1/w3 only (it slows w2, which runs 4 waves per SIMD).
+// the measured best on MI355X: direct loads issued as buffer loads, fragment
+// reads in burst order, for every use; raised priority for w1/w3 only (it
+// slows w2, which runs 4 waves per SIMD).
 #ifndef MOE_W13_SCHED
-#define MOE_W13_SCHED 7
+#define MOE_W13_SCHED 31
 #endif
 #ifndef MOE_W2_SCHED
-#define MOE_W2_SCHED 6
+#define MOE_W2_SCHED 30
 #endif
 #ifndef MOE_DENSE_SCHED
-#define MOE_DENSE_SCHED 6
+#define MOE_DENSE_SCHED 30
 #endif
 
 namespace moe {
@@ -67,7 +68,16 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 // matrix-core burst; SCHED_MIDSTORE (register-staged path) stores the next
 // tile to LDS halfway through the burst instead of after it; SCHED_DIRECT
 // takes the direct global->LDS path where it applies.
-constexpr int SCHED_PRIO = 1, SCHED_MIDSTORE = 2, SCHED_DIRECT = 4;
+// SCHED_QSPLIT (direct path) reads a K step's fragments in the order the
+// burst consumes them -- lane-half k columns 0-3 of every operand first, then
+// 4-7 -- and runs the burst operand by operand, so the first MFMAs wait only
+// for the reads they use instead of all of them.
+// SCHED_BUFLDS (direct path) issues the global->LDS loads as buffer loads
+// (a resource per operand, fixed 32-bit lane offsets, the K step in the
+// scalar offset); the compiler counts those on the vector-memory counter
+// only, so the fragment reads of a K step get partial waits.
+constexpr int SCHED_PRIO = 1, SCHED_MIDSTORE = 2, SCHED_DIRECT = 4, SCHED_QSPLIT = 8,
+              SCHED_BUFLDS = 16;
 
 template <int BM_, int BN_, int BK_, int WM_, int WN_>
 struct Cfg {
@@ -388,7 +398,8 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_kernel(const GemmArgs p) {
 }
 
 // ---------------------------------------------------------------------------
-// GEMM with direct global->LDS loads (gfx950 global_load_lds_dwordx4).
+// GEMM with direct global->LDS loads (gfx950 buffer_load_dwordx4 ... lds,
+// or global_load_lds_dwordx4 where an operand's byte offsets pass 2^31).
 //
 // Lane L of a load instruction writes its 16 bytes at LDS base + 16*L, from
 // any global address it chooses, so each lane fetches the chunk that belongs
@@ -401,6 +412,16 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_kernel(const GemmArgs p) {
 // the MFMA burst, then waits for its loads and meets the other waves at the
 // barrier.  Requires K % 16 == 0 and 16-byte aligned rows.
 //
+// The buffer form (SCHED_BUFLDS) keeps each lane's source as a fixed 32-bit
+// offset from a wave-uniform base and advances K through the scalar offset,
+// so a K step spends no vector instructions on 64-bit addresses.  The
+// compiler also counts the global form against the LDS counter (it is a
+// FLAT instruction that writes LDS), which forces a wait for every fragment
+// read before the first MFMA; the buffer form leaves that counter to the
+// fragment reads, and the first MFMAs wait only for their own operands.
+// Measured on MI355X: dense NT 8192^3 119 -> 138 TFLOP/s, config-3 w2
+// 8.03 -> 7.72 ms, config-5 w2 0.51 -> 0.47 ms, w1/w3 unchanged.
+//
 // NN B ([K, N] row-major) stays k-major in LDS: one load instruction moves
 // 256 consecutive floats of the tile, 256 / BN k-rows of BN columns, and
 // instructions sit NN_PAD floats apart so that k-rows 8 apart (the two lane
@@ -409,6 +430,26 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_kernel(const GemmArgs p) {
 // N % 4 == 0 as well.
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(1))) const void glb_void;
+
+// Raw buffer resource over [p, p + 4 GiB): no stride, no range clamp.  `p`
+// must be wave-uniform; it is read from the first lane so the resource
+// lives in scalar registers.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const float* p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint64_t lo = static_cast<uint32_t>(
+        __builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(v))));
+    const uint64_t hi = static_cast<uint32_t>(
+        __builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(v >> 32))));
+    return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>((hi << 32) | lo),
+                                             static_cast<short>(0), -1, 0x00020000);
+}
+
+// One 16-byte-per-lane buffer load into LDS at `dst` + 16 * lane, from
+// `base` + `voff` (per lane) + `soff` (uniform) bytes.
+__device__ __forceinline__ void buffer_load_lds16(const float* base, lds_void* dst, uint32_t voff,
+                                                  uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(raw_rsrc(base), dst, 16, voff, soff, 0, 0);
+}
 
 __device__ __forceinline__ int swz(int row) { return (row >> 2) & 3; }
 
@@ -542,15 +583,50 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
                 bsrc[nb][j] = B[nb] + n * p.ldb + 4 * (lslot ^ swz(r));
             }
         }
+    // SCHED_BUFLDS: byte offsets of the same sources from wave-uniform bases
+    // (A: the matrix when rows are gathered, else the tile's first row; B:
+    // the tile's first row (NT) or column (NN)).  The host takes this path
+    // only when every offset stays below 2^31.
+    const float* abase = (GROUPED && p.gather != nullptr) ? Ab : Ab + row0 * p.lda;
+    const float* bbase[NB];
+    uint32_t aoff[A_INS], boff32[NB][B_INS];
+    if (SCHED & SCHED_BUFLDS) {
+#pragma unroll
+        for (int j = 0; j < A_INS; ++j) aoff[j] = static_cast<uint32_t>((asrc[j] - abase) * 4);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            bbase[nb] = NN ? B[nb] + n0 : B[nb] + n0 * p.ldb;
+#pragma unroll
+            for (int j = 0; j < B_INS; ++j)
+                boff32[nb][j] = static_cast<uint32_t>((bsrc[nb][j] - bbase[nb]) * 4);
+        }
+    }
     auto issue = [&](int buf, int64_t k0) {
+        const int64_t boff = NN ? k0 * p.ldb : k0;
+        constexpr int BSTEP = NN ? NnB<BN>::STRIDE : 256;
+        if (SCHED & SCHED_BUFLDS) {
+            const uint32_t ak = static_cast<uint32_t>(k0 * 4), bk = static_cast<uint32_t>(boff * 4);
+#pragma unroll
+            for (int j = 0; j < A_INS; ++j)
+                if (A_INS * NW == A_TOT || wave * A_INS + j < A_TOT)
+                    buffer_load_lds16(abase, (lds_void*)&As[buf][(wave * A_INS + j) * 256],
+                                      aoff[j], ak);
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                for (int j = 0; j < B_INS; ++j)
+                    if (B_INS * NW == B_TOT || wave * B_INS + j < B_TOT)
+                        buffer_load_lds16(bbase[nb],
+                                          (lds_void*)&Bs[buf][nb][(wave * B_INS + j) * BSTEP],
+                                          boff32[nb][j], bk);
+            return;
+        }
 #pragma unroll
         for (int j = 0; j < A_INS; ++j)
             if (A_INS * NW == A_TOT || wave * A_INS + j < A_TOT)
                 __builtin_amdgcn_global_load_lds((glb_void*)(asrc[j] + k0),
                                                  (lds_void*)&As[buf][(wave * A_INS + j) * 256],
                                                  16, 0, 0);
-        const int64_t boff = NN ? k0 * p.ldb : k0;
-        constexpr int BSTEP = NN ? NnB<BN>::STRIDE : 256;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
@@ -590,49 +666,72 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
         // all fragments of this K step first (no LDS read may follow the
         // next stage's loads: they would have to wait for them)
         f32x4 a[FM][2], b[NB][FN][2];
+        auto read_a = [&](int q) {
 #pragma unroll
-        for (int bi = 0; bi < FM; ++bi) {
-            const int r = arow0 + bi * 32 + lr;
-            const float* base = &As[cur][r * BK];
-            a[bi][0] = *reinterpret_cast<const f32x4*>(base + 4 * ((2 * lh) ^ swz(r)));
-            a[bi][1] = *reinterpret_cast<const f32x4*>(base + 4 * ((2 * lh + 1) ^ swz(r)));
-        }
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
+            for (int bi = 0; bi < FM; ++bi) {
+                const int r = arow0 + bi * 32 + lr;
+                a[bi][q] = *reinterpret_cast<const f32x4*>(&As[cur][r * BK] +
+                                                           4 * ((2 * lh + q) ^ swz(r)));
+            }
+        };
+        auto read_b = [&](int nb, int q) {
 #pragma unroll
             for (int bj = 0; bj < FN; ++bj) {
                 const int r = bcol0 + bj * 32 + lr;
                 if (NN) {
                     // the same k order as A: slot s of half q is k = 8 lh + 4 q + s
 #pragma unroll
-                    for (int q = 0; q < 2; ++q)
-#pragma unroll
-                        for (int s = 0; s < 4; ++s)
-                            b[nb][bj][q][s] = Bs[cur][nb][NnB<BN>::at(8 * lh + 4 * q + s, r)];
+                    for (int s = 0; s < 4; ++s)
+                        b[nb][bj][q][s] = Bs[cur][nb][NnB<BN>::at(8 * lh + 4 * q + s, r)];
                 } else {
-                    const float* base = &Bs[cur][nb][r * BK];
-                    b[nb][bj][0] = *reinterpret_cast<const f32x4*>(base + 4 * ((2 * lh) ^ swz(r)));
-                    b[nb][bj][1] =
-                        *reinterpret_cast<const f32x4*>(base + 4 * ((2 * lh + 1) ^ swz(r)));
+                    b[nb][bj][q] = *reinterpret_cast<const f32x4*>(&Bs[cur][nb][r * BK] +
+                                                                   4 * ((2 * lh + q) ^ swz(r)));
                 }
             }
+        };
+        if (SCHED & SCHED_QSPLIT) {
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                read_a(q);
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb) read_b(nb, q);
+            }
+        } else {
+            read_a(0);
+            read_a(1);
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                read_b(nb, 0);
+                read_b(nb, 1);
+            }
+        }
         if (kt + 1 < nk) issue(cur ^ 1, kbeg + (kt + 1) * BK);
         if (SCHED & SCHED_PRIO) __builtin_amdgcn_s_setprio(1);
         // the burst over the first NBLK 32-row blocks of this wave
         auto burst = [&](auto nblk) {
             constexpr int NBLK = decltype(nblk)::value;
+            auto step = [&](int q, int s, int nb) {
 #pragma unroll
-            for (int q = 0; q < 2; ++q)
+                for (int bi = 0; bi < NBLK; ++bi)
 #pragma unroll
-                for (int s = 0; s < 4; ++s)
+                    for (int bj = 0; bj < FN; ++bj)
+                        acc[nb][bi][bj] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                            a[bi][q][s], b[nb][bj][q][s], acc[nb][bi][bj], 0, 0, 0);
+            };
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                if (SCHED & SCHED_QSPLIT) {
 #pragma unroll
                     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-                        for (int bi = 0; bi < NBLK; ++bi)
+                        for (int s = 0; s < 4; ++s) step(q, s, nb);
+                } else {
 #pragma unroll
-                            for (int bj = 0; bj < FN; ++bj)
-                                acc[nb][bi][bj] = __builtin_amdgcn_mfma_f32_32x32x2f32(
-                                    a[bi][q][s], b[nb][bj][q][s], acc[nb][bi][bj], 0, 0, 0);
+                    for (int s = 0; s < 4; ++s)
+#pragma unroll
+                        for (int nb = 0; nb < NB; ++nb) step(q, s, nb);
+                }
+            }
         };
         // Blocks whose 32 rows all lie past the tile's last real row (the
         // ragged end of an expert) are skipped: wave-uniform branches.
@@ -666,6 +765,16 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
             }
 }
 
+// Whether every byte offset of a SCHED_BUFLDS launch (lane offset from the
+// operand's base plus the K step's scalar offset) stays below 2^31.
+bool buf_offsets_fit(const GemmArgs& a, int bm, int bn, bool nn, bool grouped) {
+    constexpr int64_t lim = int64_t(1) << 31;
+    const int64_t a_rows = grouped && a.gather != nullptr ? a.gather_rows : bm;
+    const int64_t a_bytes = (a_rows + 1) * a.lda * 4;
+    const int64_t b_bytes = nn ? (a.K + 16) * a.ldb * 4 + int64_t(bn) * 4 : (int64_t(bn) + 1) * a.ldb * 4;
+    return a_bytes < lim && b_bytes < lim;
+}
+
 template <class C, int SCHED, bool NN, bool GROUPED, int NB, int EPI>
 void launch_cfg(const GemmArgs& a, bool vec, hipStream_t s) {
     // direct global->LDS path: 16-byte aligned rows, K a multiple of 16 (NN:
@@ -674,11 +783,15 @@ void launch_cfg(const GemmArgs& a, bool vec, hipStream_t s) {
         const bool b_ok = !NN || (a.ldb % 4 == 0 && a.N % 4 == 0 &&
                                   reinterpret_cast<uintptr_t>(a.B0) % 16 == 0);
         if (vec && b_ok && a.K % 16 == 0 && a.k_split_len % 16 == 0) {
-            hipLaunchKernelGGL(
-                (gemm_direct_kernel<C, SCHED, NN, GROUPED, NB, EPI>),
-                dim3(static_cast<unsigned>(a.m_tiles) * static_cast<unsigned>(a.n_tiles) *
-                     static_cast<unsigned>(a.k_splits)),
-                dim3(C::THREADS), 0, s, a);
+            const dim3 grid(static_cast<unsigned>(a.m_tiles) * static_cast<unsigned>(a.n_tiles) *
+                            static_cast<unsigned>(a.k_splits));
+            if (!(SCHED & SCHED_BUFLDS) || buf_offsets_fit(a, C::BM, C::BN, NN, GROUPED))
+                hipLaunchKernelGGL((gemm_direct_kernel<C, SCHED, NN, GROUPED, NB, EPI>), grid,
+                                   dim3(C::THREADS), 0, s, a);
+            else
+                hipLaunchKernelGGL(
+                    (gemm_direct_kernel<C, (SCHED & ~SCHED_BUFLDS), NN, GROUPED, NB, EPI>), grid,
+                    dim3(C::THREADS), 0, s, a);
             return;
         }
     }
@@ -734,10 +847,14 @@ void launch_batched_cfg(const GemmArgs& args, int batches, hipStream_t s) {
     a.k_split_len = a.K;
     a.c_split_stride = 0;
     constexpr int SCHED = MOE_DENSE_SCHED | SCHED_DIRECT;
-    hipLaunchKernelGGL((gemm_direct_kernel<C, SCHED, NN, false, 1, EPI_BIAS>),
-                       dim3(static_cast<unsigned>(a.m_tiles) * static_cast<unsigned>(a.n_tiles),
-                            static_cast<unsigned>(batches)),
-                       dim3(C::THREADS), 0, s, a);
+    const dim3 grid(static_cast<unsigned>(a.m_tiles) * static_cast<unsigned>(a.n_tiles),
+                    static_cast<unsigned>(batches));
+    if (!(SCHED & SCHED_BUFLDS) || buf_offsets_fit(a, C::BM, C::BN, NN, false))
+        hipLaunchKernelGGL((gemm_direct_kernel<C, SCHED, NN, false, 1, EPI_BIAS>), grid,
+                           dim3(C::THREADS), 0, s, a);
+    else
+        hipLaunchKernelGGL((gemm_direct_kernel<C, (SCHED & ~SCHED_BUFLDS), NN, false, 1, EPI_BIAS>),
+                           grid, dim3(C::THREADS), 0, s, a);
 }
 }  // namespace
 

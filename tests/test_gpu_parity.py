@@ -143,6 +143,32 @@ def test_sgemm_skinny_config2_row_sample(ctx, torch, orc, m):
     assert torch.equal(c, c2)
 
 
+def test_sgemm_operands_past_2gib(ctx, torch, orc):
+    """Operands whose per-tile byte offsets pass 2^31 take the kernel's 64-bit
+    address path instead of the buffer loads: an NN B of 2 GiB and an NT B of
+    128 rows of 2^22 floats, checked on a sample of outputs."""
+    g = torch.Generator(device="cuda").manual_seed(31)
+    print("sgemm nn 16 x 32768 x 16384 (B 2 GiB)", flush=True)
+    m, n, k = 16, 32768, 16384
+    a = torch.rand((m, k), device="cuda", generator=g) * 2 - 1
+    b = torch.rand((k, n), device="cuda", generator=g) * 2 - 1
+    c = torch.empty((m, n), device="cuda")
+    ctx.sgemm_nn(a, b, c)
+    cols = torch.tensor(np.linspace(0, n - 1, 64).astype(np.int64), device="cuda")
+    ref = orc.matmul_nn(host(a), host(b[:, cols].contiguous()))
+    assert_close(host(c[:, cols]), ref, what="nn past 2 GiB")
+    del b, c
+    print("sgemm nt 8 x 128 x 4194304 (B 2 GiB)", flush=True)
+    m, n, k = 8, 128, 1 << 22
+    a = torch.rand((m, k), device="cuda", generator=g) * 2 - 1
+    b = torch.rand((n, k), device="cuda", generator=g) * 2 - 1
+    c = torch.empty((m, n), device="cuda")
+    ctx.sgemm_nt(a, b, c)
+    rows, bn = [0, 7], [0, 1, 63, 64, 127]
+    ref = orc.matmul_nt(host(a[rows]), host(b[bn]))
+    assert_close(host(c[rows][:, bn]), ref, what="nt past 2 GiB")
+
+
 # ------------------------------------------------------------ elementwise
 def test_silu_mul_bit_exact(ctx, torch, orc):
     rng = np.random.default_rng(12)
@@ -304,6 +330,35 @@ def test_expert_ffn_vs_oracle(ctx, torch, orc, T, d, E, k, d_ff, act, skew):
                            None if w3 is None else dev(torch, w3), dev(torch, w2), k, h, out,
                            act=act)
     assert_close(host(out), ref, what="expert rows")
+
+
+def test_expert_ffn_gather_past_2gib(ctx, torch, orc):
+    """x of 2 GiB: the w1/w3 row gather's byte offsets pass 2^31, so w1/w3 take
+    the kernel's 64-bit address path (w2 reads packed rows from the tile's
+    base and keeps the buffer loads).  Sampled tokens against the oracle run
+    on just those tokens."""
+    T, d, E, k, d_ff = 131072, 4096, 2, 1, 64
+    print(f"ffn gather T={T} d={d} (x 2 GiB)", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(7)
+    x = torch.randn((T, d), device="cuda", generator=g)
+    rng = np.random.default_rng(7)
+    w1, w3 = normal(rng, (E, d_ff, d), 0.02), normal(rng, (E, d_ff, d), 0.02)
+    w2 = normal(rng, (E, d, d_ff), 0.02)
+    topk = rng.integers(0, E, size=(T, k)).astype(np.int32)
+    offsets = torch.empty(E + 1, dtype=torch.int32, device="cuda")
+    perm = torch.empty(T * k, dtype=torch.int32, device="cuda")
+    inv = torch.empty((T, k), dtype=torch.int32, device="cuda")
+    ctx.permute(dev(torch, topk), E, offsets, perm, inv)
+    h = torch.empty((T * k, d_ff), device="cuda")
+    out = torch.empty((T * k, d), device="cuda")
+    ctx.expert_ffn_grouped(x, perm, offsets, dev(torch, w1), dev(torch, w3), dev(torch, w2), k,
+                           h, out)
+    toks = np.unique(np.concatenate([[0, T - 1], rng.integers(0, T, size=62)]))
+    sub_x = host(x[torch.from_numpy(toks).to("cuda")])
+    roff, rperm, rinv = orc.permute(topk[toks], E)
+    ref = orc.expert_ffn(sub_x, rperm, roff, w1, w3, w2, act=0)
+    got = host(out[inv[torch.from_numpy(toks).to("cuda"), 0].long()])
+    assert_close(got, ref[rinv[:, 0]], what="gathered rows past 2 GiB")
 
 
 @pytest.mark.parametrize("contract", [0, 1])
