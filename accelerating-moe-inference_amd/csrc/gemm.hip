@@ -160,12 +160,51 @@ __device__ __forceinline__ bool find_expert(const int32_t* __restrict__ offsets,
         if (m != 0ull) {
             const int l = __ffsll(static_cast<long long>(m)) - 1;
             expert = e0 + l;
-            first_tile = __shfl(start, l, 64);
+            first_tile = __builtin_amdgcn_readfirstlane(__shfl(start, l, 64));
             return true;
         }
-        carry += __shfl(incl, 63, 64);
+        carry += __builtin_amdgcn_readfirstlane(__shfl(incl, 63, 64));
     }
     return false;
+}
+
+// Real m-tiles of a grouped launch: the sum over experts of ceil(n_e / BM),
+// read from the offsets with a wave-wide sum (every lane gets the total).
+template <int BM>
+__device__ __forceinline__ int grouped_real_m_tiles(const int32_t* __restrict__ offsets, int E) {
+    const int lane = threadIdx.x & 63;
+    int cnt = 0;
+    for (int e = lane; e < E; e += 64) {
+        const int n = offsets[e + 1] - offsets[e];
+        cnt += n > 0 ? (n + BM - 1) / BM : 0;
+    }
+    for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off, 64);
+    // every lane holds the total; reading it from the first lane tells the
+    // compiler so, and the tile indices derived from it stay scalar
+    return __builtin_amdgcn_readfirstlane(cnt);
+}
+
+// The tile of this workgroup: (mt, nt) and its K split.  A grouped launch
+// sizes its grid for the worst case (ceil(pairs / BM) + E m-tiles, every
+// expert's last tile partial); here the real tiles are counted, workgroups
+// past them exit at once, and only the real tiles are dealt to the XCDs --
+// so each XCD gets an even share of real work whatever the raster group
+// (the surplus ids are spread over the XCDs by the round-robin dispatch).
+template <int BM, bool GROUPED>
+__device__ __forceinline__ bool launch_tile(const GemmArgs& p, int& mt, int& nt, int& split) {
+    int m_tiles = p.m_tiles;
+    if (GROUPED) {
+        const int real = grouped_real_m_tiles<BM>(p.offsets, p.E);
+        m_tiles = real < m_tiles ? real : m_tiles;
+    }
+    const int tiles_mn = m_tiles * p.n_tiles;
+    const int total = GROUPED ? tiles_mn * p.k_splits : static_cast<int>(gridDim.x);
+    if (static_cast<int>(blockIdx.x) >= total) return false;
+    const int logical = xcd_remap(blockIdx.x, total);
+    split = logical / tiles_mn;
+    tile_of(logical % tiles_mn, m_tiles, p.n_tiles, p.group_m < m_tiles ? p.group_m : m_tiles, mt,
+            nt);
+    return true;
 }
 
 // The reference's SiLU: x / (1 + float(exp(double(-x)))) (src/tensor.cu:
@@ -197,11 +236,8 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_kernel(const GemmArgs p) {
     __shared__ __align__(16) float Bs[2][NB][BN * LDS];
 
     const int tid = threadIdx.x;
-    int mt, nt;
-    const int tiles_mn = p.m_tiles * p.n_tiles;
-    const int logical = xcd_remap(blockIdx.x, gridDim.x);
-    const int split = logical / tiles_mn;  // K range of this tile (split-K)
-    tile_of(logical % tiles_mn, p.m_tiles, p.n_tiles, p.group_m, mt, nt);
+    int mt, nt, split;  // split: K range of this tile (split-K)
+    if (!launch_tile<BM, GROUPED>(p, mt, nt, split)) return;  // surplus workgroup
 
     // ---- which rows / which expert this workgroup owns
     int64_t row0;
@@ -486,11 +522,8 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    int mt, nt;
-    const int tiles_mn = p.m_tiles * p.n_tiles;
-    const int logical = xcd_remap(blockIdx.x, gridDim.x);
-    const int split = logical / tiles_mn;  // K range of this tile (split-K)
-    tile_of(logical % tiles_mn, p.m_tiles, p.n_tiles, p.group_m, mt, nt);
+    int mt, nt, split;  // split: K range of this tile (split-K)
+    if (!launch_tile<BM, GROUPED>(p, mt, nt, split)) return;  // surplus workgroup
 
     int64_t row0;
     int rows;
