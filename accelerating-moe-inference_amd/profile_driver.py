@@ -23,7 +23,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("what", choices=["copy", "layer"])
     ap.add_argument("--mib", type=int, default=1024)
-    ap.add_argument("--config", default="c3", choices=["c3", "c4", "c5"])
+    ap.add_argument("--config", default="c3", choices=["c3", "c4", "c5", "ref"])
     ap.add_argument("--steps", type=int, default=2)
     args = ap.parse_args()
 
@@ -57,7 +57,8 @@ def main():
     if cfg["zipf"] is not None:
         weights["expert_bias"] = torch.from_numpy(bench.zipf_bias(E, cfg["zipf"])).cuda()
     y = torch.empty((T, d), device="cuda")
-    desc = pkg.make_desc(T, d, E, k, d_ff, act=pkg.ACT_SWIGLU, router=pkg.ROUTER_SOFTMAX_TOPK)
+    router = pkg.ROUTER_PHI_QUANT if cfg.get("router") == "phi_quant" else pkg.ROUTER_SOFTMAX_TOPK
+    desc = pkg.make_desc(T, d, E, k, d_ff, act=pkg.ACT_SWIGLU, router=router)
     ctx = pkg.Context(0)
     ctx.reserve(desc)
     for i in range(1 + args.steps):
