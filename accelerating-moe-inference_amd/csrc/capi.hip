@@ -87,9 +87,9 @@ int env_int(const char* name, int fallback) {
 }
 
 // Tile shape and K splits of a dense SGEMM, from a cost model fitted to a
-// tile x split sweep of the SGEMM shapes on MI355X (every choice it makes
-// there is within 8 % of the best measured one; the sweep's run-to-run
-// spread is about 5 %).  Per CU, the workgroups
+// tile x split sweep of the SGEMM shapes on MI355X (its choices there are on
+// average 2 % and at worst 15 % slower than the best measured one; the
+// sweep's run-to-run spread is about 5 %).  Per CU, the workgroups
 // dealt to it run `occupancy` at a time; each K step of the resident ones
 // costs the larger of their matrix-core time (the rows a wave really
 // computes: 32-row blocks past M are skipped) and the latency of one load
@@ -116,9 +116,9 @@ DensePlan plan_dense(moe_ctx* ctx, bool nn, bool direct, int64_t M, int64_t N, i
     // fitted constants: MFMA efficiency per tile shape, latency of one load
     // stage, start-up and drain of a round of workgroups, achievable HBM
     // bandwidth, launch and reduction overheads
-    static constexpr double kEff[moe::kDenseTiles] = {0.80, 0.70, 0.60};
-    constexpr double kStageLatency = 0.5e-6, kRound = 4e-6, kHbm = 5.0e12, kLaunch = 2e-6,
-                     kReduce = 5e-6;
+    static constexpr double kEff[moe::kDenseTiles] = {0.80, 0.80, 0.50};
+    constexpr double kStageLatency = 0.6e-6, kRound = 1e-6, kHbm = 5.0e12, kLaunch = 2e-6,
+                     kReduce = 2e-6;
     // each tile shape runs 4 waves, one per SIMD
     const double simd_rate = 157.3e12 / (4.0 * ctx->cus);
     double best_t = 1e30;
