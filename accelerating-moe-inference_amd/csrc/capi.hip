@@ -231,8 +231,10 @@ int64_t grouped_m_tiles(int64_t pairs, int64_t E, int bm) {
 // the rest of the GPU for a whole tile time.  Splitting K S ways makes the
 // rounds S times shorter, so the fill is w / ceil(w) with w = tiles * S /
 // slots.  The smallest S in {1, 2, 4} whose fill reaches 95 % is taken (else
-// the best); each split must be a multiple of 16 columns.  MOE_W2_SPLITS
-// overrides for tuning.
+// the best): every split adds a partial row buffer the combine must read
+// (at the reference's layer shape S = 2 costs 0.11 ms there and 0.1 ms of
+// w2 against S = 1).  Each split must be a multiple of 16 columns.
+// MOE_W2_SPLITS overrides for tuning.
 struct W2Plan {
     int tile;    // GemmArgs::tile of the w2 launch: 0 wide (W2), 1 128x128 (W2Narrow)
     int splits;  // K splits
@@ -264,7 +266,11 @@ int choose_w2_splits(moe_ctx* ctx, int64_t pairs, int64_t d, int64_t d_ff, int64
     int& occ = w2_tile == 1 ? ctx->w2n_blocks_per_cu : ctx->w2_blocks_per_cu;
     if (occ == 0) occ = moe::gemm_blocks_per_cu(use);
     const moe::GemmTile tile = moe::gemm_tile(use);
-    const double tiles = double(grouped_m_tiles(pairs, E, tile.bm) * moe::ceil_div(d, tile.bn));
+    // the kernel deals only real tiles: sum over experts of ceil(n_e / BM),
+    // expected ceil(pairs / BM) + E / 2 (each expert's last tile half full)
+    const int64_t m_expected = std::min<int64_t>(moe::ceil_div(pairs, tile.bm) + E / 2,
+                                                 grouped_m_tiles(pairs, E, tile.bm));
+    const double tiles = double(m_expected * moe::ceil_div(d, tile.bn));
     const double slots = double(int64_t(ctx->cus) * occ);
     int best = 1;
     double best_fill = 0.0;
