@@ -478,11 +478,14 @@ def test_layer_skewed_config4_full_size(ctx, pkg, torch, orc):
 
 # ------------------------------------------------------------- layer norm
 @pytest.mark.parametrize("contract", [0, 1])
-# rows held in LDS (whole rows per workgroup, 16-byte and scalar paths; h =
-# 20220 is the widest row that fits) and, for h = 30000, the streaming
-# kernels for rows too wide for LDS
+# rows held in LDS (whole rows per workgroup, 16-byte and scalar paths, h up
+# to 1260 when aligned); wider aligned rows stream through the ring kernel with 8, 16 or
+# 32 rows per wave (65 x 4096 and 3 x 30000: 8, a one-row last wave and a
+# partial last stage; 8200 x 2600: 16; 32800 x 2528: 32); 2 x 30001, wide
+# and unaligned, takes the register-staged streaming pair
 @pytest.mark.parametrize("rows,h", [(1, 1), (3, 5), (64, 64), (65, 4096), (200, 1000),
-                                    (130, 33), (4096, 1024), (70, 20220), (3, 30000)])
+                                    (130, 33), (4096, 1024), (70, 20220), (3, 30000),
+                                    (8200, 2600), (32800, 2528), (2, 30001)])
 def test_layer_norm_bit_exact(ctx, torch, orc, contract, rows, h):
     print(f"layer_norm {rows}x{h} contract={contract}", flush=True)
     rng = np.random.default_rng(rows * 7 + h + contract)
@@ -507,7 +510,7 @@ def test_layer_norm_bit_exact(ctx, torch, orc, contract, rows, h):
 
 @pytest.mark.parametrize("contract", [0, 1])
 @pytest.mark.parametrize("rows,h", [(1, 1), (3, 5), (65, 4096), (130, 33), (4096, 1024),
-                                    (3, 30000)])
+                                    (3, 30000), (8200, 2600), (2, 30001)])
 def test_rms_norm_bit_exact(ctx, torch, orc, contract, rows, h):
     print(f"rms_norm {rows}x{h} contract={contract}", flush=True)
     rng = np.random.default_rng(rows * 3 + h + contract)
