@@ -46,13 +46,14 @@
 #endif
 // Main-loop schedule per use, a bit mask of SCHED_* (below).  Defaults are
 // the measured best on MI355X: direct loads issued as buffer loads, fragment
-// reads in burst order, for every use; raised priority for w1/w3 only (it
-// slows w2, which runs 4 waves per SIMD).
+// reads in burst order, for every use; the three-stage ring for the expert
+// GEMMs (0.3-0.9 % faster at configs 3-5 and the reference's layer shape);
+// raised priority for w1/w3 only (it slows w2).
 #ifndef MOE_W13_SCHED
-#define MOE_W13_SCHED 31
+#define MOE_W13_SCHED 63
 #endif
 #ifndef MOE_W2_SCHED
-#define MOE_W2_SCHED 30
+#define MOE_W2_SCHED 62
 #endif
 #ifndef MOE_DENSE_SCHED
 #define MOE_DENSE_SCHED 30
@@ -76,8 +77,11 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 // (a resource per operand, fixed 32-bit lane offsets, the K step in the
 // scalar offset); the compiler counts those on the vector-memory counter
 // only, so the fragment reads of a K step get partial waits.
+// SCHED_RING3 (direct path, with SCHED_BUFLDS) keeps three LDS stages, one
+// __shared__ array each, and loads two K steps ahead: the wait before each
+// barrier leaves the newest stage's loads in flight.
 constexpr int SCHED_PRIO = 1, SCHED_MIDSTORE = 2, SCHED_DIRECT = 4, SCHED_QSPLIT = 8,
-              SCHED_BUFLDS = 16;
+              SCHED_BUFLDS = 16, SCHED_RING3 = 32;
 
 template <int BM_, int BN_, int BK_, int WM_, int WN_>
 struct Cfg {
@@ -634,7 +638,9 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
                 boff32[nb][j] = static_cast<uint32_t>((bsrc[nb][j] - bbase[nb]) * 4);
         }
     }
-    auto issue = [&](int buf, int64_t k0) {
+    // loads of the K step at k0 into the stage at (adst, bdst): A tile, then
+    // the NB B tiles B_SIZE floats apart
+    auto issue_to = [&](float* adst, float* bdst, int64_t k0) {
         const int64_t boff = NN ? k0 * p.ldb : k0;
         constexpr int BSTEP = NN ? NnB<BN>::STRIDE : 256;
         if (SCHED & SCHED_BUFLDS) {
@@ -642,15 +648,15 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
 #pragma unroll
             for (int j = 0; j < A_INS; ++j)
                 if (A_INS * NW == A_TOT || wave * A_INS + j < A_TOT)
-                    buffer_load_lds16(abase, (lds_void*)&As[buf][(wave * A_INS + j) * 256],
-                                      aoff[j], ak);
+                    buffer_load_lds16(abase, (lds_void*)&adst[(wave * A_INS + j) * 256], aoff[j],
+                                      ak);
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
                 for (int j = 0; j < B_INS; ++j)
                     if (B_INS * NW == B_TOT || wave * B_INS + j < B_TOT)
                         buffer_load_lds16(bbase[nb],
-                                          (lds_void*)&Bs[buf][nb][(wave * B_INS + j) * BSTEP],
+                                          (lds_void*)&bdst[nb * B_SIZE + (wave * B_INS + j) * BSTEP],
                                           boff32[nb][j], bk);
             return;
         }
@@ -658,8 +664,8 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
         for (int j = 0; j < A_INS; ++j)
             if (A_INS * NW == A_TOT || wave * A_INS + j < A_TOT)
                 __builtin_amdgcn_global_load_lds((glb_void*)(asrc[j] + k0),
-                                                 (lds_void*)&As[buf][(wave * A_INS + j) * 256],
-                                                 16, 0, 0);
+                                                 (lds_void*)&adst[(wave * A_INS + j) * 256], 16, 0,
+                                                 0);
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
@@ -667,8 +673,9 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
                 if (B_INS * NW == B_TOT || wave * B_INS + j < B_TOT)
                     __builtin_amdgcn_global_load_lds(
                         (glb_void*)(bsrc[nb][j] + boff),
-                        (lds_void*)&Bs[buf][nb][(wave * B_INS + j) * BSTEP], 16, 0, 0);
+                        (lds_void*)&bdst[nb * B_SIZE + (wave * B_INS + j) * BSTEP], 16, 0, 0);
     };
+    auto issue = [&](int buf, int64_t k0) { issue_to(As[buf], &Bs[buf][0][0], k0); };
 
     const int wm = wave % C::WM, wn = wave / C::WM;
     const int lr = lane & 31, lh = lane >> 5;
@@ -689,21 +696,15 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
     const int live = live_rows <= 0 ? 0 : (live_rows >= FM * 32 ? FM : (live_rows + 31) / 32);
 
     const int64_t nk = (K - kbeg) / BK;
-    if (nk > 0) {
-        issue(0, kbeg);
-        __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0): this wave's loads landed
-        __syncthreads();                      // ... and every other wave's
-    }
-    for (int64_t kt = 0; kt < nk; ++kt) {
-        const int cur = static_cast<int>(kt & 1);
-        // all fragments of this K step first (no LDS read may follow the
-        // next stage's loads: they would have to wait for them)
-        f32x4 a[FM][2], b[NB][FN][2];
+    f32x4 a[FM][2], b[NB][FN][2];
+    // all fragments of one K step from the stage at (Acur, Bcur) (no LDS
+    // read may follow the next stage's loads: they would have to wait)
+    auto read_frags = [&](const float* Acur, const float* Bcur) {
         auto read_a = [&](int q) {
 #pragma unroll
             for (int bi = 0; bi < FM; ++bi) {
                 const int r = arow0 + bi * 32 + lr;
-                a[bi][q] = *reinterpret_cast<const f32x4*>(&As[cur][r * BK] +
+                a[bi][q] = *reinterpret_cast<const f32x4*>(&Acur[r * BK] +
                                                            4 * ((2 * lh + q) ^ swz(r)));
             }
         };
@@ -715,9 +716,9 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
                     // the same k order as A: slot s of half q is k = 8 lh + 4 q + s
 #pragma unroll
                     for (int s = 0; s < 4; ++s)
-                        b[nb][bj][q][s] = Bs[cur][nb][NnB<BN>::at(8 * lh + 4 * q + s, r)];
+                        b[nb][bj][q][s] = Bcur[nb * B_SIZE + NnB<BN>::at(8 * lh + 4 * q + s, r)];
                 } else {
-                    b[nb][bj][q] = *reinterpret_cast<const f32x4*>(&Bs[cur][nb][r * BK] +
+                    b[nb][bj][q] = *reinterpret_cast<const f32x4*>(&Bcur[nb * B_SIZE + r * BK] +
                                                                    4 * ((2 * lh + q) ^ swz(r)));
                 }
             }
@@ -738,7 +739,9 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
                 read_b(nb, 1);
             }
         }
-        if (kt + 1 < nk) issue(cur ^ 1, kbeg + (kt + 1) * BK);
+    };
+    // the MFMA burst of one K step over this wave's live 32-row blocks
+    auto mfma_step = [&]() {
         if (SCHED & SCHED_PRIO) __builtin_amdgcn_s_setprio(1);
         // the burst over the first NBLK 32-row blocks of this wave
         auto burst = [&](auto nblk) {
@@ -772,8 +775,78 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
         else if (FM > 1 && live == 1) burst(std::integral_constant<int, 1>{});
         else if (live > 0) burst(std::integral_constant<int, FM>{});
         if (SCHED & SCHED_PRIO) __builtin_amdgcn_s_setprio(0);
-        __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
-        __syncthreads();
+    };
+
+    if constexpr ((SCHED & SCHED_RING3) != 0) {
+        // Three stages, one __shared__ array each (the compiler then waits
+        // only for the loads landing in the stage it reads), the K loop
+        // unrolled by three so every step names its arrays.  Step kt reads
+        // stage kt % 3, issues the loads of step kt + 2 into the stage step
+        // kt - 1 read (every wave passed the barrier after reading it), runs
+        // its burst, and before the barrier waits for step kt + 1's loads:
+        // only step kt + 2's, LPS per wave, may still be in flight.
+        static_assert((SCHED & SCHED_BUFLDS) != 0, "the ring uses buffer loads");
+        static_assert(A_INS * NW == A_TOT && B_INS * NW == B_TOT,
+                      "the ring's wait counts need the same loads on every wave");
+        constexpr int LPS = A_INS + NB * B_INS;
+        static_assert(LPS <= 63, "vmcnt range");
+        constexpr int VM_LPS = 0x3f70 | (LPS & 15) | ((LPS >> 4) << 14);
+        __shared__ __align__(16) float RA0[BM * BK], RA1[BM * BK], RA2[BM * BK];
+        __shared__ __align__(16) float RB0[NB * B_SIZE], RB1[NB * B_SIZE], RB2[NB * B_SIZE];
+        auto ra = [&](auto u) -> float* {
+            if constexpr (decltype(u)::value == 0) return RA0;
+            else if constexpr (decltype(u)::value == 1) return RA1;
+            else return RA2;
+        };
+        auto rb = [&](auto u) -> float* {
+            if constexpr (decltype(u)::value == 0) return RB0;
+            else if constexpr (decltype(u)::value == 1) return RB1;
+            else return RB2;
+        };
+        using S0 = std::integral_constant<int, 0>;
+        using S1 = std::integral_constant<int, 1>;
+        using S2 = std::integral_constant<int, 2>;
+        if (nk > 0) {
+            issue_to(RA0, RB0, kbeg);
+            if (nk > 1) {
+                issue_to(RA1, RB1, kbeg + BK);
+                __builtin_amdgcn_s_waitcnt(VM_LPS);
+            } else {
+                __builtin_amdgcn_s_waitcnt(0x3f70);
+            }
+            __syncthreads();
+        }
+        for (int64_t kt0 = 0; kt0 < nk; kt0 += 3) {
+            auto one = [&](auto u) {
+                constexpr int U = decltype(u)::value;
+                const int64_t kt = kt0 + U;
+                if (kt >= nk) return;
+                read_frags(ra(u), rb(u));
+                using N2 = std::integral_constant<int, (U + 2) % 3>;
+                if (kt + 2 < nk) issue_to(ra(N2{}), rb(N2{}), kbeg + (kt + 2) * BK);
+                mfma_step();
+                if (kt + 2 < nk) __builtin_amdgcn_s_waitcnt(VM_LPS);
+                else __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
+                __syncthreads();
+            };
+            one(S0{});
+            one(S1{});
+            one(S2{});
+        }
+    } else {
+        if (nk > 0) {
+            issue(0, kbeg);
+            __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0): this wave's loads landed
+            __syncthreads();                      // ... and every other wave's
+        }
+        for (int64_t kt = 0; kt < nk; ++kt) {
+            const int cur = static_cast<int>(kt & 1);
+            read_frags(As[cur], &Bs[cur][0][0]);
+            if (kt + 1 < nk) issue(cur ^ 1, kbeg + (kt + 1) * BK);
+            mfma_step();
+            __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
+            __syncthreads();
+        }
     }
 
 #pragma unroll
@@ -823,7 +896,7 @@ void launch_cfg(const GemmArgs& a, bool vec, hipStream_t s) {
                                    dim3(C::THREADS), 0, s, a);
             else
                 hipLaunchKernelGGL(
-                    (gemm_direct_kernel<C, (SCHED & ~SCHED_BUFLDS), NN, GROUPED, NB, EPI>), grid,
+                    (gemm_direct_kernel<C, (SCHED & ~(SCHED_BUFLDS | SCHED_RING3)), NN, GROUPED, NB, EPI>), grid,
                     dim3(C::THREADS), 0, s, a);
             return;
         }
@@ -886,7 +959,7 @@ void launch_batched_cfg(const GemmArgs& args, int batches, hipStream_t s) {
         hipLaunchKernelGGL((gemm_direct_kernel<C, SCHED, NN, false, 1, EPI_BIAS>), grid,
                            dim3(C::THREADS), 0, s, a);
     else
-        hipLaunchKernelGGL((gemm_direct_kernel<C, (SCHED & ~SCHED_BUFLDS), NN, false, 1, EPI_BIAS>),
+        hipLaunchKernelGGL((gemm_direct_kernel<C, (SCHED & ~(SCHED_BUFLDS | SCHED_RING3)), NN, false, 1, EPI_BIAS>),
                            grid, dim3(C::THREADS), 0, s, a);
 }
 }  // namespace
