@@ -31,6 +31,7 @@
 
 #include <cstdlib>
 #include <type_traits>
+#include <utility>
 
 // Tile configurations (index into CFG_TABLE below) chosen per use; the
 // defaults are the measured best on MI355X and can be overridden at build
@@ -484,6 +485,11 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const float* p) {
                                              static_cast<short>(0), -1, 0x00020000);
 }
 
+template <int... I, class F>
+__device__ __forceinline__ void static_for_int(std::integer_sequence<int, I...>, F&& f) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+
 // One 16-byte-per-lane buffer load into LDS at `dst` + 16 * lane, from
 // `base` + `voff` (per lane) + `soff` (uniform) bytes.
 __device__ __forceinline__ void buffer_load_lds16(const float* base, lds_void* dst, uint32_t voff,
@@ -786,11 +792,24 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
         // its burst, and before the barrier waits for step kt + 1's loads:
         // only step kt + 2's, LPS per wave, may still be in flight.
         static_assert((SCHED & SCHED_BUFLDS) != 0, "the ring uses buffer loads");
-        static_assert(A_INS * NW == A_TOT && B_INS * NW == B_TOT,
-                      "the ring's wait counts need the same loads on every wave");
-        constexpr int LPS = A_INS + NB * B_INS;
-        static_assert(LPS <= 63, "vmcnt range");
-        constexpr int VM_LPS = 0x3f70 | (LPS & 15) | ((LPS >> 4) << 14);
+        // this wave's loads per stage (tiles with fewer load instructions
+        // than waves leave some waves without an A or B load)
+        int lps = 0;
+#pragma unroll
+        for (int j = 0; j < A_INS; ++j) lps += (A_INS * NW == A_TOT || wave * A_INS + j < A_TOT);
+#pragma unroll
+        for (int j = 0; j < B_INS; ++j)
+            lps += NB * (B_INS * NW == B_TOT || wave * B_INS + j < B_TOT);
+        constexpr int LPS_MAX = A_INS + NB * B_INS;
+        static_assert(LPS_MAX <= 63, "vmcnt range");
+        // s_waitcnt vmcnt(lps): the count is wave-uniform, the wait needs an
+        // immediate, so dispatch over the possible values
+        auto wait_lps = [&]() {
+            static_for_int(std::make_integer_sequence<int, LPS_MAX + 1>{}, [&](auto v) {
+                constexpr int V = decltype(v)::value;
+                if (lps == V) __builtin_amdgcn_s_waitcnt(0x3f70 | (V & 15) | ((V >> 4) << 14));
+            });
+        };
         __shared__ __align__(16) float RA0[BM * BK], RA1[BM * BK], RA2[BM * BK];
         __shared__ __align__(16) float RB0[NB * B_SIZE], RB1[NB * B_SIZE], RB2[NB * B_SIZE];
         auto ra = [&](auto u) -> float* {
@@ -810,7 +829,7 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
             issue_to(RA0, RB0, kbeg);
             if (nk > 1) {
                 issue_to(RA1, RB1, kbeg + BK);
-                __builtin_amdgcn_s_waitcnt(VM_LPS);
+                wait_lps();
             } else {
                 __builtin_amdgcn_s_waitcnt(0x3f70);
             }
@@ -825,7 +844,7 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
                 using N2 = std::integral_constant<int, (U + 2) % 3>;
                 if (kt + 2 < nk) issue_to(ra(N2{}), rb(N2{}), kbeg + (kt + 2) * BK);
                 mfma_step();
-                if (kt + 2 < nk) __builtin_amdgcn_s_waitcnt(VM_LPS);
+                if (kt + 2 < nk) wait_lps();
                 else __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
                 __syncthreads();
             };
