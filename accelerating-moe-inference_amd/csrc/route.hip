@@ -13,6 +13,7 @@
 
 #include <climits>
 #include <cmath>
+#include <utility>
 
 namespace moe {
 namespace {
@@ -131,6 +132,151 @@ __global__ __launch_bounds__(256) void gate_logits_kernel(
         const int64_t t = t0 + r * TB + u;
         if (t < T && e < E) logits[t * E + e] = acc[u];
     }
+}
+
+// Small E (up to 8): the ring form.  One wave per workgroup; lane
+// (r, e) = (lane / EB, lane % EB) owns the chain of token t0 + r and expert
+// e.  The R token rows and the EB expert rows stream through an LDS ring of
+// 64-column stages, filled with direct global->LDS buffer loads RING - 1
+// stages ahead (load instruction i of a stage fills 16-byte slot
+// p = 64 i + lane: row p / 16, slot p % 16, which holds the row's chunk
+// (p % 16) ^ (row % 16), so the lanes' reads of one chunk from different
+// rows hit different banks).  Each stage is its own __shared__ array and the
+// stage loop is unrolled over the ring, so the compiler waits only for the
+// stage being read.  Every lane then runs 64 multiply-adds per stage in
+// column order -- the chain of the kernel above -- with T/R workgroups
+// instead of T/32 (at config 3, 512 instead of 128).
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+constexpr int kGateRingCols = 64;
+constexpr int kGateRing = 8;
+
+typedef __attribute__((address_space(3))) void gate_lds_t;
+
+__device__ __forceinline__ void gate_load16(const float* base, gate_lds_t* dst, uint32_t voff) {
+    const uint64_t v = reinterpret_cast<uint64_t>(base);
+    const uint64_t lo = static_cast<uint32_t>(
+        __builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(v))));
+    const uint64_t hi = static_cast<uint32_t>(
+        __builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(v >> 32))));
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        reinterpret_cast<void*>((hi << 32) | lo), static_cast<short>(0), -1, 0x00020000);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, voff, 0, 0, 0);
+}
+
+template <int... I, class F>
+__device__ __forceinline__ void gate_static_for(std::integer_sequence<int, I...>, F&& f) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+
+template <int CONTRACT, int EB>
+__global__ __launch_bounds__(64) void gate_ring_kernel(
+        const float* __restrict__ x, const float* __restrict__ w,
+        float* __restrict__ logits, int64_t T, int64_t d, int64_t E) {
+    constexpr int R = 64 / EB;                     // token rows per wave
+    constexpr int ROWS = R + EB;                   // staged rows: tokens, then experts
+    constexpr int STAGE = ROWS * kGateRingCols;    // floats per stage
+    constexpr int INS = ROWS * 16 / 64;            // load instructions per stage
+    constexpr int RING = kGateRing;
+    static_assert(R % 4 == 0 && EB % 4 == 0, "an instruction's 4 rows come from one matrix");
+    static_assert((RING - 2) * INS <= 63, "vmcnt range");
+    __shared__ __align__(16) float r0[STAGE], r1[STAGE], r2[STAGE], r3[STAGE], r4[STAGE],
+        r5[STAGE], r6[STAGE], r7[STAGE];
+    auto buf = [&](auto u) __attribute__((always_inline)) -> float* {
+        constexpr int U = decltype(u)::value;
+        if constexpr (U == 0) return r0;
+        else if constexpr (U == 1) return r1;
+        else if constexpr (U == 2) return r2;
+        else if constexpr (U == 3) return r3;
+        else if constexpr (U == 4) return r4;
+        else if constexpr (U == 5) return r5;
+        else if constexpr (U == 6) return r6;
+        else return r7;
+    };
+
+    const int lane = threadIdx.x;
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * R;
+    const int64_t nt = T - t0 < R ? T - t0 : R;  // tokens of this wave (>= 1)
+    const int64_t nst = (d + kGateRingCols - 1) / kGateRingCols;
+
+    // instruction i: rows 4i .. 4i + 3 of the stage, one matrix each
+    const float* ibase[INS];
+    uint32_t ioff[INS];
+#pragma unroll
+    for (int i = 0; i < INS; ++i) {
+        const int p = 64 * i + lane, row = p / 16, sl = p % 16;
+        const int chunk = sl ^ (row % 16);
+        if (4 * i < R) {  // token rows
+            const int64_t rr = row < nt ? row : nt - 1;
+            ibase[i] = x + t0 * d;
+            ioff[i] = static_cast<uint32_t>((rr * d + 4 * chunk) * 4);
+        } else {          // expert rows
+            const int64_t e = row - R < E ? row - R : E - 1;
+            ibase[i] = w;
+            ioff[i] = static_cast<uint32_t>((e * d + 4 * chunk) * 4);
+        }
+    }
+    auto issue = [&](int64_t st, float* dst) __attribute__((always_inline)) {
+        const int64_t j0 = st * kGateRingCols;
+#pragma unroll
+        for (int i = 0; i < INS; ++i) {
+            // a chunk past the row end loads the row's last chunk (never used)
+            const int chunk = (64 * i + lane) % 16 ^ (((64 * i + lane) / 16) % 16);
+            const int64_t shift = j0 + 4 * chunk <= d - 4 ? j0 : d - 4 - 4 * chunk;
+            gate_load16(ibase[i], (gate_lds_t*)(dst + 256 * i),
+                        static_cast<uint32_t>(ioff[i] + shift * 4));
+        }
+    };
+    auto wait_stage = [&](int64_t st) __attribute__((always_inline)) {
+        if (st + RING - 2 < nst) {
+            constexpr int N = (RING - 2) * INS;
+            __builtin_amdgcn_s_waitcnt(0x3f70 | (N & 15) | ((N >> 4) << 14));
+        } else {
+            __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
+        }
+    };
+
+    const int r = lane / EB, e = lane % EB;
+    const int xsw = r % 16, wsw = (R + e) % 16;
+    float acc = 0.0f;
+    auto consume = [&](const float* stage, int64_t st) __attribute__((always_inline)) {
+        const float* xr = stage + r * kGateRingCols;
+        const float* wr = stage + (R + e) * kGateRingCols;
+        const int64_t j0 = st * kGateRingCols;
+        if (j0 + kGateRingCols <= d) {
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const f32x4_t xv = *reinterpret_cast<const f32x4_t*>(xr + 4 * (q ^ xsw));
+                const f32x4_t wv = *reinterpret_cast<const f32x4_t*>(wr + 4 * (q ^ wsw));
+#pragma unroll
+                for (int c = 0; c < 4; ++c) acc = mac<CONTRACT>(acc, xv[c], wv[c]);
+            }
+        } else {
+            for (int q = 0; q < 16; ++q) {
+                const f32x4_t xv = *reinterpret_cast<const f32x4_t*>(xr + 4 * (q ^ xsw));
+                const f32x4_t wv = *reinterpret_cast<const f32x4_t*>(wr + 4 * (q ^ wsw));
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    if (j0 + 4 * q + c < d) acc = mac<CONTRACT>(acc, xv[c], wv[c]);
+            }
+        }
+    };
+    gate_static_for(std::make_integer_sequence<int, RING - 1>{}, [&](auto u) __attribute__((always_inline)) {
+        if (decltype(u)::value < nst) issue(decltype(u)::value, buf(u));
+    });
+    for (int64_t st0 = 0; st0 < nst; st0 += RING) {
+        gate_static_for(std::make_integer_sequence<int, RING>{}, [&](auto u) __attribute__((always_inline)) {
+            constexpr int U = decltype(u)::value;
+            const int64_t st = st0 + U;
+            if (st < nst) {
+                wait_stage(st);
+                consume(buf(u), st);
+                __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this stage is read
+                if (st + RING - 1 < nst)
+                    issue(st + RING - 1, buf(std::integral_constant<int, (U + RING - 1) % RING>{}));
+            }
+        });
+    }
+    if (r < nt && e < E) logits[(t0 + r) * E + e] = acc;
 }
 
 // -------------------------------------------------------------- routers
@@ -414,6 +560,25 @@ void launch_gate_logits(const float* x, const float* w, float* logits,
                         int64_t T, int64_t d, int64_t E, int contract,
                         hipStream_t s) {
     if (T == 0 || E == 0) return;
+    auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    // The ring form for E <= 8 (16 token rows x 4 experts or 8 x 8 per wave).
+    // At E = 16 a wave would hold 4 tokens and stream 16 expert rows for
+    // them -- 4x the token bytes (measured 2.4x slower at the reference's
+    // layer shape) -- so E > 8 keeps the kernel above.
+    if (E <= 8 && d % 4 == 0 && d >= 4 && al(x) && al(w) && d * 16 * 4 < (int64_t(1) << 31)) {
+        const int eb = E <= 4 ? 4 : 8;
+        const dim3 grid(static_cast<unsigned>(ceil_div(T, 64 / eb)));
+        auto go = [&](auto kernel) {
+            hipLaunchKernelGGL(kernel, grid, dim3(64), 0, s, x, w, logits, T, d, E);
+        };
+        switch (eb * 2 + (contract ? 1 : 0)) {
+            case 8: go(gate_ring_kernel<0, 4>); break;
+            case 9: go(gate_ring_kernel<1, 4>); break;
+            case 16: go(gate_ring_kernel<0, 8>); break;
+            default: go(gate_ring_kernel<1, 8>); break;
+        }
+        return;
+    }
     int eb = 8;
     while (eb < E && eb < 64) eb <<= 1;
     // 4 tokens per thread from 32 experts up (small E keeps one output per
