@@ -59,6 +59,12 @@
 #ifndef MOE_DENSE_SCHED
 #define MOE_DENSE_SCHED 30
 #endif
+// The small dense tiles (64 x 128, 32 x 128) serve short and skinny
+// products whose few workgroups per CU cannot hide HBM latency with two
+// stages: they take the ring too, for a second step of loads in flight.
+#ifndef MOE_DENSE_SMALL_SCHED
+#define MOE_DENSE_SMALL_SCHED 62
+#endif
 
 namespace moe {
 namespace {
@@ -943,12 +949,11 @@ using W2NarrowCfg = CfgOf<0>::T;  // w2 with d too narrow for the wide tile's n-
 
 template <class C, bool NN>
 void launch_dense(const GemmArgs& a, bool vec, hipStream_t s) {
-    launch_cfg<C, MOE_DENSE_SCHED | SCHED_DIRECT, NN, false, 1, EPI_BIAS>(a, vec, s);
+    launch_cfg<C, MOE_DENSE_SMALL_SCHED | SCHED_DIRECT, NN, false, 1, EPI_BIAS>(a, vec, s);
 }
 
-template <class C>
+template <class C, int SCHED>
 int dense_occupancy(bool nn) {
-    constexpr int SCHED = MOE_DENSE_SCHED | SCHED_DIRECT;
     int n = 0;
     const hipError_t e =
         nn ? hipOccupancyMaxActiveBlocksPerMultiprocessor(
@@ -1010,9 +1015,9 @@ GemmTile dense_tile(int tile) {
 
 int dense_blocks_per_cu(int tile, bool nn) {
     switch (tile) {
-        case 1: return dense_occupancy<DenseMidCfg>(nn);
-        case 2: return dense_occupancy<DenseSmallCfg>(nn);
-        default: return dense_occupancy<DenseCfg>(nn);
+        case 1: return dense_occupancy<DenseMidCfg, MOE_DENSE_SMALL_SCHED | SCHED_DIRECT>(nn);
+        case 2: return dense_occupancy<DenseSmallCfg, MOE_DENSE_SMALL_SCHED | SCHED_DIRECT>(nn);
+        default: return dense_occupancy<DenseCfg, MOE_DENSE_SCHED | SCHED_DIRECT>(nn);
     }
 }
 
