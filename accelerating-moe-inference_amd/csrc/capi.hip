@@ -115,10 +115,12 @@ DensePlan plan_dense(moe_ctx* ctx, bool nn, bool direct, int64_t M, int64_t N, i
     };
     // fitted constants: MFMA efficiency per tile shape, latency of one load
     // stage, start-up and drain of a round of workgroups, achievable HBM
-    // bandwidth, launch and reduction overheads
+    // bandwidth, launch and reduction overheads, and the slowdown of a
+    // workgroup alone on its CU (4096 x 1024 x 1024: 128 x 128 tiles, one
+    // per CU, 95.6 us; 64 x 128 tiles, two per CU, 87.4 us)
     static constexpr double kEff[moe::kDenseTiles] = {0.80, 0.80, 0.50};
     constexpr double kStageLatency = 0.6e-6, kRound = 1e-6, kHbm = 5.0e12, kLaunch = 2e-6,
-                     kReduce = 2e-6;
+                     kReduce = 2e-6, kSolo = 1.15;
     // each tile shape runs 4 waves, one per SIMD
     const double simd_rate = 157.3e12 / (4.0 * ctx->cus);
     double best_t = 1e30;
@@ -140,8 +142,14 @@ DensePlan plan_dense(moe_ctx* ctx, bool nn, bool direct, int64_t M, int64_t N, i
             // rounds of `occ` resident workgroups, then a last partial round
             const int64_t per_cu = moe::ceil_div(blocks, ctx->cus);
             const int64_t full = per_cu / occ, rest = per_cu % occ;
-            double t_cu = full * (steps * std::max(occ * step_mma, kStageLatency) + kRound);
-            if (rest > 0) t_cu += steps * std::max(rest * step_mma, kStageLatency) + kRound;
+            // a round of r resident workgroups; alone on its CU a workgroup's
+            // waves cannot hide their own fragment reads and barriers
+            auto round_time = [&](int64_t r) {
+                const double mma = double(r) * step_mma * (r == 1 ? kSolo : 1.0);
+                return steps * std::max(mma, kStageLatency) + kRound;
+            };
+            double t_cu = double(full) * round_time(occ);
+            if (rest > 0) t_cu += round_time(rest);
             double bytes = 4.0 * (double(M) * K + double(K) * N * mt + double(M) * N);
             if (S > 1) bytes += 8.0 * S * double(M) * N;
             double est = std::max(t_cu, bytes / kHbm) + kLaunch;
