@@ -14,11 +14,14 @@
 // key.  No transpose through LDS, no S x S buffer in HBM.
 //
 // Softmax (PhiAttention::forward, src/layer.cu:118-140): score / sqrt(hd),
-// keys ki <= qi within the window, weights float(exp(double(s - m))); the
-// maximum is carried online (rescaling the partial sums by
-// float(exp(double(m_old - m_new)))), and the output divides the weighted sum
-// by the denominator at the end -- the same values as the reference's loop
-// up to rounding.
+// keys ki <= qi within the window, weights exp(s - m); the maximum is carried
+// online (rescaling the partial sums by exp(m_old - m_new)), and the output
+// divides the weighted sum by the denominator at the end -- the same values
+// as the reference's loop up to rounding.  The reference rounds
+// float(exp(double(x))); here exp is the single-precision hardware exp2 of
+// x * log2(e) (relative error about |x| * 6e-8 + 1 ulp, x <= 0), which the
+// online rescaling's different rounding already puts outside bit-exactness:
+// the fp64 exp took about half as long as the MFMAs of a key block.
 #include "common.hpp"
 
 #include <cmath>
@@ -32,8 +35,9 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int kQTile = 128;  // queries per workgroup (4 waves x 32)
 constexpr int kKBlock = 32;  // keys per block
 
-__device__ __forceinline__ float exp_ref(float x) {
-    return static_cast<float>(exp(static_cast<double>(x)));
+// exp(x) for x <= 0 (or -inf: 0)
+__device__ __forceinline__ float exp_fast(float x) {
+    return __builtin_amdgcn_exp2f(x * 1.44269504088896340736f);
 }
 
 template <int HD>
@@ -163,11 +167,11 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(const float* __restrict
             const float m_new = fmaxf(m_run, bmax);
             // rescale of the sums so far (none yet, or nothing visible: 1)
             const float alpha = m_run == -INFINITY || m_new == -INFINITY ? 1.0f
-                                                                        : exp_ref(m_run - m_new);
+                                                                        : exp_fast(m_run - m_new);
             float psum = 0.0f;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                s[r] = s[r] == -INFINITY ? 0.0f : exp_ref(s[r] - m_new);
+                s[r] = s[r] == -INFINITY ? 0.0f : exp_fast(s[r] - m_new);
                 psum += s[r];
             }
             den = den * alpha + psum;
