@@ -640,3 +640,41 @@ def test_errors_are_reported(ctx, pkg, torch):
     with pytest.raises(pkg.MoeInvalidArgument):
         pkg._check(pkg.load_library().moe_gate_logits(
             ctx.handle, None, None, None, 4, 8, 2000, 1, None))
+
+
+@pytest.mark.parametrize("router", [0, 1])
+def test_layer_empty_batch_and_single_expert(ctx, pkg, torch, orc, router):
+    """T = 0: the call succeeds and writes nothing (the outputs keep their
+    contents).  E = 1, k = 1: every token goes to the one expert; routing,
+    weights and the layer output match the oracle."""
+    print(f"layer edge cases router={router}", flush=True)
+    d, d_ff = 64, 96
+    rng = np.random.default_rng(11 + router)
+    w = {"gate_w": dev(torch, normal(rng, (4, d), 0.1)),
+         "w1": dev(torch, normal(rng, (4, d_ff, d), 0.05)),
+         "w3": dev(torch, normal(rng, (4, d_ff, d), 0.05)),
+         "w2": dev(torch, normal(rng, (4, d, d_ff), 0.05))}
+    desc = pkg.make_desc(0, d, 4, 2, d_ff, act=pkg.ACT_SWIGLU, router=router)
+    y0 = torch.full((1, d), 3.0, device="cuda")
+    ctx.layer_forward(desc, w, torch.zeros((1, d), device="cuda"), y0)
+    torch.cuda.synchronize()
+    assert torch.all(y0 == 3.0)
+
+    T = 37
+    x = normal(rng, (T, d))
+    gw = normal(rng, (1, d), 0.1)
+    w1 = normal(rng, (1, d_ff, d), 0.05)
+    w3 = normal(rng, (1, d_ff, d), 0.05)
+    w2 = normal(rng, (1, d, d_ff), 0.05)
+    desc = pkg.make_desc(T, d, 1, 1, d_ff, act=pkg.ACT_SWIGLU, router=router)
+    y = torch.empty((T, d), device="cuda")
+    idx = torch.full((T, 1), -1, dtype=torch.int32, device="cuda")
+    tw = torch.empty((T, 1), device="cuda")
+    ctx.layer_forward(desc, {"gate_w": dev(torch, gw), "w1": dev(torch, w1),
+                             "w3": dev(torch, w3), "w2": dev(torch, w2)},
+                      dev(torch, x), y, idx, tw)
+    ry, ridx, rw = orc.moe_forward(x, gw, w1, w3, w2, 1, act=orc.ACT_SWIGLU,
+                                   router_mode=router)
+    assert np.array_equal(host(idx), ridx) and not np.any(host(idx))
+    assert np.array_equal(host(tw), rw)
+    assert_close(host(y), ry, what="E=1 layer")
