@@ -3,6 +3,7 @@
 // scenario as an extern "C" function for tests/test_dropin.py (ctypes).
 // Exceptions come back as codes: 1 invalid_argument, 2 runtime_error,
 // 3 logic_error, 4 out_of_range, 5 other; shim_error() holds the message.
+#include <chrono>
 #include <cmath>
 #include <cstdint>
 #include <cstring>
@@ -264,6 +265,23 @@ int shim_moe(const char* path, int64_t layer, int contract, const float* x, int6
         expect(Y.ndim() == 2 && Y.size(0) == size_t(rows) && Y.size(1) == size_t(h), "y shape");
         std::memcpy(y, Y.data(), Y.size() * sizeof(float));
         std::memcpy(topk, idx.data(), idx.size() * sizeof(int32_t));
+    });
+}
+
+// Host-to-host time of PhiMoE::forward (the drop-in's PCIe copies included):
+// builds the layer once, runs `warmup` untimed and `iters` timed forwards of
+// x [rows, h], and returns the mean milliseconds per forward.
+int shim_moe_time(const char* path, int64_t layer, const float* x, int64_t rows, int64_t h,
+                  int64_t warmup, int64_t iters, double* ms) {
+    return guarded([&] {
+        ModelLoader l(path);
+        PhiMoE moe(l, size_t(layer));
+        Tensor X = make(x, {size_t(rows), size_t(h)}), Y;
+        for (int64_t i = 0; i < warmup; ++i) moe.forward(X, Y);
+        const auto t0 = std::chrono::steady_clock::now();
+        for (int64_t i = 0; i < iters; ++i) moe.forward(X, Y);
+        const auto t1 = std::chrono::steady_clock::now();
+        *ms = std::chrono::duration<double, std::milli>(t1 - t0).count() / double(iters);
     });
 }
 

@@ -205,6 +205,11 @@ def test_linear_mlp_moe_vs_oracle(shim, orc, tmp_path):
                                       stack("w3"), stack("w2"), 2, contract=contract)
         assert np.array_equal(topk, ridx)
         assert_close(y, ry, what=f"PhiMoE contract={contract}")
+    # the host-to-host timing entry (PCIe copies included) runs the same layer
+    ms = ctypes.c_double(0.0)
+    assert shim.shim_moe_time(path, I(3), fptr(x), I(rows), I(h), I(1), I(2),
+                              ctypes.byref(ms)) == 0, err(shim)
+    assert ms.value > 0.0
 
 
 def test_moe_missing_expert_raises(shim, tmp_path):
