@@ -394,7 +394,9 @@ struct LayerWs {
     size_t bytes;
 };
 
-LayerWs carve_layer(void* base, const moe_layer_desc& d) {
+// w2_splits: the K splits of the layer's w2 (choose_w2_plan); out_rows holds
+// that many partial row buffers.
+LayerWs carve_layer(void* base, const moe_layer_desc& d, int w2_splits) {
     Carve c(base);
     LayerWs w{};
     const int64_t pairs = d.T * d.k;
@@ -407,7 +409,7 @@ LayerWs carve_layer(void* base, const moe_layer_desc& d) {
     w.perm = c.take<int32_t>(pairs);
     w.inv = c.take<int32_t>(pairs);
     w.h = c.take<float>(pairs * d.d_ff);
-    w.out_rows = c.take<float>(pairs * d.d * moe::kMaxW2Splits);
+    w.out_rows = c.take<float>(pairs * d.d * std::max(w2_splits, 1));
     if (d.norm != MOE_NORM_NONE) {
         w.norm_mean = c.take<float>(d.T);
         w.norm_inv = c.take<float>(d.T);
@@ -415,6 +417,65 @@ LayerWs carve_layer(void* base, const moe_layer_desc& d) {
     }
     w.bytes = c.off + 256;
     return w;
+}
+
+// The MoE layer forward on a workspace at `base` carved by carve_layer
+// (the context's grow-only workspace).
+void layer_forward(moe_ctx* ctx, const moe_layer_desc& D, const moe_layer_weights& weights,
+                   const float* x, float* y, int32_t* topk_idx_out, float* topk_w_out,
+                   hipStream_t s, void* base, const W2Plan& plan) {
+    check_ptr(x, "x");
+    check_ptr(y, "y");
+    check_ptr(weights.gate_w, "gate_w");
+    if (D.d_ff > 0) {
+        check_ptr(weights.w1, "w1");
+        check_ptr(weights.w2, "w2");
+        if (D.act == MOE_ACT_SWIGLU) check_ptr(weights.w3, "w3");
+    }
+    moe::require(D.d % 4 != 0 || (aligned16(x) && aligned16(y)),
+                 "layer: x and y must be 16-byte aligned");
+    const bool norm = D.norm != MOE_NORM_NONE, rms = D.norm == MOE_NORM_RMS;
+    if (norm) {
+        moe::require(D.d > 0, "norm: d must be > 0");
+        check_ptr(weights.norm_w, "norm_w");
+        if (!rms) check_ptr(weights.norm_b, "norm_b");
+    }
+    const int splits = plan.splits;
+    LayerWs ws = carve_layer(base, D, splits);
+    int32_t* idx = topk_idx_out != nullptr ? topk_idx_out : ws.idx;
+    float* w = topk_w_out != nullptr ? topk_w_out : ws.w;
+    const int64_t nb = moe::ceil_div(D.T, moe::kPermTokens);
+
+    // The experts' input: x, or its normalised copy (written once, read
+    // by the gate and the w1/w3 GEMM; the residual stays x).
+    const float* xin = x;
+    if (norm) {
+        ctx->launch(rms ? "rms_norm" : "layer_norm", s, [&] {
+            moe::launch_layer_norm(x, weights.norm_w, rms ? nullptr : weights.norm_b, D.T, D.d,
+                                   D.norm_eps, D.contract, rms, ws.norm_mean, ws.norm_inv,
+                                   ws.xnorm, ctx->cus, s);
+        });
+        xin = ws.xnorm;
+    }
+
+    ctx->launch("gate_logits", s, [&] {
+        moe::launch_gate_logits(xin, weights.gate_w, ws.logits, D.T, D.d, D.E, D.contract, s);
+    });
+    ctx->launch(D.router == MOE_ROUTER_PHI_QUANT ? "route_phi" : "route_softmax", s, [&] {
+        moe::launch_route(ws.logits, weights.expert_bias, D.T, D.E, D.k, D.router, D.quantum,
+                          D.tie_eps, idx, w, s);
+    });
+    ctx->launch("perm_count", s, [&] { moe::launch_perm_count(idx, D.T, D.k, D.E, ws.counts, s); });
+    ctx->launch("perm_scan", s, [&] { moe::launch_perm_scan(ws.counts, nb, D.E, ws.offsets, s); });
+    ctx->launch("perm_place", s, [&] {
+        moe::launch_perm_place(idx, D.T, D.k, D.E, ws.counts, ws.perm, ws.inv, s);
+    });
+    expert_ffn(ctx, xin, ws.perm, ws.offsets, weights.w1, weights.w3, weights.w2, D.act, D.T, D.k,
+               D.d, D.d_ff, D.E, ws.h, ws.out_rows, s, splits, plan.tile);
+    ctx->launch("combine", s, [&] {
+        moe::launch_combine(ws.out_rows, idx, w, ws.inv, D.residual ? x : nullptr, y, D.T, D.k,
+                            D.d, D.T * D.k, D.contract, splits, D.T * D.k * D.d, s);
+    });
 }
 
 }  // namespace
@@ -493,7 +554,9 @@ int moe_ctx_reserve(moe_ctx* ctx, const moe_layer_desc* desc) {
         check_ctx(ctx);
         check_desc(desc);
         DeviceScope dev(ctx->device);
-        ctx->workspace(carve_layer(nullptr, *desc).bytes);
+        const W2Plan plan =
+            choose_w2_plan(ctx, desc->T * desc->k, desc->d, desc->d_ff, desc->E);
+        ctx->workspace(carve_layer(nullptr, *desc, plan.splits).bytes);
     });
 }
 
@@ -1026,65 +1089,12 @@ int moe_layer_forward(moe_ctx* ctx, const moe_layer_desc* desc,
         check_ctx(ctx);
         check_desc(desc);
         check_ptr(weights, "weights");
-        const moe_layer_desc& D = *desc;
-        if (D.T == 0) return;
-        check_ptr(x, "x");
-        check_ptr(y, "y");
-        check_ptr(weights->gate_w, "gate_w");
-        if (D.d_ff > 0) {
-            check_ptr(weights->w1, "w1");
-            check_ptr(weights->w2, "w2");
-            if (D.act == MOE_ACT_SWIGLU) check_ptr(weights->w3, "w3");
-        }
-        moe::require(D.d % 4 != 0 || (aligned16(x) && aligned16(y)),
-                     "layer: x and y must be 16-byte aligned");
-        const bool norm = D.norm != MOE_NORM_NONE, rms = D.norm == MOE_NORM_RMS;
-        if (norm) {
-            moe::require(D.d > 0, "norm: d must be > 0");
-            check_ptr(weights->norm_w, "norm_w");
-            if (!rms) check_ptr(weights->norm_b, "norm_b");
-        }
+        if (desc->T == 0) return;
         DeviceScope dev(ctx->device);
-        hipStream_t s = as_stream(stream);
-        LayerWs ws = carve_layer(ctx->workspace(carve_layer(nullptr, D).bytes), D);
-        int32_t* idx = topk_idx_out != nullptr ? topk_idx_out : ws.idx;
-        float* w = topk_w_out != nullptr ? topk_w_out : ws.w;
-        const int64_t nb = moe::ceil_div(D.T, moe::kPermTokens);
-
-        // The experts' input: x, or its normalised copy (written once, read
-        // by the gate and the w1/w3 GEMM; the residual stays x).
-        const float* xin = x;
-        if (norm) {
-            ctx->launch(rms ? "rms_norm" : "layer_norm", s, [&] {
-                moe::launch_layer_norm(x, weights->norm_w, rms ? nullptr : weights->norm_b, D.T,
-                                       D.d, D.norm_eps, D.contract, rms, ws.norm_mean,
-                                       ws.norm_inv, ws.xnorm, ctx->cus, s);
-            });
-            xin = ws.xnorm;
-        }
-
-        ctx->launch("gate_logits", s, [&] {
-            moe::launch_gate_logits(xin, weights->gate_w, ws.logits, D.T, D.d, D.E, D.contract, s);
-        });
-        ctx->launch(D.router == MOE_ROUTER_PHI_QUANT ? "route_phi" : "route_softmax", s, [&] {
-            moe::launch_route(ws.logits, weights->expert_bias, D.T, D.E, D.k, D.router, D.quantum,
-                              D.tie_eps, idx, w, s);
-        });
-        ctx->launch("perm_count", s, [&] { moe::launch_perm_count(idx, D.T, D.k, D.E, ws.counts, s); });
-        ctx->launch("perm_scan", s, [&] {
-            moe::launch_perm_scan(ws.counts, nb, D.E, ws.offsets, s);
-        });
-        ctx->launch("perm_place", s, [&] {
-            moe::launch_perm_place(idx, D.T, D.k, D.E, ws.counts, ws.perm, ws.inv, s);
-        });
-        const W2Plan plan = choose_w2_plan(ctx, D.T * D.k, D.d, D.d_ff, D.E);
-        const int splits = plan.splits;
-        expert_ffn(ctx, xin, ws.perm, ws.offsets, weights->w1, weights->w3, weights->w2, D.act,
-                   D.T, D.k, D.d, D.d_ff, D.E, ws.h, ws.out_rows, s, splits, plan.tile);
-        ctx->launch("combine", s, [&] {
-            moe::launch_combine(ws.out_rows, idx, w, ws.inv, D.residual ? x : nullptr, y, D.T,
-                                D.k, D.d, D.T * D.k, D.contract, splits, D.T * D.k * D.d, s);
-        });
+        const W2Plan plan = choose_w2_plan(ctx, desc->T * desc->k, desc->d, desc->d_ff, desc->E);
+        void* base = ctx->workspace(carve_layer(nullptr, *desc, plan.splits).bytes);
+        layer_forward(ctx, *desc, *weights, x, y, topk_idx_out, topk_w_out, as_stream(stream),
+                      base, plan);
     });
 }
 

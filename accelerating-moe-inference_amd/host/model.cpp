@@ -2,8 +2,8 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <numeric>
 #include <stdexcept>
-#include <unordered_map>
 
 #include "config.h"
 #include "device.h"
@@ -24,53 +24,59 @@ enum ModelSlot : std::size_t {
     kTailBeg, kTailEnd
 };
 
-// The prefix trie of a batch (src/model.cu:1624-1680): one node per distinct
-// prefix in order of first appearance, with its token, depth and root path.
+// The prefix trie of a batch: one node (one activation row) per distinct
+// prefix, so a prefix several sequences share is computed once -- the row set
+// of the reference's generate() (src/model.cu:1624-1680); node order does not
+// change any row's arithmetic.  Built by sorting: in lexicographic order a
+// sequence shares with its predecessor exactly their longest common prefix,
+// so one walk over the sorted batch creates the nodes in depth-first order,
+// each new node extending the root path the walk holds, which is also the
+// node's attention key list.
 struct Trie {
-    std::vector<int32_t> token, depth, parent, key_off, key_rows, last;
+    std::vector<int32_t> token, depth;  // per node
+    std::vector<int32_t> key_off;       // node i's key list: key_rows[key_off[i] .. key_off[i+1])
+    std::vector<int32_t> key_rows;      // root paths, each ending at its own node
+    std::vector<int32_t> last;          // per input sequence: the node of its last token
     std::size_t max_len = 0;
 };
 
 Trie build_trie(const std::vector<std::vector<int>>& seqs, std::size_t vocab) {
-    Trie t;
-    std::unordered_map<long long, int32_t> child;
-    child.reserve(seqs.size() * 64);
+    // validation in input order, so an input raises the reference's error
     for (const std::vector<int>& seq : seqs) {
         if (seq.empty()) throw std::invalid_argument("empty input");
         if (seq.size() > apss26::MAX_POSITION_EMBEDDINGS)
             throw std::invalid_argument("sequence is too long");
-        int32_t parent = -1;
-        for (std::size_t si = 0; si < seq.size(); ++si) {
-            const int token = seq[si];
+        for (const int token : seq)
             if (token < 0 || static_cast<std::size_t>(token) >= vocab)
                 throw std::invalid_argument("token out of vocabulary");
-            const long long key =
-                (static_cast<long long>(parent) + 1) * static_cast<long long>(vocab) + token;
-            const auto it = child.find(key);
-            if (it != child.end()) {
-                parent = it->second;
-                continue;
-            }
-            const auto node = static_cast<int32_t>(t.token.size());
-            t.token.push_back(token);
-            t.parent.push_back(parent);
-            t.depth.push_back(static_cast<int32_t>(si));
-            child.emplace(key, node);
-            parent = node;
-        }
-        t.last.push_back(parent);
     }
-    const std::size_t n = t.token.size();
-    t.key_off.assign(n + 1, 0);
-    for (std::size_t i = 0; i < n; ++i) t.key_off[i + 1] = t.key_off[i] + t.depth[i] + 1;
-    t.key_rows.resize(static_cast<std::size_t>(t.key_off[n]));
-    for (std::size_t i = 0; i < n; ++i) {
-        int32_t* dst = t.key_rows.data() + t.key_off[i];
-        const int32_t p = t.parent[i];
-        if (p >= 0)  // the parent's path is this node's minus its last entry
-            for (int32_t j = 0; j < t.depth[i]; ++j) dst[j] = t.key_rows[t.key_off[p] + j];
-        dst[t.depth[i]] = static_cast<int32_t>(i);
-        t.max_len = std::max<std::size_t>(t.max_len, static_cast<std::size_t>(t.depth[i]) + 1);
+    std::vector<std::size_t> order(seqs.size());
+    std::iota(order.begin(), order.end(), std::size_t(0));
+    std::stable_sort(order.begin(), order.end(),
+                     [&](std::size_t a, std::size_t b) { return seqs[a] < seqs[b]; });
+    Trie t;
+    t.last.assign(seqs.size(), -1);
+    t.key_off.push_back(0);
+    std::vector<int32_t> walk;  // walk[p]: the node at depth p of the current sequence
+    const std::vector<int>* prev = nullptr;
+    for (const std::size_t b : order) {
+        const std::vector<int>& seq = seqs[b];
+        std::size_t shared = 0;
+        if (prev != nullptr)
+            shared = static_cast<std::size_t>(
+                std::mismatch(seq.begin(), seq.end(), prev->begin(), prev->end()).first -
+                seq.begin());
+        walk.resize(shared);
+        for (std::size_t p = shared; p < seq.size(); ++p) {
+            walk.push_back(static_cast<int32_t>(t.token.size()));
+            t.token.push_back(seq[p]);
+            t.depth.push_back(static_cast<int32_t>(p));
+            t.key_rows.insert(t.key_rows.end(), walk.begin(), walk.end());
+            t.key_off.push_back(static_cast<int32_t>(t.key_rows.size()));
+        }
+        t.last[b] = walk[seq.size() - 1];
+        t.max_len = std::max(t.max_len, seq.size());
+        prev = &seq;
     }
     return t;
 }

@@ -160,10 +160,37 @@ def host_cpu():
     return f"{model}, {os.cpu_count()} logical cores on the host"
 
 
+def tile_cover_sample(gidx, E, bm=128, block=32):
+    """Tokens whose packed rows land in every bm-row m-tile of every expert of
+    the grouped GEMMs (per tile its last row, so each expert's ragged last
+    tile, and one row of a further 32-row MFMA block), then every other token
+    in ascending order.  Routing is per token, so the layer recomputed on any
+    subset gives exactly those rows of the full layer."""
+    import numpy as np
+    T, k = gidx.shape
+    order = np.argsort(gidx.ravel(), kind="stable")
+    tok = order // k
+    offsets = np.concatenate([[0], np.cumsum(np.bincount(gidx.ravel(), minlength=E))])
+    pick = {0, T - 1}
+    for e in range(E):
+        n = int(offsets[e + 1] - offsets[e])
+        for j in range((n + bm - 1) // bm):
+            base, rows = int(offsets[e]) + j * bm, min(bm, n - j * bm)
+            pick.add(int(tok[base + rows - 1]))
+            lo = ((j + e) % ((rows + block - 1) // block)) * block
+            pick.add(int(tok[base + lo + (j * 7 + e * 13) % min(block, rows - lo)]))
+    cover = np.array(sorted(pick), dtype=np.int64)
+    rest = np.setdiff1d(np.arange(T), cover)
+    return np.concatenate([cover, rest]), len(cover)
+
+
 def cpu_baseline(x, weights, cfg, pkg_outputs, target_s):
-    """The oracle's PhiMoE::forward restatement on a prefix of the tokens,
-    sized to about target_s seconds of CPU work.  Test infrastructure: timed
-    here as the reported CPU baseline, never part of the GPU measurement."""
+    """The oracle's PhiMoE::forward restatement on a token sample sized to
+    about target_s seconds of CPU work (at least the tokens that cover every
+    m-tile of every expert), checked against the GPU's rows; and the oracle's
+    gate and router on every token, checked against the GPU's routing.  Test
+    infrastructure: timed here as the reported CPU baseline, never part of
+    the GPU measurement."""
     import numpy as np
     sys.path.insert(0, ROOT)
     import oracle
@@ -173,40 +200,47 @@ def cpu_baseline(x, weights, cfg, pkg_outputs, target_s):
     gw, w1, w3, w2, bias = (weights[n] for n in ("gate_w", "w1", "w3", "w2", "expert_bias"))
     nw, nb = weights.get("norm_w"), weights.get("norm_b")
     k = cfg["k"]
+    router = (oracle.ROUTER_PHI_QUANT if cfg.get("router") == "phi_quant"
+              else oracle.ROUTER_SOFTMAX_TOPK)
+    gy, gidx = pkg_outputs
 
-    def run(n):
+    def normed(xs):
+        if nw is None:
+            return xs
+        if nb is None:
+            return oracle.rms_norm(xs, nw, NORM_EPS, oracle.CONTRACT_FMA)[0]
+        return oracle.layer_norm(xs, nw, nb, NORM_EPS, oracle.CONTRACT_FMA)[0]
+
+    def run(toks):
         t0 = time.perf_counter()
-        xin = x[:n]
-        if nw is not None:  # the decoder block: y = x + MoE(norm(x))
-            if nb is None:
-                xin, _ = oracle.rms_norm(xin, nw, NORM_EPS, oracle.CONTRACT_FMA)
-            else:
-                xin, _, _ = oracle.layer_norm(xin, nw, nb, NORM_EPS, oracle.CONTRACT_FMA)
-        y, idx, w = oracle.moe_forward(xin, gw, w1, w3, w2, k, act=oracle.ACT_SWIGLU,
-                                       router_mode=(oracle.ROUTER_PHI_QUANT
-                                                    if cfg.get("router") == "phi_quant"
-                                                    else oracle.ROUTER_SOFTMAX_TOPK),
+        y, idx, w = oracle.moe_forward(normed(x[toks]), gw, w1, w3, w2, k,
+                                       act=oracle.ACT_SWIGLU, router_mode=router,
                                        expert_bias=bias)
-        if nw is not None:
-            y = y + x[:n]
+        if nw is not None:  # the decoder block: y = x + MoE(norm(x))
+            y = y + x[toks]
         return time.perf_counter() - t0, y, idx
 
-    # Grow the prefix until it takes about target_s: small prefixes leave
+    order, n_cover = tile_cover_sample(gidx, cfg["E"])
+    # Grow the sample until it takes about target_s: small samples leave
     # most of the threads idle (the reference parallelises over an expert's
     # rows), so the per-token time only settles once experts hold >= threads
     # rows each.
-    n = 16
+    n = max(16, n_cover)
     while True:
-        dt, y, idx = run(n)
+        toks = np.sort(order[:n])
+        dt, y, idx = run(toks)
         if dt >= 0.5 * target_s or n >= cfg["T"]:
             break
         n = int(min(cfg["T"], max(2 * n, round(0.9 * n * target_s / max(dt, 1e-9)))))
-    gy, gidx = pkg_outputs
     ref_scale = float(np.max(np.abs(y))) or 1.0
+    all_idx, _ = oracle.route(oracle.matmul_nt(normed(x), gw, oracle.CONTRACT_FMA), k,
+                              mode=router, expert_bias=bias)
     parity = {
         "tokens": n,
-        "routing_bit_exact": bool(np.array_equal(gidx[:n], idx)),
-        "max_rel_err": float(np.max(np.abs(gy[:n] - y)) / ref_scale),
+        "tile_covering_tokens": n_cover,
+        "routing_bit_exact": bool(np.array_equal(gidx[toks], idx)),
+        "routing_bit_exact_all_tokens": bool(np.array_equal(gidx, all_idx)),
+        "max_rel_err": float(np.max(np.abs(gy[toks] - y)) / ref_scale),
     }
     return {
         "value": n / dt,
@@ -214,8 +248,10 @@ def cpu_baseline(x, weights, cfg, pkg_outputs, target_s):
         "cores": oracle.get_threads(),
         "kind": "port",
         "host": host_cpu(),
-        "sample": (f"first {n} of {cfg['T']} tokens of the same layer (same weights; "
-                   f"routing is per token), {dt:.1f} s on {oracle.get_threads()} threads"),
+        "sample": (f"{n} of {cfg['T']} tokens of the same layer (same weights; routing is "
+                   f"per token): the {n_cover} whose packed rows cover every 128-row m-tile "
+                   f"of every expert, then the lowest-numbered others; {dt:.1f} s on "
+                   f"{oracle.get_threads()} threads"),
     }, parity
 
 
@@ -457,14 +493,22 @@ def main():
     for _ in range(args.warmup):
         ctx.layer_forward(desc, weights, x, y, idx, w)
     torch.cuda.synchronize()
-    ctx.reset_timing()
-    ctx.set_timing(True)  # HIP events around every launch, on the launch stream
-    torch.cuda.synchronize()
+    # the timed steps: no per-kernel events
     t0 = time.perf_counter()
     for _ in range(args.steps):
         ctx.layer_forward(desc, weights, x, y, idx, w)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    # an instrumented pass of as many steps: HIP events around every launch,
+    # on the stream the kernels run on (per-kernel times and the roofline)
+    ctx.reset_timing()
+    ctx.set_timing(True)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    for _ in range(args.steps):
+        ctx.layer_forward(desc, weights, x, y, idx, w)
+    torch.cuda.synchronize()
+    instrumented = time.perf_counter() - t1
     ctx.set_timing(False)
     kt = ctx.kernel_times()
 
@@ -533,6 +577,9 @@ def main():
         "expert_rows": counts.tolist(),
         "cpu_baseline": cpu,
         "cpu_sample_parity": parity,
+        "timing": (f"ms_per_step from {args.steps} steps without per-kernel events; "
+                   f"kernel_avg_ms and the roofline from HIP events over {args.steps} more "
+                   f"steps ({1e3 * instrumented / args.steps:.3f} ms per instrumented step)"),
     }
     if args.config == "ref":
         # the reference's own per-layer expert GEMM times at this shape (RTX 3090)

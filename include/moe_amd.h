@@ -118,7 +118,11 @@ typedef struct moe_layer_weights {
 /* ---- context: device binding, grow-only workspace, optional kernel timing.
  * Replaces the reference's DeviceBuffer/Scratch (src/model.cu:45-68,
  * 1294-1324).  A context is not safe for concurrent calls from several
- * threads (the reference's generate() is not either, include/model.h:124-127). */
+ * threads (the reference's generate() is not either, include/model.h:124-127).
+ * Every call on a context uses the same workspace: calls on different streams
+ * must be ordered by the caller (an event, or one stream), since two in
+ * flight at once would share it.  Growing the workspace synchronises the
+ * device before the old buffer is freed. */
 int moe_ctx_create(int device, moe_ctx** out);
 int moe_ctx_destroy(moe_ctx* ctx);
 /* Grow the workspace so that moe_layer_forward(desc) allocates nothing. */

@@ -69,3 +69,39 @@ def zipf_bias(E, s=1.2):
     p = ranks ** -s
     p /= p.sum()
     return np.log(p).astype(np.float32)
+
+
+def packed_rows(topk_idx, E):
+    """The packed order of the (token, slot) pairs: stable by expert, tokens
+    ascending within an expert.  Returns (offsets[E+1], token of each packed
+    row).  Used only to choose which tokens a full-size test recomputes."""
+    idx = np.asarray(topk_idx)
+    T, k = idx.shape
+    order = np.argsort(idx.ravel(), kind="stable")
+    counts = np.bincount(idx.ravel(), minlength=E)
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    return offsets, (order // k).astype(np.int64)
+
+
+def tile_cover_tokens(topk_idx, E, bm=128, block=32, salt=0):
+    """A token sample whose packed rows land in every bm-row m-tile of every
+    expert of a grouped GEMM: per tile its last row (an expert's ragged last
+    tile included) and one row of a further 32-row MFMA block, rotating over
+    the tile's blocks; plus the first and last token.  Routing is per token,
+    so the layer recomputed on these tokens alone gives exactly those rows of
+    the full layer."""
+    offsets, tok = packed_rows(topk_idx, E)
+    T = np.asarray(topk_idx).shape[0]
+    pick = {0, T - 1}
+    for e in range(E):
+        n = int(offsets[e + 1] - offsets[e])
+        for j in range((n + bm - 1) // bm):
+            base = int(offsets[e]) + j * bm
+            rows = min(bm, n - j * bm)
+            pick.add(int(tok[base + rows - 1]))
+            nblk = (rows + block - 1) // block
+            b = (j + e + salt) % nblk
+            lo = b * block
+            span = min(block, rows - lo)
+            pick.add(int(tok[base + lo + (j * 7 + e * 13 + salt) % span]))
+    return np.array(sorted(pick), dtype=np.int64)

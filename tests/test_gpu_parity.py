@@ -11,7 +11,8 @@ import os
 import numpy as np
 import pytest
 
-from helpers import REL_TOL, assert_close, load_pkg, normal, rel_err, zipf_bias
+from helpers import (REL_TOL, assert_close, load_pkg, normal, rel_err, tile_cover_tokens,
+                     zipf_bias)
 
 pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
@@ -121,6 +122,31 @@ def test_sgemm_square_config2(ctx, torch, orc, n):
     assert_close(host(c), orc.matmul_nn(host(a), host(b)), what=f"nn {n}")
     ctx.sgemm_nt(a, b, c)
     assert_close(host(c), orc.matmul_nt(host(a), host(b)), what=f"nt {n}")
+
+
+@pytest.mark.parametrize("n", [4096, 8192])
+def test_sgemm_square_config2_row_sample(ctx, torch, orc, n):
+    """Config-2 squares 4096^3 and 8192^3 through moe_sgemm_nn / moe_sgemm_nt
+    (the planner's unsplit 128 x 128 tiles): the oracle recomputes whole
+    output rows (each depends only on its A row), two in every 128-row m-tile
+    at rotating positions, so every (m-tile, n-tile) output tile is checked."""
+    print(f"sgemm square {n} (row sample)", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(n + 1)
+    a = torch.rand((n, n), device="cuda", generator=g) * 2 - 1
+    b = torch.rand((n, n), device="cuda", generator=g) * 2 - 1
+    c = torch.empty((n, n), device="cuda")
+    tiles = np.arange(n // 128)
+    rows = np.unique(np.concatenate([tiles * 128 + (tiles * 37) % 128,
+                                     tiles * 128 + 127 - (tiles * 11) % 64]))
+    ah, bh = host(a[torch.from_numpy(rows).to("cuda")]), host(b)
+    ctx.sgemm_nn(a, b, c)
+    # the oracle's NN equals its NT on B^T bit for bit (tests/test_oracle.py);
+    # the NT loop reads B row-wise, which a 256 MB B needs on the host
+    assert_close(host(c[torch.from_numpy(rows).to("cuda")]),
+                 orc.matmul_nt(ah, np.ascontiguousarray(bh.T)), what=f"nn {n} rows")
+    ctx.sgemm_nt(a, b, c)
+    assert_close(host(c[torch.from_numpy(rows).to("cuda")]), orc.matmul_nt(ah, bh),
+                 what=f"nt {n} rows")
 
 
 @pytest.mark.parametrize("m", [16, 64, 256, 512])
@@ -445,7 +471,17 @@ def test_layer_deterministic(ctx, pkg, torch):
     assert torch.equal(y1, y2) and torch.equal(i1, i2) and torch.equal(w1, w2)
 
 
-def _big_layer(ctx, pkg, torch, orc, T, d, E, k, d_ff, mode, bias, sample, seed):
+def _check_all_routing(orc, xin, gw, k, mode, bias, idx, w, contract=1):
+    """Routing of every token against the oracle's gate and router: indices
+    bit-exact; weights bit-exact (PHI_QUANT) or within 1 ulp (softmax)."""
+    logits = orc.matmul_nt(xin, gw, contract=contract)
+    ridx, rw = orc.route(logits, k, mode=mode, expert_bias=bias)
+    assert np.array_equal(idx, ridx), f"routing differs on {int(np.any(idx != ridx, axis=1).sum())} tokens"
+    ulp = np.abs(w.view(np.int32).astype(np.int64) - rw.view(np.int32))
+    assert ulp.max() <= (0 if mode == 0 else 1), "routing weights"
+
+
+def _big_layer(ctx, pkg, torch, orc, T, d, E, k, d_ff, mode, bias, seed):
     g = torch.Generator(device="cuda").manual_seed(seed)
     x = torch.randn((T, d), device="cuda", generator=g)
     gw = torch.randn((E, d), device="cuda", generator=g) * 0.02
@@ -454,31 +490,48 @@ def _big_layer(ctx, pkg, torch, orc, T, d, E, k, d_ff, mode, bias, sample, seed)
     w2 = torch.randn((E, d, d_ff), device="cuda", generator=g) * 0.02
     bias_t = None if bias is None else dev(torch, bias)
     y, idx, w = _layer(ctx, pkg, torch, x, gw, w1, w3, w2, k, act=0, mode=mode, bias=bias_t)
-    counts = np.bincount(host(idx).ravel(), minlength=E)
+    gidx = host(idx)
+    counts = np.bincount(gidx.ravel(), minlength=E)
     assert counts.sum() == T * k
-    xs = host(x)[:sample]
-    ry, ridx, rw = orc.moe_forward(xs, host(gw), host(w1), host(w3), host(w2), k, act=0,
+    xh, gwh = host(x), host(gw)
+    _check_all_routing(orc, xh, gwh, k, mode, bias, gidx, host(w))
+    # every 128-row m-tile of every expert (both grouped GEMMs tile by 128
+    # rows), its ragged last tile and the last token
+    toks = tile_cover_tokens(gidx, E)
+    print(f"full-size layer: routing of all {T} tokens bit-exact; oracle on {len(toks)} "
+          f"tile-covering tokens", flush=True)
+    ry, ridx, rw = orc.moe_forward(xh[toks], gwh, host(w1), host(w3), host(w2), k, act=0,
                                    router_mode=mode, expert_bias=bias)
-    assert np.array_equal(host(idx)[:sample], ridx)
-    assert_close(host(y)[:sample], ry, what="sampled tokens")
+    assert np.array_equal(gidx[toks], ridx)
+    assert_close(host(y)[toks], ry, what="tile-covering tokens")
     return counts
 
 
 def test_layer_mixtral_config3_full_size(ctx, pkg, torch, orc):
-    """Config 3 at full size (4096 x 4096, E=8, top-2 softmax, SwiGLU 14336);
-    the oracle recomputes the first 24 tokens (routing is per token, so their
-    routing and outputs are exactly the full layer's)."""
+    """Config 3 at full size (4096 x 4096, E=8, top-2 softmax, SwiGLU 14336):
+    routing of every token against the oracle, and the outputs of a token
+    sample that covers every m-tile of every expert (routing is per token, so
+    the oracle's layer on those tokens gives exactly their rows)."""
     counts = _big_layer(ctx, pkg, torch, orc, 4096, 4096, 8, 2, 14336, mode=1, bias=None,
-                        sample=24, seed=3)
+                        seed=3)
     assert counts.min() > 0
 
 
 def test_layer_skewed_config4_full_size(ctx, pkg, torch, orc):
     """Config 4 at full size (16384 x 2048, E=64, top-8, SwiGLU 1408, Zipf(1.2)
-    router bias); the oracle recomputes the first 48 tokens."""
+    router bias): routing of every token, outputs on a tile-covering sample."""
     counts = _big_layer(ctx, pkg, torch, orc, 16384, 2048, 64, 8, 1408, mode=1,
-                        bias=zipf_bias(64), sample=48, seed=4)
+                        bias=zipf_bias(64), seed=4)
     assert counts.max() > 4 * counts.mean()  # heavily imbalanced loads
+
+
+def test_layer_reference_shape_full_size(ctx, pkg, torch, orc):
+    """The reference's own layer shape (Phi-tiny-MoE: d 4096, 16 experts of
+    d_ff 448, its quantised top-2 router) at its contest input's 15,583 rows:
+    routing of every token, outputs on a tile-covering sample."""
+    counts = _big_layer(ctx, pkg, torch, orc, 15583, 4096, 16, 2, 448, mode=0, bias=None,
+                        seed=6)
+    assert counts.min() > 0
 
 
 # ------------------------------------------------------------- layer norm
@@ -605,8 +658,9 @@ def test_layer_norm_block_without_residual(ctx, pkg, torch, orc):
 def test_layer_norm_block_config5_moe_ffn(ctx, pkg, torch, orc, norm):
     """Config 5's MoE block at full size (8 x 512 tokens, d 1024, E=8, top-2,
     SwiGLU 2816) behind its norm (the RMSNorm config 5 names, and the
-    reference's layer norm), with the residual; the oracle recomputes 32
-    tokens (every step is per token)."""
+    reference's layer norm), with the residual: routing of every token against
+    the oracle's norm, gate and router, and the block's output on a token
+    sample covering every m-tile of every expert (every step is per token)."""
     print(f"config5 block norm={norm}", flush=True)
     rms = norm == "rms"
     T, d, E, k, d_ff = 4096, 1024, 8, 2, 2816
@@ -620,11 +674,17 @@ def test_layer_norm_block_config5_moe_ffn(ctx, pkg, torch, orc, norm):
     nb = 0.1 * torch.randn(d, device="cuda", generator=g)
     y, idx, w = _norm_block(ctx, pkg, torch, x, gw, w1, w3, w2, nw, None if rms else nb, k, 0,
                             1, 1, norm=pkg.NORM_RMS if rms else pkg.NORM_LAYER)
-    s = 32
-    ry, ridx, rw = _norm_block_oracle(orc, host(x)[:s], host(gw), host(w1), host(w3), host(w2),
-                                      host(nw), host(nb), k, 0, 1, 1, residual=True, rms=rms)
-    assert np.array_equal(host(idx)[:s], ridx)
-    assert_close(host(y)[:s], ry, what="config5 block sample")
+    xh, gwh, nwh, nbh = host(x), host(gw), host(nw), host(nb)
+    xn = orc.rms_norm(xh, nwh, 1e-5, 1)[0] if rms else orc.layer_norm(xh, nwh, nbh, 1e-5, 1)[0]
+    gidx = host(idx)
+    _check_all_routing(orc, xn, gwh, k, 1, None, gidx, host(w))
+    toks = tile_cover_tokens(gidx, E)
+    print(f"config5 block: routing of all {T} tokens bit-exact; oracle on {len(toks)} "
+          f"tile-covering tokens", flush=True)
+    ry, ridx, rw = _norm_block_oracle(orc, xh[toks], gwh, host(w1), host(w3), host(w2),
+                                      nwh, nbh, k, 0, 1, 1, residual=True, rms=rms)
+    assert np.array_equal(gidx[toks], ridx)
+    assert_close(host(y)[toks], ry, what="config5 block, tile-covering tokens")
 
 
 # ------------------------------------------------------------------ errors
