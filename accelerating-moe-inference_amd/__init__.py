@@ -38,7 +38,7 @@ EXPORTS = (
     "moe_attention_last", "moe_rope_rows", "moe_attention_paths", "moe_add",
     "moe_add_bias", "moe_embed", "moe_gate_logits",
     "moe_route", "moe_permute", "moe_expert_ffn_grouped", "moe_combine",
-    "moe_layer_forward", "moe_layer_w2_splits",
+    "moe_layer_forward", "moe_layer_forward_noalloc", "moe_layer_w2_splits",
 )
 
 
@@ -117,6 +117,8 @@ def load_library(path: str = LIB_PATH):
         "moe_combine": ([P, P, P, P, P, P, P, I64, I64, I64, I, P], I),
         "moe_layer_forward": ([P, ctypes.POINTER(LayerDesc),
                                ctypes.POINTER(LayerWeights), P, P, P, P, P], I),
+        "moe_layer_forward_noalloc": ([P, ctypes.POINTER(LayerDesc),
+                                       ctypes.POINTER(LayerWeights), P, P, P, P, P], I),
         "moe_layer_w2_splits": ([P, ctypes.POINTER(LayerDesc), ctypes.POINTER(ctypes.c_int32)],
                                 I),
     }
@@ -381,7 +383,9 @@ class Context:
         return y
 
     def layer_forward(self, desc: LayerDesc, weights: dict, x, y,
-                      topk_idx=None, topk_w=None):
+                      topk_idx=None, topk_w=None, noalloc=False):
+        """moe_layer_forward, or (noalloc) moe_layer_forward_noalloc: the same
+        layer on the library's fixed per-GPU scratch, allocating nothing."""
         W = LayerWeights(
             gate_w=_f32(weights["gate_w"], "gate_w"),
             expert_bias=_f32(weights.get("expert_bias"), "expert_bias"),
@@ -389,10 +393,10 @@ class Context:
             w2=_f32(weights["w2"], "w2"),
             norm_w=_f32(weights.get("norm_w"), "norm_w"),
             norm_b=_f32(weights.get("norm_b"), "norm_b"))
-        _check(_lib.moe_layer_forward(self.handle, ctypes.byref(desc),
-                                      ctypes.byref(W), _f32(x, "x"),
-                                      _f32(y, "y"), _i32(topk_idx, "topk_idx"),
-                                      _f32(topk_w, "topk_w"), _stream()))
+        fn = _lib.moe_layer_forward_noalloc if noalloc else _lib.moe_layer_forward
+        _check(fn(self.handle, ctypes.byref(desc), ctypes.byref(W), _f32(x, "x"),
+                  _f32(y, "y"), _i32(topk_idx, "topk_idx"), _f32(topk_w, "topk_w"),
+                  _stream()))
         return y
 
     def w2_splits(self, desc: LayerDesc) -> int:

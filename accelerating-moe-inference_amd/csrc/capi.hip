@@ -7,10 +7,36 @@
 #include <climits>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 
 namespace {
 
 thread_local std::string g_last_error;
+
+// Scratch of moe_layer_forward_noalloc: one array per GPU the library runs
+// on, held until the process ends.  Host code never uses the array's name
+// as an address (on the host it names a stand-in, not device memory): each
+// device's address comes from hipGetSymbolAddress, taken once per device
+// when the first context on it is created, and is what every kernel gets.
+constexpr size_t kNoAllocScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of this device's scratch (the device must be current).
+void* bind_scratch(int device) {
+    moe::require(device < kMaxDevices, "device ordinal beyond the library's device table");
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[device] == nullptr) {
+        void* p = nullptr;
+        moe::hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)),
+                       "hipGetSymbolAddress(scratch)");
+        moe::require(p != nullptr, "hipGetSymbolAddress(scratch) returned null");
+        g_scratch_ptr[device] = p;
+    }
+    return g_scratch_ptr[device];
+}
 
 template <class F>
 int guarded(F&& f) {
@@ -420,7 +446,7 @@ LayerWs carve_layer(void* base, const moe_layer_desc& d, int w2_splits) {
 }
 
 // The MoE layer forward on a workspace at `base` carved by carve_layer
-// (the context's grow-only workspace).
+// (the context's grow-only workspace, or the no-alloc scratch).
 void layer_forward(moe_ctx* ctx, const moe_layer_desc& D, const moe_layer_weights& weights,
                    const float* x, float* y, int32_t* topk_idx_out, float* topk_w_out,
                    hipStream_t s, void* base, const W2Plan& plan) {
@@ -478,6 +504,14 @@ void layer_forward(moe_ctx* ctx, const moe_layer_desc& D, const moe_layer_weight
     });
 }
 
+// Suspends a context's kernel timing for the duration of a call.
+struct TimingPause {
+    moe_ctx* ctx;
+    bool was;
+    explicit TimingPause(moe_ctx* c) : ctx(c), was(c->timing) { c->timing = false; }
+    ~TimingPause() { ctx->timing = was; }
+};
+
 }  // namespace
 
 void* moe_ctx::workspace(size_t bytes) {
@@ -527,9 +561,15 @@ int moe_ctx_create(int device, moe_ctx** out) {
         if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
             throw moe::Unsupported(std::string("kernels are built for gfx950, device is ") +
                                    prop.gcnArchName);
+        void* scr = nullptr;
+        {
+            DeviceScope dev(device);
+            scr = bind_scratch(device);
+        }
         auto* c = new moe_ctx();
         c->device = device;
         c->cus = prop.multiProcessorCount;
+        c->scratch = scr;
         *out = c;
     });
 }
@@ -1095,6 +1135,31 @@ int moe_layer_forward(moe_ctx* ctx, const moe_layer_desc* desc,
         void* base = ctx->workspace(carve_layer(nullptr, *desc, plan.splits).bytes);
         layer_forward(ctx, *desc, *weights, x, y, topk_idx_out, topk_w_out, as_stream(stream),
                       base, plan);
+    });
+}
+
+int moe_layer_forward_noalloc(moe_ctx* ctx, const moe_layer_desc* desc,
+                              const moe_layer_weights* weights, const float* x, float* y,
+                              int32_t* topk_idx_out, float* topk_w_out, void* stream) {
+    return guarded([&] {
+        check_ctx(ctx);
+        check_desc(desc);
+        check_ptr(weights, "weights");
+        if (desc->T == 0) return;
+        moe::require(ctx->scratch != nullptr, "no-alloc scratch not bound to this context");
+        DeviceScope dev(ctx->device);
+        const W2Plan plan = choose_w2_plan(ctx, desc->T * desc->k, desc->d, desc->d_ff, desc->E);
+        const size_t need = carve_layer(nullptr, *desc, plan.splits).bytes;
+        if (need > kNoAllocScratchBytes)
+            throw moe::InvalidArg("moe_layer_forward_noalloc: this layer needs " +
+                                  std::to_string(need) + " bytes of scratch, more than the " +
+                                  std::to_string(kNoAllocScratchBytes) +
+                                  " the library holds per GPU; use moe_layer_forward");
+        // no events either: timing records them, and this entry point
+        // creates nothing
+        TimingPause pause(ctx);
+        layer_forward(ctx, *desc, *weights, x, y, topk_idx_out, topk_w_out, as_stream(stream),
+                      ctx->scratch, plan);
     });
 }
 

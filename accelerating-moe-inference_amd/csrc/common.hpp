@@ -201,6 +201,7 @@ struct moe_ctx {
     int dense_blocks_per_cu[2][moe::kDenseTiles] = {};  // [nn][tile], lazily queried
     void* ws = nullptr;
     size_t ws_bytes = 0;
+    void* scratch = nullptr;   // this device's no-alloc scratch (moe_layer_forward_noalloc)
     bool timing = false;
     struct Pending {
         const char* name;

@@ -297,6 +297,23 @@ int moe_layer_forward(moe_ctx* ctx, const moe_layer_desc* desc,
                       float* y, int32_t* topk_idx_out, float* topk_w_out,
                       void* stream);
 
+/* ---- moe_layer_forward without any allocation.  No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * layer's workspace (logits, routing, permutation, hidden rows, w2 partials,
+ * norm statistics) lives in a fixed 64 MiB array the library holds on every
+ * GPU it runs on, until the process ends; a layer needing more (about 1,200
+ * tokens at config 5's shape, 1,800 at the reference's) is rejected with
+ * MOE_ERR_INVALID.  The call allocates nothing and records no timing events.
+ * Every call on one GPU shares that GPU's array, which keeps the last call's
+ * contents: calls that overlap on one GPU (two streams, two threads, two
+ * contexts) race and must be serialised by the caller.  Same arguments,
+ * results and errors as moe_layer_forward otherwise. */
+int moe_layer_forward_noalloc(moe_ctx* ctx, const moe_layer_desc* desc,
+                              const moe_layer_weights* weights, const float* x,
+                              float* y, int32_t* topk_idx_out, float* topk_w_out,
+                              void* stream);
+
 /* ---- the number of K splits moe_layer_forward(desc) runs its w2 GEMM with
  * on this context's device (its combine then reads that many partial row
  * buffers).  No reference counterpart: an introspection query for
