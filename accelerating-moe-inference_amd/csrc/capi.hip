@@ -321,6 +321,16 @@ int choose_w2_splits(moe_ctx* ctx, int64_t pairs, int64_t d, int64_t d_ff, int64
     return best;
 }
 
+// The w1/w3 tile: 128 rows x 128 columns of each operand, or, when d_ff is
+// a multiple of 64 but not of 128 (the reference's 448), 256 rows x 64
+// columns, so the n-tiles cover d_ff exactly instead of leaving the last one
+// half empty.  MOE_W13_TILE = 0 / 1 overrides.
+int choose_w13_tile(int64_t d_ff) {
+    static const int env_tile = env_int("MOE_W13_TILE", -1);
+    if (env_tile == 0 || env_tile == 1) return env_tile;
+    return (d_ff % 128 != 0 && d_ff % 64 == 0) ? 1 : 0;
+}
+
 // w2_splits > 1 (layer path only): out_rows holds w2_splits partial row
 // buffers of pairs x d, one per K range, that the combine adds up.
 void expert_ffn(moe_ctx* ctx, const float* x, const int32_t* perm,
@@ -332,8 +342,11 @@ void expert_ffn(moe_ctx* ctx, const float* x, const int32_t* perm,
     if (pairs == 0 || d == 0) return;
     const bool swiglu = act == MOE_ACT_SWIGLU;
     if (d_ff > 0) {
-        const moe::GemmTile tile = moe::gemm_tile(moe::GemmUse::W13);
+        const int w13_tile = choose_w13_tile(d_ff);
+        const moe::GemmTile tile =
+            moe::gemm_tile(w13_tile == 1 ? moe::GemmUse::W13Tall : moe::GemmUse::W13);
         moe::GemmArgs a{};
+        a.tile = w13_tile;
         a.A = x;
         a.lda = d;
         a.gather = perm;

@@ -46,7 +46,9 @@ constexpr int kGemmGroupM = 8;
 // The GEMM uses whose tile shape the host needs for grid sizing.
 // W2Narrow: the w2 GEMM on the 128x128 tile (GemmArgs::tile = 1 on the
 // grouped EPI_STORE path), for widths d whose wide tile leaves few n-tiles.
-enum class GemmUse { Dense, W13, W2, W2Narrow };
+// W13Tall: w1/w3 on the 256 x 64 tile (GemmArgs::tile = 1 on the grouped
+// SwiGLU / SiLU path), for d_ff % 128 == 64.
+enum class GemmUse { Dense, W13, W13Tall, W2, W2Narrow };
 struct GemmTile {
     int bm, bn;
 };
@@ -94,7 +96,8 @@ struct GemmArgs {
     int32_t k_splits;        // K ranges computed by separate tiles (>= 1)
     int64_t k_split_len;     // K per split (a multiple of 16)
     int64_t c_split_stride;  // elements between the outputs of consecutive splits
-    int32_t tile;            // dense: tile shape (kDenseTiles); grouped w2: 1 = 128x128
+    int32_t tile;            // dense: tile shape (kDenseTiles); grouped w2: 1 = 128x128;
+                             // grouped w1/w3: 1 = 256x64
     // Batched dense GEMMs (attention; grid.y = batches): batch z splits into
     // zo = z / batch_inner, zi = z % batch_inner, and the operands start at
     // A + zo*a_so + zi*a_si, B + zo*b_so + (zi / b_group)*b_si,

@@ -118,6 +118,11 @@ template <> struct CfgOf<6> { using T = Cfg<256, 256, 16, 4, 2>; };
 template <> struct CfgOf<7> { using T = Cfg<64, 128, 16, 1, 2>; };
 template <> struct CfgOf<8> { using T = Cfg<64, 128, 16, 2, 2>; };  // direct only
 template <> struct CfgOf<9> { using T = Cfg<32, 128, 16, 1, 4>; };  // direct only
+// w1/w3 on 256 rows x 64 columns per operand: the same per-wave work as the
+// 128 x 128 dual tile (64 rows x 64 columns of each operand), for d_ff that
+// is a multiple of 64 but not of 128 (448: exactly 7 n-tiles instead of 4,
+// the last of them half empty)
+template <> struct CfgOf<10> { using T = Cfg<256, 64, 16, 4, 1>; };
 
 // Workgroup ids are dealt round-robin over the XCDs.  Renumber them so each
 // XCD works through a contiguous run of logical tiles: tiles that share an
@@ -233,6 +238,23 @@ __device__ __forceinline__ float silu_ref(float g) {
     const float e = static_cast<float>(exp(-static_cast<double>(g)));
 #endif
     return g / (1.0f + e);
+}
+
+// The store of one output element (row `row` of the launch, column n) under
+// epilogue EPI; v0, v1: the accumulators of the first and the second B
+// operand.
+template <int EPI>
+__device__ __forceinline__ void epi_store(const GemmArgs& p, float* Cb, int split, int64_t row,
+                                          int64_t n, float v0, float v1) {
+    float v = v0;
+    if (EPI == EPI_BIAS) {
+        if (p.bias != nullptr) v = v + p.bias[n];
+    } else if (EPI == EPI_SILU) {
+        v = silu_ref(v);
+    } else if (EPI == EPI_SWIGLU) {
+        v = silu_ref(v) * v1;
+    }
+    Cb[split * p.c_split_stride + row * p.ldc + n] = v;
 }
 
 template <bool VEC>
@@ -440,17 +462,9 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_kernel(const GemmArgs p) {
             for (int r = 0; r < 16; ++r) {
                 const int i = arow0 + bi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
                 const int64_t n = n0 + bcol0 + bj * 32 + lr;
-                if (i < rows && n < N) {
-                    float v = acc[0][bi][bj][r];
-                    if (EPI == EPI_BIAS) {
-                        if (p.bias != nullptr) v = v + p.bias[n];
-                    } else if (EPI == EPI_SILU) {
-                        v = silu_ref(v);
-                    } else if (EPI == EPI_SWIGLU) {
-                        v = silu_ref(v) * acc[NB - 1][bi][bj][r];
-                    }
-                    p.C[split * p.c_split_stride + (row0 + i) * p.ldc + n] = v;
-                }
+                if (i < rows && n < N)
+                    epi_store<EPI>(p, p.C, split, row0 + i, n, acc[0][bi][bj][r],
+                                   acc[NB - 1][bi][bj][r]);
             }
 }
 
@@ -514,6 +528,23 @@ __device__ __forceinline__ void buffer_load_lds16(const float* base, lds_void* d
 }
 
 __device__ __forceinline__ int swz(int row) { return (row >> 2) & 3; }
+
+// The K-step barrier of the three-stage ring.  __syncthreads() carries a
+// workgroup fence, and a fence must wait for every load that writes LDS --
+// the stage two steps ahead included (the compiler emits vmcnt(0) before each
+// barrier), which leaves only one step for those loads to land.  The ring
+// orders its stages itself: before the barrier each wave has waited for its
+// loads of the next stage (vmcnt(loads per stage)) and for its own LDS reads
+// (lgkmcnt(0); the matrix cores have consumed them), so after it every wave's
+// next stage has landed and no wave still reads the stage the following step
+// overwrites.  The empty asm statements keep the compiler from moving memory
+// operations across the barrier.
+__device__ __forceinline__ void ring_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
 
 template <int BN>
 struct NnB {
@@ -714,7 +745,9 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
                 for (int r = 0; r < 16; ++r) acc[nb][bi][bj][r] = 0.0f;
 
     // 32-row blocks of this wave that hold at least one real row
-    const int live_rows = rows - arow0;
+    // A wave whose columns all lie past N (the last n-tile of an N that is
+    // not a multiple of BN) has no real output either: it skips its bursts.
+    const int live_rows = n0 + bcol0 < N ? rows - arow0 : 0;
     const int live = live_rows <= 0 ? 0 : (live_rows >= FM * 32 ? FM : (live_rows + 31) / 32);
 
     const int64_t nk = (K - kbeg) / BK;
@@ -849,7 +882,7 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
             } else {
                 __builtin_amdgcn_s_waitcnt(0x3f70);
             }
-            __syncthreads();
+            ring_barrier();
         }
         for (int64_t kt0 = 0; kt0 < nk; kt0 += 3) {
             auto one = [&](auto u) {
@@ -862,7 +895,7 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
                 mfma_step();
                 if (kt + 2 < nk) wait_lps();
                 else __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
-                __syncthreads();
+                ring_barrier();
             };
             one(S0{});
             one(S1{});
@@ -892,17 +925,9 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
             for (int r = 0; r < 16; ++r) {
                 const int i = arow0 + bi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
                 const int64_t n = n0 + bcol0 + bj * 32 + lr;
-                if (i < rows && n < N) {
-                    float v = acc[0][bi][bj][r];
-                    if (EPI == EPI_BIAS) {
-                        if (p.bias != nullptr) v = v + p.bias[n];
-                    } else if (EPI == EPI_SILU) {
-                        v = silu_ref(v);
-                    } else if (EPI == EPI_SWIGLU) {
-                        v = silu_ref(v) * acc[NB - 1][bi][bj][r];
-                    }
-                    Cb[split * p.c_split_stride + (row0 + i) * p.ldc + n] = v;
-                }
+                if (i < rows && n < N)
+                    epi_store<EPI>(p, Cb, split, row0 + i, n, acc[0][bi][bj][r],
+                                   acc[NB - 1][bi][bj][r]);
             }
 }
 
@@ -956,6 +981,7 @@ using DenseSmallCfg = CfgOf<9>::T;
 using W13Cfg = CfgOf<MOE_W13_CFG>::T;
 using W2Cfg = CfgOf<MOE_W2_CFG>::T;
 using W2NarrowCfg = CfgOf<0>::T;  // w2 with d too narrow for the wide tile's n-tiles
+using W13TallCfg = CfgOf<10>::T;  // w1/w3 with d_ff % 128 == 64
 
 template <class C, bool NN>
 void launch_dense(const GemmArgs& a, bool vec, hipStream_t s) {
@@ -1069,6 +1095,7 @@ GemmTile gemm_tile(GemmUse use) {
         case GemmUse::Dense: return {DenseCfg::BM, DenseCfg::BN};
         case GemmUse::W13: return {W13Cfg::BM, W13Cfg::BN};
         case GemmUse::W2Narrow: return {W2NarrowCfg::BM, W2NarrowCfg::BN};
+        case GemmUse::W13Tall: return {W13TallCfg::BM, W13TallCfg::BN};
         default: return {W2Cfg::BM, W2Cfg::BN};
     }
 }
@@ -1112,8 +1139,18 @@ void launch_gemm(const GemmArgs& args, bool nn, bool grouped, int epi, bool vec,
     }
     if (nn) throw Unsupported("grouped NN GEMM");
     switch (epi) {
-        case EPI_SWIGLU: launch_cfg<W13Cfg, MOE_W13_SCHED, false, true, 2, EPI_SWIGLU>(a, vec, s); break;
-        case EPI_SILU: launch_cfg<W13Cfg, MOE_W13_SCHED, false, true, 1, EPI_SILU>(a, vec, s); break;
+        case EPI_SWIGLU:
+            if (a.tile == 1)
+                launch_cfg<W13TallCfg, MOE_W13_SCHED, false, true, 2, EPI_SWIGLU>(a, vec, s);
+            else
+                launch_cfg<W13Cfg, MOE_W13_SCHED, false, true, 2, EPI_SWIGLU>(a, vec, s);
+            break;
+        case EPI_SILU:
+            if (a.tile == 1)
+                launch_cfg<W13TallCfg, MOE_W13_SCHED, false, true, 1, EPI_SILU>(a, vec, s);
+            else
+                launch_cfg<W13Cfg, MOE_W13_SCHED, false, true, 1, EPI_SILU>(a, vec, s);
+            break;
         case EPI_STORE:
             if (a.tile == 1)
                 launch_cfg<W2NarrowCfg, MOE_W2_SCHED | SCHED_DIRECT, false, true, 1, EPI_STORE>(

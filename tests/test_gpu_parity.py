@@ -348,6 +348,15 @@ def _ffn_case(rng, T, d, E, k, d_ff, act, skew=False):
     (300, 128, 64, 8, 96, 0, True),      # ragged, tiny experts
     (50, 132, 4, 2, 70, 0, False),       # d, d_ff not multiples of the tile
     (33, 36, 16, 3, 17, 1, True),
+    # d_ff % 128 == 64: w1/w3 on the 256 x 64 tile (dual SwiGLU, single SiLU,
+    # and the register-staged kernel for K % 16 != 0)
+    (700, 256, 8, 2, 448, 0, False),
+    (150, 128, 4, 2, 192, 1, True),
+    (90, 132, 4, 2, 320, 0, False),
+    # more than 64 experts (the grouped kernels' expert lookup reads the
+    # offsets instead of a register table); K = 32, two K steps per w1/w3 tile
+    (400, 64, 100, 4, 64, 0, True),
+    (100, 32, 8, 2, 64, 0, False),
 ])
 def test_expert_ffn_vs_oracle(ctx, torch, orc, T, d, E, k, d_ff, act, skew):
     print(f"ffn T={T} d={d} E={E} k={k} d_ff={d_ff} act={act}", flush=True)
