@@ -5,6 +5,7 @@
 #include <algorithm>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 #include <memory>
 #include <mutex>
 #include <stdexcept>
@@ -113,6 +114,99 @@ const int32_t* Scratch::upload(std::size_t slot, const int32_t* src, std::size_t
     int32_t* p = i32(slot, count);
     bufs_[slot].upload(src, count * sizeof(int32_t));
     return p;
+}
+
+namespace {
+
+struct Staging {
+    std::mutex mu;
+    char* host = nullptr;  // pinned, 2 * half bytes
+    std::size_t half = 0;
+    hipEvent_t done[2] = {nullptr, nullptr};  // the last DMA out of / into each half
+    bool pending[2] = {false, false};
+    Scratch io;
+    ~Staging() {
+        if (host != nullptr) (void)hipHostFree(host);
+        for (hipEvent_t e : done)
+            if (e != nullptr) (void)hipEventDestroy(e);
+    }
+    // Grow the pinned halves to min(bytes, 32 MiB) each.
+    void reserve(std::size_t bytes) {
+        constexpr std::size_t kMaxHalf = std::size_t(32) << 20;
+        const std::size_t want = std::min(std::max<std::size_t>(bytes, 1 << 16), kMaxHalf);
+        if (want <= half) return;
+        wait(0);
+        wait(1);
+        if (host != nullptr) hip(hipHostFree(host), "hipHostFree");
+        host = nullptr;
+        half = 0;
+        hip(hipHostMalloc(reinterpret_cast<void**>(&host), 2 * want, hipHostMallocDefault),
+            "hipHostMalloc staging");
+        half = want;
+        for (hipEvent_t& e : done)
+            if (e == nullptr) hip(hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreate");
+    }
+    void wait(int h) {
+        if (pending[h]) hip(hipEventSynchronize(done[h]), "hipEventSynchronize");
+        pending[h] = false;
+    }
+};
+
+Staging& staging() {
+    static Staging s;
+    return s;
+}
+
+}  // namespace
+
+std::unique_lock<std::mutex> io_lock() { return std::unique_lock<std::mutex>(staging().mu); }
+
+Scratch& io_scratch() { return staging().io; }
+
+void to_device(void* dst, const void* src, std::size_t bytes) {
+    if (bytes == 0) return;
+    Staging& st = staging();
+    st.reserve(bytes);
+    for (std::size_t off = 0, c = 0; off < bytes; off += st.half, ++c) {
+        const int h = static_cast<int>(c & 1);
+        const std::size_t n = std::min(st.half, bytes - off);
+        st.wait(h);  // the DMA that last read this half is done
+        char* stage = st.host + h * st.half;
+        std::memcpy(stage, static_cast<const char*>(src) + off, n);
+        hip(hipMemcpyAsync(static_cast<char*>(dst) + off, stage, n, hipMemcpyHostToDevice, nullptr),
+            "hipMemcpyAsync H2D");
+        hip(hipEventRecord(st.done[h], nullptr), "hipEventRecord");
+        st.pending[h] = true;
+    }
+}
+
+void zero_device(void* dst, std::size_t bytes) {
+    if (bytes != 0) hip(hipMemsetAsync(dst, 0, bytes, nullptr), "hipMemsetAsync");
+}
+
+void to_host(void* dst, const void* src, std::size_t bytes) {
+    if (bytes == 0) return;
+    Staging& st = staging();
+    st.reserve(bytes);
+    const std::size_t chunks = (bytes + st.half - 1) / st.half;
+    auto issue = [&](std::size_t c) {
+        const int h = static_cast<int>(c & 1);
+        const std::size_t off = c * st.half, n = std::min(st.half, bytes - off);
+        st.wait(h);
+        hip(hipMemcpyAsync(st.host + h * st.half, static_cast<const char*>(src) + off, n,
+                           hipMemcpyDeviceToHost, nullptr),
+            "hipMemcpyAsync D2H");
+        hip(hipEventRecord(st.done[h], nullptr), "hipEventRecord");
+        st.pending[h] = true;
+    };
+    issue(0);
+    for (std::size_t c = 0; c < chunks; ++c) {
+        if (c + 1 < chunks) issue(c + 1);  // the next chunk moves while this one is copied out
+        const int h = static_cast<int>(c & 1);
+        st.wait(h);
+        const std::size_t off = c * st.half, n = std::min(st.half, bytes - off);
+        std::memcpy(static_cast<char*>(dst) + off, st.host + h * st.half, n);
+    }
 }
 
 }  // namespace moe_dropin

@@ -4,6 +4,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <mutex>
 #include <vector>
 
 #include "../../include/moe_amd.h"
@@ -65,5 +66,22 @@ private:
     std::vector<DeviceBuffer> bufs_;
     void* get(std::size_t slot, std::size_t bytes);
 };
+
+// The drop-in's copies of pageable host tensors.  They go through a
+// grow-only pinned staging buffer (at most 64 MiB, two halves): the CPU
+// copies one chunk into a half while the DMA engine moves the other, on the
+// stream the drop-in's kernels use.  to_device returns once every chunk is
+// staged (src may be reused; the transfer may still be in flight);
+// to_host returns with dst filled.  Callers hold io_lock().
+void to_device(void* dst, const void* src, std::size_t bytes);
+void to_host(void* dst, const void* src, std::size_t bytes);
+// Sets bytes of device memory at dst to 0, on the drop-in's stream.
+void zero_device(void* dst, std::size_t bytes);
+
+// The per-call device buffers of the drop-in's inputs and outputs: grow-only
+// slots, so repeated calls of one shape allocate nothing.  Callers hold
+// io_lock() while they use them.
+Scratch& io_scratch();
+std::unique_lock<std::mutex> io_lock();
 
 }  // namespace moe_dropin

@@ -50,6 +50,18 @@ std::shared_ptr<const DeviceBuffer> shared_rope_table() {
     return table;
 }
 
+// y takes `shape`, reusing its buffer when it holds enough elements (every
+// element is overwritten by the caller's copy-out).
+void shape_output(Tensor& y, std::vector<std::size_t> shape) {
+    std::size_t n = 1;
+    for (std::size_t d : shape) n *= d;
+    if (y.capacity() >= n && y.data() != nullptr) y.reshape_within_capacity(std::move(shape));
+    else y = Tensor(std::move(shape));
+}
+
+// Slots of the drop-in's per-call device buffers (moe_dropin::io_scratch).
+enum IoSlot : std::size_t { kIoX, kIoY, kIoH, kIoIdx, kIoPerm, kIoOff, kIoQ, kIoK, kIoV, kIoA, kIoN };
+
 void sgemm_nt(const float* a, const DeviceBuffer& w, const std::shared_ptr<const DeviceBuffer>& b,
               float* c, std::size_t m, std::size_t n, std::size_t k) {
     check(moe_sgemm_nt(moe_dropin::context(), a, w.as<float>(), b ? b->as<float>() : nullptr, c,
@@ -78,14 +90,16 @@ void Linear::forward(const Tensor& x, Tensor& y) const {
     const std::size_t in = x.size(x.ndim() - 1);
     const std::size_t rows = x.size() / in;
     if (in != in_) throw std::invalid_argument("matmul_transposed shape");
-    y = Tensor({rows, out_});
-    DeviceBuffer dx(x.size() * sizeof(float)), dy(rows * out_ * sizeof(float));
-    dx.upload(x.data(), x.size() * sizeof(float));
-    check(moe_sgemm_nt(moe_dropin::context(), dx.as<float>(), weight_->as<float>(),
-                       bias_ ? bias_->as<float>() : nullptr, dy.as<float>(),
-                       static_cast<int64_t>(rows), static_cast<int64_t>(out_),
-                       static_cast<int64_t>(in_), nullptr));
-    dy.download(y.data(), rows * out_ * sizeof(float));
+    auto lock = moe_dropin::io_lock();
+    moe_dropin::Scratch& io = moe_dropin::io_scratch();
+    float* dx = io.f32(kIoX, x.size());
+    float* dy = io.f32(kIoY, rows * out_);
+    moe_dropin::to_device(dx, x.data(), x.size() * sizeof(float));
+    check(moe_sgemm_nt(moe_dropin::context(), dx, weight_->as<float>(),
+                       bias_ ? bias_->as<float>() : nullptr, dy, static_cast<int64_t>(rows),
+                       static_cast<int64_t>(out_), static_cast<int64_t>(in_), nullptr));
+    shape_output(y, {rows, out_});
+    moe_dropin::to_host(y.data(), dy, rows * out_ * sizeof(float));
 }
 
 // ------------------------------------------------------------------ PhiMLP
@@ -111,20 +125,20 @@ void PhiMLP::forward(const Tensor& x, Tensor& y) const {
     std::vector<int32_t> perm(rows);
     std::iota(perm.begin(), perm.end(), 0);
     const int32_t offsets[2] = {0, static_cast<int32_t>(rows)};
-    DeviceBuffer dx(x.size() * sizeof(float)), dperm(rows * sizeof(int32_t)),
-        doff(sizeof(offsets)), dh(rows * ff_ * sizeof(float)), dout(rows * hidden_ * sizeof(float));
-    dx.upload(x.data(), x.size() * sizeof(float));
-    dperm.upload(perm.data(), rows * sizeof(int32_t));
-    doff.upload(offsets, sizeof(offsets));
-    check(moe_expert_ffn_grouped(moe_dropin::context(), dx.as<float>(), dperm.as<int32_t>(),
-                                 doff.as<int32_t>(), w1_->as<float>(), w3_->as<float>(),
-                                 w2_->as<float>(), MOE_ACT_SWIGLU, static_cast<int64_t>(rows), 1,
-                                 static_cast<int64_t>(hidden_), static_cast<int64_t>(ff_), 1,
-                                 dh.as<float>(), dout.as<float>(), nullptr));
-    Tensor out({rows, hidden_});
-    dout.download(out.data(), rows * hidden_ * sizeof(float));
-    out.reshape(x.shape());
-    y = std::move(out);
+    auto lock = moe_dropin::io_lock();
+    moe_dropin::Scratch& io = moe_dropin::io_scratch();
+    float* dx = io.f32(kIoX, x.size());
+    float* dh = io.f32(kIoH, rows * ff_);
+    float* dout = io.f32(kIoY, rows * hidden_);
+    moe_dropin::to_device(dx, x.data(), x.size() * sizeof(float));
+    const int32_t* dperm = io.upload(kIoPerm, perm.data(), rows);
+    const int32_t* doff = io.upload(kIoOff, offsets, 2);
+    check(moe_expert_ffn_grouped(moe_dropin::context(), dx, dperm, doff, w1_->as<float>(),
+                                 w3_->as<float>(), w2_->as<float>(), MOE_ACT_SWIGLU,
+                                 static_cast<int64_t>(rows), 1, static_cast<int64_t>(hidden_),
+                                 static_cast<int64_t>(ff_), 1, dh, dout, nullptr));
+    shape_output(y, x.shape());
+    moe_dropin::to_host(y.data(), dout, rows * hidden_ * sizeof(float));
 }
 
 // ------------------------------------------------------------------ PhiMoE
@@ -161,16 +175,18 @@ void PhiMoE::forward(const Tensor& x, Tensor& y, std::vector<int32_t>* topk_idx)
     const std::size_t rows = x.size(0), h = x.size(1);
     if (h != hidden_) throw std::invalid_argument("matmul_transposed shape");
     const std::size_t k = apss26::TOP_K < experts_ ? apss26::TOP_K : experts_;
-    DeviceBuffer dx(x.size() * sizeof(float)), dy(rows * hidden_ * sizeof(float)),
-        didx(rows * k * sizeof(int32_t));
-    dx.upload(x.data(), x.size() * sizeof(float));
-    forward_device(dx.as<float>(), dy.as<float>(), rows, MOE_NORM_NONE, nullptr, nullptr, 0,
-                   didx.as<int32_t>());
-    y = Tensor({rows, h});
-    dy.download(y.data(), rows * h * sizeof(float));
+    auto lock = moe_dropin::io_lock();
+    moe_dropin::Scratch& io = moe_dropin::io_scratch();
+    float* dx = io.f32(kIoX, x.size());
+    float* dy = io.f32(kIoY, rows * hidden_);
+    int32_t* didx = io.i32(kIoIdx, rows * k);
+    moe_dropin::to_device(dx, x.data(), x.size() * sizeof(float));
+    forward_device(dx, dy, rows, MOE_NORM_NONE, nullptr, nullptr, 0, didx);
+    shape_output(y, {rows, h});
+    moe_dropin::to_host(y.data(), dy, rows * h * sizeof(float));
     if (topk_idx != nullptr) {
         topk_idx->resize(rows * k);
-        didx.download(topk_idx->data(), rows * k * sizeof(int32_t));
+        moe_dropin::to_host(topk_idx->data(), didx, rows * k * sizeof(int32_t));
     }
 }
 
@@ -235,11 +251,15 @@ void PhiAttention::forward_device(const float* dx, float* dy, std::size_t s) con
     const std::size_t sp = padded_rows(s);
     const std::size_t H = apss26::NUM_ATTENTION_HEADS, KVH = apss26::NUM_KV_HEADS,
                       hd = apss26::HEAD_DIM;
-    DeviceBuffer q(sp * H * hd * sizeof(float)), k(sp * KVH * hd * sizeof(float)),
-        v(sp * KVH * hd * sizeof(float)), a(sp * H * hd * sizeof(float));
-    sgemm_nt(dx, *wq_, bq_, q.as<float>(), sp, H * hd, hidden_);
-    sgemm_nt(dx, *wk_, bk_, k.as<float>(), sp, KVH * hd, hidden_);
-    sgemm_nt(dx, *wv_, bv_, v.as<float>(), sp, KVH * hd, hidden_);
+    // the caller holds io_lock()
+    moe_dropin::Scratch& io = moe_dropin::io_scratch();
+    float* q = io.f32(kIoQ, sp * H * hd);
+    float* k = io.f32(kIoK, sp * KVH * hd);
+    float* v = io.f32(kIoV, sp * KVH * hd);
+    float* a = io.f32(kIoA, sp * H * hd);
+    sgemm_nt(dx, *wq_, bq_, q, sp, H * hd, hidden_);
+    sgemm_nt(dx, *wk_, bk_, k, sp, KVH * hd, hidden_);
+    sgemm_nt(dx, *wv_, bv_, v, sp, KVH * hd, hidden_);
     std::shared_ptr<const DeviceBuffer> table = rope_;
     std::size_t positions = rope_positions_;
     if (s > positions) {
@@ -250,27 +270,34 @@ void PhiAttention::forward_device(const float* dx, float* dy, std::size_t s) con
     // Rows past s come from finite padding rows and sit after every real
     // query, so the causal mask hides them: the padded attention is exact
     // for the rows < s.
-    check(moe_rope(ctx, q.as<float>(), k.as<float>(), table->as<float>(),
+    check(moe_rope(ctx, q, k, table->as<float>(),
                    static_cast<int64_t>(positions), 1, static_cast<int64_t>(s), 0,
                    static_cast<int64_t>(H), static_cast<int64_t>(KVH), static_cast<int64_t>(hd),
                    nullptr));
-    check(moe_attention(ctx, q.as<float>(), k.as<float>(), v.as<float>(), a.as<float>(), 1,
+    check(moe_attention(ctx, q, k, v, a, 1,
                         static_cast<int64_t>(sp), static_cast<int64_t>(H),
                         static_cast<int64_t>(KVH), static_cast<int64_t>(hd),
                         static_cast<int64_t>(apss26::SLIDING_WINDOW), nullptr));
-    sgemm_nt(a.as<float>(), *wo_, bo_, dy, sp, hidden_, H * hd);
+    sgemm_nt(a, *wo_, bo_, dy, sp, hidden_, H * hd);
 }
 
 void PhiAttention::forward(const Tensor& x, Tensor& y) const {
     if (x.ndim() != 2 || x.size(1) != hidden_) throw std::invalid_argument("matmul_transposed shape");
     const std::size_t s = x.size(0), sp = padded_rows(s);
-    y = Tensor({s, hidden_});
-    if (s == 0) return;
-    DeviceBuffer dx(sp * hidden_ * sizeof(float)), dy(sp * hidden_ * sizeof(float));
-    dx.zero();
-    dx.upload(x.data(), x.size() * sizeof(float));
-    forward_device(dx.as<float>(), dy.as<float>(), s);
-    dy.download(y.data(), s * hidden_ * sizeof(float));
+    if (s == 0) {
+        y = Tensor({s, hidden_});
+        return;
+    }
+    auto lock = moe_dropin::io_lock();
+    moe_dropin::Scratch& io = moe_dropin::io_scratch();
+    float* dx = io.f32(kIoX, sp * hidden_);
+    float* dy = io.f32(kIoY, sp * hidden_);
+    // the padding rows are zero: finite inputs the causal mask hides
+    moe_dropin::zero_device(dx + s * hidden_, (sp - s) * hidden_ * sizeof(float));
+    moe_dropin::to_device(dx, x.data(), x.size() * sizeof(float));
+    forward_device(dx, dy, s);
+    shape_output(y, {s, hidden_});
+    moe_dropin::to_host(y.data(), dy, s * hidden_ * sizeof(float));
 }
 
 void PhiAttention::forward_nodes(const float* dn, float* dy, const NodeRows& nb, bool tail,
@@ -335,21 +362,28 @@ void PhiDecoderLayer::forward(const Tensor& x, Tensor& y) const {
     const std::size_t h = attention_.hidden();
     if (x.ndim() != 2 || x.size(1) != h) throw std::invalid_argument("layer norm shape");
     const std::size_t s = x.size(0), sp = PhiAttention::padded_rows(s);
-    y = Tensor({s, h});
-    if (s == 0) return;
-    DeviceBuffer dx(sp * h * sizeof(float)), dn(sp * h * sizeof(float)),
-        da(sp * h * sizeof(float)), dy(s * h * sizeof(float));
-    dx.zero();
-    dx.upload(x.data(), x.size() * sizeof(float));
+    if (s == 0) {
+        y = Tensor({s, h});
+        return;
+    }
+    auto lock = moe_dropin::io_lock();
+    moe_dropin::Scratch& io = moe_dropin::io_scratch();
+    float* dx = io.f32(kIoX, sp * h);
+    float* dn = io.f32(kIoN, sp * h);
+    float* da = io.f32(kIoH, sp * h);
+    float* dy = io.f32(kIoY, s * h);
+    moe_dropin::zero_device(dx + s * h, (sp - s) * h * sizeof(float));
+    moe_dropin::to_device(dx, x.data(), x.size() * sizeof(float));
     moe_ctx* ctx = moe_dropin::context();
-    check(moe_layer_norm(ctx, dx.as<float>(), in_w_->as<float>(), in_b_->as<float>(),
-                         apss26::NORM_EPS, static_cast<int64_t>(sp), static_cast<int64_t>(h),
-                         MOE_CONTRACT_FMA, dn.as<float>(), nullptr, nullptr, nullptr));
-    attention_.forward_device(dn.as<float>(), da.as<float>(), s);
-    check(moe_add(ctx, da.as<float>(), dx.as<float>(), static_cast<int64_t>(s * h), nullptr));
-    moe_.forward_device(da.as<float>(), dy.as<float>(), s, MOE_NORM_LAYER, post_w_->as<float>(),
-                        post_b_->as<float>(), 1, nullptr);
-    dy.download(y.data(), s * h * sizeof(float));
+    check(moe_layer_norm(ctx, dx, in_w_->as<float>(), in_b_->as<float>(), apss26::NORM_EPS,
+                         static_cast<int64_t>(sp), static_cast<int64_t>(h), MOE_CONTRACT_FMA, dn,
+                         nullptr, nullptr, nullptr));
+    attention_.forward_device(dn, da, s);
+    check(moe_add(ctx, da, dx, static_cast<int64_t>(s * h), nullptr));
+    moe_.forward_device(da, dy, s, MOE_NORM_LAYER, post_w_->as<float>(), post_b_->as<float>(), 1,
+                        nullptr);
+    shape_output(y, {s, h});
+    moe_dropin::to_host(y.data(), dy, s * h * sizeof(float));
 }
 
 // The layer over trie rows; with `tail` (the reference's pruned last layer,

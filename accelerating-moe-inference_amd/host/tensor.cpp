@@ -140,12 +140,20 @@ namespace tensor_ops {
 namespace {
 
 using moe_dropin::check;
-using moe_dropin::DeviceBuffer;
 
-DeviceBuffer to_device(const Tensor& t) {
-    DeviceBuffer b(t.size() * sizeof(float));
-    b.upload(t.data(), t.size() * sizeof(float));
-    return b;
+// Per-call device copies live in the drop-in's grow-only io slots (no
+// allocation once a shape has been seen); the copies go through its pinned
+// staging.  Every op holds io_lock() while it uses them.
+enum Slot : std::size_t { kA, kB, kC, kD };
+
+float* stage_in(std::size_t slot, const Tensor& t) {
+    float* d = moe_dropin::io_scratch().f32(slot, t.size());
+    moe_dropin::to_device(d, t.data(), t.size() * sizeof(float));
+    return d;
+}
+
+void stage_out(Tensor& t, const float* d) {
+    moe_dropin::to_host(t.data(), d, t.size() * sizeof(float));
 }
 
 void gemm(bool nn, const Tensor& a, const Tensor& b, Tensor& c, const char* what) {
@@ -155,14 +163,15 @@ void gemm(bool nn, const Tensor& a, const Tensor& b, Tensor& c, const char* what
     if (a.ndim() != 2 || b.ndim() != 2 || c.ndim() != 2 || bk != k || c.size(0) != m ||
         c.size(1) != n)
         throw std::invalid_argument(what);
-    DeviceBuffer da = to_device(a), db = to_device(b), dc(m * n * sizeof(float));
+    auto lock = moe_dropin::io_lock();
+    const float* da = stage_in(kA, a);
+    const float* db = stage_in(kB, b);
+    float* dc = moe_dropin::io_scratch().f32(kC, m * n);
     moe_ctx* ctx = moe_dropin::context();
     const auto M = static_cast<int64_t>(m), N = static_cast<int64_t>(n), K = static_cast<int64_t>(k);
-    check(nn ? moe_sgemm_nn(ctx, da.as<float>(), db.as<float>(), nullptr, dc.as<float>(), M, N, K,
-                            nullptr)
-             : moe_sgemm_nt(ctx, da.as<float>(), db.as<float>(), nullptr, dc.as<float>(), M, N, K,
-                            nullptr));
-    dc.download(c.data(), m * n * sizeof(float));
+    check(nn ? moe_sgemm_nn(ctx, da, db, nullptr, dc, M, N, K, nullptr)
+             : moe_sgemm_nt(ctx, da, db, nullptr, dc, M, N, K, nullptr));
+    stage_out(c, dc);
 }
 
 }  // namespace
@@ -175,28 +184,31 @@ void matmul_transposed(const Tensor& a, const Tensor& b, Tensor& c) {
 
 void mul(const Tensor& a, const Tensor& b, Tensor& c) {
     if (a.size() != b.size() || c.size() != a.size()) throw std::invalid_argument("mul shape");
-    DeviceBuffer da = to_device(a), db = to_device(b), dc(c.size() * sizeof(float));
-    check(moe_mul(moe_dropin::context(), da.as<float>(), db.as<float>(), dc.as<float>(),
-                  static_cast<int64_t>(a.size()), nullptr));
-    dc.download(c.data(), c.size() * sizeof(float));
+    auto lock = moe_dropin::io_lock();
+    const float* da = stage_in(kA, a);
+    const float* db = stage_in(kB, b);
+    float* dc = moe_dropin::io_scratch().f32(kC, c.size());
+    check(moe_mul(moe_dropin::context(), da, db, dc, static_cast<int64_t>(a.size()), nullptr));
+    stage_out(c, dc);
 }
 
 void silu(const Tensor& x, Tensor& y) {
     if (x.size() != y.size()) throw std::invalid_argument("silu shape");
-    DeviceBuffer dx = to_device(x);
-    check(moe_silu(moe_dropin::context(), dx.as<float>(), dx.as<float>(),
-                   static_cast<int64_t>(x.size()), nullptr));
-    dx.download(y.data(), y.size() * sizeof(float));
+    auto lock = moe_dropin::io_lock();
+    float* dx = stage_in(kA, x);
+    check(moe_silu(moe_dropin::context(), dx, dx, static_cast<int64_t>(x.size()), nullptr));
+    stage_out(y, dx);
 }
 
 // a[i] += b[i] (src/tensor.cu:150-154).
 void add_inplace(Tensor& a, const Tensor& b) {
     if (a.size() != b.size()) throw std::invalid_argument("add shape");
     if (a.size() == 0) return;
-    DeviceBuffer da = to_device(a), db = to_device(b);
-    check(moe_add(moe_dropin::context(), da.as<float>(), db.as<float>(),
-                  static_cast<int64_t>(a.size()), nullptr));
-    da.download(a.data(), a.size() * sizeof(float));
+    auto lock = moe_dropin::io_lock();
+    float* da = stage_in(kA, a);
+    const float* db = stage_in(kB, b);
+    check(moe_add(moe_dropin::context(), da, db, static_cast<int64_t>(a.size()), nullptr));
+    stage_out(a, da);
 }
 
 // a[i] += bias[i % h] with h = the last dimension (src/tensor.cu:156-161).
@@ -205,10 +217,12 @@ void add_bias_inplace(Tensor& a, const Tensor& bias) {
         throw std::invalid_argument("bias shape");
     const std::size_t h = bias.size(0);
     if (a.size() == 0) return;
-    DeviceBuffer da = to_device(a), db = to_device(bias);
-    check(moe_add_bias(moe_dropin::context(), da.as<float>(), db.as<float>(),
-                       static_cast<int64_t>(a.size() / h), static_cast<int64_t>(h), nullptr));
-    da.download(a.data(), a.size() * sizeof(float));
+    auto lock = moe_dropin::io_lock();
+    float* da = stage_in(kA, a);
+    const float* db = stage_in(kB, bias);
+    check(moe_add_bias(moe_dropin::context(), da, db, static_cast<int64_t>(a.size() / h),
+                       static_cast<int64_t>(h), nullptr));
+    stage_out(a, da);
 }
 
 // include/tensor.h:67 of the reference declares it; no source defines it.
@@ -224,11 +238,14 @@ void layer_norm(const Tensor& x, const Tensor& weight, const Tensor& bias, float
     if (h == 0 || weight.size() != h || bias.size() != h || y.size() != x.size())
         throw std::invalid_argument("layer norm shape");
     const std::size_t rows = x.size() / h;
-    DeviceBuffer dx = to_device(x), dw = to_device(weight), db = to_device(bias);
-    check(moe_layer_norm(moe_dropin::context(), dx.as<float>(), dw.as<float>(), db.as<float>(),
-                         eps, static_cast<int64_t>(rows), static_cast<int64_t>(h),
-                         MOE_CONTRACT_FMA, dx.as<float>(), nullptr, nullptr, nullptr));
-    dx.download(y.data(), y.size() * sizeof(float));
+    auto lock = moe_dropin::io_lock();
+    float* dx = stage_in(kA, x);
+    const float* dw = stage_in(kB, weight);
+    const float* db = stage_in(kC, bias);
+    check(moe_layer_norm(moe_dropin::context(), dx, dw, db, eps, static_cast<int64_t>(rows),
+                         static_cast<int64_t>(h), MOE_CONTRACT_FMA, dx, nullptr, nullptr,
+                         nullptr));
+    stage_out(y, dx);
 }
 // src/tensor.cu:191-210 on the GPU: the cos/sin table comes from the same
 // float libm calls (moe_rope_table, on the host), the rotation rounds each
@@ -245,15 +262,16 @@ void apply_rope(Tensor& q, Tensor& k, std::size_t seq_len, std::size_t q_heads,
     std::vector<float> table(seq_len * head_dim);
     check(moe_rope_table(theta, static_cast<int64_t>(head_dim), static_cast<int64_t>(seq_len),
                          table.data()));
-    DeviceBuffer dt(table.size() * sizeof(float));
-    dt.upload(table.data(), table.size() * sizeof(float));
-    DeviceBuffer dq = to_device(q), dk = to_device(k);
-    check(moe_rope(moe_dropin::context(), dq.as<float>(), dk.as<float>(), dt.as<float>(),
-                   static_cast<int64_t>(seq_len), 1, static_cast<int64_t>(seq_len), 0,
-                   static_cast<int64_t>(q_heads), static_cast<int64_t>(kv_heads),
-                   static_cast<int64_t>(head_dim), nullptr));
-    dq.download(q.data(), q.size() * sizeof(float));
-    dk.download(k.data(), k.size() * sizeof(float));
+    auto lock = moe_dropin::io_lock();
+    float* dt = moe_dropin::io_scratch().f32(kC, table.size());
+    moe_dropin::to_device(dt, table.data(), table.size() * sizeof(float));
+    float* dq = stage_in(kA, q);
+    float* dk = stage_in(kB, k);
+    check(moe_rope(moe_dropin::context(), dq, dk, dt, static_cast<int64_t>(seq_len), 1,
+                   static_cast<int64_t>(seq_len), 0, static_cast<int64_t>(q_heads),
+                   static_cast<int64_t>(kv_heads), static_cast<int64_t>(head_dim), nullptr));
+    stage_out(q, dq);
+    stage_out(k, dk);
 }
 
 }  // namespace tensor_ops

@@ -4,6 +4,8 @@
                     [--cpu-seconds S]
     python bench.py --sgemm        (config 2: the SGEMM sweep, a line per shape)
     python bench.py --decoder      (config 5: the whole 4-layer decoder prefill)
+    python bench.py --dropin       (the C++ drop-in PhiMoE::forward, host tensors,
+                                    at the reference's layer shape)
 
 A step is one moe_layer_forward (gate -> route -> permute -> grouped expert
 FFN -> combine) over one batch of synthetic tokens whose inputs and weights
@@ -297,6 +299,68 @@ def decoder_cpu_baseline(tokens, W, cfg, gpu_hidden, target_s):
     }, parity
 
 
+def write_model_bin(path, tensors):
+    """The reference's model.bin layout (src/model_loader.cu:14-30): u32 count;
+    per tensor u32 name length, name, u32 ndim, u32 dims, u64 offset, u64
+    bytes; the fp32 data at the offsets."""
+    import struct
+    import numpy as np
+    header = 4 + sum(4 + len(n.encode()) + 4 + 4 * a.ndim + 16 for n, a in tensors.items())
+    blob = bytearray(struct.pack("<I", len(tensors)))
+    off = header
+    for name, a in tensors.items():
+        nb = name.encode()
+        blob += struct.pack("<I", len(nb)) + nb + struct.pack("<I", a.ndim)
+        blob += struct.pack(f"<{a.ndim}I", *a.shape) + struct.pack("<QQ", off, a.nbytes)
+        off += a.nbytes
+    with open(path, "wb") as f:
+        f.write(bytes(blob))
+        for a in tensors.values():
+            f.write(np.ascontiguousarray(a, dtype=np.float32).tobytes())
+
+
+def dropin_bench(args):
+    """The C++ drop-in's PhiMoE::forward (host Tensors in and out, so the PCIe
+    copies are inside the time) at the reference's layer shape, through the
+    C shim the drop-in tests use (tests/cpp/libdropin_shim.so): weights in a
+    model.bin of the reference's format, 15,583 rows of d 4096."""
+    import ctypes
+    import tempfile
+    import numpy as np
+    cfg = CONFIGS["ref"]
+    T, d, E, d_ff = cfg["T"], cfg["d"], cfg["E"], cfg["d_ff"]
+    rng = np.random.default_rng(0)
+    base = "model.layers.0.block_sparse_moe"
+    tensors = {f"{base}.gate.weight": (0.02 * rng.standard_normal((E, d))).astype(np.float32)}
+    for e in range(E):
+        for name, shape in (("w1", (d_ff, d)), ("w2", (d, d_ff)), ("w3", (d_ff, d))):
+            tensors[f"{base}.experts.{e}.{name}.weight"] = (
+                0.02 * rng.standard_normal(shape)).astype(np.float32)
+    x = rng.standard_normal((T, d)).astype(np.float32)
+    shim = ctypes.CDLL(os.path.join(ROOT, "tests", "cpp", "libdropin_shim.so"))
+    shim.shim_error.restype = ctypes.c_char_p
+    I = ctypes.c_int64
+    ms = ctypes.c_double(0.0)
+    with tempfile.TemporaryDirectory() as tmp:
+        path = os.path.join(tmp, "model.bin")
+        write_model_bin(path, tensors)
+        rc = shim.shim_moe_time(path.encode(), I(0), x.ctypes.data_as(ctypes.c_void_p), I(T),
+                                I(d), I(args.warmup), I(args.steps), ctypes.byref(ms))
+    if rc != 0:
+        raise RuntimeError(f"shim_moe_time: {shim.shim_error().decode()}")
+    print(json.dumps({
+        "metric": "drop-in PhiMoE::forward tokens/sec, host tensors in and out (PCIe-inclusive), "
+                  "1 MI355X",
+        "value": T / (ms.value * 1e-3), "unit": "tokens/s", "ms_per_call": ms.value,
+        "steps": args.steps, "warmup": args.warmup, "dtype": "f32",
+        "data": "synthetic (seeded: x ~ N(0,1), weights ~ N(0,0.02))",
+        "config": {"workload": cfg["workload"], "tokens": T, "d_model": d, "experts": E,
+                   "top_k": cfg["k"], "d_ff": d_ff,
+                   "router": "quantised top-2, weights 1/2 (PhiMoE::route)",
+                   "io": "pageable host Tensors through the drop-in's pinned staging"},
+    }))
+
+
 def decoder_bench(args, pkg):
     """Config 5 as a whole: the 4-layer decoder prefill of 8 x 512 tokens
     (embedding, per layer RMS norm, q/k/v projections, RoPE, causal
@@ -442,6 +506,9 @@ def main():
                     help="config 5's whole decoder prefill (8 x 512 tokens, 4 layers)")
     ap.add_argument("--no-graph", action="store_true",
                     help="--decoder: time eager steps instead of HIP-graph replays")
+    ap.add_argument("--dropin", action="store_true",
+                    help="the C++ drop-in PhiMoE::forward at the reference's layer shape, host "
+                         "tensors in and out (PCIe-inclusive)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported "
@@ -454,6 +521,9 @@ def main():
         return
     if args.decoder:
         decoder_bench(args, load_pkg())
+        return
+    if args.dropin:
+        dropin_bench(args)
         return
 
     import numpy as np

@@ -274,6 +274,8 @@ int shim_moe(const char* path, int64_t layer, int contract, const float* x, int6
 int shim_moe_time(const char* path, int64_t layer, const float* x, int64_t rows, int64_t h,
                   int64_t warmup, int64_t iters, double* ms) {
     return guarded([&] {
+        if (iters <= 0 || warmup < 0)
+            throw std::invalid_argument("iters must be > 0 and warmup >= 0");
         ModelLoader l(path);
         PhiMoE moe(l, size_t(layer));
         Tensor X = make(x, {size_t(rows), size_t(h)}), Y;

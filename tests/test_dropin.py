@@ -121,6 +121,16 @@ def test_shape_errors_before_any_device_work(shim):
     assert err(shim) == "layer norm shape"
 
 
+def test_moe_timing_rejects_nonpositive_iterations(shim):
+    x = np.zeros((2, 4), np.float32)
+    I = ctypes.c_int64
+    ms = ctypes.c_double(0.0)
+    for warmup, iters in ((1, 0), (1, -3), (-1, 2)):
+        assert shim.shim_moe_time(b"/nonexistent/model.bin", I(0), fptr(x), I(2), I(4), I(warmup),
+                                  I(iters), ctypes.byref(ms)) == INVALID
+        assert "iters" in err(shim)
+
+
 # ---------------------------------------------------------------- GPU side
 @pytest.mark.gpu
 def test_tensor_pinned(shim):
