@@ -144,7 +144,8 @@ DensePlan plan_dense(moe_ctx* ctx, bool nn, bool direct, int64_t M, int64_t N, i
     // bandwidth, launch and reduction overheads, and the slowdown of a
     // workgroup alone on its CU (4096 x 1024 x 1024: 128 x 128 tiles, one
     // per CU, 95.6 us; 64 x 128 tiles, two per CU, 87.4 us)
-    static constexpr double kEff[moe::kDenseTiles] = {0.80, 0.80, 0.50};
+    // (tile 3, NN only, reads its B fragments 16 bytes at a time: the NT rate)
+    static constexpr double kEff[moe::kDenseTiles] = {0.80, 0.80, 0.50, 0.86};
     constexpr double kStageLatency = 0.6e-6, kRound = 1e-6, kHbm = 5.0e12, kLaunch = 2e-6,
                      kReduce = 2e-6, kSolo = 1.15;
     // each tile shape runs 4 waves, one per SIMD
@@ -152,10 +153,12 @@ DensePlan plan_dense(moe_ctx* ctx, bool nn, bool direct, int64_t M, int64_t N, i
     double best_t = 1e30;
     for (int t = 0; t < moe::kDenseTiles; ++t) {
         if (env_tile >= 0 && t != env_tile) continue;
+        if (t == 3 && !nn) continue;  // the 256 x 128 tile is NN only
         int& occ = ctx->dense_blocks_per_cu[nn ? 1 : 0][t];
         if (occ == 0) occ = moe::dense_blocks_per_cu(t, nn);
         const moe::GemmTile g = moe::dense_tile(t);
-        const int wm = g.bm >= 64 ? 2 : 1;  // wave grid: 2x2, or 1x4 for the 32-row tile
+        // wave grid: 2x2; 1x4 for the 32-row tile; 4x1 for the 256-row tile
+        const int wm = g.bm >= 256 ? 4 : (g.bm >= 64 ? 2 : 1);
         const int wn = 4 / wm;
         const int64_t mt = moe::ceil_div(M, g.bm), nt = moe::ceil_div(N, g.bn);
         const int64_t rows_w = std::min<int64_t>(g.bm / wm, 32 * moe::ceil_div(std::min<int64_t>(M, g.bm), 32));

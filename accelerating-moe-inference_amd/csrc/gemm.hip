@@ -59,6 +59,11 @@
 #ifndef MOE_DENSE_SCHED
 #define MOE_DENSE_SCHED 30
 #endif
+// The 256 x 128 NN tile takes the three-stage ring, like the expert GEMMs
+// whose per-wave work it shares.
+#ifndef MOE_DENSE_NN_SCHED
+#define MOE_DENSE_NN_SCHED 62
+#endif
 // The small dense tiles (64 x 128, 32 x 128) serve short and skinny
 // products whose few workgroups per CU cannot hide HBM latency with two
 // stages: they take the ring too, for a second step of loads in flight.
@@ -123,6 +128,9 @@ template <> struct CfgOf<9> { using T = Cfg<32, 128, 16, 1, 4>; };  // direct on
 // is a multiple of 64 but not of 128 (448: exactly 7 n-tiles instead of 4,
 // the last of them half empty)
 template <> struct CfgOf<10> { using T = Cfg<256, 64, 16, 4, 1>; };
+// Dense NN on 256 rows x 128 columns, each wave 64 rows x all 128 columns
+// (4 32 x 32 blocks): its B fragments are read column-strided (below).
+template <> struct CfgOf<11> { using T = Cfg<256, 128, 16, 4, 1>; };
 
 // Workgroup ids are dealt round-robin over the XCDs.  Renumber them so each
 // XCD works through a contiguous run of logical tiles: tiles that share an
@@ -574,6 +582,12 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
     static_assert(A_INS * NW == A_TOT || A_TOT < NW, "A load split");
     static_assert(B_INS * NW == B_TOT || B_TOT < NW, "B load split");
     constexpr int B_SIZE = NN ? B_TOT * NnB<BN>::STRIDE : BN * BK;
+    // NN with 4 column blocks per wave: block bj holds the columns
+    // 4 c + bj (c = lane % 32), so one 16-byte LDS read of a k-row gives a
+    // lane its B value for all 4 blocks (NN B sits k-major in LDS; with
+    // 32-column blocks each value would be a separate 4-byte read), and the
+    // epilogue writes 4 adjacent columns per lane.
+    constexpr bool NSTRIDE = NN && FN == 4;
     __shared__ __align__(16) float As[2][BM * BK];
     __shared__ __align__(16) float Bs[2][NB][B_SIZE];
 
@@ -764,6 +778,16 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
             }
         };
         auto read_b = [&](int nb, int q) {
+            if constexpr (NSTRIDE) {
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const f32x4 v = *reinterpret_cast<const f32x4*>(
+                        &Bcur[nb * B_SIZE + NnB<BN>::at(8 * lh + 4 * q + s, bcol0 + 4 * lr)]);
+#pragma unroll
+                    for (int bj = 0; bj < 4; ++bj) b[nb][bj][q][s] = v[bj];
+                }
+                return;
+            }
 #pragma unroll
             for (int bj = 0; bj < FN; ++bj) {
                 const int r = bcol0 + bj * 32 + lr;
@@ -917,6 +941,36 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
         }
     }
 
+    if constexpr (NSTRIDE) {
+        // 4 adjacent columns per lane and row: one 16-byte store when they
+        // all lie inside N and the row start is 16-byte aligned
+        const int64_t nc = n0 + bcol0 + 4 * lr;
+        const bool vec4 = nc + 3 < N && p.ldc % 4 == 0 && p.c_split_stride % 4 == 0 &&
+                          (reinterpret_cast<uintptr_t>(Cb) & 15) == 0;
+#pragma unroll
+        for (int bi = 0; bi < FM; ++bi)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int i = arow0 + bi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                if (i >= rows) continue;
+                if (vec4) {
+                    f32x4 v;
+#pragma unroll
+                    for (int bj = 0; bj < 4; ++bj) {
+                        v[bj] = acc[0][bi][bj][r];
+                        if (EPI == EPI_BIAS && p.bias != nullptr) v[bj] = v[bj] + p.bias[nc + bj];
+                    }
+                    *reinterpret_cast<f32x4*>(&Cb[split * p.c_split_stride + (row0 + i) * p.ldc + nc]) = v;
+                } else {
+#pragma unroll
+                    for (int bj = 0; bj < 4; ++bj)
+                        if (nc + bj < N)
+                            epi_store<EPI>(p, Cb, split, row0 + i, nc + bj, acc[0][bi][bj][r],
+                                           acc[NB - 1][bi][bj][r]);
+                }
+            }
+        return;
+    }
 #pragma unroll
     for (int bi = 0; bi < FM; ++bi)
 #pragma unroll
@@ -978,6 +1032,7 @@ void launch_cfg(const GemmArgs& a, bool vec, hipStream_t s) {
 using DenseCfg = CfgOf<MOE_DENSE_CFG>::T;
 using DenseMidCfg = CfgOf<8>::T;
 using DenseSmallCfg = CfgOf<9>::T;
+using DenseNnCfg = CfgOf<11>::T;  // NN only (column-strided B fragments)
 using W13Cfg = CfgOf<MOE_W13_CFG>::T;
 using W2Cfg = CfgOf<MOE_W2_CFG>::T;
 using W2NarrowCfg = CfgOf<0>::T;  // w2 with d too narrow for the wide tile's n-tiles
@@ -1045,6 +1100,7 @@ GemmTile dense_tile(int tile) {
     switch (tile) {
         case 1: return {DenseMidCfg::BM, DenseMidCfg::BN};
         case 2: return {DenseSmallCfg::BM, DenseSmallCfg::BN};
+        case 3: return {DenseNnCfg::BM, DenseNnCfg::BN};
         default: return {DenseCfg::BM, DenseCfg::BN};
     }
 }
@@ -1053,6 +1109,7 @@ int dense_blocks_per_cu(int tile, bool nn) {
     switch (tile) {
         case 1: return dense_occupancy<DenseMidCfg, MOE_DENSE_SMALL_SCHED | SCHED_DIRECT>(nn);
         case 2: return dense_occupancy<DenseSmallCfg, MOE_DENSE_SMALL_SCHED | SCHED_DIRECT>(nn);
+        case 3: return dense_occupancy<DenseNnCfg, MOE_DENSE_NN_SCHED | SCHED_DIRECT>(true);
         default: return dense_occupancy<DenseCfg, MOE_DENSE_SCHED | SCHED_DIRECT>(nn);
     }
 }
@@ -1132,6 +1189,11 @@ void launch_gemm(const GemmArgs& args, bool nn, bool grouped, int epi, bool vec,
             case 2:
                 if (nn) launch_dense<DenseSmallCfg, true>(a, vec, s);
                 else launch_dense<DenseSmallCfg, false>(a, vec, s);
+                break;
+            case 3:
+                if (!nn) throw Unsupported("dense tile 3 is NN only");
+                launch_cfg<DenseNnCfg, MOE_DENSE_NN_SCHED | SCHED_DIRECT, true, false, 1, EPI_BIAS>(
+                    a, vec, s);
                 break;
             default: throw Unsupported("dense GEMM tile shape");
         }
