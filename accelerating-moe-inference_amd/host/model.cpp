@@ -171,8 +171,15 @@ void PhiTinyMoEModel::generate(const std::vector<std::vector<int>>& input_ids,
     check(moe_sgemm_nt(ctx, last_n, lm_w_->as<float>(), lm_b_ ? lm_b_->as<float>() : nullptr, out,
                        static_cast<int64_t>(batch), static_cast<int64_t>(vocab_),
                        static_cast<int64_t>(h), nullptr));
-    logits = Tensor({batch, vocab_});
-    sc.download(kLogits, logits.data(), batch * vocab_ * sizeof(float));
+    // the caller's Tensor is reused when it holds enough elements; the
+    // copy goes through the drop-in's pinned staging
+    const std::size_t n = batch * vocab_;
+    if (logits.capacity() >= n && logits.data() != nullptr)
+        logits.reshape_within_capacity({batch, vocab_});
+    else
+        logits = Tensor({batch, vocab_});
+    auto lock = moe_dropin::io_lock();
+    moe_dropin::to_host(logits.data(), out, n * sizeof(float));
 }
 
 void PhiTinyMoEModel::generate_decode(const std::vector<std::vector<int>>& input_ids,

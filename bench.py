@@ -6,6 +6,8 @@
     python bench.py --decoder      (config 5: the whole 4-layer decoder prefill)
     python bench.py --dropin       (the C++ drop-in PhiMoE::forward, host tensors,
                                     at the reference's layer shape)
+    python bench.py --model        (the C++ drop-in PhiTinyMoEModel::generate on the
+                                    reference's model shape and batch)
 
 A step is one moe_layer_forward (gate -> route -> permute -> grouped expert
 FFN -> combine) over one batch of synthetic tokens whose inputs and weights
@@ -361,6 +363,102 @@ def dropin_bench(args):
     }))
 
 
+def model_bench(args):
+    """The C++ drop-in's PhiTinyMoEModel::generate (the reference's timed
+    end-to-end call, src/main.cpp:584-601) on the reference's model shape
+    (Phi-tiny-MoE: 32 layers, d 4096, 16 query / 4 key heads of 128, 16
+    experts of d_ff 448, vocabulary 32064; random weights) over a batch
+    shaped like the reference's contest input: 1024 sequences, 10-29 tokens
+    each, whose first 4 tokens come from 64 shared prefixes, so the prefix
+    trie removes about a fifth of the rows (the reference's input: 19,803
+    tokens, 15,583 trie rows).  Host token lists in, host logits out."""
+    import ctypes
+    import struct
+    import tempfile
+    import numpy as np
+    L_, h, E, ff, vocab, qw, kw = 32, 4096, 16, 448, 32064, 16 * 128, 4 * 128
+    specs = [("model.embed_tokens.weight", (vocab, h), 1.0, 0.0),
+             ("model.norm.weight", (h,), 0.1, 1.0), ("model.norm.bias", (h,), 0.1, 0.0),
+             ("lm_head.weight", (vocab, h), 0.02, 0.0), ("lm_head.bias", (vocab,), 0.02, 0.0)]
+    for li in range(L_):
+        p = f"model.layers.{li}"
+        specs += [(f"{p}.input_layernorm.weight", (h,), 0.1, 1.0),
+                  (f"{p}.input_layernorm.bias", (h,), 0.1, 0.0),
+                  (f"{p}.post_attention_layernorm.weight", (h,), 0.1, 1.0),
+                  (f"{p}.post_attention_layernorm.bias", (h,), 0.1, 0.0),
+                  (f"{p}.block_sparse_moe.gate.weight", (E, h), 0.02, 0.0)]
+        for name, out, inp in (("q_proj", qw, h), ("k_proj", kw, h), ("v_proj", kw, h),
+                               ("o_proj", h, qw)):
+            specs += [(f"{p}.self_attn.{name}.weight", (out, inp), 0.02, 0.0),
+                      (f"{p}.self_attn.{name}.bias", (out,), 0.02, 0.0)]
+        for e in range(E):
+            specs += [(f"{p}.block_sparse_moe.experts.{e}.w1.weight", (ff, h), 0.02, 0.0),
+                      (f"{p}.block_sparse_moe.experts.{e}.w3.weight", (ff, h), 0.02, 0.0),
+                      (f"{p}.block_sparse_moe.experts.{e}.w2.weight", (h, ff), 0.02, 0.0)]
+    # every tensor is a window of one seeded N(0,1) pool (64 MiB), at its own
+    # offset, scaled and shifted; each gate gets its own fresh draws
+    rng = np.random.default_rng(0)
+    pool = rng.standard_normal(1 << 24).astype(np.float32)
+    sizes = [int(np.prod(shape)) for _, shape, _, _ in specs]
+    header = 4 + sum(4 + len(n.encode()) + 4 + 4 * len(shape) + 16 for n, shape, _, _ in specs)
+    # the batch: 1024 sequences, lengths 10..29, the first 4 tokens from one
+    # of 64 shared prefixes
+    tr = np.random.default_rng(1)
+    prefixes = tr.integers(0, 32000, (64, 4))
+    lens = tr.integers(10, 30, 1024).astype(np.int32)
+    seqs = [np.concatenate([prefixes[tr.integers(0, 64)], tr.integers(0, 32000, n - 4)])
+            for n in lens]
+    nodes = len({tuple(sq[:i + 1]) for sq in seqs for i in range(len(sq))})
+    ids = np.concatenate(seqs).astype(np.int32)
+    shim = ctypes.CDLL(os.path.join(ROOT, "tests", "cpp", "libdropin_shim.so"))
+    shim.shim_error.restype = ctypes.c_char_p
+    I, D = ctypes.c_int64, ctypes.c_double
+    load_s, ms = D(0.0), D(0.0)
+    t0 = time.perf_counter()
+    with tempfile.TemporaryDirectory() as tmp:
+        path = os.path.join(tmp, "model.bin")
+        with open(path, "wb") as f:
+            blob = bytearray(struct.pack("<I", len(specs)))
+            off = header
+            for (name, shape, _, _), n in zip(specs, sizes):
+                nb = name.encode()
+                blob += struct.pack("<I", len(nb)) + nb + struct.pack("<I", len(shape))
+                blob += struct.pack(f"<{len(shape)}I", *shape) + struct.pack("<QQ", off, 4 * n)
+                off += 4 * n
+            f.write(bytes(blob))
+            for i, ((name, shape, scale, shift), n) in enumerate(zip(specs, sizes)):
+                if ".gate." in name:
+                    a = rng.standard_normal(n).astype(np.float32)
+                else:
+                    a = np.resize(np.roll(pool, -((i * 7919 * 4096) % pool.size)), n)
+                (a * np.float32(scale) + np.float32(shift)).astype(np.float32).tofile(f)
+        write_s = time.perf_counter() - t0
+        print(f"model.bin written ({off / 2**30:.1f} GiB, {write_s:.0f} s); timing generate()",
+              file=sys.stderr, flush=True)
+        rc = shim.shim_model_time(path.encode(), lens.ctypes.data_as(ctypes.c_void_p),
+                                  ids.ctypes.data_as(ctypes.c_void_p), I(len(lens)),
+                                  I(args.warmup), I(args.steps), ctypes.byref(load_s),
+                                  ctypes.byref(ms))
+    if rc != 0:
+        raise RuntimeError(f"shim_model_time: {shim.shim_error().decode()}")
+    seq_s = len(lens) / (ms.value * 1e-3)
+    print(json.dumps({
+        "metric": "drop-in PhiTinyMoEModel::generate sequences/sec (prefill, logits of the last "
+                  "position), 1 MI355X",
+        "value": seq_s, "unit": "seq/s", "ms_per_call": ms.value, "steps": args.steps,
+        "warmup": args.warmup, "dtype": "f32",
+        "data": "synthetic (seeded random weights; random token ids with 64 shared prefixes)",
+        "config": {"workload": "phi_tiny_moe_generate_fp32", "sequences": int(len(lens)),
+                   "tokens": int(lens.sum()), "trie_rows": nodes, "layers": L_, "d_model": h,
+                   "experts": E, "top_k": 2, "d_ff": ff, "vocab": vocab,
+                   "router": "quantised top-2, weights 1/2 (PhiMoE::route)"},
+        "reference_gpu_seq_s": 687.8,
+        "reference_note": "the reference's end-to-end figure on one RTX 3090, 1024 sequences / "
+                          "19,803 tokens of its contest input (docs/report/report.html:96)",
+        "model_load_s": load_s.value,
+    }))
+
+
 def decoder_bench(args, pkg):
     """Config 5 as a whole: the 4-layer decoder prefill of 8 x 512 tokens
     (embedding, per layer RMS norm, q/k/v projections, RoPE, causal
@@ -506,6 +604,9 @@ def main():
                     help="config 5's whole decoder prefill (8 x 512 tokens, 4 layers)")
     ap.add_argument("--no-graph", action="store_true",
                     help="--decoder: time eager steps instead of HIP-graph replays")
+    ap.add_argument("--model", action="store_true",
+                    help="the C++ drop-in PhiTinyMoEModel::generate on the reference's model "
+                         "shape (32 layers; writes a ~15 GiB model.bin to a temporary directory)")
     ap.add_argument("--dropin", action="store_true",
                     help="the C++ drop-in PhiMoE::forward at the reference's layer shape, host "
                          "tensors in and out (PCIe-inclusive)")
@@ -524,6 +625,9 @@ def main():
         return
     if args.dropin:
         dropin_bench(args)
+        return
+    if args.model:
+        model_bench(args)
         return
 
     import numpy as np

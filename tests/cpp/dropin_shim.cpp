@@ -347,6 +347,28 @@ int shim_model_generate(const char* path, const int32_t* lens, const int32_t* id
     });
 }
 
+// Times PhiTinyMoEModel: construction from the file (load_s, seconds) and
+// generate() over the batch (ms per call, after `warmup` calls); nodes: the
+// rows of the batch's prefix trie (distinct prefixes).
+int shim_model_time(const char* path, const int32_t* lens, const int32_t* ids, int64_t batch,
+                    int64_t warmup, int64_t iters, double* load_s, double* ms) {
+    return guarded([&] {
+        if (iters <= 0 || warmup < 0)
+            throw std::invalid_argument("iters must be > 0 and warmup >= 0");
+        const auto t0 = std::chrono::steady_clock::now();
+        PhiTinyMoEModel m(path);
+        const auto t1 = std::chrono::steady_clock::now();
+        *load_s = std::chrono::duration<double>(t1 - t0).count();
+        const std::vector<std::vector<int>> seqs = unpack(lens, ids, batch);
+        Tensor L;
+        for (int64_t i = 0; i < warmup; ++i) m.generate(seqs, L);
+        const auto t2 = std::chrono::steady_clock::now();
+        for (int64_t i = 0; i < iters; ++i) m.generate(seqs, L);
+        const auto t3 = std::chrono::steady_clock::now();
+        *ms = std::chrono::duration<double, std::milli>(t3 - t2).count() / double(iters);
+    });
+}
+
 int shim_model_decode(const char* path, const int32_t* lens, const int32_t* ids, int64_t batch,
                       int64_t max_new, float* logits, int32_t* gen_lens, int32_t* gen_ids) {
     return guarded([&] {
