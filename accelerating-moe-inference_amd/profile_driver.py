@@ -2,11 +2,15 @@
 
     rocprofv3 --pmc FETCH_SIZE -d OUT -o copy -- python3 profile_driver.py copy --mib 1024
     rocprofv3 --pmc FETCH_SIZE -d OUT -o c3   -- python3 profile_driver.py layer --config c3
+    rocprofv3 --pmc FETCH_SIZE -d OUT -o c2   -- python3 profile_driver.py sgemm
 
 `copy` launches one elementwise kernel that reads and writes exactly
 --mib MiB (torch.neg into a second buffer): the calibration of the TCC byte
 counters against a known traffic.  `layer` runs --steps MoE layer forwards
 of a bench configuration (same seeded data as bench.py) after one warm-up.
+`sgemm` runs every config-2 SGEMM shape twice, NN then NT (bench.py's
+SGEMM_SHAPES, A and B ~ U[-1, 1]), printing each shape before its calls so
+dispatches can be matched to shapes.
 """
 from __future__ import annotations
 
@@ -21,7 +25,7 @@ ROOT = os.path.dirname(HERE)
 
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("what", choices=["copy", "layer"])
+    ap.add_argument("what", choices=["copy", "layer", "sgemm"])
     ap.add_argument("--mib", type=int, default=1024)
     ap.add_argument("--config", default="c3", choices=["c3", "c4", "c5", "ref"])
     ap.add_argument("--steps", type=int, default=2)
@@ -42,8 +46,24 @@ def main():
     spec = importlib.util.spec_from_file_location("bench", os.path.join(ROOT, "bench.py"))
     bench = importlib.util.module_from_spec(spec)
     spec.loader.exec_module(bench)
-    cfg = bench.CONFIGS[args.config]
     pkg = bench.load_pkg()
+    if args.what == "sgemm":
+        ctx = pkg.Context(0)
+        g = torch.Generator(device="cuda").manual_seed(0)
+        for layout in ("nn", "nt"):
+            for M, N, K in bench.SGEMM_SHAPES:
+                a = torch.rand((M, K), device="cuda", generator=g) * 2 - 1
+                b = torch.rand((K, N) if layout == "nn" else (N, K), device="cuda", generator=g) * 2 - 1
+                c = torch.empty((M, N), device="cuda")
+                torch.cuda.synchronize()
+                print(f"sgemm {layout} {M} {N} {K}", flush=True)
+                for _ in range(2):
+                    (ctx.sgemm_nn if layout == "nn" else ctx.sgemm_nt)(a, b, c)
+                torch.cuda.synchronize()
+                del a, b, c
+        ctx.close()
+        return
+    cfg = bench.CONFIGS[args.config]
     T, d, E, k, d_ff = cfg["T"], cfg["d"], cfg["E"], cfg["k"], cfg["d_ff"]
     g = torch.Generator(device="cuda").manual_seed(0)
     x = torch.randn((T, d), device="cuda", generator=g)
