@@ -39,6 +39,7 @@ EXPORTS = (
     "moe_add_bias", "moe_embed", "moe_gate_logits",
     "moe_route", "moe_permute", "moe_expert_ffn_grouped", "moe_combine",
     "moe_layer_forward", "moe_layer_forward_noalloc", "moe_layer_w2_splits",
+    "moe_ctx_set_stream_k",
 )
 
 
@@ -121,6 +122,7 @@ def load_library(path: str = LIB_PATH):
                                        ctypes.POINTER(LayerWeights), P, P, P, P, P], I),
         "moe_layer_w2_splits": ([P, ctypes.POINTER(LayerDesc), ctypes.POINTER(ctypes.c_int32)],
                                 I),
+        "moe_ctx_set_stream_k": ([P, I], I),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -398,6 +400,11 @@ class Context:
                   _f32(y, "y"), _i32(topk_idx, "topk_idx"), _f32(topk_w, "topk_w"),
                   _stream()))
         return y
+
+    def set_stream_k(self, mode: int) -> None:
+        """moe_ctx_set_stream_k: -1 planner, 0 one tile per workgroup, 1
+        stream-K for the grouped expert GEMMs of this context."""
+        _check(_lib.moe_ctx_set_stream_k(self.handle, int(mode)))
 
     def w2_splits(self, desc: LayerDesc) -> int:
         """K splits layer_forward(desc) uses for w2 on this context's GPU."""

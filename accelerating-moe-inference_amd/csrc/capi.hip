@@ -18,7 +18,7 @@ thread_local std::string g_last_error;
 // as an address (on the host it names a stand-in, not device memory): each
 // device's address comes from hipGetSymbolAddress, taken once per device
 // when the first context on it is created, and is what every kernel gets.
-constexpr size_t kNoAllocScratchBytes = size_t(64) << 20;
+constexpr size_t kNoAllocScratchBytes = size_t(256) << 20;
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mutex;
@@ -263,33 +263,122 @@ int64_t grouped_m_tiles(int64_t pairs, int64_t E, int bm) {
     return std::min<int64_t>(moe::ceil_div(pairs, bm) + E, pairs);
 }
 
-// K splits S of the layer's w2.  Its tiles run in rounds of `slots`
-// concurrent workgroups; a last, partly filled round of long-K tiles wastes
-// the rest of the GPU for a whole tile time.  Splitting K S ways makes the
-// rounds S times shorter, so the fill is w / ceil(w) with w = tiles * S /
-// slots.  The smallest S in {1, 2, 4} whose fill reaches 95 % is taken (else
-// the best): every split adds a partial row buffer the combine must read
-// (at the reference's layer shape S = 2 costs 0.11 ms there and 0.1 ms of
-// w2 against S = 1).  Each split must be a multiple of 16 columns.
-// MOE_W2_SPLITS overrides for tuning.
-struct W2Plan {
-    int tile;    // GemmArgs::tile of the w2 launch: 0 wide (W2), 1 128x128 (W2Narrow)
-    int splits;  // K splits
+// K splits S of the layer's w2 on the one-tile-per-workgroup kernel.  Its
+// tiles run in rounds of `slots` concurrent workgroups; a last, partly
+// filled round of long-K tiles wastes the rest of the GPU for a whole tile
+// time.  Splitting K S ways makes the rounds S times shorter, so the fill
+// is w / ceil(w) with w = tiles * S / slots.  The smallest S in {1, 2, 4}
+// whose fill reaches 95 % is taken (else the best): every split adds a
+// partial row buffer the combine must read (at the reference's layer shape
+// S = 2 costs 0.11 ms there and 0.1 ms of w2 against S = 1).  Each split
+// must be a multiple of 16 columns.  MOE_W2_SPLITS overrides for tuning.
+struct FfnPlan {
+    int w13_tile = 0;  // GemmArgs::tile of w1/w3: 0 128x128 (W13), 1 256x64 (W13Tall)
+    int w13_sk = 0;    // stream-K grid of w1/w3 (0: one tile per workgroup)
+    int tile = 0;      // GemmArgs::tile of w2: 0 wide (W2), 1 128x128 (W2Narrow)
+    int splits = 1;    // K splits of w2 (1 under stream-K)
+    int w2_sk = 0;     // stream-K grid of w2
+    int64_t sk_floats = 0;  // partial-tile floats the stream-K launches need
 };
 
 int choose_w2_splits(moe_ctx* ctx, int64_t pairs, int64_t d, int64_t d_ff, int64_t E, int w2_tile);
 
-// The w2 plan of a layer: the tile and its K splits.  The wide tile (its
-// 256 columns halve the B traffic per MFMA) unless d gives it at most 4
-// n-tiles: then each expert's rows form so few tiles that the 128x128 tile's
-// extra parallelism wins (a tile x split sweep on MI355X: config 5, d = 1024,
-// 1.545 -> 1.488 ms per layer; configs 3 and 4, with 16 and 8 wide n-tiles,
-// 3-5 % slower on the narrow tile).  MOE_W2_TILE = 0 / 1 overrides.
-W2Plan choose_w2_plan(moe_ctx* ctx, int64_t pairs, int64_t d, int64_t d_ff, int64_t E) {
+// The w1/w3 tile: 128 rows x 128 columns of each operand, or, when d_ff is
+// a multiple of 64 but not of 128 (the reference's 448), 256 rows x 64
+// columns, so the n-tiles cover d_ff exactly instead of leaving the last one
+// half empty.  MOE_W13_TILE = 0 / 1 overrides.
+int choose_w13_tile(int64_t d_ff) {
+    static const int env_tile = env_int("MOE_W13_TILE", -1);
+    if (env_tile == 0 || env_tile == 1) return env_tile;
+    return (d_ff % 128 != 0 && d_ff % 64 == 0) ? 1 : 0;
+}
+
+// Expected real m-tiles of a grouped launch: ceil(pairs / BM) plus half a
+// tile per expert (each expert's last tile half full), at most the bound.
+int64_t expected_m_tiles(int64_t pairs, int64_t E, int bm) {
+    return std::min<int64_t>(moe::ceil_div(pairs, bm) + E / 2, grouped_m_tiles(pairs, E, bm));
+}
+
+// Stream-K or one tile per workgroup.  One tile per workgroup runs the
+// tiles in rounds of `slots` (w2: of its S K splits); its fill is w /
+// ceil(w), w = tiles * S / slots.  Stream-K runs the full rounds the same
+// way and deals the K steps of the tiles left over to its G workgroups in
+// contiguous ranges, at the price of partial stores and a fix-up launch for
+// the cut tiles and of L2 sharing in the dealt part (its workgroups read
+// unrelated K offsets).  Measured on MI355X at configs 3-5 and the
+// reference's layer shape with 64 tokens to full size, it wins where the
+// one-tile fill is under 96 % and
+//   w1/w3 (no K splits there): K is at least 128 steps of 16 -- shorter
+//     tiles lose more to the dealt part's start-ups and L2 misses than the
+//     fill gains (config 5, K = 1024);
+//   w2 (against its best split plan, whose combine reads every split's
+//     partial rows): each workgroup's dealt range is at least 64 K steps.
+// Pieces are kept at 32 K steps or more: with fewer tiles than slots, G is
+// cut to tiles x K-steps / 32 (at least the tiles).  MOE_SK = 0 / 1 (or
+// moe_ctx_set_stream_k) forces either (1: on every launch the direct
+// buffer-load path applies to, on all slots).  Returns the stream-K grid, 0
+// for one tile per workgroup.
+int choose_sk(moe_ctx* ctx, moe::GemmUse use, int64_t pairs, int64_t E, int64_t N, int64_t K,
+              int dp_splits, int dp_slots) {
+    static const int env_mode = env_int("MOE_SK", -1);
+    const int env = ctx->sk_mode >= 0 ? ctx->sk_mode : env_mode;
+    if (env == 0 || pairs == 0 || K % 16 != 0 || K < 32) return 0;
+    const moe::GemmTile t = moe::gemm_tile(use);
+    const int64_t bound_tiles = grouped_m_tiles(pairs, E, t.bm) * moe::ceil_div(N, t.bn);
+    if (bound_tiles * (K / 16) > INT32_MAX) return 0;
+    int& occ = ctx->sk_blocks_per_cu[static_cast<int>(use)];
+    if (occ == 0) occ = moe::gemm_sk_blocks_per_cu(use);
+    const int slots = ctx->cus * occ;
+    if (env == 1) return slots;
+    const double nk = double(K / 16);
+    const double tiles = double(expected_m_tiles(pairs, E, t.bm) * moe::ceil_div(N, t.bn));
+    const int S = std::max(dp_splits, 1);
+    const double w = tiles * S / dp_slots;
+    if (w / std::ceil(w) >= 0.96) return 0;
+    const bool w2 = use == moe::GemmUse::W2 || use == moe::GemmUse::W2Narrow;
+    if (!w2 && nk < 128) return 0;
+    const double left = tiles - std::floor(tiles / slots) * slots;
+    if (w2 && left * nk / slots < 64) return 0;
+    double G = slots;
+    if (tiles < G) G = std::min(G, std::max(tiles, std::floor(tiles * nk / 32.0)));
+    return static_cast<int>(G);
+}
+
+// The FFN plan of a layer.  w2: the wide tile (its 256 columns halve the B
+// traffic per MFMA) unless d gives it at most 4 n-tiles: then each expert's
+// rows form so few tiles that the 128x128 tile's extra parallelism wins (a
+// tile x split sweep on MI355X: config 5, d = 1024, 1.545 -> 1.488 ms per
+// layer; configs 3 and 4, with 16 and 8 wide n-tiles, 3-5 % slower on the
+// narrow tile).  MOE_W2_TILE = 0 / 1 overrides.  Then stream-K where the
+// one-tile rounds fill badly (choose_sk), else K splits for w2.
+FfnPlan choose_ffn_plan(moe_ctx* ctx, int64_t pairs, int64_t d, int64_t d_ff, int64_t E) {
+    FfnPlan f;
     static const int env_tile = env_int("MOE_W2_TILE", -1);
-    int tile = moe::ceil_div(d, moe::gemm_tile(moe::GemmUse::W2).bn) <= 4 ? 1 : 0;
-    if (env_tile == 0 || env_tile == 1) tile = env_tile;
-    return {tile, choose_w2_splits(ctx, pairs, d, d_ff, E, tile)};
+    f.tile = moe::ceil_div(d, moe::gemm_tile(moe::GemmUse::W2).bn) <= 4 ? 1 : 0;
+    if (env_tile == 0 || env_tile == 1) f.tile = env_tile;
+    f.w13_tile = choose_w13_tile(d_ff);
+    if (d_ff == 0 || d == 0) {
+        f.splits = 1;
+        return f;
+    }
+    // workgroups of the one-tile-per-workgroup kernel of `use` the GPU holds
+    auto slots_of = [&](moe::GemmUse use) {
+        int& occ = use == moe::GemmUse::W2Narrow ? ctx->w2n_blocks_per_cu
+                   : use == moe::GemmUse::W2     ? ctx->w2_blocks_per_cu
+                                                 : ctx->w13_blocks_per_cu[f.w13_tile];
+        if (occ == 0) occ = moe::gemm_blocks_per_cu(use);
+        return ctx->cus * occ;
+    };
+    const moe::GemmUse u13 = f.w13_tile == 1 ? moe::GemmUse::W13Tall : moe::GemmUse::W13;
+    const moe::GemmUse u2 = f.tile == 1 ? moe::GemmUse::W2Narrow : moe::GemmUse::W2;
+    f.splits = choose_w2_splits(ctx, pairs, d, d_ff, E, f.tile);
+    f.w13_sk = choose_sk(ctx, u13, pairs, E, d_ff, d, 1, slots_of(u13));
+    // w2: against its best split plan
+    f.w2_sk = choose_sk(ctx, u2, pairs, E, d, d_ff, f.splits, slots_of(u2));
+    if (f.w2_sk > 0) f.splits = 1;
+    if (f.w13_sk > 0) f.sk_floats = moe::gemm_sk_part_floats(u13, f.w13_sk);
+    if (f.w2_sk > 0) f.sk_floats = std::max(f.sk_floats, moe::gemm_sk_part_floats(u2, f.w2_sk));
+    return f;
 }
 
 int choose_w2_splits(moe_ctx* ctx, int64_t pairs, int64_t d, int64_t d_ff, int64_t E, int w2_tile) {
@@ -305,9 +394,7 @@ int choose_w2_splits(moe_ctx* ctx, int64_t pairs, int64_t d, int64_t d_ff, int64
     const moe::GemmTile tile = moe::gemm_tile(use);
     // the kernel deals only real tiles: sum over experts of ceil(n_e / BM),
     // expected ceil(pairs / BM) + E / 2 (each expert's last tile half full)
-    const int64_t m_expected = std::min<int64_t>(moe::ceil_div(pairs, tile.bm) + E / 2,
-                                                 grouped_m_tiles(pairs, E, tile.bm));
-    const double tiles = double(m_expected * moe::ceil_div(d, tile.bn));
+    const double tiles = double(expected_m_tiles(pairs, E, tile.bm) * moe::ceil_div(d, tile.bn));
     const double slots = double(int64_t(ctx->cus) * occ);
     int best = 1;
     double best_fill = 0.0;
@@ -324,32 +411,22 @@ int choose_w2_splits(moe_ctx* ctx, int64_t pairs, int64_t d, int64_t d_ff, int64
     return best;
 }
 
-// The w1/w3 tile: 128 rows x 128 columns of each operand, or, when d_ff is
-// a multiple of 64 but not of 128 (the reference's 448), 256 rows x 64
-// columns, so the n-tiles cover d_ff exactly instead of leaving the last one
-// half empty.  MOE_W13_TILE = 0 / 1 overrides.
-int choose_w13_tile(int64_t d_ff) {
-    static const int env_tile = env_int("MOE_W13_TILE", -1);
-    if (env_tile == 0 || env_tile == 1) return env_tile;
-    return (d_ff % 128 != 0 && d_ff % 64 == 0) ? 1 : 0;
-}
-
-// w2_splits > 1 (layer path only): out_rows holds w2_splits partial row
-// buffers of pairs x d, one per K range, that the combine adds up.
+// w2 with f.splits > 1 (layer path only): out_rows holds f.splits partial
+// row buffers of pairs x d, one per K range, that the combine adds up.
+// sk_part: f.sk_floats floats for the stream-K launches' partial tiles.
 void expert_ffn(moe_ctx* ctx, const float* x, const int32_t* perm,
                 const int32_t* offsets, const float* w1, const float* w3,
                 const float* w2, int act, int64_t T, int64_t k, int64_t d,
                 int64_t d_ff, int64_t E, float* h, float* out_rows, hipStream_t s,
-                int w2_splits = 1, int w2_tile = 0) {
+                const FfnPlan& f, float* sk_part) {
     const int64_t pairs = T * k;
     if (pairs == 0 || d == 0) return;
     const bool swiglu = act == MOE_ACT_SWIGLU;
     if (d_ff > 0) {
-        const int w13_tile = choose_w13_tile(d_ff);
         const moe::GemmTile tile =
-            moe::gemm_tile(w13_tile == 1 ? moe::GemmUse::W13Tall : moe::GemmUse::W13);
+            moe::gemm_tile(f.w13_tile == 1 ? moe::GemmUse::W13Tall : moe::GemmUse::W13);
         moe::GemmArgs a{};
-        a.tile = w13_tile;
+        a.tile = f.w13_tile;
         a.A = x;
         a.lda = d;
         a.gather = perm;
@@ -368,15 +445,19 @@ void expert_ffn(moe_ctx* ctx, const float* x, const int32_t* perm,
         a.m_tiles = static_cast<int32_t>(grouped_m_tiles(pairs, E, tile.bm));
         a.n_tiles = static_cast<int32_t>(moe::ceil_div(d_ff, tile.bn));
         moe::require(int64_t(a.m_tiles) * a.n_tiles <= INT32_MAX, "w13 grid too large");
+        if (f.w13_sk > 0) {
+            a.sk_grid = f.w13_sk;
+            a.sk_part = sk_part;
+        }
         const bool vec = d % 4 == 0 && aligned16(x) && aligned16(w1) && (!swiglu || aligned16(w3));
         ctx->launch(swiglu ? "expert_w13_swiglu" : "expert_w1_silu", s, [&] {
             moe::launch_gemm(a, false, true, swiglu ? moe::EPI_SWIGLU : moe::EPI_SILU, vec, s);
         });
     }
     const moe::GemmTile tile =
-        moe::gemm_tile(w2_tile == 1 ? moe::GemmUse::W2Narrow : moe::GemmUse::W2);
+        moe::gemm_tile(f.tile == 1 ? moe::GemmUse::W2Narrow : moe::GemmUse::W2);
     moe::GemmArgs b{};
-    b.tile = w2_tile;
+    b.tile = f.tile;
     b.A = d_ff > 0 ? h : out_rows;
     b.lda = d_ff;
     b.B0 = d_ff > 0 ? w2 : out_rows;
@@ -392,12 +473,16 @@ void expert_ffn(moe_ctx* ctx, const float* x, const int32_t* perm,
     b.E = static_cast<int32_t>(E);
     b.m_tiles = static_cast<int32_t>(grouped_m_tiles(pairs, E, tile.bm));
     b.n_tiles = static_cast<int32_t>(moe::ceil_div(d, tile.bn));
-    if (w2_splits > 1) {
-        b.k_splits = w2_splits;
-        b.k_split_len = moe::ceil_div(moe::ceil_div(d_ff, w2_splits), 16) * 16;
+    if (f.splits > 1) {
+        b.k_splits = f.splits;
+        b.k_split_len = moe::ceil_div(moe::ceil_div(d_ff, f.splits), 16) * 16;
         b.c_split_stride = pairs * d;
     }
-    moe::require(int64_t(b.m_tiles) * b.n_tiles * std::max(w2_splits, 1) <= INT32_MAX,
+    if (f.w2_sk > 0 && d_ff > 0) {
+        b.sk_grid = f.w2_sk;
+        b.sk_part = sk_part;
+    }
+    moe::require(int64_t(b.m_tiles) * b.n_tiles * std::max(f.splits, 1) <= INT32_MAX,
                  "w2 grid too large");
     const bool vec = d_ff % 4 == 0 && aligned16(h) && aligned16(w2);
     ctx->launch("expert_w2", s, [&] { moe::launch_gemm(b, false, true, moe::EPI_STORE, vec, s); });
@@ -430,15 +515,16 @@ struct LayerWs {
     int32_t* inv;
     float* h;
     float* out_rows;
+    float* sk_part;    // stream-K partial tiles of w1/w3 and w2 (FfnPlan::sk_floats)
     float* norm_mean;  // MOE_NORM_LAYER / RMS: per-token statistics
     float* norm_inv;
     float* xnorm;      // MOE_NORM_LAYER / RMS: the normalised x [T, d] the experts read
     size_t bytes;
 };
 
-// w2_splits: the K splits of the layer's w2 (choose_w2_plan); out_rows holds
-// that many partial row buffers.
-LayerWs carve_layer(void* base, const moe_layer_desc& d, int w2_splits) {
+// f: the layer's FFN plan (choose_ffn_plan); out_rows holds f.splits
+// partial row buffers, sk_part the stream-K partial tiles.
+LayerWs carve_layer(void* base, const moe_layer_desc& d, const FfnPlan& f) {
     Carve c(base);
     LayerWs w{};
     const int64_t pairs = d.T * d.k;
@@ -451,7 +537,8 @@ LayerWs carve_layer(void* base, const moe_layer_desc& d, int w2_splits) {
     w.perm = c.take<int32_t>(pairs);
     w.inv = c.take<int32_t>(pairs);
     w.h = c.take<float>(pairs * d.d_ff);
-    w.out_rows = c.take<float>(pairs * d.d * std::max(w2_splits, 1));
+    w.out_rows = c.take<float>(pairs * d.d * std::max(f.splits, 1));
+    w.sk_part = f.sk_floats > 0 ? c.take<float>(f.sk_floats) : nullptr;
     if (d.norm != MOE_NORM_NONE) {
         w.norm_mean = c.take<float>(d.T);
         w.norm_inv = c.take<float>(d.T);
@@ -465,7 +552,7 @@ LayerWs carve_layer(void* base, const moe_layer_desc& d, int w2_splits) {
 // (the context's grow-only workspace, or the no-alloc scratch).
 void layer_forward(moe_ctx* ctx, const moe_layer_desc& D, const moe_layer_weights& weights,
                    const float* x, float* y, int32_t* topk_idx_out, float* topk_w_out,
-                   hipStream_t s, void* base, const W2Plan& plan) {
+                   hipStream_t s, void* base, const FfnPlan& plan) {
     check_ptr(x, "x");
     check_ptr(y, "y");
     check_ptr(weights.gate_w, "gate_w");
@@ -483,7 +570,7 @@ void layer_forward(moe_ctx* ctx, const moe_layer_desc& D, const moe_layer_weight
         if (!rms) check_ptr(weights.norm_b, "norm_b");
     }
     const int splits = plan.splits;
-    LayerWs ws = carve_layer(base, D, splits);
+    LayerWs ws = carve_layer(base, D, plan);
     int32_t* idx = topk_idx_out != nullptr ? topk_idx_out : ws.idx;
     float* w = topk_w_out != nullptr ? topk_w_out : ws.w;
     const int64_t nb = moe::ceil_div(D.T, moe::kPermTokens);
@@ -513,7 +600,7 @@ void layer_forward(moe_ctx* ctx, const moe_layer_desc& D, const moe_layer_weight
         moe::launch_perm_place(idx, D.T, D.k, D.E, ws.counts, ws.perm, ws.inv, s);
     });
     expert_ffn(ctx, xin, ws.perm, ws.offsets, weights.w1, weights.w3, weights.w2, D.act, D.T, D.k,
-               D.d, D.d_ff, D.E, ws.h, ws.out_rows, s, splits, plan.tile);
+               D.d, D.d_ff, D.E, ws.h, ws.out_rows, s, plan, ws.sk_part);
     ctx->launch("combine", s, [&] {
         moe::launch_combine(ws.out_rows, idx, w, ws.inv, D.residual ? x : nullptr, y, D.T, D.k,
                             D.d, D.T * D.k, D.contract, splits, D.T * D.k * D.d, s);
@@ -610,9 +697,17 @@ int moe_ctx_reserve(moe_ctx* ctx, const moe_layer_desc* desc) {
         check_ctx(ctx);
         check_desc(desc);
         DeviceScope dev(ctx->device);
-        const W2Plan plan =
-            choose_w2_plan(ctx, desc->T * desc->k, desc->d, desc->d_ff, desc->E);
-        ctx->workspace(carve_layer(nullptr, *desc, plan.splits).bytes);
+        const FfnPlan plan =
+            choose_ffn_plan(ctx, desc->T * desc->k, desc->d, desc->d_ff, desc->E);
+        ctx->workspace(carve_layer(nullptr, *desc, plan).bytes);
+    });
+}
+
+int moe_ctx_set_stream_k(moe_ctx* ctx, int mode) {
+    return guarded([&] {
+        check_ctx(ctx);
+        moe::require(mode >= -1 && mode <= 1, "stream-K mode must be -1, 0 or 1");
+        ctx->sk_mode = mode;
     });
 }
 
@@ -1105,8 +1200,15 @@ int moe_expert_ffn_grouped(moe_ctx* ctx, const float* x, const int32_t* perm,
         }
         DeviceScope dev(ctx->device);
         hipStream_t s = as_stream(stream);
+        // one K range for w2 (out_rows holds one row per pair); stream-K
+        // where the planner takes it, its partial tiles in the workspace
+        FfnPlan plan = choose_ffn_plan(ctx, T * k, d, d_ff, E);
+        if (plan.splits > 1) plan.splits = 1;
+        float* sk_part = nullptr;
+        if (plan.sk_floats > 0)
+            sk_part = static_cast<float*>(ctx->workspace(size_t(plan.sk_floats) * sizeof(float)));
         expert_ffn(ctx, x, perm, expert_offsets, w1, w3, w2, act, T, k, d, d_ff, E, h, out_rows,
-                   s);
+                   s, plan, sk_part);
     });
 }
 
@@ -1147,8 +1249,9 @@ int moe_layer_forward(moe_ctx* ctx, const moe_layer_desc* desc,
         check_ptr(weights, "weights");
         if (desc->T == 0) return;
         DeviceScope dev(ctx->device);
-        const W2Plan plan = choose_w2_plan(ctx, desc->T * desc->k, desc->d, desc->d_ff, desc->E);
-        void* base = ctx->workspace(carve_layer(nullptr, *desc, plan.splits).bytes);
+        const FfnPlan plan =
+            choose_ffn_plan(ctx, desc->T * desc->k, desc->d, desc->d_ff, desc->E);
+        void* base = ctx->workspace(carve_layer(nullptr, *desc, plan).bytes);
         layer_forward(ctx, *desc, *weights, x, y, topk_idx_out, topk_w_out, as_stream(stream),
                       base, plan);
     });
@@ -1164,8 +1267,9 @@ int moe_layer_forward_noalloc(moe_ctx* ctx, const moe_layer_desc* desc,
         if (desc->T == 0) return;
         moe::require(ctx->scratch != nullptr, "no-alloc scratch not bound to this context");
         DeviceScope dev(ctx->device);
-        const W2Plan plan = choose_w2_plan(ctx, desc->T * desc->k, desc->d, desc->d_ff, desc->E);
-        const size_t need = carve_layer(nullptr, *desc, plan.splits).bytes;
+        const FfnPlan plan =
+            choose_ffn_plan(ctx, desc->T * desc->k, desc->d, desc->d_ff, desc->E);
+        const size_t need = carve_layer(nullptr, *desc, plan).bytes;
         if (need > kNoAllocScratchBytes)
             throw moe::InvalidArg("moe_layer_forward_noalloc: this layer needs " +
                                   std::to_string(need) + " bytes of scratch, more than the " +
@@ -1185,7 +1289,7 @@ int moe_layer_w2_splits(moe_ctx* ctx, const moe_layer_desc* desc, int32_t* split
         check_desc(desc);
         check_ptr(splits, "splits");
         DeviceScope dev(ctx->device);
-        *splits = choose_w2_plan(ctx, desc->T * desc->k, desc->d, desc->d_ff, desc->E).splits;
+        *splits = choose_ffn_plan(ctx, desc->T * desc->k, desc->d, desc->d_ff, desc->E).splits;
     });
 }
 

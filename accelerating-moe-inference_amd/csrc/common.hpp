@@ -55,6 +55,11 @@ struct GemmTile {
 GemmTile gemm_tile(GemmUse use);
 // Workgroups of the grouped kernel of `use` one CU holds at once.
 int gemm_blocks_per_cu(GemmUse use);
+// ... of its stream-K kernel (GemmArgs::sk_grid > 0).
+int gemm_sk_blocks_per_cu(GemmUse use);
+// Floats of GemmArgs::sk_part a stream-K launch of `use` on `grid`
+// workgroups needs.
+int64_t gemm_sk_part_floats(GemmUse use, int grid);
 constexpr int kMaxW2Splits = 4;  // split-K of the layer's w2 (partials summed by the combine)
 
 // Dense SGEMM tile shapes, GemmArgs::tile: 0 = 128x128 (any shape), 1 =
@@ -110,6 +115,11 @@ struct GemmArgs {
     // tile's rows -- the probabilities outside it are zero.
     int32_t causal;
     int32_t window;
+    // Stream-K grouped launch (sk_grid > 0): sk_grid workgroups share the
+    // tiles' K steps evenly; sk_part holds 2 * sk_grid partial tiles of
+    // NB * BM * BN floats for the tiles their range boundaries cut.
+    int32_t sk_grid;
+    float* sk_part;
 };
 
 enum Causal : int { CAUSAL_NONE = 0, CAUSAL_SCORES = 1, CAUSAL_PV = 2 };
@@ -201,6 +211,9 @@ struct moe_ctx {
     int cus = 0;               // compute units of the device
     int w2_blocks_per_cu = 0;  // occupancy of the grouped w2 kernel (lazily queried)
     int w2n_blocks_per_cu = 0;  // ... of its 128x128-tile variant
+    int w13_blocks_per_cu[2] = {};  // ... of the w1/w3 kernel, per tile (GemmArgs::tile)
+    int sk_blocks_per_cu[5] = {};   // ... of the stream-K kernels, per GemmUse
+    int sk_mode = -1;  // moe_ctx_set_stream_k: -1 planner (or MOE_SK), 0 off, 1 on
     int dense_blocks_per_cu[2][moe::kDenseTiles] = {};  // [nn][tile], lazily queried
     void* ws = nullptr;
     size_t ws_bytes = 0;

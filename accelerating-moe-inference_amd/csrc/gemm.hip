@@ -566,8 +566,66 @@ struct NnB {
     }
 };
 
-template <class C, int SCHED, bool NN, bool GROUPED, int NB, int EPI>
-__global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmArgs p) {
+// Grouped GEMMs: rows [row0, row0 + rows) of m-tile `mt` and its expert e.
+// False for a surplus tile of the worst-case grid (or inconsistent offsets).
+template <int BM>
+__device__ __forceinline__ bool grouped_tile_rows(const GemmArgs& p, int mt, int& e,
+                                                  int64_t& row0, int& rows) {
+    int first;
+    if (!find_expert<BM>(p.offsets, p.E, mt, e, first)) return false;
+    int64_t e_end = p.offsets[e + 1];
+    e_end = e_end < p.rows_limit ? e_end : p.rows_limit;
+    row0 = p.offsets[e] + static_cast<int64_t>(mt - first) * BM;
+    if (row0 < 0 || row0 >= e_end) return false;
+    rows = static_cast<int>(e_end - row0 < BM ? e_end - row0 : BM);
+    return true;
+}
+
+// The epilogue of one output tile: every accumulator of this lane that lies
+// inside [rows, N) goes through epi_store.  32x32 accumulator layout: lane l,
+// register r holds row 8*(r/4) + 4*(l/32) + r%4, column l%32 of its block.
+template <class C, int NB, int EPI>
+__device__ __forceinline__ void store_tile(const GemmArgs& p, float* Cb, int split, int64_t row0,
+                                           int rows, int64_t n0,
+                                           const f32x16 (&acc)[NB][C::FM][C::FN], int tid) {
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave % C::WM, wn = wave / C::WM;
+    const int lr = lane & 31, lh = lane >> 5;
+    const int arow0 = wm * (C::BM / C::WM), bcol0 = wn * (C::BN / C::WN);
+#pragma unroll
+    for (int bi = 0; bi < C::FM; ++bi)
+#pragma unroll
+        for (int bj = 0; bj < C::FN; ++bj)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int i = arow0 + bi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                const int64_t n = n0 + bcol0 + bj * 32 + lr;
+                if (i < rows && n < p.N)
+                    epi_store<EPI>(p, Cb, split, row0 + i, n, acc[0][bi][bj][r],
+                                   acc[NB - 1][bi][bj][r]);
+            }
+}
+
+// Stream-K partial tiles: the accumulators of one K segment of a tile, stored
+// lane by lane (16 bytes per lane and instruction, coalesced) in slot `part`
+// of NB * BM * BN floats; the fix-up kernel reads them back in the same
+// order with the same lanes.
+template <class C, int NB>
+__device__ __forceinline__ int sk_part_index(int nb, int bi, int bj, int r4, int tid) {
+    return (((nb * C::FM + bi) * C::FN + bj) * 4 + r4) * C::THREADS + tid;
+}
+
+// One output tile (mt, nt) of the direct-load GEMM, over K split `split`
+// or, with seg_lo >= 0, over K steps [seg_lo, seg_hi) of it (a stream-K
+// segment).  part == nullptr: the epilogue writes the tile; otherwise the
+// raw accumulators go to the partial slot `part`.  LOOPED: called once per
+// segment in a loop; the lane index is then hidden from the optimiser, so
+// the per-lane LDS and store addresses are recomputed in each segment
+// instead of being hoisted out of the loop and held in registers across it
+// (they cost 60-90 more VGPRs, past the budget of two workgroups per CU).
+template <class C, int SCHED, bool NN, bool GROUPED, int NB, int EPI, bool LOOPED = false>
+__device__ __forceinline__ void direct_tile(const GemmArgs& p, int mt, int nt, int split,
+                                            int64_t seg_lo, int64_t seg_hi, float* part) {
     constexpr int BM = C::BM, BN = C::BN, BK = C::BK;
     constexpr int FM = C::FM, FN = C::FN;
     constexpr int NW = C::THREADS / 64;
@@ -591,10 +649,9 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
     __shared__ __align__(16) float As[2][BM * BK];
     __shared__ __align__(16) float Bs[2][NB][B_SIZE];
 
-    const int tid = threadIdx.x;
+    int tid = threadIdx.x;
+    if constexpr (LOOPED) asm volatile("" : "+v"(tid));
     const int lane = tid & 63, wave = tid >> 6;
-    int mt, nt, split;  // split: K range of this tile (split-K)
-    if (!launch_tile<BM, GROUPED>(p, mt, nt, split)) return;  // surplus workgroup
 
     int64_t row0;
     int rows;
@@ -602,13 +659,9 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
     const float* Ab = p.A;
     float* Cb = p.C;
     if (GROUPED) {
-        int e, first;
-        if (!find_expert<BM>(p.offsets, p.E, mt, e, first)) return;  // surplus tile
-        int64_t e_end = p.offsets[e + 1];
-        e_end = e_end < p.rows_limit ? e_end : p.rows_limit;
-        row0 = p.offsets[e] + static_cast<int64_t>(mt - first) * BM;
-        if (row0 < 0 || row0 >= e_end) return;  // only reachable with inconsistent offsets
-        rows = static_cast<int>(e_end - row0 < BM ? e_end - row0 : BM);
+        int e;
+        // surplus tile, or (only with inconsistent offsets) no rows
+        if (!grouped_tile_rows<BM>(p, mt, e, row0, rows)) return;
         B[0] = p.B0 + e * p.b_expert_stride;
         if (NB == 2) B[NB - 1] = p.B1 + e * p.b_expert_stride;
     } else {
@@ -629,6 +682,11 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
     // K columns [kbeg, K) of this split; loads are bounded by K
     int64_t kbeg = split * p.k_split_len;
     int64_t K = p.K - kbeg < p.k_split_len ? p.K : kbeg + p.k_split_len;
+    if (seg_lo >= 0) {
+        // a stream-K segment: K steps [seg_lo, seg_hi) of the split
+        K = kbeg + seg_hi * BK;
+        kbeg += seg_lo * BK;
+    }
     if (!GROUPED && p.causal == CAUSAL_SCORES) {
         // keys n0.. all after the last query row, or (window) all too old for
         // the first: nothing of this tile is ever read
@@ -971,18 +1029,170 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmAr
             }
         return;
     }
+    if (part != nullptr) {
+        f32x4* dst = reinterpret_cast<f32x4*>(part);
 #pragma unroll
-    for (int bi = 0; bi < FM; ++bi)
+        for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-        for (int bj = 0; bj < FN; ++bj)
+            for (int bi = 0; bi < FM; ++bi)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int i = arow0 + bi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                const int64_t n = n0 + bcol0 + bj * 32 + lr;
-                if (i < rows && n < N)
-                    epi_store<EPI>(p, Cb, split, row0 + i, n, acc[0][bi][bj][r],
-                                   acc[NB - 1][bi][bj][r]);
-            }
+                for (int bj = 0; bj < FN; ++bj)
+#pragma unroll
+                    for (int r4 = 0; r4 < 4; ++r4)
+                        dst[sk_part_index<C, NB>(nb, bi, bj, r4, tid)] =
+                            f32x4{acc[nb][bi][bj][4 * r4], acc[nb][bi][bj][4 * r4 + 1],
+                                  acc[nb][bi][bj][4 * r4 + 2], acc[nb][bi][bj][4 * r4 + 3]};
+        return;
+    }
+    store_tile<C, NB, EPI>(p, Cb, split, row0, rows, n0, acc, tid);
+}
+
+template <class C, int SCHED, bool NN, bool GROUPED, int NB, int EPI>
+__global__ __launch_bounds__(C::THREADS, 2) void gemm_direct_kernel(const GemmArgs p) {
+    int mt, nt, split;  // split: K range of this tile (split-K)
+    if (!launch_tile<C::BM, GROUPED>(p, mt, nt, split)) return;  // surplus workgroup
+    direct_tile<C, SCHED, NN, GROUPED, NB, EPI>(p, mt, nt, split, -1, -1, nullptr);
+}
+
+// ---------------------------------------------------------------------------
+// Stream-K grouped GEMM.  The grid holds as many workgroups G as the GPU
+// runs at once.  The real tiles of the launch (counted from the offsets), in
+// raster order, first go out whole, G at a time, for as many full rounds as
+// they fill (tiles / G); the tiles left over, fewer than G, are laid end to
+// end, K steps within a tile, and their I = tiles x K-steps iterations are
+// dealt in contiguous ranges, q = I / G to each logical workgroup and one
+// more to the first I % G: every workgroup does the same number of K steps
+// (within one), so the launch has no partly filled last round of whole
+// tiles.  (Dealing every tile that way puts the workgroups of an XCD at
+// unrelated K offsets, so tiles that share an operand panel no longer read
+// it from L2 together: measured 7-10 % slower per K step.)  A tile that lies
+// within one workgroup's range is written by its epilogue as usual; a tile
+// cut by range boundaries leaves one partial accumulator set per piece, the
+// piece at the start of a workgroup's range in slot 2w, the piece at its end
+// in slot 2w + 1, and the fix-up kernel (a second launch on the same stream)
+// adds the pieces in K order and runs the epilogue.  No workgroup waits for
+// another.  Logical workgroups are dealt to the XCDs in contiguous runs, so
+// each XCD works through a contiguous run of tiles.
+struct SkSched {
+    int m_tiles, tiles, group, nk;
+    int rounds;  // whole-tile rounds before the stream-K part: tiles / G
+    int base;    // first iteration of the stream-K part: rounds * G * nk
+    int q, r;    // its iterations per workgroup: q + 1 for the first r workgroups, q after
+};
+
+// The schedule of a stream-K launch on G workgroups (every count fits 31
+// bits: the host checks tiles x K steps).
+template <int BM, int BK>
+__device__ __forceinline__ SkSched sk_sched(const GemmArgs& p, int G) {
+    SkSched s;
+    const int real = grouped_real_m_tiles<BM>(p.offsets, p.E);
+    s.m_tiles = real < p.m_tiles ? real : p.m_tiles;
+    s.tiles = s.m_tiles * p.n_tiles;
+    s.group = p.group_m < s.m_tiles ? p.group_m : s.m_tiles;
+    s.nk = static_cast<int>(p.K / BK);
+    s.rounds = s.tiles / G;
+    s.base = s.rounds * G * s.nk;
+    const int iters = (s.tiles - s.rounds * G) * s.nk;
+    s.q = iters / G;
+    s.r = iters - s.q * G;
+    return s;
+}
+
+// First iteration of logical workgroup w in the stream-K part (w = G: the
+// end of the launch).
+__device__ __forceinline__ int sk_begin(const SkSched& s, int w) {
+    return s.base + w * s.q + (w < s.r ? w : s.r);
+}
+
+template <class C, int SCHED, int NB, int EPI>
+__global__ __launch_bounds__(C::THREADS, 2) void gemm_sk_kernel(const GemmArgs p) {
+    const int G = static_cast<int>(gridDim.x);
+    const SkSched s = sk_sched<C::BM, C::BK>(p, G);
+    const int w = xcd_remap(blockIdx.x, G);
+    // whole tiles first, round by round (the workgroups of an XCD run a
+    // contiguous run of tiles in step, as the one-tile kernel does), then
+    // this workgroup's range of the rest; one call site, so the tile code is
+    // inlined once
+    const int beg = sk_begin(s, w), end = sk_begin(s, w + 1);
+    constexpr int64_t SLOT = int64_t(NB) * C::BM * C::BN;
+    int round = 0, it = beg;
+    for (;;) {
+        int t, ks, ke;
+        float* part = nullptr;
+        if (round < s.rounds) {
+            t = round * G + w;
+            ks = 0;
+            ke = s.nk;
+            ++round;
+        } else if (it < end) {
+            t = it / s.nk;
+            ks = it - t * s.nk;
+            ke = s.nk - ks < end - it ? s.nk : ks + (end - it);
+            if (ks != 0 || ke != s.nk)
+                part = p.sk_part + (2 * int64_t(w) + (it == beg ? 0 : 1)) * SLOT;
+            it += ke - ks;
+        } else {
+            break;
+        }
+        int mt, nt;
+        tile_of(t, s.m_tiles, p.n_tiles, s.group, mt, nt);
+        direct_tile<C, SCHED, false, true, NB, EPI, true>(p, mt, nt, 0, ks, ke, part);
+    }
+}
+
+// The fix-up of the stream-K launch with the same arguments: block b looks
+// at the boundary between logical workgroups b and b + 1.  When it cuts a
+// tile and workgroup b's range holds that tile's first K step (so no earlier
+// boundary cuts it), the block adds the tile's pieces in K order -- the
+// piece of workgroup b, then those of b + 1, b + 2, ... up to the tile's
+// end -- and writes the tile through the epilogue.
+template <class C, int NB, int EPI>
+__global__ __launch_bounds__(C::THREADS, 2) void gemm_sk_fixup_kernel(const GemmArgs p) {
+    const int G = p.sk_grid;
+    const SkSched s = sk_sched<C::BM, C::BK>(p, G);
+    const int w = static_cast<int>(blockIdx.x) + 1;
+    const int b = sk_begin(s, w);
+    if (b >= sk_begin(s, G)) return;
+    const int t = b / s.nk, t0 = t * s.nk, t1 = t0 + s.nk;
+    if (b == t0) return;                       // the boundary falls between tiles
+    const int prev = sk_begin(s, w - 1);
+    if (prev > t0) return;                     // an earlier boundary cuts this tile
+    constexpr int64_t SLOT = int64_t(NB) * C::BM * C::BN;
+    constexpr int FM = C::FM, FN = C::FN;
+    const int tid = threadIdx.x;
+    f32x16 acc[NB][FM][FN];
+    auto add_slot = [&](int64_t slot, bool first) {
+        const f32x4* src = reinterpret_cast<const f32x4*>(p.sk_part + slot * SLOT);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int bi = 0; bi < FM; ++bi)
+#pragma unroll
+                for (int bj = 0; bj < FN; ++bj)
+#pragma unroll
+                    for (int r4 = 0; r4 < 4; ++r4) {
+                        const f32x4 v = src[sk_part_index<C, NB>(nb, bi, bj, r4, tid)];
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            acc[nb][bi][bj][4 * r4 + j] =
+                                first ? v[j] : acc[nb][bi][bj][4 * r4 + j] + v[j];
+                    }
+    };
+    // workgroup w - 1 holds the tile's first piece: in its start slot when
+    // its range begins at the tile's start, else in its end slot
+    add_slot(2 * int64_t(w - 1) + (prev == t0 ? 0 : 1), true);
+    for (int u = w; u < G; ++u) {
+        const int bu = sk_begin(s, u);
+        if (bu >= t1) break;
+        if (sk_begin(s, u + 1) == bu) continue;  // an empty range
+        add_slot(2 * int64_t(u), false);
+    }
+    int mt, nt;
+    tile_of(t, s.m_tiles, p.n_tiles, s.group, mt, nt);
+    int e, rows;
+    int64_t row0;
+    if (!grouped_tile_rows<C::BM>(p, mt, e, row0, rows)) return;
+    store_tile<C, NB, EPI>(p, p.C, 0, row0, rows, static_cast<int64_t>(nt) * C::BN, acc, tid);
 }
 
 // Whether every byte offset of a SCHED_BUFLDS launch (lane offset from the
@@ -1027,6 +1237,26 @@ void launch_cfg(const GemmArgs& a, bool vec, hipStream_t s) {
     } else {
         throw Unsupported("GEMM tile shape needs aligned rows and K % 16 == 0");
     }
+}
+
+// The stream-K launch of a grouped GEMM and its fix-up (grid sk_grid - 1:
+// one block per range boundary).  It needs the direct buffer-load path:
+// where that does not apply (unaligned rows, K % 16 != 0, operands past
+// 2 GiB), the one-tile-per-workgroup launch runs instead.
+template <class C, int SCHED, int NB, int EPI>
+void launch_sk(const GemmArgs& a, bool vec, hipStream_t s) {
+    static_assert((SCHED & SCHED_BUFLDS) != 0 && (SCHED & SCHED_DIRECT) != 0, "stream-K path");
+    if (!vec || a.K % 16 != 0 || !buf_offsets_fit(a, C::BM, C::BN, false, true)) {
+        GemmArgs d = a;
+        d.sk_grid = 0;
+        launch_cfg<C, SCHED, false, true, NB, EPI>(d, vec, s);
+        return;
+    }
+    hipLaunchKernelGGL((gemm_sk_kernel<C, SCHED, NB, EPI>), dim3(a.sk_grid), dim3(C::THREADS), 0,
+                       s, a);
+    if (a.sk_grid > 1)
+        hipLaunchKernelGGL((gemm_sk_fixup_kernel<C, NB, EPI>), dim3(a.sk_grid - 1),
+                           dim3(C::THREADS), 0, s, a);
 }
 
 using DenseCfg = CfgOf<MOE_DENSE_CFG>::T;
@@ -1134,6 +1364,10 @@ int gemm_blocks_per_cu(GemmUse use) {
                 query(gemm_kernel<W2Cfg, MOE_W2_SCHED, false, true, true, 1, EPI_STORE>,
                       W2Cfg::THREADS);
             break;
+        case GemmUse::W13Tall:
+            query(gemm_direct_kernel<W13TallCfg, MOE_W13_SCHED, false, true, 2, EPI_SWIGLU>,
+                  W13TallCfg::THREADS);
+            break;
         default:
             if constexpr ((MOE_W13_SCHED & SCHED_DIRECT) != 0 && W13Cfg::BK == 16)
                 query(gemm_direct_kernel<W13Cfg, MOE_W13_SCHED, false, true, 2, EPI_SWIGLU>,
@@ -1145,6 +1379,40 @@ int gemm_blocks_per_cu(GemmUse use) {
     }
     hip_check(e, "hipOccupancyMaxActiveBlocksPerMultiprocessor");
     return n > 0 ? n : 1;
+}
+
+int gemm_sk_blocks_per_cu(GemmUse use) {
+    int n = 0;
+    hipError_t e = hipSuccess;
+    auto query = [&](auto kernel, int threads) {
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, 0);
+    };
+    switch (use) {
+        case GemmUse::W2Narrow:
+            query(gemm_sk_kernel<W2NarrowCfg, MOE_W2_SCHED | SCHED_DIRECT, 1, EPI_STORE>,
+                  W2NarrowCfg::THREADS);
+            break;
+        case GemmUse::W2:
+            query(gemm_sk_kernel<W2Cfg, MOE_W2_SCHED | SCHED_DIRECT, 1, EPI_STORE>,
+                  W2Cfg::THREADS);
+            break;
+        case GemmUse::W13Tall:
+            query(gemm_sk_kernel<W13TallCfg, MOE_W13_SCHED | SCHED_DIRECT, 2, EPI_SWIGLU>,
+                  W13TallCfg::THREADS);
+            break;
+        default:
+            query(gemm_sk_kernel<W13Cfg, MOE_W13_SCHED | SCHED_DIRECT, 2, EPI_SWIGLU>,
+                  W13Cfg::THREADS);
+            break;
+    }
+    hip_check(e, "hipOccupancyMaxActiveBlocksPerMultiprocessor");
+    return n > 0 ? n : 1;
+}
+
+int64_t gemm_sk_part_floats(GemmUse use, int grid) {
+    const GemmTile t = gemm_tile(use);
+    const int nb = (use == GemmUse::W13 || use == GemmUse::W13Tall) ? 2 : 1;
+    return 2 * int64_t(grid) * nb * t.bm * t.bn;
 }
 
 GemmTile gemm_tile(GemmUse use) {
@@ -1200,6 +1468,26 @@ void launch_gemm(const GemmArgs& args, bool nn, bool grouped, int epi, bool vec,
         return;
     }
     if (nn) throw Unsupported("grouped NN GEMM");
+    if (a.sk_grid > 0) {
+        // stream-K: the host checked the direct path's requirements
+        if (a.k_splits != 1 || a.sk_part == nullptr) throw Unsupported("stream-K arguments");
+        switch (epi) {
+            case EPI_SWIGLU:
+                if (a.tile == 1) launch_sk<W13TallCfg, MOE_W13_SCHED | SCHED_DIRECT, 2, EPI_SWIGLU>(a, vec, s);
+                else launch_sk<W13Cfg, MOE_W13_SCHED | SCHED_DIRECT, 2, EPI_SWIGLU>(a, vec, s);
+                break;
+            case EPI_SILU:
+                if (a.tile == 1) launch_sk<W13TallCfg, MOE_W13_SCHED | SCHED_DIRECT, 1, EPI_SILU>(a, vec, s);
+                else launch_sk<W13Cfg, MOE_W13_SCHED | SCHED_DIRECT, 1, EPI_SILU>(a, vec, s);
+                break;
+            case EPI_STORE:
+                if (a.tile == 1) launch_sk<W2NarrowCfg, MOE_W2_SCHED | SCHED_DIRECT, 1, EPI_STORE>(a, vec, s);
+                else launch_sk<W2Cfg, MOE_W2_SCHED | SCHED_DIRECT, 1, EPI_STORE>(a, vec, s);
+                break;
+            default: throw Unsupported("grouped GEMM epilogue");
+        }
+        return;
+    }
     switch (epi) {
         case EPI_SWIGLU:
             if (a.tile == 1)

@@ -595,6 +595,8 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
+    ap.add_argument("--tokens", type=int, default=None,
+                    help="tokens of the layer forward (default: the configuration's)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="target CPU time of the cpu_baseline sample (0 = skip)")
     ap.add_argument("--sgemm", action="store_true",
@@ -636,6 +638,8 @@ def main():
 
     cfg = CONFIGS[args.config]
     T, d, E, k, d_ff = cfg["T"], cfg["d"], cfg["E"], cfg["k"], cfg["d_ff"]
+    if args.tokens is not None:
+        T = args.tokens  # a batch-size point of the configuration's layer shape
     pkg = load_pkg()
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(0)

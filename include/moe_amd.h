@@ -301,9 +301,10 @@ int moe_layer_forward(moe_ctx* ctx, const moe_layer_desc* desc,
  * reference: for callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
  * layer's workspace (logits, routing, permutation, hidden rows, w2 partials,
- * norm statistics) lives in a fixed 64 MiB array the library holds on every
- * GPU it runs on, until the process ends; a layer needing more (about 1,200
- * tokens at config 5's shape, 1,800 at the reference's) is rejected with
+ * norm statistics, stream-K partial tiles) lives in a fixed 256 MiB array the
+ * library holds on every GPU it runs on, until the process ends; a layer
+ * needing more (beyond about 4,800 tokens at config 5's shape, 3,600 at the
+ * reference's, 2,500 there behind its layer norm) is rejected with
  * MOE_ERR_INVALID.  The call allocates nothing and records no timing events.
  * Every call on one GPU shares that GPU's array, which keeps the last call's
  * contents: calls that overlap on one GPU (two streams, two threads, two
@@ -313,6 +314,16 @@ int moe_layer_forward_noalloc(moe_ctx* ctx, const moe_layer_desc* desc,
                               const moe_layer_weights* weights, const float* x,
                               float* y, int32_t* topk_idx_out, float* topk_w_out,
                               void* stream);
+
+/* ---- how the grouped expert GEMMs deal their tiles on this context: mode
+ * -1 (the default) lets the planner choose per launch, 0 always runs one
+ * tile per workgroup, 1 always runs stream-K (every workgroup the same
+ * number of K steps, tiles cut at range boundaries joined by a fix-up
+ * launch) wherever the direct-load path applies.  Results of the two differ
+ * only in the rounding of the cut tiles' K sums.  No reference counterpart:
+ * a tuning and testing control (the environment variable MOE_SK = 0 / 1
+ * sets the process default). */
+int moe_ctx_set_stream_k(moe_ctx* ctx, int mode);
 
 /* ---- the number of K splits moe_layer_forward(desc) runs its w2 GEMM with
  * on this context's device (its combine then reads that many partial row

@@ -37,6 +37,16 @@ def ctx(pkg, torch):
     c.close()
 
 
+@pytest.fixture
+def request_reset_stream_k():
+    """Calling it with a context puts that context back to the planner's
+    stream-K choice when the test ends."""
+    held = []
+    yield held.append
+    for c in held:
+        c.set_stream_k(-1)
+
+
 def dev(torch, a):
     return torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
 
@@ -358,8 +368,15 @@ def _ffn_case(rng, T, d, E, k, d_ff, act, skew=False):
     (400, 64, 100, 4, 64, 0, True),
     (100, 32, 8, 2, 64, 0, False),
 ])
-def test_expert_ffn_vs_oracle(ctx, torch, orc, T, d, E, k, d_ff, act, skew):
-    print(f"ffn T={T} d={d} E={E} k={k} d_ff={d_ff} act={act}", flush=True)
+@pytest.mark.parametrize("sk", [0, 1])
+def test_expert_ffn_vs_oracle(ctx, torch, orc, request_reset_stream_k, T, d, E, k, d_ff, act,
+                              skew, sk):
+    """Both ways of dealing the grouped GEMMs' tiles: one tile per workgroup
+    (sk 0) and stream-K with its fix-up of the cut tiles (sk 1; shapes whose
+    K is not a multiple of 16 fall back to one tile per workgroup)."""
+    print(f"ffn T={T} d={d} E={E} k={k} d_ff={d_ff} act={act} sk={sk}", flush=True)
+    ctx.set_stream_k(sk)
+    request_reset_stream_k(ctx)
     rng = np.random.default_rng(T + d + E + d_ff)
     x, w1, w3, w2, topk = _ffn_case(rng, T, d, E, k, d_ff, act, skew)
     roff, rperm, rinv = orc.permute(topk, E)
@@ -450,10 +467,13 @@ def test_layer_config1(ctx, pkg, torch, orc):
     assert_close(host(y), ry, what="config1 y")
 
 
-@pytest.mark.parametrize("contract", [0, 1])
-def test_layer_phi_router_swiglu(ctx, pkg, torch, orc, contract):
+@pytest.mark.parametrize("contract,sk", [(0, -1), (1, -1), (1, 0), (1, 1)])
+def test_layer_phi_router_swiglu(ctx, pkg, torch, orc, request_reset_stream_k, contract, sk):
     """The reference's own layer semantics: quantised top-2 with 0.5/0.5
-    weights and SwiGLU experts (src/layer.cu:32-103), 16 experts."""
+    weights and SwiGLU experts (src/layer.cu:32-103), 16 experts; under the
+    planner's tile dealing (sk -1) and both forced ones."""
+    ctx.set_stream_k(sk)
+    request_reset_stream_k(ctx)
     rng = np.random.default_rng(5)
     T, d, E, k, d_ff = 300, 256, 16, 2, 448
     x = normal(rng, (T, d))
@@ -532,6 +552,16 @@ def test_layer_skewed_config4_full_size(ctx, pkg, torch, orc):
     counts = _big_layer(ctx, pkg, torch, orc, 16384, 2048, 64, 8, 1408, mode=1,
                         bias=zipf_bias(64), seed=4)
     assert counts.max() > 4 * counts.mean()  # heavily imbalanced loads
+
+
+@pytest.mark.parametrize("T", [64, 1000])
+def test_layer_reference_shape_small_batches(ctx, pkg, torch, orc, T):
+    """The reference's layer shape at small batches, where the planner deals
+    w1/w3 stream-K (64 tokens: a grid cut to keep pieces of 32 K steps;
+    1000 tokens: every slot): routing of every token and the outputs of a
+    tile-covering sample against the oracle."""
+    ctx.set_stream_k(-1)
+    _big_layer(ctx, pkg, torch, orc, T, 4096, 16, 2, 448, mode=0, bias=None, seed=60 + T)
 
 
 def test_layer_reference_shape_full_size(ctx, pkg, torch, orc):
