@@ -91,9 +91,16 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 // only, so the fragment reads of a K step get partial waits.
 // SCHED_RING3 (direct path, with SCHED_BUFLDS) keeps three LDS stages, one
 // __shared__ array each, and loads two K steps ahead: the wait before each
-// barrier leaves the newest stage's loads in flight.
+// barrier leaves the newest stage's loads in flight (SCHED_RING(n): n
+// stages, n - 1 steps ahead).
 constexpr int SCHED_PRIO = 1, SCHED_MIDSTORE = 2, SCHED_DIRECT = 4, SCHED_QSPLIT = 8,
               SCHED_BUFLDS = 16, SCHED_RING3 = 32;
+// With SCHED_RING3, bits 8-11 may give the ring a depth other than three
+// (4-8 stages, loads that many steps minus one ahead): SCHED_RING(n).
+constexpr int SCHED_RING(int n) { return SCHED_RING3 | (n << 8); }
+constexpr int ring_stages(int sched) {
+    return (sched & SCHED_RING3) == 0 ? 0 : (((sched >> 8) & 15) != 0 ? (sched >> 8) & 15 : 3);
+}
 
 template <int BM_, int BN_, int BK_, int WM_, int WN_>
 struct Cfg {
@@ -584,26 +591,34 @@ __device__ __forceinline__ bool grouped_tile_rows(const GemmArgs& p, int mt, int
 // The epilogue of one output tile: every accumulator of this lane that lies
 // inside [rows, N) goes through epi_store.  32x32 accumulator layout: lane l,
 // register r holds row 8*(r/4) + 4*(l/32) + r%4, column l%32 of its block.
-template <class C, int NB, int EPI>
-__device__ __forceinline__ void store_tile(const GemmArgs& p, float* Cb, int split, int64_t row0,
-                                           int rows, int64_t n0,
-                                           const f32x16 (&acc)[NB][C::FM][C::FN], int tid) {
+// One 32x32 block (bi, bj) of this lane's accumulators, a0 and a1 its
+// values for the first and the last B operand.
+template <class C, int EPI>
+__device__ __forceinline__ void store_block(const GemmArgs& p, float* Cb, int split, int64_t row0,
+                                            int rows, int64_t n0, int bi, int bj, const f32x16& a0,
+                                            const f32x16& a1, int tid) {
     const int lane = tid & 63, wave = tid >> 6;
     const int wm = wave % C::WM, wn = wave / C::WM;
     const int lr = lane & 31, lh = lane >> 5;
     const int arow0 = wm * (C::BM / C::WM), bcol0 = wn * (C::BN / C::WN);
 #pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int i = arow0 + bi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+        const int64_t n = n0 + bcol0 + bj * 32 + lr;
+        if (i < rows && n < p.N) epi_store<EPI>(p, Cb, split, row0 + i, n, a0[r], a1[r]);
+    }
+}
+
+template <class C, int NB, int EPI>
+__device__ __forceinline__ void store_tile(const GemmArgs& p, float* Cb, int split, int64_t row0,
+                                           int rows, int64_t n0,
+                                           const f32x16 (&acc)[NB][C::FM][C::FN], int tid) {
+#pragma unroll
     for (int bi = 0; bi < C::FM; ++bi)
 #pragma unroll
         for (int bj = 0; bj < C::FN; ++bj)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int i = arow0 + bi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                const int64_t n = n0 + bcol0 + bj * 32 + lr;
-                if (i < rows && n < p.N)
-                    epi_store<EPI>(p, Cb, split, row0 + i, n, acc[0][bi][bj][r],
-                                   acc[NB - 1][bi][bj][r]);
-            }
+            store_block<C, EPI>(p, Cb, split, row0, rows, n0, bi, bj, acc[0][bi][bj],
+                                acc[NB - 1][bi][bj], tid);
 }
 
 // Stream-K partial tiles: the accumulators of one K segment of a tile, stored
@@ -915,13 +930,9 @@ __device__ __forceinline__ void direct_tile(const GemmArgs& p, int mt, int nt, i
     };
 
     if constexpr ((SCHED & SCHED_RING3) != 0) {
-        // Three stages, one __shared__ array each (the compiler then waits
-        // only for the loads landing in the stage it reads), the K loop
-        // unrolled by three so every step names its arrays.  Step kt reads
-        // stage kt % 3, issues the loads of step kt + 2 into the stage step
-        // kt - 1 read (every wave passed the barrier after reading it), runs
-        // its burst, and before the barrier waits for step kt + 1's loads:
-        // only step kt + 2's, LPS per wave, may still be in flight.
+        // RS stages (three by default), one __shared__ array each (the
+        // compiler then waits only for the loads landing in the stage it
+        // reads), the K loop unrolled by RS so every step names its arrays.
         static_assert((SCHED & SCHED_BUFLDS) != 0, "the ring uses buffer loads");
         // this wave's loads per stage (tiles with fewer load instructions
         // than waves leave some waves without an A or B load)
@@ -932,56 +943,74 @@ __device__ __forceinline__ void direct_tile(const GemmArgs& p, int mt, int nt, i
         for (int j = 0; j < B_INS; ++j)
             lps += NB * (B_INS * NW == B_TOT || wave * B_INS + j < B_TOT);
         constexpr int LPS_MAX = A_INS + NB * B_INS;
-        static_assert(LPS_MAX <= 63, "vmcnt range");
-        // s_waitcnt vmcnt(lps): the count is wave-uniform, the wait needs an
-        // immediate, so dispatch over the possible values
-        auto wait_lps = [&]() {
-            static_for_int(std::make_integer_sequence<int, LPS_MAX + 1>{}, [&](auto v) {
-                constexpr int V = decltype(v)::value;
-                if (lps == V) __builtin_amdgcn_s_waitcnt(0x3f70 | (V & 15) | ((V >> 4) << 14));
-            });
-        };
-        __shared__ __align__(16) float RA0[BM * BK], RA1[BM * BK], RA2[BM * BK];
-        __shared__ __align__(16) float RB0[NB * B_SIZE], RB1[NB * B_SIZE], RB2[NB * B_SIZE];
+        // RS stage arrays (unused ones shrink to one float)
+        constexpr int RS = ring_stages(SCHED);
+        static_assert(RS >= 3 && RS <= 8, "ring stages");
+        static_assert((RS - 2) * LPS_MAX <= 63, "vmcnt range");
+        constexpr int SA = BM * BK, SB = NB * B_SIZE;
+        __shared__ __align__(16) float RA0[SA], RA1[SA], RA2[SA], RA3[RS > 3 ? SA : 1],
+            RA4[RS > 4 ? SA : 1], RA5[RS > 5 ? SA : 1], RA6[RS > 6 ? SA : 1], RA7[RS > 7 ? SA : 1];
+        __shared__ __align__(16) float RB0[SB], RB1[SB], RB2[SB], RB3[RS > 3 ? SB : 1],
+            RB4[RS > 4 ? SB : 1], RB5[RS > 5 ? SB : 1], RB6[RS > 6 ? SB : 1], RB7[RS > 7 ? SB : 1];
         auto ra = [&](auto u) -> float* {
-            if constexpr (decltype(u)::value == 0) return RA0;
-            else if constexpr (decltype(u)::value == 1) return RA1;
-            else return RA2;
+            constexpr int U = decltype(u)::value;
+            if constexpr (U == 0) return RA0;
+            else if constexpr (U == 1) return RA1;
+            else if constexpr (U == 2) return RA2;
+            else if constexpr (U == 3) return RA3;
+            else if constexpr (U == 4) return RA4;
+            else if constexpr (U == 5) return RA5;
+            else if constexpr (U == 6) return RA6;
+            else return RA7;
         };
         auto rb = [&](auto u) -> float* {
-            if constexpr (decltype(u)::value == 0) return RB0;
-            else if constexpr (decltype(u)::value == 1) return RB1;
-            else return RB2;
+            constexpr int U = decltype(u)::value;
+            if constexpr (U == 0) return RB0;
+            else if constexpr (U == 1) return RB1;
+            else if constexpr (U == 2) return RB2;
+            else if constexpr (U == 3) return RB3;
+            else if constexpr (U == 4) return RB4;
+            else if constexpr (U == 5) return RB5;
+            else if constexpr (U == 6) return RB6;
+            else return RB7;
         };
-        using S0 = std::integral_constant<int, 0>;
-        using S1 = std::integral_constant<int, 1>;
-        using S2 = std::integral_constant<int, 2>;
+        // s_waitcnt vmcnt(m * lps): at most m newer stages' loads may stay in
+        // flight (m <= RS - 2; the count is wave-uniform, the wait needs an
+        // immediate, so dispatch over the possible values)
+        auto wait_stages = [&](int64_t m) {
+            const int v = m <= 0 ? 0 : static_cast<int>(m) * lps;
+            static_for_int(std::make_integer_sequence<int, (RS - 2) * LPS_MAX + 1>{}, [&](auto c) {
+                constexpr int V = decltype(c)::value;
+                if (v == V) __builtin_amdgcn_s_waitcnt(0x3f70 | (V & 15) | ((V >> 4) << 14));
+            });
+        };
         if (nk > 0) {
-            issue_to(RA0, RB0, kbeg);
-            if (nk > 1) {
-                issue_to(RA1, RB1, kbeg + BK);
-                wait_lps();
-            } else {
-                __builtin_amdgcn_s_waitcnt(0x3f70);
-            }
+            // the first RS - 1 stages, then wait for the first of them
+            static_for_int(std::make_integer_sequence<int, RS - 1>{}, [&](auto u) {
+                if (decltype(u)::value < nk) issue_to(ra(u), rb(u), kbeg + decltype(u)::value * BK);
+            });
+            wait_stages(nk - 1 < RS - 2 ? nk - 1 : RS - 2);
             ring_barrier();
         }
-        for (int64_t kt0 = 0; kt0 < nk; kt0 += 3) {
-            auto one = [&](auto u) {
-                constexpr int U = decltype(u)::value;
-                const int64_t kt = kt0 + U;
+        for (int64_t kt0 = 0; kt0 < nk; kt0 += RS) {
+            // Step kt reads stage kt % RS, issues the loads of step kt + RS - 1
+            // into the stage step kt - 1 read (every wave passed the barrier
+            // after reading it), runs its burst, and before the barrier waits
+            // for step kt + 1's loads: the later steps' may still be in flight.
+            auto one = [&](auto off) {
+                constexpr int OFF = decltype(off)::value;
+                using U = std::integral_constant<int, OFF>;
+                const int64_t kt = kt0 + OFF;
                 if (kt >= nk) return;
-                read_frags(ra(u), rb(u));
-                using N2 = std::integral_constant<int, (U + 2) % 3>;
-                if (kt + 2 < nk) issue_to(ra(N2{}), rb(N2{}), kbeg + (kt + 2) * BK);
+                read_frags(ra(U{}), rb(U{}));
+                using NX = std::integral_constant<int, (OFF + RS - 1) % RS>;
+                if (kt + RS - 1 < nk) issue_to(ra(NX{}), rb(NX{}), kbeg + (kt + RS - 1) * BK);
                 mfma_step();
-                if (kt + 2 < nk) wait_lps();
-                else __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
+                const int64_t last = kt + RS - 1 < nk - 1 ? kt + RS - 1 : nk - 1;
+                wait_stages(last - (kt + 1));
                 ring_barrier();
             };
-            one(S0{});
-            one(S1{});
-            one(S2{});
+            static_for_int(std::make_integer_sequence<int, RS>{}, [&](auto off) { one(off); });
         }
     } else {
         if (nk > 0) {
@@ -1140,12 +1169,15 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_sk_kernel(const GemmArgs p
     }
 }
 
-// The fix-up of the stream-K launch with the same arguments: block b looks
-// at the boundary between logical workgroups b and b + 1.  When it cuts a
-// tile and workgroup b's range holds that tile's first K step (so no earlier
-// boundary cuts it), the block adds the tile's pieces in K order -- the
-// piece of workgroup b, then those of b + 1, b + 2, ... up to the tile's
-// end -- and writes the tile through the epilogue.
+// The fix-up of the stream-K launch with the same arguments: block (b, q)
+// looks at the boundary between logical workgroups b and b + 1.  When it
+// cuts a tile and workgroup b's range holds that tile's first K step (so no
+// earlier boundary cuts it), the block adds the pieces of the tile's
+// accumulator block q (one 32x32 block per wave, for every B operand) in K
+// order -- the piece of workgroup b, then those of b + 1, b + 2, ... up to
+// the tile's end -- and writes it through the epilogue.  FM x FN blocks per
+// tile keep each block's chain of dependent loads short (one block per tile
+// took 0.16 ms at config 3's w2, whose 64 cut tiles have 8 pieces each).
 template <class C, int NB, int EPI>
 __global__ __launch_bounds__(C::THREADS, 2) void gemm_sk_fixup_kernel(const GemmArgs p) {
     const int G = p.sk_grid;
@@ -1158,25 +1190,20 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_sk_fixup_kernel(const Gemm
     const int prev = sk_begin(s, w - 1);
     if (prev > t0) return;                     // an earlier boundary cuts this tile
     constexpr int64_t SLOT = int64_t(NB) * C::BM * C::BN;
-    constexpr int FM = C::FM, FN = C::FN;
+    const int bi = static_cast<int>(blockIdx.y) / C::FN, bj = static_cast<int>(blockIdx.y) % C::FN;
     const int tid = threadIdx.x;
-    f32x16 acc[NB][FM][FN];
+    f32x16 acc[NB];
     auto add_slot = [&](int64_t slot, bool first) {
         const f32x4* src = reinterpret_cast<const f32x4*>(p.sk_part + slot * SLOT);
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-            for (int bi = 0; bi < FM; ++bi)
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const f32x4 v = src[sk_part_index<C, NB>(nb, bi, bj, r4, tid)];
 #pragma unroll
-                for (int bj = 0; bj < FN; ++bj)
-#pragma unroll
-                    for (int r4 = 0; r4 < 4; ++r4) {
-                        const f32x4 v = src[sk_part_index<C, NB>(nb, bi, bj, r4, tid)];
-#pragma unroll
-                        for (int j = 0; j < 4; ++j)
-                            acc[nb][bi][bj][4 * r4 + j] =
-                                first ? v[j] : acc[nb][bi][bj][4 * r4 + j] + v[j];
-                    }
+                for (int j = 0; j < 4; ++j)
+                    acc[nb][4 * r4 + j] = first ? v[j] : acc[nb][4 * r4 + j] + v[j];
+            }
     };
     // workgroup w - 1 holds the tile's first piece: in its start slot when
     // its range begins at the tile's start, else in its end slot
@@ -1192,7 +1219,8 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_sk_fixup_kernel(const Gemm
     int e, rows;
     int64_t row0;
     if (!grouped_tile_rows<C::BM>(p, mt, e, row0, rows)) return;
-    store_tile<C, NB, EPI>(p, p.C, 0, row0, rows, static_cast<int64_t>(nt) * C::BN, acc, tid);
+    store_block<C, EPI>(p, p.C, 0, row0, rows, static_cast<int64_t>(nt) * C::BN, bi, bj, acc[0],
+                        acc[NB - 1], tid);
 }
 
 // Whether every byte offset of a SCHED_BUFLDS launch (lane offset from the
@@ -1255,8 +1283,8 @@ void launch_sk(const GemmArgs& a, bool vec, hipStream_t s) {
     hipLaunchKernelGGL((gemm_sk_kernel<C, SCHED, NB, EPI>), dim3(a.sk_grid), dim3(C::THREADS), 0,
                        s, a);
     if (a.sk_grid > 1)
-        hipLaunchKernelGGL((gemm_sk_fixup_kernel<C, NB, EPI>), dim3(a.sk_grid - 1),
-                           dim3(C::THREADS), 0, s, a);
+        hipLaunchKernelGGL((gemm_sk_fixup_kernel<C, NB, EPI>),
+                           dim3(a.sk_grid - 1, C::FM * C::FN), dim3(C::THREADS), 0, s, a);
 }
 
 using DenseCfg = CfgOf<MOE_DENSE_CFG>::T;
