@@ -151,8 +151,25 @@ DensePlan plan_dense(moe_ctx* ctx, bool nn, bool direct, int64_t M, int64_t N, i
     // each tile shape runs 4 waves, one per SIMD
     const double simd_rate = 157.3e12 / (4.0 * ctx->cus);
     double best_t = 1e30;
+    // Up to 32 rows the skinny kernel (B streamed once into registers, 16-row
+    // MFMAs, no LDS) takes every aligned shape: measured on MI355X at N =
+    // 14336, K = 4096, M = 16 NN 40.5 us against 50-54 us on the best tile
+    // and split (0.73 of the HBM roofline), M = 32 51 us; at M = 64, where the
+    // product turns MFMA-bound, the tiles are as fast and keep it.  Its waves
+    // need K splits to keep HBM busy: the most (up to 16) that keep the grid
+    // at about 1024 waves (measured best at 896: 4 splits of N = 14336; 8 or
+    // 16 add split-sum reads, 1 or 2 leave HBM idle).
+    if (M <= 32 && (!nn || N % 4 == 0) && (env_tile < 0 || env_tile == moe::kSkinnyTile)) {
+        best.tile = moe::kSkinnyTile;
+        best.splits = 1;
+        for (int S = 2; S <= moe::kMaxDenseSplits; S *= 2)
+            if (split_ok(S) && moe::ceil_div(N, 64) * S <= 1024) best.splits = S;
+        if (env_splits > 0 && split_ok(env_splits)) best.splits = env_splits;
+        return best;
+    }
     for (int t = 0; t < moe::kDenseTiles; ++t) {
         if (env_tile >= 0 && t != env_tile) continue;
+
         if (t == 3 && !nn) continue;  // the 256 x 128 tile is NN only
         int& occ = ctx->dense_blocks_per_cu[nn ? 1 : 0][t];
         if (occ == 0) occ = moe::dense_blocks_per_cu(t, nn);

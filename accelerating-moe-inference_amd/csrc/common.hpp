@@ -66,6 +66,9 @@ constexpr int kMaxW2Splits = 4;  // split-K of the layer's w2 (partials summed b
 // 64x128 and 2 = 32x128 (direct-load path only: 16-byte aligned rows,
 // K % 16 == 0, and for NN N % 4 == 0), 3 = 256x128 (NN only, direct path).
 constexpr int kDenseTiles = 4;
+// GemmArgs::tile of the skinny dense kernel (M <= 64, direct rows only; not
+// one of the kDenseTiles tile shapes).
+constexpr int kSkinnyTile = 4;
 GemmTile dense_tile(int tile);
 // Workgroups of dense tile shape `tile` (direct-load kernel) one CU holds at once.
 int dense_blocks_per_cu(int tile, bool nn);

@@ -1223,6 +1223,137 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_sk_fixup_kernel(const Gemm
                         acc[NB - 1], tid);
 }
 
+// ---------------------------------------------------------------------------
+// Skinny dense GEMM (M <= 64): B streams once from HBM straight into
+// registers, no LDS and no barriers.  Each wave owns 64 columns and all
+// 16 * MB rows of the product over its K range (K splits: grid.y), on
+// v_mfma_f32_16x16x4_f32 -- 16 rows per MFMA, so M = 16 wastes no matrix-core
+// work (the 32 x 32 tiles compute twice the rows).  In a 16-wide K chunk lane
+// (j, g) = (lane % 16, lane / 16) holds k = k0 + 4g .. k0 + 4g + 3, one per
+// MFMA step s, for A (one 16-byte load per 16-row block: row 16 mb + j) and
+// B, so the four steps cover the chunk's 16 k exactly once:
+//   NN ([K, N]): B row k0 + 4g + s, columns n0 + 4j .. 4j + 3 (16 bytes; the
+//     four column blocks c are the columns 4j + c, so a lane ends up with 4
+//     adjacent columns of each output row: one 16-byte store);
+//   NT ([N, K]): B rows n0 + 16c + j, k0 + 4g .. 4g + 3 (16 bytes per block c).
+// 16x16 accumulator layout: lane l, register r holds row 4 (l / 16) + r,
+// column block entry l % 16.  Chunks are loaded PF ahead into a register
+// ring (the K loop unrolled over it).  Rows past M and columns past N load a
+// valid row or column and are masked at the store.  Requires K % 16 == 0,
+// 16-byte aligned rows, and for NN N % 4 == 0.
+typedef float f32x4s __attribute__((ext_vector_type(4)));
+
+template <bool NN, int MB, int EPI>
+__global__ __launch_bounds__(256) void gemm_skinny_kernel(const GemmArgs p) {
+    constexpr int PF = MB >= 4 ? 3 : 4;  // chunks in flight besides the one computed
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int j = lane & 15, g = lane >> 4;
+    const int64_t N = p.N, M = p.M;
+    const int64_t n0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * 64;
+    if (n0 >= N) return;  // a wave past the last column block (no barrier in this kernel)
+    const int split = blockIdx.y;
+    const int64_t kbeg = split * p.k_split_len;
+    const int64_t kend = p.K - kbeg < p.k_split_len ? p.K : kbeg + p.k_split_len;
+    const int64_t nch = (kend - kbeg) / 16;
+
+    const float* arow[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+        int64_t r = 16 * mb + j;
+        r = r < M ? r : M - 1;
+        arow[mb] = p.A + r * p.lda + 4 * g;
+    }
+    const float* bptr[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        if (NN) {
+            int64_t c = n0 + 4 * j;
+            c = c < N ? c : N - 4;
+            bptr[q] = p.B0 + (4 * g + q) * p.ldb + c;  // step q's k-row
+        } else {
+            int64_t n = n0 + 16 * q + j;
+            n = n < N ? n : N - 1;
+            bptr[q] = p.B0 + n * p.ldb + 4 * g;        // block q's column
+        }
+    }
+    struct Chunk {
+        f32x4s a[MB], b[4];
+    };
+    auto load = [&](Chunk& c, int64_t k0) {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) c.a[mb] = *reinterpret_cast<const f32x4s*>(arow[mb] + k0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            c.b[q] = *reinterpret_cast<const f32x4s*>(bptr[q] + (NN ? k0 * p.ldb : k0));
+    };
+    f32x4s acc[MB][4];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[mb][c] = f32x4s{0.f, 0.f, 0.f, 0.f};
+    auto compute = [&](const Chunk& c) {
+#pragma unroll
+        for (int st = 0; st < 4; ++st)
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb)
+                    acc[mb][cb] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                        c.a[mb][st], NN ? c.b[st][cb] : c.b[cb][st], acc[mb][cb], 0, 0, 0);
+    };
+    Chunk ring[PF + 1];
+#pragma unroll
+    for (int u = 0; u < PF; ++u)
+        if (u < nch) load(ring[u], kbeg + 16 * u);
+    for (int64_t c0 = 0; c0 < nch; c0 += PF + 1) {
+#pragma unroll
+        for (int u = 0; u <= PF; ++u) {
+            const int64_t ci = c0 + u;
+            if (ci < nch) {
+                if (ci + PF < nch) load(ring[(u + PF) % (PF + 1)], kbeg + 16 * (ci + PF));
+                compute(ring[u]);
+            }
+        }
+    }
+
+    // epilogue: split partials (no bias) or the output with bias
+    float* Cb = p.C + split * p.c_split_stride;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t row = 16 * mb + 4 * g + r;
+            if (row >= M) continue;
+            if (NN) {
+                const int64_t col = n0 + 4 * j;
+                if (col >= N) continue;
+                f32x4s v{acc[mb][0][r], acc[mb][1][r], acc[mb][2][r], acc[mb][3][r]};
+                if (EPI == EPI_BIAS && p.bias != nullptr)
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) v[c] = v[c] + p.bias[col + c];
+                *reinterpret_cast<f32x4s*>(Cb + row * p.ldc + col) = v;
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int64_t col = n0 + 16 * c + j;
+                    if (col >= N) continue;
+                    float v = acc[mb][c][r];
+                    if (EPI == EPI_BIAS && p.bias != nullptr) v = v + p.bias[col];
+                    Cb[row * p.ldc + col] = v;
+                }
+            }
+        }
+}
+
+template <bool NN>
+void launch_skinny(const GemmArgs& a, hipStream_t s) {
+    const dim3 grid(static_cast<unsigned>(ceil_div(a.N, 256)), static_cast<unsigned>(a.k_splits));
+    const int mb = static_cast<int>(ceil_div(a.M, 16));
+    if (mb <= 1) hipLaunchKernelGGL((gemm_skinny_kernel<NN, 1, EPI_BIAS>), grid, dim3(256), 0, s, a);
+    else if (mb <= 2) hipLaunchKernelGGL((gemm_skinny_kernel<NN, 2, EPI_BIAS>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((gemm_skinny_kernel<NN, 4, EPI_BIAS>), grid, dim3(256), 0, s, a);
+}
+
 // Whether every byte offset of a SCHED_BUFLDS launch (lane offset from the
 // operand's base plus the K step's scalar offset) stays below 2^31.
 bool buf_offsets_fit(const GemmArgs& a, int bm, int bn, bool nn, bool grouped) {
@@ -1490,6 +1621,14 @@ void launch_gemm(const GemmArgs& args, bool nn, bool grouped, int epi, bool vec,
                 if (!nn) throw Unsupported("dense tile 3 is NN only");
                 launch_cfg<DenseNnCfg, MOE_DENSE_NN_SCHED | SCHED_DIRECT, true, false, 1, EPI_BIAS>(
                     a, vec, s);
+                break;
+            case kSkinnyTile:
+                // the planner checked M <= 64, K % 16 == 0 (per split), aligned rows
+                if (a.M > 64 || a.K % 16 != 0 || a.k_split_len % 16 != 0 || !vec ||
+                    (nn && a.N % 4 != 0))
+                    throw Unsupported("skinny GEMM shape");
+                if (nn) launch_skinny<true>(a, s);
+                else launch_skinny<false>(a, s);
                 break;
             default: throw Unsupported("dense GEMM tile shape");
         }

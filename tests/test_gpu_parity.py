@@ -61,10 +61,15 @@ def host(t):
 # 32x128 tile with K splits, (64, 1408, 2048) the 64x128 tile with splits,
 # (200, 520, 64) the 32x128 tile unsplit, (33, 250, 512) ragged M and N on a
 # small tile, (64, 130, 256) an NN B whose rows are not 16-byte multiples.
+# Up to 32 rows with K % 16 == 0 the skinny kernel runs: (1, 1000, 256) one
+# row, (17, 200, 512) a second 16-row block 1 row deep and a last column block
+# past N, (32, 132, 1024) two full row blocks with K splits, (9, 4, 64) one
+# 4-column output.
 SGEMM_SHAPES = [(1, 1, 1), (7, 5, 33), (129, 130, 17), (128, 128, 128),
                 (256, 384, 512), (33, 200, 1000), (300, 64, 4), (5, 700, 2),
                 (40, 384, 4096), (100, 300, 512), (64, 1408, 2048), (200, 520, 64),
-                (33, 250, 512), (64, 130, 256)]
+                (33, 250, 512), (64, 130, 256), (1, 1000, 256), (17, 200, 512),
+                (32, 132, 1024), (9, 4, 64)]
 
 
 @pytest.mark.parametrize("m,n,k", SGEMM_SHAPES)
