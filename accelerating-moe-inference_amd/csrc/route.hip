@@ -477,39 +477,48 @@ __global__ __launch_bounds__(256) void perm_place_kernel(
 // order of the reference's expert loop (src/layer.cu:93-101).  resid, when
 // given, is added last (the decoder's add_inplace, src/layer.cu:160).  When
 // the w2 GEMM ran split-K, a row is the sum of its PARTS partial rows, added
-// in part order before weighting.
+// in part order before weighting.  Threads 0..k-1 load one slot each (expert,
+// packed row, weight: independent loads, one latency) and place it at its
+// rank among the token's live slots -- the order a sequential selection by
+// (expert, slot) would give.
 template <int CONTRACT, int PARTS>
 __global__ __launch_bounds__(256) void combine_kernel(
         const float* __restrict__ out_rows, const int32_t* __restrict__ idx,
         const float* __restrict__ wts, const int32_t* __restrict__ inv,
         const float* __restrict__ resid, float* __restrict__ y, int64_t T,
         int64_t k, int64_t d, int64_t rows_total, int64_t part_stride) {
+    __shared__ int32_t slot_e[kMaxTopK];
+    __shared__ int32_t slot_live[kMaxTopK];
     __shared__ int32_t order_row[kMaxTopK];
     __shared__ float order_w[kMaxTopK];
     __shared__ int n_live;
     const int64_t t = blockIdx.x;
-    if (threadIdx.x == 0) {
-        int prev_e = -1, prev_s = -1, n = 0;
+    const int s = threadIdx.x;
+    int32_t my_e = 0, my_r = 0;
+    float my_w = 0.0f;
+    bool live = false;
+    if (s < k) {
+        my_e = idx[t * k + s];
+        my_r = inv[t * k + s];
+        my_w = wts[t * k + s];
+        live = my_r >= 0 && my_r < rows_total;
+        slot_e[s] = my_e;
+        slot_live[s] = live ? 1 : 0;
+    }
+    __syncthreads();
+    if (s < k) {
+        int rank = 0, n = 0;
         for (int q = 0; q < k; ++q) {
-            int best_e = INT_MAX, best_s = INT_MAX;
-            for (int s = 0; s < k; ++s) {
-                const int e = idx[t * k + s];
-                const bool after = e > prev_e || (e == prev_e && s > prev_s);
-                if (after && (e < best_e || (e == best_e && s < best_s))) {
-                    best_e = e;
-                    best_s = s;
-                }
-            }
-            prev_e = best_e;
-            prev_s = best_s;
-            const int32_t r = inv[t * k + best_s];
-            if (r >= 0 && r < rows_total) {
-                order_row[n] = r;
-                order_w[n] = wts[t * k + best_s];
-                ++n;
-            }
+            if (!slot_live[q]) continue;
+            ++n;
+            const int e = slot_e[q];
+            rank += (e < my_e || (e == my_e && q < s)) ? 1 : 0;
         }
-        n_live = n;
+        if (live) {
+            order_row[rank] = my_r;
+            order_w[rank] = my_w;
+        }
+        if (s == 0) n_live = n;
     }
     __syncthreads();
     const int n = n_live;
