@@ -34,10 +34,12 @@ def _weights(torch, rng, d, E, d_ff, norm):
 
 # (d, E, k, d_ff, router, norm, residual, T of the first call, T of the second):
 # the reference's router and block (layer norm + residual) on 16 experts of
-# d_ff 448, and softmax top-4 on 64 experts with a K-split w2
+# d_ff 448, softmax top-4 on 64 experts with a K-split w2, and the reference's
+# full width d 4096, whose w1/w3 runs stream-K (partial tiles in the scratch)
 @pytest.mark.parametrize("d,E,k,d_ff,router,norm,residual,T1,T2", [
     (512, 16, 2, 448, 0, 1, True, 900, 333),
     (256, 64, 4, 96, 1, 0, False, 2000, 129),
+    (4096, 16, 2, 448, 0, 0, False, 900, 333),
 ])
 def test_noalloc_matches_layer_forward(torch, d, E, k, d_ff, router, norm, residual, T1, T2):
     pkg = load_pkg()
