@@ -261,6 +261,95 @@ __global__ __launch_bounds__(256) void attn_paths_kernel(
     }
 }
 
+// The same attention for lists of up to 64 keys (prefix-trie paths are
+// short: the reference's contest sequences are 10-29 tokens), one wave per
+// (query, key head), all G query heads of that key head at once: lane t owns
+// key t's G scores (each the same d-ascending chain as above, the key row
+// read once for the G heads), the max is a wave reduction, every lane runs
+// the denominator's t-ascending chain from shuffled weights, and each output
+// value's t-ascending chain runs on the lane of its column -- the order of
+// attn_paths_kernel, so the results are bit-identical to it, on 1/4 of the
+// threads with no barrier (one workgroup of 256 per (query, head) left most
+// of its lanes idle: the reference's model shape spent 2.2 ms per layer
+// there).  head_dim a multiple of 4, at most 256; 16-byte aligned q and k.
+template <int G>
+__global__ __launch_bounds__(256) void attn_paths_wave_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    float* __restrict__ out, const int32_t* __restrict__ key_rows,
+    const int32_t* __restrict__ key_beg, const int32_t* __restrict__ key_end, int64_t nq,
+    int64_t kv_rows, int64_t key_total, int64_t KVH, int64_t hd, int64_t window, float scale) {
+    const int lane = threadIdx.x & 63;
+    const int64_t gw = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (gw >= nq * KVH) return;  // no barrier in this kernel
+    const int64_t i = gw / KVH, kh = gw % KVH, H = KVH * G;
+    const int64_t kw = KVH * hd;
+    int64_t beg = key_beg[i];
+    const int64_t end = key_end[i];
+    if (window > 0 && end - beg > window) beg = end - window;
+    const int64_t len = end > beg ? end - beg : 0;
+    float* o = out + i * H * hd + kh * G * hd;  // G heads side by side
+    if (len == 0) {
+        for (int64_t d = lane; d < G * hd; d += 64) o[d] = 0.0f;
+        return;
+    }
+    if (!(key_beg[i] >= 0 && end <= key_total && len <= 64)) {
+        for (int64_t d = lane; d < G * hd; d += 64) o[d] = NAN;
+        return;
+    }
+    const float* qi = q + i * H * hd + kh * G * hd;
+    int64_t my_row = 0;
+    float sc[G];
+    if (lane < len) {
+        int64_t r = key_rows[beg + lane];
+        my_row = r < 0 ? 0 : (r >= kv_rows ? kv_rows - 1 : r);
+        const float* kr = k + my_row * kw + kh * hd;
+        float acc[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) acc[g] = 0.0f;
+        for (int64_t d = 0; d < hd; d += 4) {
+            const float4 c = *reinterpret_cast<const float4*>(kr + d);
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float4 a = *reinterpret_cast<const float4*>(qi + g * hd + d);
+                acc[g] += a.x * c.x;
+                acc[g] += a.y * c.y;
+                acc[g] += a.z * c.z;
+                acc[g] += a.w * c.w;
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) sc[g] = acc[g] / scale;
+    } else {
+#pragma unroll
+        for (int g = 0; g < G; ++g) sc[g] = -INFINITY;
+    }
+    float den[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const float m = wave_max(sc[g]);
+        sc[g] = lane < len ? static_cast<float>(exp(static_cast<double>(sc[g] - m))) : 0.0f;
+        float dsum = 0.0f;
+        for (int64_t t = 0; t < len; ++t) dsum += __shfl(sc[g], static_cast<int>(t), 64);
+        den[g] = dsum;
+    }
+    for (int64_t d = lane; d < hd; d += 64) {
+        float value[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) value[g] = 0.0f;
+        for (int64_t t = 0; t < len; ++t) {
+            const int64_t r = __shfl(my_row, static_cast<int>(t), 64);
+            const float vv = v[r * kw + kh * hd + d];
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float pr = __shfl(sc[g], static_cast<int>(t), 64);
+                value[g] += pr / den[g] * vv;
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) o[g * hd + d] = value[g];
+    }
+}
+
 __global__ __launch_bounds__(256) void add_kernel(float* __restrict__ a, const float* __restrict__ b,
                                                   int64_t n) {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
@@ -361,6 +450,19 @@ void launch_attn_paths(const float* q, const float* k, const float* v, float* ou
                            out, scores, key_rows, key_beg, key_end, kv_rows, key_total,
                            scores_floats, q_heads, kv_heads, head_dim, window, scale);
     };
+    const int64_t G = q_heads / kv_heads;
+    if (vec4 && max_len <= 64 && head_dim <= 256 && (G == 1 || G == 2 || G == 4 || G == 8)) {
+        const dim3 grid(static_cast<unsigned>(ceil_div(nq * kv_heads, 4)));
+        auto wave = [&](auto kernel) {
+            hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, q, k, v, out, key_rows, key_beg,
+                               key_end, nq, kv_rows, key_total, kv_heads, head_dim, window, scale);
+        };
+        if (G == 1) wave(attn_paths_wave_kernel<1>);
+        else if (G == 2) wave(attn_paths_wave_kernel<2>);
+        else if (G == 4) wave(attn_paths_wave_kernel<4>);
+        else wave(attn_paths_wave_kernel<8>);
+        return;
+    }
     const bool lds = max_len <= kAttnLastLds;
     if (vec4 && lds) go(attn_paths_kernel<true, true>);
     else if (vec4) go(attn_paths_kernel<true, false>);
