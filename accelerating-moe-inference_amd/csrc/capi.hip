@@ -283,12 +283,11 @@ int64_t grouped_m_tiles(int64_t pairs, int64_t E, int bm) {
 // K splits S of the layer's w2 on the one-tile-per-workgroup kernel.  Its
 // tiles run in rounds of `slots` concurrent workgroups; a last, partly
 // filled round of long-K tiles wastes the rest of the GPU for a whole tile
-// time.  Splitting K S ways makes the rounds S times shorter, so the fill
-// is w / ceil(w) with w = tiles * S / slots.  The smallest S in {1, 2, 4}
-// whose fill reaches 95 % is taken (else the best): every split adds a
-// partial row buffer the combine must read (at the reference's layer shape
-// S = 2 costs 0.11 ms there and 0.1 ms of w2 against S = 1).  Each split
-// must be a multiple of 16 columns.  MOE_W2_SPLITS overrides for tuning.
+// time.  Splitting K S ways makes the rounds S times shorter, but every
+// split adds a partial row buffer w2 writes and the combine reads; the S in
+// {1, 2, 4} with the least modelled time is taken (choose_w2_splits).  Each
+// split must be a multiple of 16 columns.  MOE_W2_SPLITS overrides for
+// tuning.
 struct FfnPlan {
     int w13_tile = 0;  // GemmArgs::tile of w1/w3: 0 128x128 (W13), 1 256x64 (W13Tall)
     int w13_sk = 0;    // stream-K grid of w1/w3 (0: one tile per workgroup)
@@ -413,16 +412,22 @@ int choose_w2_splits(moe_ctx* ctx, int64_t pairs, int64_t d, int64_t d_ff, int64
     // expected ceil(pairs / BM) + E / 2 (each expert's last tile half full)
     const double tiles = double(expected_m_tiles(pairs, E, tile.bm) * moe::ceil_div(d, tile.bn));
     const double slots = double(int64_t(ctx->cus) * occ);
+    // Time of S splits: ceil(tiles * S / slots) rounds of K / S steps, plus
+    // the S - 1 extra partial row buffers w2 writes and the combine reads.
+    // Per K step of a round: 3.9 us on the wide tile (64 MFMAs per wave, two
+    // workgroups per CU), 2.9 us on the 128 x 128 one (32, three per CU):
+    // measured on MI355X.
+    const double step_us = w2_tile == 1 ? 2.9 : 3.9;
+    const double nk = double(std::max<int64_t>(d_ff / 16, 1));
     int best = 1;
-    double best_fill = 0.0;
+    double best_t = 1e30;
     for (int S : {1, 2, 4}) {
         if (S > moe::kMaxW2Splits || !allowed(S)) continue;
-        const double w = tiles * S / slots;
-        const double fill = w / std::ceil(w);
-        if (fill >= 0.95) return S;
-        if (fill > best_fill) {
+        const double rounds = std::ceil(tiles * S / slots);
+        const double t = rounds * nk / S * step_us + (S - 1) * double(pairs) * d * 8.0 / 6e6;
+        if (t < best_t * 0.99) {
             best = S;
-            best_fill = fill;
+            best_t = t;
         }
     }
     return best;
