@@ -285,7 +285,7 @@ int64_t grouped_m_tiles(int64_t pairs, int64_t E, int bm) {
 // filled round of long-K tiles wastes the rest of the GPU for a whole tile
 // time.  Splitting K S ways makes the rounds S times shorter, but every
 // split adds a partial row buffer w2 writes and the combine reads; the S in
-// {1, 2, 4} with the least modelled time is taken (choose_w2_splits).  Each
+// {1, 2, 4} with the least modelled time is taken (choose_w2_split_plan).  Each
 // split must be a multiple of 16 columns.  MOE_W2_SPLITS overrides for
 // tuning.
 struct FfnPlan {
@@ -297,7 +297,14 @@ struct FfnPlan {
     int64_t sk_floats = 0;  // partial-tile floats the stream-K launches need
 };
 
-int choose_w2_splits(moe_ctx* ctx, int64_t pairs, int64_t d, int64_t d_ff, int64_t E, int w2_tile);
+// The K splits of w2 on one w2 tile and their modelled time (choose_w2_split_plan).
+struct W2SplitPlan {
+    int splits = 1;
+    double us = 0.0;
+};
+
+W2SplitPlan choose_w2_split_plan(moe_ctx* ctx, int64_t pairs, int64_t d, int64_t d_ff, int64_t E,
+                                 int w2_tile);
 
 // The w1/w3 tile: 128 rows x 128 columns of each operand, or, when d_ff is
 // a multiple of 64 but not of 128 (the reference's 448), 256 rows x 64
@@ -365,13 +372,20 @@ int choose_sk(moe_ctx* ctx, moe::GemmUse use, int64_t pairs, int64_t E, int64_t 
 // rows form so few tiles that the 128x128 tile's extra parallelism wins (a
 // tile x split sweep on MI355X: config 5, d = 1024, 1.545 -> 1.488 ms per
 // layer; configs 3 and 4, with 16 and 8 wide n-tiles, 3-5 % slower on the
-// narrow tile).  MOE_W2_TILE = 0 / 1 overrides.  Then stream-K where the
-// one-tile rounds fill badly (choose_sk), else K splits for w2.
+// narrow tile).  Where the wide tile runs one tile per workgroup, the
+// narrow one is taken if its rounds' modelled time is less: both tiles
+// move the same work per CU and microsecond, so the choice is the rounds'
+// fill (the reference's shape at 16,080 rows: wide 9 rounds, 8.1 full,
+// narrow 11 rounds, 10.8 full: w2 1.039 -> 0.996 ms; 8,192 rows 0.581 ->
+// 0.522 ms; 15,583 rows equal, wide kept).  MOE_W2_TILE = 0 / 1 overrides.
+// Then stream-K where the one-tile rounds fill badly (choose_sk), else K
+// splits for w2.
 FfnPlan choose_ffn_plan(moe_ctx* ctx, int64_t pairs, int64_t d, int64_t d_ff, int64_t E) {
     FfnPlan f;
     static const int env_tile = env_int("MOE_W2_TILE", -1);
+    const bool tile_pinned = env_tile == 0 || env_tile == 1;
     f.tile = moe::ceil_div(d, moe::gemm_tile(moe::GemmUse::W2).bn) <= 4 ? 1 : 0;
-    if (env_tile == 0 || env_tile == 1) f.tile = env_tile;
+    if (tile_pinned) f.tile = env_tile;
     f.w13_tile = choose_w13_tile(d_ff);
     if (d_ff == 0 || d == 0) {
         f.splits = 1;
@@ -386,24 +400,34 @@ FfnPlan choose_ffn_plan(moe_ctx* ctx, int64_t pairs, int64_t d, int64_t d_ff, in
         return ctx->cus * occ;
     };
     const moe::GemmUse u13 = f.w13_tile == 1 ? moe::GemmUse::W13Tall : moe::GemmUse::W13;
-    const moe::GemmUse u2 = f.tile == 1 ? moe::GemmUse::W2Narrow : moe::GemmUse::W2;
-    f.splits = choose_w2_splits(ctx, pairs, d, d_ff, E, f.tile);
+    auto use_of = [](int tile) { return tile == 1 ? moe::GemmUse::W2Narrow : moe::GemmUse::W2; };
+    W2SplitPlan w2 = choose_w2_split_plan(ctx, pairs, d, d_ff, E, f.tile);
     f.w13_sk = choose_sk(ctx, u13, pairs, E, d_ff, d, 1, slots_of(u13));
-    // w2: against its best split plan
-    f.w2_sk = choose_sk(ctx, u2, pairs, E, d, d_ff, f.splits, slots_of(u2));
-    if (f.w2_sk > 0) f.splits = 1;
+    // w2: stream-K against its best split plan
+    f.w2_sk = choose_sk(ctx, use_of(f.tile), pairs, E, d, d_ff, w2.splits, slots_of(use_of(f.tile)));
+    if (!tile_pinned && f.tile == 0 && f.w2_sk == 0) {
+        const W2SplitPlan narrow = choose_w2_split_plan(ctx, pairs, d, d_ff, E, 1);
+        if (narrow.us < w2.us) {
+            f.tile = 1;
+            w2 = narrow;
+            f.w2_sk = choose_sk(ctx, use_of(1), pairs, E, d, d_ff, w2.splits, slots_of(use_of(1)));
+        }
+    }
+    f.splits = f.w2_sk > 0 ? 1 : w2.splits;
+    const moe::GemmUse u2 = use_of(f.tile);
     if (f.w13_sk > 0) f.sk_floats = moe::gemm_sk_part_floats(u13, f.w13_sk);
     if (f.w2_sk > 0) f.sk_floats = std::max(f.sk_floats, moe::gemm_sk_part_floats(u2, f.w2_sk));
     return f;
 }
 
-int choose_w2_splits(moe_ctx* ctx, int64_t pairs, int64_t d, int64_t d_ff, int64_t E, int w2_tile) {
+W2SplitPlan choose_w2_split_plan(moe_ctx* ctx, int64_t pairs, int64_t d, int64_t d_ff, int64_t E,
+                                 int w2_tile) {
     static const int env = [] {
         const char* v = std::getenv("MOE_W2_SPLITS");
         return v != nullptr ? std::atoi(v) : 0;
     }();
     auto allowed = [&](int S) { return S == 1 || (d_ff > 0 && d_ff % (16 * S) == 0); };
-    if (env == 1 || env == 2 || env == 4) return allowed(env) ? env : 1;
+    const bool pinned = env == 1 || env == 2 || env == 4;
     const moe::GemmUse use = w2_tile == 1 ? moe::GemmUse::W2Narrow : moe::GemmUse::W2;
     int& occ = w2_tile == 1 ? ctx->w2n_blocks_per_cu : ctx->w2_blocks_per_cu;
     if (occ == 0) occ = moe::gemm_blocks_per_cu(use);
@@ -414,21 +438,25 @@ int choose_w2_splits(moe_ctx* ctx, int64_t pairs, int64_t d, int64_t d_ff, int64
     const double slots = double(int64_t(ctx->cus) * occ);
     // Time of S splits: ceil(tiles * S / slots) rounds of K / S steps, plus
     // the S - 1 extra partial row buffers w2 writes and the combine reads.
-    // Per K step of a round: 3.9 us on the wide tile (64 MFMAs per wave, two
-    // workgroups per CU), 2.9 us on the 128 x 128 one (32, three per CU):
-    // measured on MI355X.
-    const double step_us = w2_tile == 1 ? 2.9 : 3.9;
+    // A round of n K steps: 3.9 n + 9 us on the wide tile (64 MFMAs per wave
+    // and step, two workgroups per CU), 3.2 n us on the 128 x 128 one (32,
+    // three per CU): fitted to rounds measured on MI355X at n = 28 (the
+    // reference's d_ff 448), 88 (config 4) and 896 (config 3).
     const double nk = double(std::max<int64_t>(d_ff / 16, 1));
-    int best = 1;
-    double best_t = 1e30;
+    auto round_us = [&](double n) { return w2_tile == 1 ? 3.2 * n : 3.9 * n + 9.0; };
+    auto time_of = [&](int S) {
+        const double rounds = std::ceil(tiles * S / slots);
+        return rounds * round_us(nk / S) + (S - 1) * double(pairs) * d * 8.0 / 6e6;
+    };
+    if (pinned) {
+        const int S = allowed(env) ? env : 1;
+        return {S, time_of(S)};
+    }
+    W2SplitPlan best{1, 1e30};
     for (int S : {1, 2, 4}) {
         if (S > moe::kMaxW2Splits || !allowed(S)) continue;
-        const double rounds = std::ceil(tiles * S / slots);
-        const double t = rounds * nk / S * step_us + (S - 1) * double(pairs) * d * 8.0 / 6e6;
-        if (t < best_t * 0.99) {
-            best = S;
-            best_t = t;
-        }
+        const double t = time_of(S);
+        if (t < best.us * 0.99) best = {S, t};
     }
     return best;
 }
