@@ -784,7 +784,13 @@ __device__ __forceinline__ void direct_tile(const GemmArgs& p, int mt, int nt, i
         const int64_t boff = NN ? k0 * p.ldb : k0;
         constexpr int BSTEP = NN ? NnB<BN>::STRIDE : 256;
         if (SCHED & SCHED_BUFLDS) {
-            const uint32_t ak = static_cast<uint32_t>(k0 * 4), bk = static_cast<uint32_t>(boff * 4);
+            // wave-uniform byte offsets of the K step (scalar operands of
+            // the loads; read from the first lane so that the compiler never
+            // treats them as per-lane values)
+            const uint32_t ak = static_cast<uint32_t>(
+                __builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(k0 * 4))));
+            const uint32_t bk = static_cast<uint32_t>(
+                __builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(boff * 4))));
 #pragma unroll
             for (int j = 0; j < A_INS; ++j)
                 if (A_INS * NW == A_TOT || wave * A_INS + j < A_TOT)
@@ -837,14 +843,18 @@ __device__ __forceinline__ void direct_tile(const GemmArgs& p, int mt, int nt, i
     const int live_rows = n0 + bcol0 < N ? rows - arow0 : 0;
     const int live = live_rows <= 0 ? 0 : (live_rows >= FM * 32 ? FM : (live_rows + 31) / 32);
 
-    const int64_t nk = (K - kbeg) / BK;
+    // K steps of this tile (wave-uniform; fits 31 bits: the host bounds K)
+    const int64_t nk = __builtin_amdgcn_readfirstlane(static_cast<int>((K - kbeg) / BK));
     f32x4 a[FM][2], b[NB][FN][2];
-    // all fragments of one K step from the stage at (Acur, Bcur) (no LDS
-    // read may follow the next stage's loads: they would have to wait)
-    auto read_frags = [&](const float* Acur, const float* Bcur) {
+    // the fragments of one K step that a burst over the first NBLK 32-row
+    // blocks uses, from the stage at (Acur, Bcur) (no LDS read may follow the
+    // next stage's loads: they would have to wait)
+    auto read_frags = [&](auto nblk, const float* Acur, const float* Bcur) {
+        constexpr int NBLK = decltype(nblk)::value < 0 ? FM : decltype(nblk)::value;
+        if constexpr (NBLK == 0) return;
         auto read_a = [&](int q) {
 #pragma unroll
-            for (int bi = 0; bi < FM; ++bi) {
+            for (int bi = 0; bi < NBLK; ++bi) {
                 const int r = arow0 + bi * 32 + lr;
                 a[bi][q] = *reinterpret_cast<const f32x4*>(&Acur[r * BK] +
                                                            4 * ((2 * lh + q) ^ swz(r)));
@@ -892,12 +902,13 @@ __device__ __forceinline__ void direct_tile(const GemmArgs& p, int mt, int nt, i
             }
         }
     };
-    // the MFMA burst of one K step over this wave's live 32-row blocks
-    auto mfma_step = [&]() {
+    // the MFMA burst of one K step over the first NBLK 32-row blocks of this
+    // wave
+    auto mfma_burst = [&](auto nblk) {
+        constexpr int NBLK = decltype(nblk)::value;
+        if constexpr (NBLK == 0) return;
         if (SCHED & SCHED_PRIO) __builtin_amdgcn_s_setprio(1);
-        // the burst over the first NBLK 32-row blocks of this wave
-        auto burst = [&](auto nblk) {
-            constexpr int NBLK = decltype(nblk)::value;
+        {
             auto step = [&](int q, int s, int nb) {
 #pragma unroll
                 for (int bi = 0; bi < NBLK; ++bi)
@@ -920,112 +931,154 @@ __device__ __forceinline__ void direct_tile(const GemmArgs& p, int mt, int nt, i
                         for (int nb = 0; nb < NB; ++nb) step(q, s, nb);
                 }
             }
-        };
-        // Blocks whose 32 rows all lie past the tile's last real row (the
-        // ragged end of an expert) are skipped: wave-uniform branches.
-        if (live == FM) burst(std::integral_constant<int, FM>{});
-        else if (FM > 1 && live == 1) burst(std::integral_constant<int, 1>{});
-        else if (live > 0) burst(std::integral_constant<int, FM>{});
+        }
         if (SCHED & SCHED_PRIO) __builtin_amdgcn_s_setprio(0);
     };
+    // NBLK < 0: this wave's live blocks chosen in every K step (wave-uniform
+    // branches)
+    auto mfma_step = [&](auto nblk) {
+        if constexpr (decltype(nblk)::value >= 0) {
+            mfma_burst(nblk);
+        } else {
+            if (live == FM) mfma_burst(std::integral_constant<int, FM>{});
+            else if (FM > 1 && live == 1) mfma_burst(std::integral_constant<int, 1>{});
+            else if (live > 0) mfma_burst(std::integral_constant<int, FM>{});
+        }
+    };
 
-    if constexpr ((SCHED & SCHED_RING3) != 0) {
-        // RS stages (three by default), one __shared__ array each (the
-        // compiler then waits only for the loads landing in the stage it
-        // reads), the K loop unrolled by RS so every step names its arrays.
-        static_assert((SCHED & SCHED_BUFLDS) != 0, "the ring uses buffer loads");
-        // this wave's loads per stage (tiles with fewer load instructions
-        // than waves leave some waves without an A or B load)
-        int lps = 0;
+    constexpr int LPS_MAX = A_INS + NB * B_INS;
+    // every wave issues LPS_MAX loads per stage (the tile has at least as
+    // many load instructions as waves, in whole multiples)
+    constexpr bool LPS_ALL = A_INS * NW == A_TOT && B_INS * NW == B_TOT;
+    // The ring's RS stage arrays (unused ones shrink to one float; kernels
+    // without the ring reference none of them, so none is allocated)
+    constexpr bool RING = (SCHED & SCHED_RING3) != 0;
+    constexpr int RS = ring_stages(SCHED);
+    static_assert(!RING || (RS >= 3 && RS <= 8), "ring stages");
+    static_assert(!RING || (RS - 2) * LPS_MAX <= 63, "vmcnt range");
+    constexpr int SA = BM * BK, SB = NB * B_SIZE;
+    __shared__ __align__(16) float RA0[SA], RA1[SA], RA2[SA], RA3[RS > 3 ? SA : 1],
+        RA4[RS > 4 ? SA : 1], RA5[RS > 5 ? SA : 1], RA6[RS > 6 ? SA : 1], RA7[RS > 7 ? SA : 1];
+    __shared__ __align__(16) float RB0[SB], RB1[SB], RB2[SB], RB3[RS > 3 ? SB : 1],
+        RB4[RS > 4 ? SB : 1], RB5[RS > 5 ? SB : 1], RB6[RS > 6 ? SB : 1], RB7[RS > 7 ? SB : 1];
+    auto ra = [&](auto u) -> float* {
+        constexpr int U = decltype(u)::value;
+        if constexpr (U == 0) return RA0;
+        else if constexpr (U == 1) return RA1;
+        else if constexpr (U == 2) return RA2;
+        else if constexpr (U == 3) return RA3;
+        else if constexpr (U == 4) return RA4;
+        else if constexpr (U == 5) return RA5;
+        else if constexpr (U == 6) return RA6;
+        else return RA7;
+    };
+    auto rb = [&](auto u) -> float* {
+        constexpr int U = decltype(u)::value;
+        if constexpr (U == 0) return RB0;
+        else if constexpr (U == 1) return RB1;
+        else if constexpr (U == 2) return RB2;
+        else if constexpr (U == 3) return RB3;
+        else if constexpr (U == 4) return RB4;
+        else if constexpr (U == 5) return RB5;
+        else if constexpr (U == 6) return RB6;
+        else return RB7;
+    };
+    // The K loop for a burst over NBLK blocks (NBLK < 0: over the live ones,
+    // chosen per step).  Blocks whose 32 rows all lie past the tile's last
+    // real row (the ragged end of an expert) are skipped.  The ring kernels
+    // instantiate the loop per burst width and each wave picks one per tile:
+    // the wave-uniform branch in every K step cost 2-3 % of the MFMA time
+    // (measured on MI355X at configs 3-5; the reference's layer shape, whose
+    // w2 tiles are 28 K steps long, gains 1 % per layer); the two-stage
+    // kernels measured 1-3 % slower so and keep one loop.
+    auto k_loop = [&](auto nblk) {
+        if constexpr (RING) {
+            // RS stages (three by default), one __shared__ array each (the
+            // compiler then waits only for the loads landing in the stage it
+            // reads), the K loop unrolled by RS so every step names its arrays.
+            static_assert((SCHED & SCHED_BUFLDS) != 0, "the ring uses buffer loads");
+            // this wave's loads per stage (tiles with fewer load instructions
+            // than waves leave some waves without an A or B load)
+            int lps = 0;
 #pragma unroll
-        for (int j = 0; j < A_INS; ++j) lps += (A_INS * NW == A_TOT || wave * A_INS + j < A_TOT);
+            for (int j = 0; j < A_INS; ++j)
+                lps += (A_INS * NW == A_TOT || wave * A_INS + j < A_TOT);
 #pragma unroll
-        for (int j = 0; j < B_INS; ++j)
-            lps += NB * (B_INS * NW == B_TOT || wave * B_INS + j < B_TOT);
-        constexpr int LPS_MAX = A_INS + NB * B_INS;
-        // RS stage arrays (unused ones shrink to one float)
-        constexpr int RS = ring_stages(SCHED);
-        static_assert(RS >= 3 && RS <= 8, "ring stages");
-        static_assert((RS - 2) * LPS_MAX <= 63, "vmcnt range");
-        constexpr int SA = BM * BK, SB = NB * B_SIZE;
-        __shared__ __align__(16) float RA0[SA], RA1[SA], RA2[SA], RA3[RS > 3 ? SA : 1],
-            RA4[RS > 4 ? SA : 1], RA5[RS > 5 ? SA : 1], RA6[RS > 6 ? SA : 1], RA7[RS > 7 ? SA : 1];
-        __shared__ __align__(16) float RB0[SB], RB1[SB], RB2[SB], RB3[RS > 3 ? SB : 1],
-            RB4[RS > 4 ? SB : 1], RB5[RS > 5 ? SB : 1], RB6[RS > 6 ? SB : 1], RB7[RS > 7 ? SB : 1];
-        auto ra = [&](auto u) -> float* {
-            constexpr int U = decltype(u)::value;
-            if constexpr (U == 0) return RA0;
-            else if constexpr (U == 1) return RA1;
-            else if constexpr (U == 2) return RA2;
-            else if constexpr (U == 3) return RA3;
-            else if constexpr (U == 4) return RA4;
-            else if constexpr (U == 5) return RA5;
-            else if constexpr (U == 6) return RA6;
-            else return RA7;
-        };
-        auto rb = [&](auto u) -> float* {
-            constexpr int U = decltype(u)::value;
-            if constexpr (U == 0) return RB0;
-            else if constexpr (U == 1) return RB1;
-            else if constexpr (U == 2) return RB2;
-            else if constexpr (U == 3) return RB3;
-            else if constexpr (U == 4) return RB4;
-            else if constexpr (U == 5) return RB5;
-            else if constexpr (U == 6) return RB6;
-            else return RB7;
-        };
-        // s_waitcnt vmcnt(m * lps): at most m newer stages' loads may stay in
-        // flight (m <= RS - 2; the count is wave-uniform, the wait needs an
-        // immediate, so dispatch over the possible values)
-        auto wait_stages = [&](int64_t m) {
-            const int v = m <= 0 ? 0 : static_cast<int>(m) * lps;
-            static_for_int(std::make_integer_sequence<int, (RS - 2) * LPS_MAX + 1>{}, [&](auto c) {
-                constexpr int V = decltype(c)::value;
-                if (v == V) __builtin_amdgcn_s_waitcnt(0x3f70 | (V & 15) | ((V >> 4) << 14));
-            });
-        };
-        if (nk > 0) {
-            // the first RS - 1 stages, then wait for the first of them
-            static_for_int(std::make_integer_sequence<int, RS - 1>{}, [&](auto u) {
-                if (decltype(u)::value < nk) issue_to(ra(u), rb(u), kbeg + decltype(u)::value * BK);
-            });
-            wait_stages(nk - 1 < RS - 2 ? nk - 1 : RS - 2);
-            ring_barrier();
-        }
-        for (int64_t kt0 = 0; kt0 < nk; kt0 += RS) {
-            // Step kt reads stage kt % RS, issues the loads of step kt + RS - 1
-            // into the stage step kt - 1 read (every wave passed the barrier
-            // after reading it), runs its burst, and before the barrier waits
-            // for step kt + 1's loads: the later steps' may still be in flight.
-            auto one = [&](auto off) {
-                constexpr int OFF = decltype(off)::value;
-                using U = std::integral_constant<int, OFF>;
-                const int64_t kt = kt0 + OFF;
-                if (kt >= nk) return;
-                read_frags(ra(U{}), rb(U{}));
-                using NX = std::integral_constant<int, (OFF + RS - 1) % RS>;
-                if (kt + RS - 1 < nk) issue_to(ra(NX{}), rb(NX{}), kbeg + (kt + RS - 1) * BK);
-                mfma_step();
-                const int64_t last = kt + RS - 1 < nk - 1 ? kt + RS - 1 : nk - 1;
-                wait_stages(last - (kt + 1));
-                ring_barrier();
+            for (int j = 0; j < B_INS; ++j)
+                lps += NB * (B_INS * NW == B_TOT || wave * B_INS + j < B_TOT);
+            // s_waitcnt vmcnt(m * lps): at most m newer stages' loads may stay in
+            // flight (m <= RS - 2; the count is wave-uniform, the wait needs an
+            // immediate, so dispatch over the possible values: the RS - 1 values
+            // of m when every wave issues LPS_MAX loads, else those of m * lps)
+            auto wait_stages = [&](int64_t m) {
+                if constexpr (LPS_ALL) {
+                    static_for_int(std::make_integer_sequence<int, RS - 1>{}, [&](auto c) {
+                        constexpr int M = decltype(c)::value, V = M * LPS_MAX;
+                        if (m == M || (M == 0 && m < 0))
+                            __builtin_amdgcn_s_waitcnt(0x3f70 | (V & 15) | ((V >> 4) << 14));
+                    });
+                    return;
+                }
+                const int v = m <= 0 ? 0 : static_cast<int>(m) * lps;
+                constexpr int VMAX = (RS - 2) * LPS_MAX;
+                static_for_int(std::make_integer_sequence<int, VMAX + 1>{}, [&](auto c) {
+                    constexpr int V = decltype(c)::value;
+                    if (v == V) __builtin_amdgcn_s_waitcnt(0x3f70 | (V & 15) | ((V >> 4) << 14));
+                });
             };
-            static_for_int(std::make_integer_sequence<int, RS>{}, [&](auto off) { one(off); });
+            if (nk > 0) {
+                // the first RS - 1 stages, then wait for the first of them
+                static_for_int(std::make_integer_sequence<int, RS - 1>{}, [&](auto u) {
+                    constexpr int U = decltype(u)::value;
+                    if (U < nk) issue_to(ra(u), rb(u), kbeg + U * BK);
+                });
+                wait_stages(nk - 1 < RS - 2 ? nk - 1 : RS - 2);
+                ring_barrier();
+            }
+            for (int64_t kt0 = 0; kt0 < nk; kt0 += RS) {
+                // Step kt reads stage kt % RS, issues the loads of step kt + RS - 1
+                // into the stage step kt - 1 read (every wave passed the barrier
+                // after reading it), runs its burst, and before the barrier waits
+                // for step kt + 1's loads: the later steps' may still be in flight.
+                auto one = [&](auto off) {
+                    constexpr int OFF = decltype(off)::value;
+                    using U = std::integral_constant<int, OFF>;
+                    const int64_t kt = kt0 + OFF;
+                    if (kt >= nk) return;
+                    read_frags(nblk, ra(U{}), rb(U{}));
+                    using NX = std::integral_constant<int, (OFF + RS - 1) % RS>;
+                    // all but the last RS - 1 steps issue loads and leave the
+                    // RS - 2 newest stages in flight; the tail waits for more
+                    const bool more = kt + RS - 1 < nk;
+                    if (more) issue_to(ra(NX{}), rb(NX{}), kbeg + (kt + RS - 1) * BK);
+                    mfma_step(nblk);
+                    wait_stages(more ? RS - 2 : nk - kt - 2);
+                    ring_barrier();
+                };
+                static_for_int(std::make_integer_sequence<int, RS>{}, [&](auto off) { one(off); });
+            }
+        } else {
+            if (nk > 0) {
+                issue(0, kbeg);
+                __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0): this wave's loads landed
+                __syncthreads();                      // ... and every other wave's
+            }
+            for (int64_t kt = 0; kt < nk; ++kt) {
+                const int cur = static_cast<int>(kt & 1);
+                read_frags(nblk, As[cur], &Bs[cur][0][0]);
+                if (kt + 1 < nk) issue(cur ^ 1, kbeg + (kt + 1) * BK);
+                mfma_step(nblk);
+                __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
+                __syncthreads();
+            }
         }
+    };
+    if constexpr (RING) {
+        if (live > 1 || (FM == 1 && live == 1)) k_loop(std::integral_constant<int, FM>{});
+        else if (live == 1) k_loop(std::integral_constant<int, 1>{});
+        else k_loop(std::integral_constant<int, 0>{});
     } else {
-        if (nk > 0) {
-            issue(0, kbeg);
-            __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0): this wave's loads landed
-            __syncthreads();                      // ... and every other wave's
-        }
-        for (int64_t kt = 0; kt < nk; ++kt) {
-            const int cur = static_cast<int>(kt & 1);
-            read_frags(As[cur], &Bs[cur][0][0]);
-            if (kt + 1 < nk) issue(cur ^ 1, kbeg + (kt + 1) * BK);
-            mfma_step();
-            __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
-            __syncthreads();
-        }
+        k_loop(std::integral_constant<int, -1>{});
     }
 
     if constexpr (NSTRIDE) {
