@@ -47,17 +47,21 @@
 #endif
 // Main-loop schedule per use, a bit mask of SCHED_* (below).  Defaults are
 // the measured best on MI355X: direct loads issued as buffer loads, fragment
-// reads in burst order, for every use; the three-stage ring for the expert
-// GEMMs (0.3-0.9 % faster at configs 3-5 and the reference's layer shape);
-// raised priority for w1/w3 only (it slows w2).
+// reads in burst order, the three-stage ring, for every use.  Raised wave
+// priority around the MFMAs once helped w1/w3 by a little, but its
+// instructions fence the scheduler, so a step's loads cannot spread among
+// its MFMAs: without it, spread, w1/w3 run 2.5 % faster (configs 3-5, the
+// reference's layer shape).  The 128 x 128 dense tile once kept two stages
+// (four workgroups per CU against the ring's three); with the loads spread,
+// the ring is 1 % faster on the large NT squares.
 #ifndef MOE_W13_SCHED
-#define MOE_W13_SCHED 63
+#define MOE_W13_SCHED 62
 #endif
 #ifndef MOE_W2_SCHED
 #define MOE_W2_SCHED 62
 #endif
 #ifndef MOE_DENSE_SCHED
-#define MOE_DENSE_SCHED 30
+#define MOE_DENSE_SCHED 62
 #endif
 // The 256 x 128 NN tile takes the three-stage ring, like the expert GEMMs
 // whose per-wave work it shares.
@@ -991,6 +995,28 @@ __device__ __forceinline__ void direct_tile(const GemmArgs& p, int mt, int nt, i
     // (measured on MI355X at configs 3-5; the reference's layer shape, whose
     // w2 tiles are 28 K steps long, gains 1 % per layer); the two-stage
     // kernels measured 1-3 % slower so and keep one loop.
+    // The order of one ring step (scheduling groups, in turn): its fragment
+    // reads, then its MFMAs with its loads spread among them, one after every
+    // PER MFMAs.  Issued in a burst ahead of the MFMAs, the loads (each a
+    // scalar LDS address move and a buffer load) held back the step's first
+    // MFMA; spread, they issue while the matrix cores run (measured on
+    // MI355X: 2-6 % less time per GEMM at configs 3-5 and the reference's
+    // layer shape).
+    auto schedule_step = [&](auto nblk) {
+        constexpr int NBLK = decltype(nblk)::value;
+        if constexpr (LPS_ALL && NBLK > 0) {
+            constexpr int MF = NBLK * FN * NB * 8;
+            constexpr int DSR =
+                NBLK * 2 + (NSTRIDE ? NB * 8 : (NN ? NB * FN * 8 : NB * FN * 2));
+            constexpr int PER = MF / (LPS_MAX + 2);
+            __builtin_amdgcn_sched_group_barrier(0x100, DSR, 0);  // LDS reads
+            static_for_int(std::make_integer_sequence<int, LPS_MAX>{}, [&](auto) {
+                __builtin_amdgcn_sched_group_barrier(0x008, PER, 0);  // MFMAs
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);    // a load
+            });
+            __builtin_amdgcn_sched_group_barrier(0x008, MF - PER * LPS_MAX, 0);
+        }
+    };
     auto k_loop = [&](auto nblk) {
         if constexpr (RING) {
             // RS stages (three by default), one __shared__ array each (the
@@ -1047,16 +1073,23 @@ __device__ __forceinline__ void direct_tile(const GemmArgs& p, int mt, int nt, i
                     if (kt >= nk) return;
                     read_frags(nblk, ra(U{}), rb(U{}));
                     using NX = std::integral_constant<int, (OFF + RS - 1) % RS>;
-                    // all but the last RS - 1 steps issue loads and leave the
-                    // RS - 2 newest stages in flight; the tail waits for more
-                    const bool more = kt + RS - 1 < nk;
-                    if (more) issue_to(ra(NX{}), rb(NX{}), kbeg + (kt + RS - 1) * BK);
+                    // Every step issues loads, so a step is one block whose
+                    // loads the scheduler can spread among its MFMAs, and
+                    // every step leaves the RS - 2 newest stages in flight:
+                    // the last RS - 1 steps load step nk - 1 again, into
+                    // stages that no later step reads.
+                    const int64_t kn = kt + RS - 1 < nk ? kt + RS - 1 : nk - 1;
+                    issue_to(ra(NX{}), rb(NX{}), kbeg + kn * BK);
                     mfma_step(nblk);
-                    wait_stages(more ? RS - 2 : nk - kt - 2);
+                    schedule_step(nblk);
+                    wait_stages(RS - 2);
                     ring_barrier();
                 };
                 static_for_int(std::make_integer_sequence<int, RS>{}, [&](auto off) { one(off); });
             }
+            // the repeated loads of the last steps land before the
+            // workgroup's LDS is used again (or released)
+            __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
         } else {
             if (nk > 0) {
                 issue(0, kbeg);
