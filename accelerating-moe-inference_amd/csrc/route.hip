@@ -279,6 +279,169 @@ __global__ __launch_bounds__(64) void gate_ring_kernel(
     if (r < nt && e < E) logits[(t0 + r) * E + e] = acc;
 }
 
+// E of 9-16: the ring form with the workgroup sharing each stage.  A wave of
+// its own would stream all EB expert rows for its few tokens (at E = 16, 4
+// tokens: four times the token bytes); here 256 threads hold
+// R = TB * 256 / EB tokens x EB experts, as in the staged kernel above
+// (thread (r, e) runs the chains of tokens r TB .. r TB + TB - 1 for expert
+// e), and the R token rows and EB expert rows stream through a RING-stage
+// LDS ring of 64-column stages filled by direct buffer loads RING - 1 stages
+// ahead, so each workgroup keeps (RING - 1) stages of loads in flight instead
+// of one register-staged chunk.  Chunk p = 256 i + tid of a stage is row
+// p / 16, slot p % 16, holding the row's chunk (p % 16) ^ (row % 16) (the
+// reads of one chunk from 16 rows hit distinct banks).  Per stage every
+// thread waits for its own loads, the workgroup meets at a barrier (so every
+// thread's loads of the stage have landed and the stage read last has been
+// consumed by all), the loads RING - 1 stages ahead go into that consumed
+// stage, and the stage is consumed: 64 multiply-adds per chain in column
+// order, the chain of the kernels above.  (Two tokens per thread, and the
+// 64-expert form with four, kept too many chains' reads in registers and ran
+// 1.5-6x slower; those keep the staged kernel.)
+// Ring depth and the waves per SIMD the register budget is set for
+// (measured on MI355X at the reference's 15,583 x 4096 x 16: 3 stages at 4
+// waves 84 us; 4 stages at 3 waves 132 us, at 4 waves 217 us; 6 at 2, 112 us;
+// 8 at 2, 242 us; the staged kernel 110 us in the same runs).
+#ifndef MOE_GATE_RING
+#define MOE_GATE_RING 3
+#endif
+#ifndef MOE_GATE_OCC
+#define MOE_GATE_OCC 4
+#endif
+template <int CONTRACT, int EB, int TB, int RING>
+__global__ __launch_bounds__(256, MOE_GATE_OCC) void gate_wg_ring_kernel(
+        const float* __restrict__ x, const float* __restrict__ w,
+        float* __restrict__ logits, int64_t T, int64_t d, int64_t E) {
+    constexpr int R = TB * (256 / EB);             // token rows per workgroup
+    constexpr int ROWS = R + EB;                   // staged rows: tokens, then experts
+    constexpr int STAGE = ROWS * kGateRingCols;    // floats per stage
+    constexpr int INS = ROWS * 16 / 256;           // load instructions per thread and stage
+    static_assert(ROWS * 16 % 256 == 0 && R % 4 == 0, "whole instructions, 4 rows of one matrix each");
+    static_assert(RING >= 3 && RING <= 8 && (RING - 2) * INS <= 63, "ring depth");
+    __shared__ __align__(16) float r0[STAGE], r1[STAGE], r2[STAGE], r3[RING > 3 ? STAGE : 1],
+        r4[RING > 4 ? STAGE : 1], r5[RING > 5 ? STAGE : 1], r6[RING > 6 ? STAGE : 1],
+        r7[RING > 7 ? STAGE : 1];
+    auto buf = [&](auto u) __attribute__((always_inline)) -> float* {
+        constexpr int U = decltype(u)::value;
+        if constexpr (U == 0) return r0;
+        else if constexpr (U == 1) return r1;
+        else if constexpr (U == 2) return r2;
+        else if constexpr (U == 3) return r3;
+        else if constexpr (U == 4) return r4;
+        else if constexpr (U == 5) return r5;
+        else if constexpr (U == 6) return r6;
+        else return r7;
+    };
+
+    const int tid = threadIdx.x;
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * R;
+    const int64_t e0 = static_cast<int64_t>(blockIdx.y) * EB;
+    const int64_t nt = T - t0 < R ? T - t0 : R;    // tokens of this workgroup (>= 1)
+    const int64_t ne = E - e0 < EB ? E - e0 : EB;  // experts of this workgroup (>= 1)
+    const int64_t nst = (d + kGateRingCols - 1) / kGateRingCols;
+
+    // instruction i of this thread: chunk 256 i + tid; the 64 lanes of a
+    // wave cover rows 4 j .. 4 j + 3 of one matrix (R is a multiple of 4)
+    const float* ibase[INS];
+    uint32_t ioff[INS];
+    int ichunk[INS];
+#pragma unroll
+    for (int i = 0; i < INS; ++i) {
+        const int p = 256 * i + tid, row = p / 16, sl = p % 16;
+        ichunk[i] = sl ^ (row % 16);
+        if (row < R) {  // token rows (past the last token: the last one, never stored)
+            const int64_t rr = row < nt ? row : nt - 1;
+            ibase[i] = x + t0 * d;
+            ioff[i] = static_cast<uint32_t>((rr * d + 4 * ichunk[i]) * 4);
+        } else {        // expert rows
+            const int64_t e = row - R < ne ? row - R : ne - 1;
+            ibase[i] = w + e0 * d;
+            ioff[i] = static_cast<uint32_t>((e * d + 4 * ichunk[i]) * 4);
+        }
+    }
+    auto issue = [&](int64_t st, float* dst) __attribute__((always_inline)) {
+        const int64_t j0 = st * kGateRingCols;
+#pragma unroll
+        for (int i = 0; i < INS; ++i) {
+            // a chunk past the row end loads the row's last chunk (never used)
+            const int64_t shift = j0 + 4 * ichunk[i] <= d - 4 ? j0 : d - 4 - 4 * ichunk[i];
+            gate_load16(ibase[i], (gate_lds_t*)(dst + 1024 * i + 256 * (tid >> 6)),
+                        static_cast<uint32_t>(ioff[i] + shift * 4));
+        }
+    };
+    // before consuming stage st: this thread's loads of it have landed; the
+    // stages issued after it (at most RING - 2) may stay in flight
+    auto wait_stage = [&](int64_t st) __attribute__((always_inline)) {
+        const int64_t after = (st + RING - 1 < nst ? st + RING - 1 : nst) - st - 1;
+        gate_static_for(std::make_integer_sequence<int, RING - 1>{}, [&](auto c) __attribute__((always_inline)) {
+            constexpr int A = decltype(c)::value, N = A * INS;
+            if (after == A) __builtin_amdgcn_s_waitcnt(0x3f70 | (N & 15) | ((N >> 4) << 14));
+        });
+    };
+
+    const int r = tid / EB, e = tid % EB;
+    const int wsw = (R + e) % 16;
+    float acc[TB];
+#pragma unroll
+    for (int u = 0; u < TB; ++u) acc[u] = 0.0f;
+    auto consume = [&](const float* stage, int64_t st) __attribute__((always_inline)) {
+        const float* wr = stage + (R + e) * kGateRingCols;
+        const int64_t j0 = st * kGateRingCols;
+        if (j0 + kGateRingCols <= d) {
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const f32x4_t wv = *reinterpret_cast<const f32x4_t*>(wr + 4 * (q ^ wsw));
+#pragma unroll
+                for (int u = 0; u < TB; ++u) {
+                    const int row = r * TB + u;
+                    const f32x4_t xv = *reinterpret_cast<const f32x4_t*>(
+                        stage + row * kGateRingCols + 4 * (q ^ (row % 16)));
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) acc[u] = mac<CONTRACT>(acc[u], xv[c], wv[c]);
+                }
+            }
+        } else {
+            for (int q = 0; q < 16; ++q) {
+                const f32x4_t wv = *reinterpret_cast<const f32x4_t*>(wr + 4 * (q ^ wsw));
+#pragma unroll
+                for (int u = 0; u < TB; ++u) {
+                    const int row = r * TB + u;
+                    const f32x4_t xv = *reinterpret_cast<const f32x4_t*>(
+                        stage + row * kGateRingCols + 4 * (q ^ (row % 16)));
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+                        if (j0 + 4 * q + c < d) acc[u] = mac<CONTRACT>(acc[u], xv[c], wv[c]);
+                }
+            }
+        }
+    };
+    gate_static_for(std::make_integer_sequence<int, RING - 1>{}, [&](auto u) __attribute__((always_inline)) {
+        if (decltype(u)::value < nst) issue(decltype(u)::value, buf(u));
+    });
+    for (int64_t st0 = 0; st0 < nst; st0 += RING) {
+        gate_static_for(std::make_integer_sequence<int, RING>{}, [&](auto u) __attribute__((always_inline)) {
+            constexpr int U = decltype(u)::value;
+            const int64_t st = st0 + U;
+            if (st < nst) {
+                wait_stage(st);
+                asm volatile("" ::: "memory");
+                __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this thread's reads of st - 1 are done
+                __builtin_amdgcn_s_barrier();
+                asm volatile("" ::: "memory");
+                if (st + RING - 1 < nst)
+                    issue(st + RING - 1, buf(std::integral_constant<int, (U + RING - 1) % RING>{}));
+                consume(buf(u), st);
+            }
+        });
+    }
+    // the ring's loads have all been waited for (the last stage's wait is
+    // vmcnt(0)), so the workgroup's LDS is quiet when it ends
+#pragma unroll
+    for (int u = 0; u < TB; ++u) {
+        const int64_t t = t0 + r * TB + u;
+        if (r * TB + u < nt && e < ne) logits[t * E + e0 + e] = acc[u];
+    }
+}
+
 // -------------------------------------------------------------- routers
 // PhiMoE::route score canonicalisation (src/layer.cu:50-55).
 __device__ __forceinline__ float quantise(float score, float quantum) {
@@ -524,29 +687,72 @@ __global__ __launch_bounds__(256) void combine_kernel(
     const int n = n_live;
     const bool vec = (d & 3) == 0;
     if (vec) {
+        // JU 16-byte columns per thread at once, 256 apart, and for the
+        // common two live slots both rows' loads (and the residual's) before
+        // any use: every load of a thread is in flight together (one memory
+        // latency per workgroup instead of one per column and slot)
         typedef float f4 __attribute__((ext_vector_type(4)));
+        constexpr int JU = 4;
         const int64_t d4 = d >> 2;
-        for (int64_t j = threadIdx.x; j < d4; j += blockDim.x) {
-            f4 acc = {0.f, 0.f, 0.f, 0.f};
-            for (int q = 0; q < n; ++q) {
-                f4 v = reinterpret_cast<const f4*>(out_rows + order_row[q] * d)[j];
+        auto row4 = [&](int q, int64_t j) __attribute__((always_inline)) -> f4 {
+            f4 v = reinterpret_cast<const f4*>(out_rows + order_row[q] * d)[j];
 #pragma unroll
-                for (int p = 1; p < PARTS; ++p) {
-                    const f4 u =
-                        reinterpret_cast<const f4*>(out_rows + p * part_stride + order_row[q] * d)[j];
+            for (int p = 1; p < PARTS; ++p) {
+                const f4 u = reinterpret_cast<const f4*>(out_rows + p * part_stride + order_row[q] * d)[j];
 #pragma unroll
-                    for (int c = 0; c < 4; ++c) v[c] = v[c] + u[c];
+                for (int c = 0; c < 4; ++c) v[c] = v[c] + u[c];
+            }
+            return v;
+        };
+        const f4 zero = {0.f, 0.f, 0.f, 0.f};
+        for (int64_t j0 = threadIdx.x; j0 < d4; j0 += int64_t(blockDim.x) * JU) {
+            f4 acc[JU], rv[JU];
+#pragma unroll
+            for (int u = 0; u < JU; ++u) {
+                const int64_t j = j0 + int64_t(u) * blockDim.x;
+                acc[u] = zero;
+                rv[u] = (resid != nullptr && j < d4) ? reinterpret_cast<const f4*>(resid + t * d)[j] : zero;
+            }
+            if (n == 2) {
+                f4 v0[JU], v1[JU];
+#pragma unroll
+                for (int u = 0; u < JU; ++u) {
+                    const int64_t j = j0 + int64_t(u) * blockDim.x;
+                    v0[u] = j < d4 ? row4(0, j) : zero;
+                    v1[u] = j < d4 ? row4(1, j) : zero;
                 }
-                const float wq = order_w[q];
+                const float w0 = order_w[0], w1 = order_w[1];
 #pragma unroll
-                for (int c = 0; c < 4; ++c) acc[c] = mac<CONTRACT>(acc[c], wq, v[c]);
-            }
-            if (resid != nullptr) {
-                const f4 rv = reinterpret_cast<const f4*>(resid + t * d)[j];
+                for (int u = 0; u < JU; ++u)
 #pragma unroll
-                for (int c = 0; c < 4; ++c) acc[c] = acc[c] + rv[c];
+                    for (int c = 0; c < 4; ++c) {
+                        acc[u][c] = mac<CONTRACT>(acc[u][c], w0, v0[u][c]);
+                        acc[u][c] = mac<CONTRACT>(acc[u][c], w1, v1[u][c]);
+                    }
+            } else {
+                for (int q = 0; q < n; ++q) {
+                    f4 v[JU];
+#pragma unroll
+                    for (int u = 0; u < JU; ++u) {
+                        const int64_t j = j0 + int64_t(u) * blockDim.x;
+                        v[u] = j < d4 ? row4(q, j) : zero;
+                    }
+                    const float wq = order_w[q];
+#pragma unroll
+                    for (int u = 0; u < JU; ++u)
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) acc[u][c] = mac<CONTRACT>(acc[u][c], wq, v[u][c]);
+                }
             }
-            reinterpret_cast<f4*>(y + t * d)[j] = acc;
+#pragma unroll
+            for (int u = 0; u < JU; ++u) {
+                const int64_t j = j0 + int64_t(u) * blockDim.x;
+                if (j >= d4) continue;
+                if (resid != nullptr)
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) acc[u][c] = acc[u][c] + rv[u][c];
+                reinterpret_cast<f4*>(y + t * d)[j] = acc[u];
+            }
         }
     } else {
         for (int64_t j = threadIdx.x; j < d; j += blockDim.x) {
@@ -573,7 +779,8 @@ void launch_gate_logits(const float* x, const float* w, float* logits,
     // The ring form for E <= 8 (16 token rows x 4 experts or 8 x 8 per wave).
     // At E = 16 a wave would hold 4 tokens and stream 16 expert rows for
     // them -- 4x the token bytes (measured 2.4x slower at the reference's
-    // layer shape) -- so E > 8 keeps the kernel above.
+    // layer shape) -- so E of 9-16 takes the workgroup ring below, whose 16
+    // expert rows serve 16 tokens.
     if (E <= 8 && d % 4 == 0 && d >= 4 && al(x) && al(w) && d * 16 * 4 < (int64_t(1) << 31)) {
         const int eb = E <= 4 ? 4 : 8;
         const dim3 grid(static_cast<unsigned>(ceil_div(T, 64 / eb)));
@@ -590,6 +797,17 @@ void launch_gate_logits(const float* x, const float* w, float* logits,
     }
     int eb = 8;
     while (eb < E && eb < 64) eb <<= 1;
+    // E of 9-16: the workgroup ring, when rows are 16-byte aligned and every
+    // load offset (16 token or expert rows) fits 31 bits
+    if (eb == 16 && d % 4 == 0 && d >= 4 && al(x) && al(w) && d * 16 * 4 < (int64_t(1) << 31)) {
+        const dim3 grid(static_cast<unsigned>(ceil_div(T, 16)), static_cast<unsigned>(ceil_div(E, 16)));
+        auto go = [&](auto kernel) {
+            hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, x, w, logits, T, d, E);
+        };
+        if (contract) go(gate_wg_ring_kernel<1, 16, 1, MOE_GATE_RING>);
+        else go(gate_wg_ring_kernel<0, 16, 1, MOE_GATE_RING>);
+        return;
+    }
     // 4 tokens per thread from 32 experts up (small E keeps one output per
     // thread: its rows per workgroup are already many, and the grid stays wide)
     const int tb = eb >= 32 ? 4 : 1;

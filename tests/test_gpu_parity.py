@@ -231,12 +231,18 @@ def test_silu_mul_bit_exact(ctx, torch, orc):
 @pytest.mark.parametrize("contract", [0, 1])
 # E <= 8 with 16-byte rows takes the ring kernel (64 x 512 x 4; 33 x 100 x 7:
 # a partial last stage and a one-token last wave; 4096 x 1024 x 8, config
-# 5's gate; 100 x 256 x 2: fewer experts than the lane block), the rest the
-# staged kernel (1037 x 4096 x 16: the reference's expert count with a
-# partial last workgroup; 45 x 196 x 11: a partial chunk, 5 experts masked)
+# 5's gate; 100 x 256 x 2: fewer experts than the lane block); E of 9-16 and
+# 33-64 with 16-byte rows the workgroup ring (300 x 4096 x 16 and 1037 x 4096
+# x 16: the reference's expert count, the latter with a partial last
+# workgroup; 45 x 196 x 11: a partial last stage, 5 experts masked; 1000 x
+# 2048 x 64; 77 x 452 x 100: two expert blocks, the second 36 wide, a
+# partial stage and a partial workgroup; 16 x 4 x 16: one 4-column stage);
+# the rest the staged kernel (70 x 130 x 130: rows of 130 floats; 5 x 1 x 3;
+# 50 x 1024 x 32)
 @pytest.mark.parametrize("T,d,E", [(64, 512, 4), (300, 4096, 16), (1000, 2048, 64),
                                    (33, 100, 7), (5, 1, 3), (70, 130, 130), (4096, 1024, 8),
-                                   (100, 256, 2), (1037, 4096, 16), (45, 196, 11)])
+                                   (100, 256, 2), (1037, 4096, 16), (45, 196, 11),
+                                   (77, 452, 100), (16, 4, 16), (50, 1024, 32)])
 def test_gate_logits_bit_exact(ctx, torch, orc, contract, T, d, E):
     print(f"gate {T}x{d}x{E} contract={contract}", flush=True)
     rng = np.random.default_rng(T + d + E)
