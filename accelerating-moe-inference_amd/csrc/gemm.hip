@@ -659,12 +659,15 @@ __device__ __forceinline__ void direct_tile(const GemmArgs& p, int mt, int nt, i
     static_assert(A_INS * NW == A_TOT || A_TOT < NW, "A load split");
     static_assert(B_INS * NW == B_TOT || B_TOT < NW, "B load split");
     constexpr int B_SIZE = NN ? B_TOT * NnB<BN>::STRIDE : BN * BK;
-    // NN with 4 column blocks per wave: block bj holds the columns
-    // 4 c + bj (c = lane % 32), so one 16-byte LDS read of a k-row gives a
-    // lane its B value for all 4 blocks (NN B sits k-major in LDS; with
-    // 32-column blocks each value would be a separate 4-byte read), and the
-    // epilogue writes 4 adjacent columns per lane.
-    constexpr bool NSTRIDE = NN && FN == 4;
+    // NN with 4 (or 2) column blocks per wave: block bj holds the columns
+    // FN c + bj (c = lane % 32), so one 16-byte (8-byte) LDS read of a k-row
+    // gives a lane its B value for all FN blocks (NN B sits k-major in LDS;
+    // with 32-column blocks each value would be a separate 4-byte read), and
+    // the epilogue writes FN adjacent columns per lane.
+#ifndef MOE_NN_STRIDE2
+#define MOE_NN_STRIDE2 1
+#endif
+    constexpr bool NSTRIDE = NN && (FN == 4 || (FN == 2 && MOE_NN_STRIDE2));
     __shared__ __align__(16) float As[2][BM * BK];
     __shared__ __align__(16) float Bs[2][NB][B_SIZE];
 
@@ -865,13 +868,23 @@ __device__ __forceinline__ void direct_tile(const GemmArgs& p, int mt, int nt, i
             }
         };
         auto read_b = [&](int nb, int q) {
-            if constexpr (NSTRIDE) {
+            if constexpr (NSTRIDE && FN == 4) {
 #pragma unroll
                 for (int s = 0; s < 4; ++s) {
                     const f32x4 v = *reinterpret_cast<const f32x4*>(
                         &Bcur[nb * B_SIZE + NnB<BN>::at(8 * lh + 4 * q + s, bcol0 + 4 * lr)]);
 #pragma unroll
                     for (int bj = 0; bj < 4; ++bj) b[nb][bj][q][s] = v[bj];
+                }
+                return;
+            } else if constexpr (NSTRIDE) {
+                typedef float f32x2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const f32x2 v = *reinterpret_cast<const f32x2*>(
+                        &Bcur[nb * B_SIZE + NnB<BN>::at(8 * lh + 4 * q + s, bcol0 + 2 * lr)]);
+#pragma unroll
+                    for (int bj = 0; bj < 2; ++bj) b[nb][bj][q][s] = v[bj];
                 }
                 return;
             }
@@ -1115,28 +1128,29 @@ __device__ __forceinline__ void direct_tile(const GemmArgs& p, int mt, int nt, i
     }
 
     if constexpr (NSTRIDE) {
-        // 4 adjacent columns per lane and row: one 16-byte store when they
-        // all lie inside N and the row start is 16-byte aligned
-        const int64_t nc = n0 + bcol0 + 4 * lr;
-        const bool vec4 = nc + 3 < N && p.ldc % 4 == 0 && p.c_split_stride % 4 == 0 &&
-                          (reinterpret_cast<uintptr_t>(Cb) & 15) == 0;
+        // FN adjacent columns per lane and row: one 4 FN-byte store when they
+        // all lie inside N and the row start is aligned to it
+        typedef float f32xw __attribute__((ext_vector_type(FN)));
+        const int64_t nc = n0 + bcol0 + FN * lr;
+        const bool vecw = nc + FN - 1 < N && p.ldc % FN == 0 && p.c_split_stride % FN == 0 &&
+                          (reinterpret_cast<uintptr_t>(Cb) & (4 * FN - 1)) == 0;
 #pragma unroll
         for (int bi = 0; bi < FM; ++bi)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int i = arow0 + bi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
                 if (i >= rows) continue;
-                if (vec4) {
-                    f32x4 v;
+                if (vecw) {
+                    f32xw v;
 #pragma unroll
-                    for (int bj = 0; bj < 4; ++bj) {
+                    for (int bj = 0; bj < FN; ++bj) {
                         v[bj] = acc[0][bi][bj][r];
                         if (EPI == EPI_BIAS && p.bias != nullptr) v[bj] = v[bj] + p.bias[nc + bj];
                     }
-                    *reinterpret_cast<f32x4*>(&Cb[split * p.c_split_stride + (row0 + i) * p.ldc + nc]) = v;
+                    *reinterpret_cast<f32xw*>(&Cb[split * p.c_split_stride + (row0 + i) * p.ldc + nc]) = v;
                 } else {
 #pragma unroll
-                    for (int bj = 0; bj < 4; ++bj)
+                    for (int bj = 0; bj < FN; ++bj)
                         if (nc + bj < N)
                             epi_store<EPI>(p, Cb, split, row0 + i, nc + bj, acc[0][bi][bj][r],
                                            acc[NB - 1][bi][bj][r]);
