@@ -1,7 +1,7 @@
 """Benchmark of the MoE layer forward on one MI355X.
 
     python bench.py [--steps K] [--warmup W] [--config c3|c4|c5|ref] [--block]
-                    [--cpu-seconds S]
+                    [--cpu-seconds S] [--no-extra]
     python bench.py --sgemm        (config 2: the SGEMM sweep, a line per shape)
     python bench.py --decoder      (config 5: the whole 4-layer decoder prefill)
     python bench.py --dropin       (the C++ drop-in PhiMoE::forward, host tensors,
@@ -20,7 +20,9 @@ Prints ONE JSON line: tokens/s of the whole layer, the roofline of the
 dominant kernel (the grouped w1/w3 SwiGLU GEMM, fp32 MFMA bound) measured
 with HIP events on the stream the kernels run on, and the CPU path (the
 oracle restatement of the reference's PhiMoE::forward) timed on a bounded
-token sample on this host's cores.
+token sample on this host's cores.  The default run (config 3) then times
+the other layer shapes (config 5's MoE FFN, the reference's own layer,
+config 4) the same way, without CPU legs, under `other_layer_shapes`.
 """
 from __future__ import annotations
 
@@ -610,6 +612,8 @@ def main():
     ap.add_argument("--model", action="store_true",
                     help="the C++ drop-in PhiTinyMoEModel::generate on the reference's model "
                          "shape (32 layers; writes a ~15 GiB model.bin to a temporary directory)")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="config 3: skip timing the other layer shapes after the headline")
     ap.add_argument("--dropin", action="store_true",
                     help="the C++ drop-in PhiMoE::forward at the reference's layer shape, host "
                          "tensors in and out (PCIe-inclusive)")
@@ -642,62 +646,12 @@ def main():
         T = args.tokens  # a batch-size point of the configuration's layer shape
     pkg = load_pkg()
     dev = torch.device("cuda:0")
-    g = torch.Generator(device=dev).manual_seed(0)
-    x = torch.randn((T, d), device=dev, generator=g)
-    weights = {
-        "gate_w": torch.randn((E, d), device=dev, generator=g) * 0.02,
-        "w1": torch.randn((E, d_ff, d), device=dev, generator=g) * 0.02,
-        "w3": torch.randn((E, d_ff, d), device=dev, generator=g) * 0.02,
-        "w2": torch.randn((E, d, d_ff), device=dev, generator=g) * 0.02,
-        "expert_bias": None,
-    }
-    if cfg["zipf"] is not None:
-        weights["expert_bias"] = torch.from_numpy(zipf_bias(E, cfg["zipf"])).to(dev)
     rms = cfg["norm"] == "rms"
-    if args.block:
-        weights["norm_w"] = 1 + 0.1 * torch.randn(d, device=dev, generator=g)
-        weights["norm_b"] = None if rms else 0.1 * torch.randn(d, device=dev, generator=g)
-    y = torch.empty((T, d), device=dev)
-    idx = torch.empty((T, k), dtype=torch.int32, device=dev)
-    w = torch.empty((T, k), device=dev)
-    desc = pkg.make_desc(T, d, E, k, d_ff, act=pkg.ACT_SWIGLU,
-                         router=(pkg.ROUTER_PHI_QUANT if cfg.get("router") == "phi_quant"
-                                 else pkg.ROUTER_SOFTMAX_TOPK), contract=pkg.CONTRACT_FMA,
-                         norm=(pkg.NORM_RMS if rms else pkg.NORM_LAYER) if args.block
-                         else pkg.NORM_NONE,
-                         norm_eps=NORM_EPS, residual=args.block)
+    x, weights, y, idx, w, desc = build_layer(pkg, cfg, T, args.block, dev)
     ctx = pkg.Context(0)
     ctx.reserve(desc)
-
-    # spin-up: the GPU takes about a second of load to reach its full clock
-    # (durations of short layers fall 10-20 % over the first second), so
-    # forwards run for at least SPINUP_S before the warm-up steps
-    spin_steps, t_spin = 0, time.perf_counter()
-    while time.perf_counter() - t_spin < SPINUP_S:
-        ctx.layer_forward(desc, weights, x, y, idx, w)
-        torch.cuda.synchronize()
-        spin_steps += 1
-    for _ in range(args.warmup):
-        ctx.layer_forward(desc, weights, x, y, idx, w)
-    torch.cuda.synchronize()
-    # the timed steps: no per-kernel events
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        ctx.layer_forward(desc, weights, x, y, idx, w)
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    # an instrumented pass of as many steps: HIP events around every launch,
-    # on the stream the kernels run on (per-kernel times and the roofline)
-    ctx.reset_timing()
-    ctx.set_timing(True)
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    for _ in range(args.steps):
-        ctx.layer_forward(desc, weights, x, y, idx, w)
-    torch.cuda.synchronize()
-    instrumented = time.perf_counter() - t1
-    ctx.set_timing(False)
-    kt = ctx.kernel_times()
+    spin_steps, elapsed, instrumented, kt = time_layer(ctx, desc, weights, x, y, idx, w,
+                                                       args.warmup, args.steps)
 
     ms_per_step = 1e3 * elapsed / args.steps
     tokens_per_s = T * args.steps / elapsed
@@ -775,7 +729,106 @@ def main():
         out["speedup_vs_reference_gpu_gemms"] = {
             n: round(REF_GEMM_MS[n] / avg[n], 2) for n in REF_GEMM_MS if n in avg}
     ctx.close()
+    if args.config == "c3" and args.tokens is None and not args.block and not args.no_extra:
+        # the other layer shapes of the configurations, timed the same way in
+        # this run (no CPU leg): the short-K expert GEMMs of config 5 and of the
+        # reference's own layer, and config 4's skewed 64 experts
+        del x, weights, y, idx, w
+        torch.cuda.empty_cache()
+        out["other_layer_shapes"] = {c: layer_point(pkg, c, dev, args.warmup, min(args.steps, 10))
+                                     for c in ("c5", "ref", "c4")}
     print(json.dumps(out))
+
+
+def build_layer(pkg, cfg, T, block, dev):
+    """Seeded inputs, weights, outputs and the descriptor of one layer shape."""
+    import torch
+    d, E, k, d_ff = cfg["d"], cfg["E"], cfg["k"], cfg["d_ff"]
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn((T, d), device=dev, generator=g)
+    weights = {
+        "gate_w": torch.randn((E, d), device=dev, generator=g) * 0.02,
+        "w1": torch.randn((E, d_ff, d), device=dev, generator=g) * 0.02,
+        "w3": torch.randn((E, d_ff, d), device=dev, generator=g) * 0.02,
+        "w2": torch.randn((E, d, d_ff), device=dev, generator=g) * 0.02,
+        "expert_bias": None,
+    }
+    if cfg["zipf"] is not None:
+        weights["expert_bias"] = torch.from_numpy(zipf_bias(E, cfg["zipf"])).to(dev)
+    rms = cfg["norm"] == "rms"
+    if block:
+        weights["norm_w"] = 1 + 0.1 * torch.randn(d, device=dev, generator=g)
+        weights["norm_b"] = None if rms else 0.1 * torch.randn(d, device=dev, generator=g)
+    y = torch.empty((T, d), device=dev)
+    idx = torch.empty((T, k), dtype=torch.int32, device=dev)
+    w = torch.empty((T, k), device=dev)
+    desc = pkg.make_desc(T, d, E, k, d_ff, act=pkg.ACT_SWIGLU,
+                         router=(pkg.ROUTER_PHI_QUANT if cfg.get("router") == "phi_quant"
+                                 else pkg.ROUTER_SOFTMAX_TOPK), contract=pkg.CONTRACT_FMA,
+                         norm=(pkg.NORM_RMS if rms else pkg.NORM_LAYER) if block
+                         else pkg.NORM_NONE,
+                         norm_eps=NORM_EPS, residual=block)
+    return x, weights, y, idx, w, desc
+
+
+def time_layer(ctx, desc, weights, x, y, idx, w, warmup, steps):
+    """Spin-up, warm-up, `steps` timed forwards without per-kernel events,
+    then as many with HIP events around every launch (on the stream the
+    kernels run on).  Returns (spin-up forwards, timed seconds, instrumented
+    seconds, per-kernel times)."""
+    import torch
+    # spin-up: the GPU takes about a second of load to reach its full clock
+    # (durations of short layers fall 10-20 % over the first second), so
+    # forwards run for at least SPINUP_S before the warm-up steps
+    spin_steps, t_spin = 0, time.perf_counter()
+    while time.perf_counter() - t_spin < SPINUP_S:
+        ctx.layer_forward(desc, weights, x, y, idx, w)
+        torch.cuda.synchronize()
+        spin_steps += 1
+    for _ in range(warmup):
+        ctx.layer_forward(desc, weights, x, y, idx, w)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        ctx.layer_forward(desc, weights, x, y, idx, w)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ctx.reset_timing()
+    ctx.set_timing(True)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    for _ in range(steps):
+        ctx.layer_forward(desc, weights, x, y, idx, w)
+    torch.cuda.synchronize()
+    instrumented = time.perf_counter() - t1
+    ctx.set_timing(False)
+    return spin_steps, elapsed, instrumented, ctx.kernel_times()
+
+
+def layer_point(pkg, name, dev, warmup, steps):
+    """One configuration's layer timed as the headline one is: tokens/s, the
+    expert GEMMs' fraction of the fp32 MFMA peak, the w1/w3 roofline."""
+    import torch
+    cfg = CONFIGS[name]
+    T, d, k, d_ff = cfg["T"], cfg["d"], cfg["k"], cfg["d_ff"]
+    x, weights, y, idx, w, desc = build_layer(pkg, cfg, T, False, dev)
+    ctx = pkg.Context(0)
+    ctx.reserve(desc)
+    _, elapsed, _, kt = time_layer(ctx, desc, weights, x, y, idx, w, warmup, steps)
+    ctx.close()
+    avg = {n: ms / c for n, (ms, c) in kt.items()}
+    pairs = T * k
+    f13, f2 = 2.0 * pairs * d * d_ff * 2, 2.0 * pairs * d_ff * d
+    w13, w2 = avg["expert_w13_swiglu"], avg["expert_w2"]
+    del x, weights, y, idx, w
+    torch.cuda.empty_cache()
+    return {"workload": cfg["workload"], "tokens": T, "ms_per_step": round(1e3 * elapsed / steps, 4),
+            "tokens_per_s": round(T * steps / elapsed),
+            "expert_gemm_frac_fp32_mfma_peak":
+                round((f13 + f2) / ((w13 + w2) * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4),
+            "w13_frac_fp32_mfma_peak": round(f13 / (w13 * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4),
+            "kernel_avg_ms": {"expert_w13_swiglu": round(w13, 4), "expert_w2": round(w2, 4)},
+            "steps": steps}
 
 
 if __name__ == "__main__":
