@@ -448,9 +448,15 @@ void launch(const float* x, const float* w, const float* b, int64_t rows, int64_
                          (y == nullptr || (aligned16(y) && aligned16(w) && (RMS || aligned16(b))));
     if (aligned && kResidentFloats / hs < kRingBelowRows &&
         int64_t(32) * h * 4 < (int64_t(1) << 31)) {
-        // rows per wave: enough waves for every CU to hold several
+        // rows per wave: enough waves for every CU to hold several (measured
+        // on MI355X: 8 rows per wave beat 16 by 1-4 % from 4,096 to 16,384
+        // rows of 2048-4096 floats, and 32 by 7-20 %)
         const int64_t c = cus > 0 ? cus : 256;
-        const int G = rows >= 32 * 4 * c ? 32 : (rows >= 16 * 2 * c ? 16 : 8);
+#ifndef MOE_NORM_RING_G
+#define MOE_NORM_RING_G 0
+#endif
+        int G = rows >= 32 * 4 * c ? 32 : 8;
+        if (MOE_NORM_RING_G == 8 || MOE_NORM_RING_G == 16 || MOE_NORM_RING_G == 32) G = MOE_NORM_RING_G;
         const dim3 grid(static_cast<unsigned>(ceil_div(rows, G)));
         auto go = [&](auto kernel) {
             hipLaunchKernelGGL(kernel, grid, dim3(64), 0, s, x, w, b, rows, h, eps, row_mean,

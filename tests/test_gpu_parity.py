@@ -588,9 +588,9 @@ def test_layer_reference_shape_full_size(ctx, pkg, torch, orc):
 # ------------------------------------------------------------- layer norm
 @pytest.mark.parametrize("contract", [0, 1])
 # rows held in LDS (whole rows per workgroup, 16-byte and scalar paths, h up
-# to 1260 when aligned); wider aligned rows stream through the ring kernel with 8, 16 or
-# 32 rows per wave (65 x 4096 and 3 x 30000: 8, a one-row last wave and a
-# partial last stage; 8200 x 2600: 16; 32800 x 2528: 32); 2 x 30001, wide
+# to 1260 when aligned); wider aligned rows stream through the ring kernel with 8 or 32
+# rows per wave (65 x 4096 and 3 x 30000: 8, a one-row last wave and a
+# partial last stage; 8200 x 2600: 8 over many waves; 32800 x 2528: 32); 2 x 30001, wide
 # and unaligned, takes the register-staged streaming pair
 @pytest.mark.parametrize("rows,h", [(1, 1), (3, 5), (64, 64), (65, 4096), (200, 1000),
                                     (130, 33), (4096, 1024), (70, 20220), (3, 30000),
