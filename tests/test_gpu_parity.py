@@ -431,9 +431,13 @@ def test_expert_ffn_gather_past_2gib(ctx, torch, orc):
 
 
 @pytest.mark.parametrize("contract", [0, 1])
-def test_combine_bit_exact(ctx, torch, orc, contract):
-    rng = np.random.default_rng(11)
-    T, k, d = 500, 8, 260
+# k = 2 (the two-slot path) with whole and partial column chunks, any other k
+# in expert order, rows of d % 4 != 0 (scalar columns), k up to 32
+@pytest.mark.parametrize("T,k,d", [(500, 8, 260), (300, 2, 4096), (129, 2, 1030), (77, 1, 64),
+                                   (50, 32, 131), (40, 3, 4100), (3, 2, 1)])
+def test_combine_bit_exact(ctx, torch, orc, contract, T, k, d):
+    print(f"combine T={T} k={k} d={d} contract={contract}", flush=True)
+    rng = np.random.default_rng(11 + T + k + d)
     topk = _rand_topk(rng, T, 64, k)
     roff, rperm, rinv = orc.permute(topk, 64)
     rows = normal(rng, (T * k, d))
