@@ -379,11 +379,13 @@ def test_rope_rows_at_explicit_positions(ctx, torch, orc):
 
 
 @pytest.mark.parametrize("window", [None, 4])
-def test_attention_paths_over_a_trie_bit_exact(ctx, torch, orc, window):
+@pytest.mark.parametrize("H,KVH,hd", [(4, 2, 32), (16, 4, 128), (2, 2, 64)])
+def test_attention_paths_over_a_trie_bit_exact(ctx, torch, orc, window, H, KVH, hd):
     # sequences with shared prefixes (and one that is a prefix of another):
-    # every node's result equals the oracle's attention over its sequence
+    # every node's result equals the oracle's attention over its sequence;
+    # (16, 4, 128) is Phi-tiny-MoE's head layout, (2, 2, 64) another
+    # compile-time head_dim
     rng = np.random.default_rng(32)
-    H, KVH, hd = 4, 2, 32
     base = rng.integers(0, 50, 30)
     seqs = [base[:30], base[:12], np.concatenate([base[:12], [7, 8, 9]]), base[:5],
             rng.integers(0, 50, 21), np.concatenate([base[:20], rng.integers(0, 50, 9)])]
