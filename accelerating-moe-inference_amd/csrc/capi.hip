@@ -128,6 +128,10 @@ struct DensePlan {
     int tile = 0, splits = 1;
 };
 
+#ifndef MOE_DENSE_KW_PLAN
+#define MOE_DENSE_KW_PLAN 1  // 0: the planner never deals the K-group tile (tuning builds)
+#endif
+
 constexpr int64_t kDenseSplitBytes = int64_t(512) << 20;  // cap on the partials
 
 DensePlan plan_dense(moe_ctx* ctx, bool nn, bool direct, int64_t M, int64_t N, int64_t K) {
@@ -145,7 +149,7 @@ DensePlan plan_dense(moe_ctx* ctx, bool nn, bool direct, int64_t M, int64_t N, i
     // workgroup alone on its CU (4096 x 1024 x 1024: 128 x 128 tiles, one
     // per CU, 95.6 us; 64 x 128 tiles, two per CU, 87.4 us)
     // (tile 3, NN only, reads its B fragments 16 bytes at a time: the NT rate)
-    static constexpr double kEff[moe::kDenseTiles] = {0.80, 0.80, 0.50, 0.86};
+    static constexpr double kEff[moe::kDenseTiles] = {0.80, 0.80, 0.50, 0.86, 0.0, 0.0};
     constexpr double kStageLatency = 0.6e-6, kRound = 1e-6, kHbm = 5.0e12, kLaunch = 2e-6,
                      kReduce = 2e-6, kSolo = 1.15;
     // each tile shape runs 4 waves, one per SIMD
@@ -167,9 +171,29 @@ DensePlan plan_dense(moe_ctx* ctx, bool nn, bool direct, int64_t M, int64_t N, i
         if (env_splits > 0 && split_ok(env_splits)) best.splits = env_splits;
         return best;
     }
+    // The K-group tile (32 x 128, K split among the waves of one workgroup)
+    // where its tiles give 3/4 to all of the CUs one workgroup each and the
+    // model's best plan would split K into a second launch (1024^3; with
+    // fewer tiles, as at 512 x 1024 x 1024, the split plans that fill every
+    // CU measured 15-50 % faster; at K = 2048 and 4096 the split plans were
+    // 3-20 % faster, their reduction spread over longer K): it needs the
+    // ring, so its buffer-load offsets (from the tile's first A row; from B's
+    // first row (NT) or column (NN)) must fit 31 bits, as the launch checks,
+    // and K whole steps per group.  The cost model below does not weigh it:
+    // its HBM term counts B once per m-tile, which the L2 and Infinity Cache
+    // serve at these sizes.
+    const moe::GemmTile kwt = moe::dense_tile(moe::kDenseKwTile);
+    const int kwg = moe::dense_tile_groups(moe::kDenseKwTile);
+    const bool kw_ok = MOE_DENSE_KW_PLAN && (env_tile < 0 || env_tile == moe::kDenseKwTile) && M >= 128 &&
+                       K % (16 * kwg) == 0 && K / kwg >= 256 && K / kwg <= 512 &&
+                       moe::ceil_div(M, kwt.bm) * moe::ceil_div(N, kwt.bn) <= ctx->cus &&
+                       moe::ceil_div(M, kwt.bm) * moe::ceil_div(N, kwt.bn) * 4 >= 3 * ctx->cus &&
+                       int64_t(kwt.bm + 1) * K * 4 < (int64_t(1) << 31) &&
+                       (nn ? (K + 16) * N * 4 + int64_t(kwt.bn) * 4
+                           : int64_t(kwt.bn + 1) * K * 4) < (int64_t(1) << 31);
     for (int t = 0; t < moe::kDenseTiles; ++t) {
         if (env_tile >= 0 && t != env_tile) continue;
-
+        if (t == moe::kSkinnyTile || t == moe::kDenseKwTile) continue;  // weighed apart
         if (t == 3 && !nn) continue;  // the 256 x 128 tile is NN only
         int& occ = ctx->dense_blocks_per_cu[nn ? 1 : 0][t];
         if (occ == 0) occ = moe::dense_blocks_per_cu(t, nn);
@@ -209,6 +233,10 @@ DensePlan plan_dense(moe_ctx* ctx, bool nn, bool direct, int64_t M, int64_t N, i
                 best.splits = S;
             }
         }
+    }
+    if (kw_ok && (best.splits > 1 || env_tile == moe::kDenseKwTile)) {
+        best.tile = moe::kDenseKwTile;
+        best.splits = 1;
     }
     return best;
 }

@@ -64,14 +64,20 @@ constexpr int kMaxW2Splits = 4;  // split-K of the layer's w2 (partials summed b
 
 // Dense SGEMM tile shapes, GemmArgs::tile: 0 = 128x128 (any shape), 1 =
 // 64x128 and 2 = 32x128 (direct-load path only: 16-byte aligned rows,
-// K % 16 == 0, and for NN N % 4 == 0), 3 = 256x128 (NN only, direct path).
-constexpr int kDenseTiles = 4;
+// K % 16 == 0, and for NN N % 4 == 0), 3 = 256x128 (NN only, direct path),
+// 5 = 32x128 with K groups (direct ring path, K a multiple of 16 x groups,
+// no K split, operands under 2 GiB).  Ids below kDenseTiles; 4 is the skinny
+// kernel.
+constexpr int kDenseTiles = 6;
 // GemmArgs::tile of the skinny dense kernel (M <= 64, direct rows only; not
-// one of the kDenseTiles tile shapes).
+// one of the tile shapes the planner's tile loop weighs).
 constexpr int kSkinnyTile = 4;
+constexpr int kDenseKwTile = 5;
 GemmTile dense_tile(int tile);
 // Workgroups of dense tile shape `tile` (direct-load kernel) one CU holds at once.
 int dense_blocks_per_cu(int tile, bool nn);
+// K groups of a dense tile shape (1, or the K-group tiles' count).
+int dense_tile_groups(int tile);
 constexpr int kMaxDenseSplits = 16;  // split-K of a dense SGEMM (partials in the workspace)
 
 // Routing constants.

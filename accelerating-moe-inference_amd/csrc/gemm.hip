@@ -106,10 +106,15 @@ constexpr int ring_stages(int sched) {
     return (sched & SCHED_RING3) == 0 ? 0 : (((sched >> 8) & 15) != 0 ? (sched >> 8) & 15 : 3);
 }
 
-template <int BM_, int BN_, int BK_, int WM_, int WN_>
+// KW_ > 1 (direct ring path, dense, no stream-K): KW groups of WM x WN
+// waves share the tile and split its K steps evenly (group g takes the g-th
+// run of K steps, each group with its own ring stages); at the end the other
+// groups' accumulators are added, through LDS, to group 0's, which writes the
+// tile.  A workgroup alone on its CU then still has KW waves per SIMD.
+template <int BM_, int BN_, int BK_, int WM_, int WN_, int KW_ = 1>
 struct Cfg {
-    static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
-    static constexpr int THREADS = 64 * WM * WN;
+    static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_, KW = KW_;
+    static constexpr int THREADS = 64 * WM * WN * KW;
     static constexpr int FM = BM / WM / 32;   // 32x32 blocks per wave along m
     static constexpr int FN = BN / WN / 32;   // ... along n (per B operand)
     static constexpr int LDS = BK + 4;        // LDS row stride in floats
@@ -119,8 +124,8 @@ struct Cfg {
     static_assert(FM >= 1 && FN >= 1 && BM % (32 * WM) == 0 && BN % (32 * WN) == 0, "tile");
     static_assert(BK % 16 == 0, "K step is a multiple of 16");
     // the register-staged kernel deals whole 16-byte chunks to every thread
-    static constexpr bool STAGED = A_LD * THREADS == BM * KQ && B_LD * THREADS == BN * KQ &&
-                                   A_LD >= 1 && B_LD >= 1;
+    static constexpr bool STAGED = KW == 1 && A_LD * THREADS == BM * KQ &&
+                                   B_LD * THREADS == BN * KQ && A_LD >= 1 && B_LD >= 1;
 };
 
 template <int ID> struct CfgOf;
@@ -142,6 +147,16 @@ template <> struct CfgOf<10> { using T = Cfg<256, 64, 16, 4, 1>; };
 // Dense NN on 256 rows x 128 columns, each wave 64 rows x all 128 columns
 // (4 32 x 32 blocks): its B fragments are read column-strided (below).
 template <> struct CfgOf<11> { using T = Cfg<256, 128, 16, 4, 1>; };
+// Dense 32 x 128 with two K groups: 8 waves, each 32 rows x 32 columns over
+// half of K -- for products whose 32 x 128 tiles give each CU one workgroup
+// (measured on MI355X at 1024^3: 29.6-30.4 us NT, 32.7-33.2 NN, against 32.2
+// and 34.2 for the best tile and split plan; four groups, 16 waves, 29.4 and
+// 31.4 us but slower on every larger shape; two groups on the 64 x 128 tile
+// no faster than that tile's plans).
+#ifndef MOE_DENSE_KW
+#define MOE_DENSE_KW 2
+#endif
+template <> struct CfgOf<12> { using T = Cfg<32, 128, 16, 1, 4, MOE_DENSE_KW>; };
 
 // Workgroup ids are dealt round-robin over the XCDs.  Renumber them so each
 // XCD works through a contiguous run of logical tiles: tiles that share an
@@ -647,7 +662,8 @@ __device__ __forceinline__ void direct_tile(const GemmArgs& p, int mt, int nt, i
                                             int64_t seg_lo, int64_t seg_hi, float* part) {
     constexpr int BM = C::BM, BN = C::BN, BK = C::BK;
     constexpr int FM = C::FM, FN = C::FN;
-    constexpr int NW = C::THREADS / 64;
+    constexpr int KW = C::KW;
+    constexpr int NW = C::THREADS / 64 / KW;  // waves per K group
     // 1 KiB load instructions per tile (16 rows x 16 k, or 256 floats of an
     // NN B tile), dealt to the waves: INS per wave, the last ones idle when
     // the tile has fewer instructions than waves.
@@ -673,7 +689,10 @@ __device__ __forceinline__ void direct_tile(const GemmArgs& p, int mt, int nt, i
 
     int tid = threadIdx.x;
     if constexpr (LOOPED) asm volatile("" : "+v"(tid));
-    const int lane = tid & 63, wave = tid >> 6;
+    // wave: this wave's index in its K group wk (the load dealing, the
+    // quadrant and the epilogue are per group)
+    const int lane = tid & 63, wk = (tid >> 6) / NW, wave = (tid >> 6) % NW;
+    static_assert(KW == 1 || (!GROUPED && !LOOPED), "K groups: dense, one tile per workgroup");
 
     int64_t row0;
     int rows;
@@ -724,6 +743,14 @@ __device__ __forceinline__ void direct_tile(const GemmArgs& p, int mt, int nt, i
             lo = lo > 0 ? (lo / 16) * 16 : 0;
             kbeg = kbeg > lo ? kbeg : lo;
         }
+    }
+    if constexpr (KW > 1) {
+        // group wk: the wk-th of KW equal runs of the K steps (the host keeps
+        // the step count a multiple of KW, so every group meets the same
+        // barriers)
+        const int64_t per = (K - kbeg) / BK / KW;
+        kbeg += wk * per * BK;
+        K = kbeg + per * BK;
     }
 
     // Per-lane source of each load instruction: instruction j of this wave
@@ -973,32 +1000,34 @@ __device__ __forceinline__ void direct_tile(const GemmArgs& p, int mt, int nt, i
     constexpr int RS = ring_stages(SCHED);
     static_assert(!RING || (RS >= 3 && RS <= 8), "ring stages");
     static_assert(!RING || (RS - 2) * LPS_MAX <= 63, "vmcnt range");
-    constexpr int SA = BM * BK, SB = NB * B_SIZE;
-    __shared__ __align__(16) float RA0[SA], RA1[SA], RA2[SA], RA3[RS > 3 ? SA : 1],
-        RA4[RS > 4 ? SA : 1], RA5[RS > 5 ? SA : 1], RA6[RS > 6 ? SA : 1], RA7[RS > 7 ? SA : 1];
-    __shared__ __align__(16) float RB0[SB], RB1[SB], RB2[SB], RB3[RS > 3 ? SB : 1],
-        RB4[RS > 4 ? SB : 1], RB5[RS > 5 ? SB : 1], RB6[RS > 6 ? SB : 1], RB7[RS > 7 ? SB : 1];
+    // each stage array holds the KW groups' stages side by side
+    constexpr int SA = BM * BK, SB = NB * B_SIZE, KSA = KW * SA, KSB = KW * SB;
+    __shared__ __align__(16) float RA0[KSA], RA1[KSA], RA2[KSA], RA3[RS > 3 ? KSA : 1],
+        RA4[RS > 4 ? KSA : 1], RA5[RS > 5 ? KSA : 1], RA6[RS > 6 ? KSA : 1], RA7[RS > 7 ? KSA : 1];
+    __shared__ __align__(16) float RB0[KSB], RB1[KSB], RB2[KSB], RB3[RS > 3 ? KSB : 1],
+        RB4[RS > 4 ? KSB : 1], RB5[RS > 5 ? KSB : 1], RB6[RS > 6 ? KSB : 1], RB7[RS > 7 ? KSB : 1];
+    const int ga = KW > 1 ? wk * SA : 0, gb = KW > 1 ? wk * SB : 0;
     auto ra = [&](auto u) -> float* {
         constexpr int U = decltype(u)::value;
-        if constexpr (U == 0) return RA0;
-        else if constexpr (U == 1) return RA1;
-        else if constexpr (U == 2) return RA2;
-        else if constexpr (U == 3) return RA3;
-        else if constexpr (U == 4) return RA4;
-        else if constexpr (U == 5) return RA5;
-        else if constexpr (U == 6) return RA6;
-        else return RA7;
+        if constexpr (U == 0) return RA0 + ga;
+        else if constexpr (U == 1) return RA1 + ga;
+        else if constexpr (U == 2) return RA2 + ga;
+        else if constexpr (U == 3) return RA3 + ga;
+        else if constexpr (U == 4) return RA4 + ga;
+        else if constexpr (U == 5) return RA5 + ga;
+        else if constexpr (U == 6) return RA6 + ga;
+        else return RA7 + ga;
     };
     auto rb = [&](auto u) -> float* {
         constexpr int U = decltype(u)::value;
-        if constexpr (U == 0) return RB0;
-        else if constexpr (U == 1) return RB1;
-        else if constexpr (U == 2) return RB2;
-        else if constexpr (U == 3) return RB3;
-        else if constexpr (U == 4) return RB4;
-        else if constexpr (U == 5) return RB5;
-        else if constexpr (U == 6) return RB6;
-        else return RB7;
+        if constexpr (U == 0) return RB0 + gb;
+        else if constexpr (U == 1) return RB1 + gb;
+        else if constexpr (U == 2) return RB2 + gb;
+        else if constexpr (U == 3) return RB3 + gb;
+        else if constexpr (U == 4) return RB4 + gb;
+        else if constexpr (U == 5) return RB5 + gb;
+        else if constexpr (U == 6) return RB6 + gb;
+        else return RB7 + gb;
     };
     // The K loop for a burst over NBLK blocks (NBLK < 0: over the live ones,
     // chosen per step).  Blocks whose 32 rows all lie past the tile's last
@@ -1126,7 +1155,55 @@ __device__ __forceinline__ void direct_tile(const GemmArgs& p, int mt, int nt, i
     } else {
         k_loop(std::integral_constant<int, -1>{});
     }
-
+    if constexpr (KW > 1) {
+        static_assert(RING, "K groups run on the ring path");
+        // Groups 1 .. KW - 1 put their accumulators in LDS, in the stage
+        // arrays RB0 and RB1 (every wave's loads have landed and every
+        // fragment read has ended at the barrier below), then group 0 adds
+        // them to its own in group order -- K's first run, then the next --
+        // and writes the tile.  Slot (g - 1) * NW + wave of PER_WAVE floats:
+        // the first SLOTS in RB0, the rest in RB1.
+        constexpr int PER_WAVE = NB * FM * FN * 16 * 64;  // floats
+        constexpr int SLOTS = KSB / PER_WAVE;
+        static_assert(2 * SLOTS >= (KW - 1) * NW, "reduction space");
+        auto slot = [&](int g) -> float* {
+            const int L = (g - 1) * NW + wave;
+            return L < SLOTS ? RB0 + L * PER_WAVE : RB1 + (L - SLOTS) * PER_WAVE;
+        };
+        __syncthreads();
+        if (wk > 0) {
+            float* red = slot(wk);
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                for (int bi = 0; bi < FM; ++bi)
+#pragma unroll
+                    for (int bj = 0; bj < FN; ++bj)
+#pragma unroll
+                        for (int r4 = 0; r4 < 4; ++r4)
+                            reinterpret_cast<f32x4*>(red)[(((nb * FM + bi) * FN + bj) * 4 + r4) * 64 + lane] =
+                                f32x4{acc[nb][bi][bj][4 * r4], acc[nb][bi][bj][4 * r4 + 1],
+                                      acc[nb][bi][bj][4 * r4 + 2], acc[nb][bi][bj][4 * r4 + 3]};
+        }
+        __syncthreads();
+        if (wk > 0) return;  // no barrier follows
+        for (int g = 1; g < KW; ++g) {
+            const float* red = slot(g);
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                for (int bi = 0; bi < FM; ++bi)
+#pragma unroll
+                    for (int bj = 0; bj < FN; ++bj)
+#pragma unroll
+                        for (int r4 = 0; r4 < 4; ++r4) {
+                            const f32x4 v = reinterpret_cast<const f32x4*>(
+                                red)[(((nb * FM + bi) * FN + bj) * 4 + r4) * 64 + lane];
+#pragma unroll
+                            for (int c = 0; c < 4; ++c) acc[nb][bi][bj][4 * r4 + c] += v[c];
+                        }
+        }
+    }
     if constexpr (NSTRIDE) {
         // FN adjacent columns per lane and row: one 4 FN-byte store when they
         // all lie inside N and the row start is aligned to it
@@ -1474,14 +1551,26 @@ void launch_cfg(const GemmArgs& a, bool vec, hipStream_t s) {
         if (vec && b_ok && a.K % 16 == 0 && a.k_split_len % 16 == 0) {
             const dim3 grid(static_cast<unsigned>(a.m_tiles) * static_cast<unsigned>(a.n_tiles) *
                             static_cast<unsigned>(a.k_splits));
-            if (!(SCHED & SCHED_BUFLDS) || buf_offsets_fit(a, C::BM, C::BN, NN, GROUPED))
+            const bool fits = buf_offsets_fit(a, C::BM, C::BN, NN, GROUPED);
+            if constexpr (C::KW > 1) {
+                // K groups: the ring path only, every group the same K steps
+                static_assert((SCHED & SCHED_BUFLDS) && (SCHED & SCHED_RING3), "K groups need the ring");
+                if (!fits || a.k_splits != 1 || (a.K / 16) % C::KW != 0)
+                    throw Unsupported("K-group GEMM tile: operands past 2 GiB or K steps not a "
+                                      "multiple of the groups");
                 hipLaunchKernelGGL((gemm_direct_kernel<C, SCHED, NN, GROUPED, NB, EPI>), grid,
                                    dim3(C::THREADS), 0, s, a);
-            else
-                hipLaunchKernelGGL(
-                    (gemm_direct_kernel<C, (SCHED & ~(SCHED_BUFLDS | SCHED_RING3)), NN, GROUPED, NB, EPI>), grid,
-                    dim3(C::THREADS), 0, s, a);
-            return;
+                return;
+            } else {
+                if (!(SCHED & SCHED_BUFLDS) || fits)
+                    hipLaunchKernelGGL((gemm_direct_kernel<C, SCHED, NN, GROUPED, NB, EPI>), grid,
+                                       dim3(C::THREADS), 0, s, a);
+                else
+                    hipLaunchKernelGGL(
+                        (gemm_direct_kernel<C, (SCHED & ~(SCHED_BUFLDS | SCHED_RING3)), NN, GROUPED, NB, EPI>), grid,
+                        dim3(C::THREADS), 0, s, a);
+                return;
+            }
         }
     }
     if constexpr (C::STAGED) {
@@ -1522,6 +1611,7 @@ using DenseCfg = CfgOf<MOE_DENSE_CFG>::T;
 using DenseMidCfg = CfgOf<8>::T;
 using DenseSmallCfg = CfgOf<9>::T;
 using DenseNnCfg = CfgOf<11>::T;  // NN only (column-strided B fragments)
+using DenseKwCfg = CfgOf<12>::T;  // 32 x 128, two K groups
 using W13Cfg = CfgOf<MOE_W13_CFG>::T;
 using W2Cfg = CfgOf<MOE_W2_CFG>::T;
 using W2NarrowCfg = CfgOf<0>::T;  // w2 with d too narrow for the wide tile's n-tiles
@@ -1587,6 +1677,7 @@ void launch_gemm_batched(const GemmArgs& a, bool nn, int batches, hipStream_t s)
 
 GemmTile dense_tile(int tile) {
     switch (tile) {
+        case kDenseKwTile: return {DenseKwCfg::BM, DenseKwCfg::BN};
         case 1: return {DenseMidCfg::BM, DenseMidCfg::BN};
         case 2: return {DenseSmallCfg::BM, DenseSmallCfg::BN};
         case 3: return {DenseNnCfg::BM, DenseNnCfg::BN};
@@ -1594,8 +1685,11 @@ GemmTile dense_tile(int tile) {
     }
 }
 
+int dense_tile_groups(int tile) { return tile == kDenseKwTile ? DenseKwCfg::KW : 1; }
+
 int dense_blocks_per_cu(int tile, bool nn) {
     switch (tile) {
+        case kDenseKwTile: return dense_occupancy<DenseKwCfg, MOE_DENSE_SMALL_SCHED | SCHED_DIRECT>(nn);
         case 1: return dense_occupancy<DenseMidCfg, MOE_DENSE_SMALL_SCHED | SCHED_DIRECT>(nn);
         case 2: return dense_occupancy<DenseSmallCfg, MOE_DENSE_SMALL_SCHED | SCHED_DIRECT>(nn);
         case 3: return dense_occupancy<DenseNnCfg, MOE_DENSE_NN_SCHED | SCHED_DIRECT>(true);
@@ -1716,6 +1810,10 @@ void launch_gemm(const GemmArgs& args, bool nn, bool grouped, int epi, bool vec,
             case 2:
                 if (nn) launch_dense<DenseSmallCfg, true>(a, vec, s);
                 else launch_dense<DenseSmallCfg, false>(a, vec, s);
+                break;
+            case kDenseKwTile:
+                if (nn) launch_dense<DenseKwCfg, true>(a, vec, s);
+                else launch_dense<DenseKwCfg, false>(a, vec, s);
                 break;
             case 3:
                 if (!nn) throw Unsupported("dense tile 3 is NN only");
