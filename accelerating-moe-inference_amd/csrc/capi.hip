@@ -128,6 +128,9 @@ struct DensePlan {
     int tile = 0, splits = 1;
 };
 
+#ifndef MOE_DENSE_KW_MIN
+#define MOE_DENSE_KW_MIN 128  // fewest K columns per group
+#endif
 #ifndef MOE_DENSE_KW_PLAN
 #define MOE_DENSE_KW_PLAN 1  // 0: the planner never deals the K-group tile (tuning builds)
 #endif
@@ -172,11 +175,12 @@ DensePlan plan_dense(moe_ctx* ctx, bool nn, bool direct, int64_t M, int64_t N, i
         return best;
     }
     // The K-group tile (32 x 128, K split among the waves of one workgroup)
-    // where its tiles give 3/4 to all of the CUs one workgroup each and the
-    // model's best plan would split K into a second launch (1024^3; with
-    // fewer tiles, as at 512 x 1024 x 1024, the split plans that fill every
-    // CU measured 15-50 % faster; at K = 2048 and 4096 the split plans were
-    // 3-20 % faster, their reduction spread over longer K): it needs the
+    // where its tiles give 3/4 to all of the CUs one workgroup each, every
+    // group gets 128-512 K columns and the model's best plan would split K
+    // into a second launch.  Measured on MI355X against the plans without
+    // it: 1024 x 1024 x K 15-20 % faster at K = 512-1024, 8-10 % at 2048,
+    // level at 4096; with fewer tiles (512 x 1024 x 1024: half the CUs) the
+    // split plans that fill every CU were 15-50 % faster.  It needs the
     // ring, so its buffer-load offsets (from the tile's first A row; from B's
     // first row (NT) or column (NN)) must fit 31 bits, as the launch checks,
     // and K whole steps per group.  The cost model below does not weigh it:
@@ -185,7 +189,7 @@ DensePlan plan_dense(moe_ctx* ctx, bool nn, bool direct, int64_t M, int64_t N, i
     const moe::GemmTile kwt = moe::dense_tile(moe::kDenseKwTile);
     const int kwg = moe::dense_tile_groups(moe::kDenseKwTile);
     const bool kw_ok = MOE_DENSE_KW_PLAN && (env_tile < 0 || env_tile == moe::kDenseKwTile) && M >= 128 &&
-                       K % (16 * kwg) == 0 && K / kwg >= 256 && K / kwg <= 512 &&
+                       K % (16 * kwg) == 0 && K / kwg >= MOE_DENSE_KW_MIN && K / kwg <= 512 &&
                        moe::ceil_div(M, kwt.bm) * moe::ceil_div(N, kwt.bn) <= ctx->cus &&
                        moe::ceil_div(M, kwt.bm) * moe::ceil_div(N, kwt.bn) * 4 >= 3 * ctx->cus &&
                        int64_t(kwt.bm + 1) * K * 4 < (int64_t(1) << 31) &&

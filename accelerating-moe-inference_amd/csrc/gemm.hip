@@ -147,16 +147,23 @@ template <> struct CfgOf<10> { using T = Cfg<256, 64, 16, 4, 1>; };
 // Dense NN on 256 rows x 128 columns, each wave 64 rows x all 128 columns
 // (4 32 x 32 blocks): its B fragments are read column-strided (below).
 template <> struct CfgOf<11> { using T = Cfg<256, 128, 16, 4, 1>; };
-// Dense 32 x 128 with two K groups: 8 waves, each 32 rows x 32 columns over
-// half of K -- for products whose 32 x 128 tiles give each CU one workgroup
-// (measured on MI355X at 1024^3: 29.6-30.4 us NT, 32.7-33.2 NN, against 32.2
-// and 34.2 for the best tile and split plan; four groups, 16 waves, 29.4 and
-// 31.4 us but slower on every larger shape; two groups on the 64 x 128 tile
-// no faster than that tile's plans).
+// Dense 32 x 128 with four K groups: 8 waves, each 32 rows x 64 columns (two
+// column blocks, so NN reads its B pairs 8 bytes at a time) over a quarter of
+// K -- for products whose 32 x 128 tiles give each CU one workgroup.
+// Measured on MI355X at 1024^3 (same box, NN / NT): 29.8-30.2 / 27.7-27.9 us
+// against 38.1-38.6 / 36.0-36.1 for the best tile and split plan; the other
+// layouts of 32 x 128 were slower: two groups of four 32 x 32 waves 32.2 /
+// 29.2-29.6, two groups of two 32 x 64 waves 29.9-30.7 / 27.4-27.7, four
+// groups of one 32 x 128 wave 30.6-31.0 / 29.2-30.4, four groups of four
+// 32 x 32 waves slower on every larger shape; two groups on the 64 x 128
+// tile no faster than that tile's plans.
 #ifndef MOE_DENSE_KW
-#define MOE_DENSE_KW 2
+#define MOE_DENSE_KW 4
 #endif
-template <> struct CfgOf<12> { using T = Cfg<32, 128, 16, 1, 4, MOE_DENSE_KW>; };
+#ifndef MOE_DENSE_KW_WN
+#define MOE_DENSE_KW_WN 2
+#endif
+template <> struct CfgOf<12> { using T = Cfg<32, 128, 16, 1, MOE_DENSE_KW_WN, MOE_DENSE_KW>; };
 
 // Workgroup ids are dealt round-robin over the XCDs.  Renumber them so each
 // XCD works through a contiguous run of logical tiles: tiles that share an

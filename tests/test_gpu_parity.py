@@ -139,6 +139,30 @@ def test_sgemm_square_config2(ctx, torch, orc, n):
     assert_close(host(c), orc.matmul_nt(host(a), host(b)), what=f"nt {n}")
 
 
+@pytest.mark.parametrize("m,n,k", [(1000, 1000, 2048), (968, 1024, 512), (800, 1020, 768),
+                                   (1024, 896, 1024)])
+@pytest.mark.parametrize("layout", ["nn", "nt"])
+def test_sgemm_k_groups(ctx, torch, orc, layout, m, n, k):
+    """Shapes the planner deals to the K-group tile (32 x 128 tiles, one per
+    CU for 3/4 to all of the CUs; four groups of 128-512 K columns each),
+    with ragged row and column edges, with and without bias."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    tiles = -(-m // 32) * -(-n // 128)
+    assert 4 * tiles >= 3 * cus and tiles <= cus and k % 64 == 0 and 128 <= k // 4 <= 512
+    print(f"sgemm {layout} {m}x{n}x{k} (K groups)", flush=True)
+    rng = np.random.default_rng(m * 3 + n * 5 + k)
+    a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    b = rng.uniform(-1, 1, (k, n) if layout == "nn" else (n, k)).astype(np.float32)
+    bias = rng.uniform(-1, 1, n).astype(np.float32)
+    c = torch.empty((m, n), device="cuda")
+    fn = ctx.sgemm_nn if layout == "nn" else ctx.sgemm_nt
+    ref = orc.matmul_nn(a, b) if layout == "nn" else orc.matmul_nt(a, b)
+    fn(dev(torch, a), dev(torch, b), c)
+    assert_close(host(c), ref, what=layout)
+    fn(dev(torch, a), dev(torch, b), c, bias=dev(torch, bias))
+    assert_close(host(c), ref + bias, what=layout + "+bias")
+
+
 @pytest.mark.parametrize("n", [4096, 8192])
 def test_sgemm_square_config2_row_sample(ctx, torch, orc, n):
     """Config-2 squares 4096^3 and 8192^3 through moe_sgemm_nn / moe_sgemm_nt
