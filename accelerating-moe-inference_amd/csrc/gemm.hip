@@ -1618,7 +1618,7 @@ using DenseCfg = CfgOf<MOE_DENSE_CFG>::T;
 using DenseMidCfg = CfgOf<8>::T;
 using DenseSmallCfg = CfgOf<9>::T;
 using DenseNnCfg = CfgOf<11>::T;  // NN only (column-strided B fragments)
-using DenseKwCfg = CfgOf<12>::T;  // 32 x 128, two K groups
+using DenseKwCfg = CfgOf<12>::T;  // 32 x 128, four K groups
 using W13Cfg = CfgOf<MOE_W13_CFG>::T;
 using W2Cfg = CfgOf<MOE_W2_CFG>::T;
 using W2NarrowCfg = CfgOf<0>::T;  // w2 with d too narrow for the wide tile's n-tiles
