@@ -151,7 +151,7 @@ DensePlan plan_dense(moe_ctx* ctx, bool nn, bool direct, int64_t M, int64_t N, i
     // bandwidth, launch and reduction overheads, and the slowdown of a
     // workgroup alone on its CU (4096 x 1024 x 1024: 128 x 128 tiles, one
     // per CU, 95.6 us; 64 x 128 tiles, two per CU, 87.4 us)
-    // (tile 3, NN only, reads its B fragments 16 bytes at a time: the NT rate)
+    // (tile 3 reads NN B fragments 16 bytes at a time, as NT reads them)
     static constexpr double kEff[moe::kDenseTiles] = {0.80, 0.80, 0.50, 0.86, 0.0, 0.0};
     constexpr double kStageLatency = 0.6e-6, kRound = 1e-6, kHbm = 5.0e12, kLaunch = 2e-6,
                      kReduce = 2e-6, kSolo = 1.15;
@@ -198,7 +198,6 @@ DensePlan plan_dense(moe_ctx* ctx, bool nn, bool direct, int64_t M, int64_t N, i
     for (int t = 0; t < moe::kDenseTiles; ++t) {
         if (env_tile >= 0 && t != env_tile) continue;
         if (t == moe::kSkinnyTile || t == moe::kDenseKwTile) continue;  // weighed apart
-        if (t == 3 && !nn) continue;  // the 256 x 128 tile is NN only
         int& occ = ctx->dense_blocks_per_cu[nn ? 1 : 0][t];
         if (occ == 0) occ = moe::dense_blocks_per_cu(t, nn);
         const moe::GemmTile g = moe::dense_tile(t);

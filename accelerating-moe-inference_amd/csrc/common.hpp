@@ -64,7 +64,7 @@ constexpr int kMaxW2Splits = 4;  // split-K of the layer's w2 (partials summed b
 
 // Dense SGEMM tile shapes, GemmArgs::tile: 0 = 128x128 (any shape), 1 =
 // 64x128 and 2 = 32x128 (direct-load path only: 16-byte aligned rows,
-// K % 16 == 0, and for NN N % 4 == 0), 3 = 256x128 (NN only, direct path),
+// K % 16 == 0, and for NN N % 4 == 0), 3 = 256x128 (direct path),
 // 5 = 32x128 with K groups (direct ring path, K a multiple of 16 x groups,
 // no K split, operands under 2 GiB).  Ids below kDenseTiles; 4 is the skinny
 // kernel.

@@ -63,10 +63,10 @@
 #ifndef MOE_DENSE_SCHED
 #define MOE_DENSE_SCHED 62
 #endif
-// The 256 x 128 NN tile takes the three-stage ring, like the expert GEMMs
+// The 256 x 128 tile takes the three-stage ring, like the expert GEMMs
 // whose per-wave work it shares.
-#ifndef MOE_DENSE_NN_SCHED
-#define MOE_DENSE_NN_SCHED 62
+#ifndef MOE_DENSE_TALL_SCHED
+#define MOE_DENSE_TALL_SCHED 62
 #endif
 // The small dense tiles (64 x 128, 32 x 128) serve short and skinny
 // products whose few workgroups per CU cannot hide HBM latency with two
@@ -144,8 +144,9 @@ template <> struct CfgOf<9> { using T = Cfg<32, 128, 16, 1, 4>; };  // direct on
 // is a multiple of 64 but not of 128 (448: exactly 7 n-tiles instead of 4,
 // the last of them half empty)
 template <> struct CfgOf<10> { using T = Cfg<256, 64, 16, 4, 1>; };
-// Dense NN on 256 rows x 128 columns, each wave 64 rows x all 128 columns
-// (4 32 x 32 blocks): its B fragments are read column-strided (below).
+// Dense 256 rows x 128 columns, each wave 64 rows x all 128 columns (2 x 4
+// blocks of 32 x 32: the most MFMA work per fragment read of the dense
+// tiles); NN reads its B fragments column-strided (below).
 template <> struct CfgOf<11> { using T = Cfg<256, 128, 16, 4, 1>; };
 // Dense 32 x 128 with four K groups: 8 waves, each 32 rows x 64 columns (two
 // column blocks, so NN reads its B pairs 8 bytes at a time) over a quarter of
@@ -1617,7 +1618,7 @@ void launch_sk(const GemmArgs& a, bool vec, hipStream_t s) {
 using DenseCfg = CfgOf<MOE_DENSE_CFG>::T;
 using DenseMidCfg = CfgOf<8>::T;
 using DenseSmallCfg = CfgOf<9>::T;
-using DenseNnCfg = CfgOf<11>::T;  // NN only (column-strided B fragments)
+using DenseTallCfg = CfgOf<11>::T;  // 256 x 128, each wave 64 rows x 128 columns
 using DenseKwCfg = CfgOf<12>::T;  // 32 x 128, four K groups
 using W13Cfg = CfgOf<MOE_W13_CFG>::T;
 using W2Cfg = CfgOf<MOE_W2_CFG>::T;
@@ -1687,7 +1688,7 @@ GemmTile dense_tile(int tile) {
         case kDenseKwTile: return {DenseKwCfg::BM, DenseKwCfg::BN};
         case 1: return {DenseMidCfg::BM, DenseMidCfg::BN};
         case 2: return {DenseSmallCfg::BM, DenseSmallCfg::BN};
-        case 3: return {DenseNnCfg::BM, DenseNnCfg::BN};
+        case 3: return {DenseTallCfg::BM, DenseTallCfg::BN};
         default: return {DenseCfg::BM, DenseCfg::BN};
     }
 }
@@ -1699,7 +1700,7 @@ int dense_blocks_per_cu(int tile, bool nn) {
         case kDenseKwTile: return dense_occupancy<DenseKwCfg, MOE_DENSE_SMALL_SCHED | SCHED_DIRECT>(nn);
         case 1: return dense_occupancy<DenseMidCfg, MOE_DENSE_SMALL_SCHED | SCHED_DIRECT>(nn);
         case 2: return dense_occupancy<DenseSmallCfg, MOE_DENSE_SMALL_SCHED | SCHED_DIRECT>(nn);
-        case 3: return dense_occupancy<DenseNnCfg, MOE_DENSE_NN_SCHED | SCHED_DIRECT>(true);
+        case 3: return dense_occupancy<DenseTallCfg, MOE_DENSE_TALL_SCHED | SCHED_DIRECT>(nn);
         default: return dense_occupancy<DenseCfg, MOE_DENSE_SCHED | SCHED_DIRECT>(nn);
     }
 }
@@ -1823,9 +1824,12 @@ void launch_gemm(const GemmArgs& args, bool nn, bool grouped, int epi, bool vec,
                 else launch_dense<DenseKwCfg, false>(a, vec, s);
                 break;
             case 3:
-                if (!nn) throw Unsupported("dense tile 3 is NN only");
-                launch_cfg<DenseNnCfg, MOE_DENSE_NN_SCHED | SCHED_DIRECT, true, false, 1, EPI_BIAS>(
-                    a, vec, s);
+                if (nn)
+                    launch_cfg<DenseTallCfg, MOE_DENSE_TALL_SCHED | SCHED_DIRECT, true, false, 1, EPI_BIAS>(
+                        a, vec, s);
+                else
+                    launch_cfg<DenseTallCfg, MOE_DENSE_TALL_SCHED | SCHED_DIRECT, false, false, 1, EPI_BIAS>(
+                        a, vec, s);
                 break;
             case kSkinnyTile:
                 // the planner checked M <= 64, K % 16 == 0 (per split), aligned rows
