@@ -67,11 +67,15 @@ SGEMM_SHAPES = [(1024, 1024, 1024), (2048, 2048, 2048), (4096, 4096, 4096), (819
 
 def sgemm_sweep(args):
     """One JSON line per config-2 shape: TFLOP/s against the fp32 MFMA peak
-    and the HBM roofline (max of flop time and byte time)."""
+    and the HBM roofline (max of flop time and byte time).  Each shape runs
+    untimed for a while first (SPINUP_S before the first shape, a fifth of
+    it before the others) so that every line is measured at the clock a
+    loaded GPU holds, as the layer bench is; the warm-up calls follow."""
     import torch
     pkg = load_pkg()
     ctx = pkg.Context(0)
     g = torch.Generator(device="cuda").manual_seed(0)
+    first = True
     for layout in ("nn", "nt"):
         for M, N, K in SGEMM_SHAPES:
             a = torch.rand((M, K), device="cuda", generator=g) * 2 - 1
@@ -79,6 +83,13 @@ def sgemm_sweep(args):
                 (torch.rand((N, K), device="cuda", generator=g) * 2 - 1)
             c = torch.empty((M, N), device="cuda")
             fn = ctx.sgemm_nn if layout == "nn" else ctx.sgemm_nt
+            spin = SPINUP_S if first else SPINUP_S / 5
+            first = False
+            t_spin = time.perf_counter()
+            while time.perf_counter() - t_spin < spin:
+                for _ in range(4):
+                    fn(a, b, c)
+                torch.cuda.synchronize()
             for _ in range(args.warmup):
                 fn(a, b, c)
             ctx.reset_timing()
