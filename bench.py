@@ -29,6 +29,7 @@ from __future__ import annotations
 import argparse
 import importlib.util
 import json
+import math
 import os
 import sys
 import time
@@ -449,9 +450,12 @@ def model_bench(args):
         write_s = time.perf_counter() - t0
         print(f"model.bin written ({off / 2**30:.1f} GiB, {write_s:.0f} s); timing generate()",
               file=sys.stderr, flush=True)
+        # at least SPINUP_S of untimed calls (a call takes about 0.3 s), so the
+        # timed calls run at the clock a loaded GPU holds
+        warm = max(args.warmup, int(math.ceil(SPINUP_S / 0.25)))
         rc = shim.shim_model_time(path.encode(), lens.ctypes.data_as(ctypes.c_void_p),
                                   ids.ctypes.data_as(ctypes.c_void_p), I(len(lens)),
-                                  I(args.warmup), I(args.steps), ctypes.byref(load_s),
+                                  I(warm), I(args.steps), ctypes.byref(load_s),
                                   ctypes.byref(ms))
     if rc != 0:
         raise RuntimeError(f"shim_model_time: {shim.shim_error().decode()}")
@@ -460,7 +464,7 @@ def model_bench(args):
         "metric": "drop-in PhiTinyMoEModel::generate sequences/sec (prefill, logits of the last "
                   "position), 1 MI355X",
         "value": seq_s, "unit": "seq/s", "ms_per_call": ms.value, "steps": args.steps,
-        "warmup": args.warmup, "dtype": "f32",
+        "warmup": warm, "dtype": "f32",
         "data": "synthetic (seeded random weights; random token ids with 64 shared prefixes)",
         "config": {"workload": "phi_tiny_moe_generate_fp32", "sequences": int(len(lens)),
                    "tokens": int(lens.sum()), "trie_rows": nodes, "layers": L_, "d_model": h,
@@ -491,6 +495,12 @@ def decoder_bench(args, pkg):
     model = pkg.DecoderModel(ctx, cfg, W)
     model.reserve(B, S)
     logits = torch.empty((B, cfg.vocab), device=dev)
+    # spin-up: prefills for at least SPINUP_S, so every timed step runs at the
+    # clock a loaded GPU holds; then the warm-up steps
+    t_spin = time.perf_counter()
+    while time.perf_counter() - t_spin < SPINUP_S:
+        model.generate(tokens, logits)
+        torch.cuda.synchronize()
     for _ in range(args.warmup):
         model.generate(tokens, logits)
     torch.cuda.synchronize()
