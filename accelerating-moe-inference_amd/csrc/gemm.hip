@@ -151,9 +151,12 @@ template <> struct CfgOf<11> { using T = Cfg<256, 128, 16, 4, 1>; };
 // Dense 32 x 128 with four K groups: 8 waves, each 32 rows x 64 columns (two
 // column blocks, so NN reads its B pairs 8 bytes at a time) over a quarter of
 // K -- for products whose 32 x 128 tiles give each CU one workgroup.
-// Measured on MI355X at 1024^3 (same box, NN / NT): 29.8-30.2 / 27.7-27.9 us
-// against 38.1-38.6 / 36.0-36.1 for the best tile and split plan; the other
-// layouts of 32 x 128 were slower: two groups of four 32 x 32 waves 32.2 /
+// Measured on MI355X at 1024^3 (same box, NN / NT, the clock spun up first):
+// 26.3-26.4 / 25.0-25.1 us against 32.0 / 31.2-31.7 for the best tile and
+// split plan; at 1024 x 1024 x 512 17.7 / 16.9 against 23.0 / 22.3, at K =
+// 2048 43.3 / 41.4 against 47.3 / 46.8.  Timed without the spin-up (this
+// layout 29.8-30.2 / 27.7-27.9 us at 1024^3), the other layouts of 32 x 128
+// were slower: two groups of four 32 x 32 waves 32.2 /
 // 29.2-29.6, two groups of two 32 x 64 waves 29.9-30.7 / 27.4-27.7, four
 // groups of one 32 x 128 wave 30.6-31.0 / 29.2-30.4, four groups of four
 // 32 x 32 waves slower on every larger shape; two groups on the 64 x 128
