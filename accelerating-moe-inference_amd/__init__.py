@@ -33,7 +33,8 @@ NORM_NONE, NORM_LAYER, NORM_RMS = 0, 1, 2
 EXPORTS = (
     "moe_ctx_create", "moe_ctx_destroy", "moe_ctx_reserve", "moe_ctx_set_timing",
     "moe_ctx_kernel_times", "moe_ctx_reset_timing", "moe_last_error",
-    "moe_version", "moe_sgemm_nt", "moe_sgemm_nn", "moe_silu", "moe_mul",
+    "moe_version", "moe_sgemm_nt", "moe_sgemm_nn", "moe_sgemm_nt_residual", "moe_silu",
+    "moe_mul",
     "moe_layer_norm", "moe_rms_norm", "moe_rope_table", "moe_rope", "moe_attention",
     "moe_attention_last", "moe_rope_rows", "moe_attention_paths", "moe_add",
     "moe_add_bias", "moe_embed", "moe_gate_logits",
@@ -96,6 +97,7 @@ def load_library(path: str = LIB_PATH):
         "moe_version": ([], ctypes.c_char_p),
         "moe_sgemm_nt": ([P, P, P, P, P, I64, I64, I64, P], I),
         "moe_sgemm_nn": ([P, P, P, P, P, I64, I64, I64, P], I),
+        "moe_sgemm_nt_residual": ([P, P, P, P, P, P, I64, I64, I64, P], I),
         "moe_silu": ([P, P, P, I64, P], I),
         "moe_mul": ([P, P, P, P, I64, P], I),
         "moe_layer_norm": ([P, P, P, P, F, I64, I64, I, P, P, P, P], I),
@@ -214,12 +216,21 @@ class Context:
         _check(_lib.moe_ctx_reserve(self.handle, ctypes.byref(desc)))
 
     # ---- operators
-    def sgemm_nt(self, A, B, C, bias=None):
+    def sgemm_nt(self, A, B, C, bias=None, residual=None):
+        """C = A B^T (+ bias) (+ residual, added after the bias in the same
+        kernel; residual may be C itself)."""
         M, K = A.shape
         N = B.shape[0]
-        _check(_lib.moe_sgemm_nt(self.handle, _f32(A, "A"), _f32(B, "B"),
-                                 _f32(bias, "bias"), _f32(C, "C"), M, N, K,
-                                 _stream()))
+        if residual is None:
+            _check(_lib.moe_sgemm_nt(self.handle, _f32(A, "A"), _f32(B, "B"),
+                                     _f32(bias, "bias"), _f32(C, "C"), M, N, K,
+                                     _stream()))
+        else:
+            if tuple(residual.shape) != (M, N):
+                raise ValueError(f"residual shape {tuple(residual.shape)} != {(M, N)}")
+            _check(_lib.moe_sgemm_nt_residual(self.handle, _f32(A, "A"), _f32(B, "B"),
+                                              _f32(bias, "bias"), _f32(residual, "residual"),
+                                              _f32(C, "C"), M, N, K, _stream()))
         return C
 
     def sgemm_nn(self, A, B, C, bias=None):

@@ -244,9 +244,12 @@ DensePlan plan_dense(moe_ctx* ctx, bool nn, bool direct, int64_t M, int64_t N, i
     return best;
 }
 
+// C = A B (+ bias) (+ resid): resid [M, N] (may be C itself) is added after
+// the bias in the GEMM's store, or in the split reduction when K is split,
+// so C is bit-identical to the GEMM followed by moe_add.
 void sgemm(moe_ctx* ctx, bool nn, const float* A, const float* B,
            const float* bias, float* C, int64_t M, int64_t N, int64_t K,
-           void* stream) {
+           void* stream, const float* resid = nullptr) {
     check_ctx(ctx);
     check_dims(M, "M");
     check_dims(N, "N");
@@ -272,6 +275,7 @@ void sgemm(moe_ctx* ctx, bool nn, const float* A, const float* B,
     a.B1 = B;
     a.ldb = nn ? N : K;
     a.bias = bias;
+    a.resid = resid;
     a.C = C;
     a.ldc = N;
     a.M = M;
@@ -294,13 +298,15 @@ void sgemm(moe_ctx* ctx, bool nn, const float* A, const float* B,
         a.C = parts;
         a.ldc = N;
         a.bias = nullptr;
+        a.resid = nullptr;
         a.k_splits = plan.splits;
         a.k_split_len = K / plan.splits;
         a.c_split_stride = M * N;
     }
     ctx->launch(nn ? "sgemm_nn" : "sgemm_nt", s, [&] {
         moe::launch_gemm(a, nn, false, moe::EPI_BIAS, vec, s);
-        if (parts != nullptr) moe::launch_split_sum(parts, plan.splits, M * N, bias, C, M, N, s);
+        if (parts != nullptr)
+            moe::launch_split_sum(parts, plan.splits, M * N, bias, resid, C, M, N, s);
     });
 }
 
@@ -839,6 +845,15 @@ int moe_sgemm_nt(moe_ctx* ctx, const float* A, const float* B, const float* bias
 int moe_sgemm_nn(moe_ctx* ctx, const float* A, const float* B, const float* bias,
                  float* C, int64_t M, int64_t N, int64_t K, void* stream) {
     return guarded([&] { sgemm(ctx, true, A, B, bias, C, M, N, K, stream); });
+}
+
+int moe_sgemm_nt_residual(moe_ctx* ctx, const float* A, const float* B, const float* bias,
+                          const float* R, float* C, int64_t M, int64_t N, int64_t K,
+                          void* stream) {
+    return guarded([&] {
+        if (M > 0 && N > 0) check_ptr(R, "R");
+        sgemm(ctx, false, A, B, bias, C, M, N, K, stream, R);
+    });
 }
 
 int moe_silu(moe_ctx* ctx, const float* x, float* y, int64_t n, void* stream) {

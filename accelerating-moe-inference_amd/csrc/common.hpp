@@ -129,6 +129,10 @@ struct GemmArgs {
     // NB * BM * BN floats for the tiles their range boundaries cut.
     int32_t sk_grid;
     float* sk_part;
+    // Dense, one batch, no K split: a residual [M, N] with C's leading dim,
+    // added after the bias, C = (A B + bias) + resid (it may be C itself);
+    // nullptr for none.
+    const float* resid;
 };
 
 enum Causal : int { CAUSAL_NONE = 0, CAUSAL_SCORES = 1, CAUSAL_PV = 2 };
@@ -193,9 +197,9 @@ void launch_perm_place(const int32_t* idx, int64_t T, int64_t k, int64_t E,
 void launch_silu(const float* x, float* y, int64_t n, hipStream_t s);
 void launch_mul(const float* a, const float* b, float* c, int64_t n, hipStream_t s);
 // c[rows, cols] (contiguous) = sum over `splits` partials part_stride apart,
-// in order, + bias[cols] (nullable).
+// in order, + bias[cols] (nullable), + resid[rows, cols] (nullable; may be c).
 void launch_split_sum(const float* parts, int splits, int64_t part_stride, const float* bias,
-                      float* c, int64_t rows, int64_t cols, hipStream_t s);
+                      const float* resid, float* c, int64_t rows, int64_t cols, hipStream_t s);
 // Layer norm (rms: RMS norm, no mean, no bias) over rows of h: per-row mean
 // and 1/sqrt(var + eps) from the CPU loop's sequential chains, and
 // (y != nullptr) the normalised rows.  row_inv (and row_mean for the layer

@@ -24,15 +24,16 @@ __global__ __launch_bounds__(256) void mul_kernel(const float* a, const float* b
         c[i] = a[i] * b[i];
 }
 
-// Split-K reduction of a dense SGEMM: c[i] = ((p_0[i] + p_1[i]) + ...) +
-// bias[i % n_cols], partial order fixed, so repeated calls agree bit for bit.
-// V floats per lane per step (V = 4 needs n_cols % 4 == 0 and 16-byte
-// aligned buffers).
+// Split-K reduction of a dense SGEMM: c[i] = (((p_0[i] + p_1[i]) + ...) +
+// bias[i % n_cols]) + resid[i], partial order fixed, so repeated calls agree
+// bit for bit.  resid (or nullptr) may be c itself: each element is read
+// before the same lane writes it.  V floats per lane per step (V = 4 needs
+// n_cols % 4 == 0 and 16-byte aligned buffers).
 template <int V>
 __global__ __launch_bounds__(256) void split_sum_kernel(const float* __restrict__ parts,
                                                         int splits, int64_t part_stride,
                                                         const float* __restrict__ bias,
-                                                        float* __restrict__ c, int64_t n,
+                                                        const float* resid, float* c, int64_t n,
                                                         int64_t n_cols) {
     typedef float fv __attribute__((ext_vector_type(V)));
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x * V;
@@ -42,6 +43,7 @@ __global__ __launch_bounds__(256) void split_sum_kernel(const float* __restrict_
         for (int s = 1; s < splits; ++s)
             acc = acc + *reinterpret_cast<const fv*>(parts + s * part_stride + i);
         if (bias != nullptr) acc = acc + *reinterpret_cast<const fv*>(bias + i % n_cols);
+        if (resid != nullptr) acc = acc + *reinterpret_cast<const fv*>(resid + i);
         *reinterpret_cast<fv*>(c + i) = acc;
     }
 }
@@ -56,17 +58,17 @@ bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0;
 }  // namespace
 
 void launch_split_sum(const float* parts, int splits, int64_t part_stride, const float* bias,
-                      float* c, int64_t rows, int64_t cols, hipStream_t s) {
+                      const float* resid, float* c, int64_t rows, int64_t cols, hipStream_t s) {
     const int64_t n = rows * cols;
     if (n <= 0) return;
     const bool v4 = cols % 4 == 0 && part_stride % 4 == 0 && aligned16(parts) && aligned16(c) &&
-                    (bias == nullptr || aligned16(bias));
+                    (bias == nullptr || aligned16(bias)) && (resid == nullptr || aligned16(resid));
     if (v4)
         hipLaunchKernelGGL(split_sum_kernel<4>, dim3(grid_for(n / 4)), dim3(256), 0, s, parts,
-                           splits, part_stride, bias, c, n, cols);
+                           splits, part_stride, bias, resid, c, n, cols);
     else
         hipLaunchKernelGGL(split_sum_kernel<1>, dim3(grid_for(n)), dim3(256), 0, s, parts, splits,
-                           part_stride, bias, c, n, cols);
+                           part_stride, bias, resid, c, n, cols);
 }
 
 void launch_silu(const float* x, float* y, int64_t n, hipStream_t s) {

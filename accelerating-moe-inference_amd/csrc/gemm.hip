@@ -294,6 +294,7 @@ __device__ __forceinline__ void epi_store(const GemmArgs& p, float* Cb, int spli
     float v = v0;
     if (EPI == EPI_BIAS) {
         if (p.bias != nullptr) v = v + p.bias[n];
+        if (p.resid != nullptr) v = v + p.resid[row * p.ldc + n];
     } else if (EPI == EPI_SILU) {
         v = silu_ref(v);
     } else if (EPI == EPI_SWIGLU) {
@@ -643,6 +644,42 @@ template <class C, int NB, int EPI>
 __device__ __forceinline__ void store_tile(const GemmArgs& p, float* Cb, int split, int64_t row0,
                                            int rows, int64_t n0,
                                            const f32x16 (&acc)[NB][C::FM][C::FN], int tid) {
+    if constexpr (EPI == EPI_BIAS) {
+        if (p.resid != nullptr) {
+            // A row of blocks at a time, all of its residual values loaded
+            // before any of its stores: resid may alias C, so the compiler
+            // would otherwise wait for each load before the next store.
+            const int lane = tid & 63, wave = tid >> 6;
+            const int wm = wave % C::WM, wn = wave / C::WM;
+            const int lr = lane & 31, lh = lane >> 5;
+            const int arow0 = wm * (C::BM / C::WM), bcol0 = wn * (C::BN / C::WN);
+#pragma unroll
+            for (int bi = 0; bi < C::FM; ++bi) {
+                float rv[C::FN][16];
+#pragma unroll
+                for (int bj = 0; bj < C::FN; ++bj)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int i = arow0 + bi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                        const int64_t n = n0 + bcol0 + bj * 32 + lr;
+                        rv[bj][r] = i < rows && n < p.N ? p.resid[(row0 + i) * p.ldc + n] : 0.0f;
+                    }
+#pragma unroll
+                for (int bj = 0; bj < C::FN; ++bj)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int i = arow0 + bi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                        const int64_t n = n0 + bcol0 + bj * 32 + lr;
+                        if (i < rows && n < p.N) {
+                            float v = acc[0][bi][bj][r];
+                            if (p.bias != nullptr) v = v + p.bias[n];
+                            Cb[split * p.c_split_stride + (row0 + i) * p.ldc + n] = v + rv[bj][r];
+                        }
+                    }
+            }
+            return;
+        }
+    }
 #pragma unroll
     for (int bi = 0; bi < C::FM; ++bi)
 #pragma unroll
@@ -1223,7 +1260,19 @@ __device__ __forceinline__ void direct_tile(const GemmArgs& p, int mt, int nt, i
         const bool vecw = nc + FN - 1 < N && p.ldc % FN == 0 && p.c_split_stride % FN == 0 &&
                           (reinterpret_cast<uintptr_t>(Cb) & (4 * FN - 1)) == 0;
 #pragma unroll
-        for (int bi = 0; bi < FM; ++bi)
+        for (int bi = 0; bi < FM; ++bi) {
+            // the residual of this row of blocks, loaded before its stores
+            // (resid may alias C: see store_tile)
+            f32xw rv[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int i = arow0 + bi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+#pragma unroll
+                for (int bj = 0; bj < FN; ++bj)
+                    rv[r][bj] = EPI == EPI_BIAS && p.resid != nullptr && vecw && i < rows
+                                    ? p.resid[(row0 + i) * p.ldc + nc + bj]
+                                    : 0.0f;
+            }
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int i = arow0 + bi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
@@ -1234,6 +1283,7 @@ __device__ __forceinline__ void direct_tile(const GemmArgs& p, int mt, int nt, i
                     for (int bj = 0; bj < FN; ++bj) {
                         v[bj] = acc[0][bi][bj][r];
                         if (EPI == EPI_BIAS && p.bias != nullptr) v[bj] = v[bj] + p.bias[nc + bj];
+                        if (EPI == EPI_BIAS && p.resid != nullptr) v[bj] = v[bj] + rv[r][bj];
                     }
                     *reinterpret_cast<f32xw*>(&Cb[split * p.c_split_stride + (row0 + i) * p.ldc + nc]) = v;
                 } else {
@@ -1244,6 +1294,7 @@ __device__ __forceinline__ void direct_tile(const GemmArgs& p, int mt, int nt, i
                                            acc[NB - 1][bi][bj][r]);
                 }
             }
+        }
         return;
     }
     if (part != nullptr) {
@@ -1519,6 +1570,9 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(const GemmArgs p) {
                 if (EPI == EPI_BIAS && p.bias != nullptr)
 #pragma unroll
                     for (int c = 0; c < 4; ++c) v[c] = v[c] + p.bias[col + c];
+                if (EPI == EPI_BIAS && p.resid != nullptr)
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) v[c] = v[c] + p.resid[row * p.ldc + col + c];
                 *reinterpret_cast<f32x4s*>(Cb + row * p.ldc + col) = v;
             } else {
 #pragma unroll
@@ -1527,6 +1581,7 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(const GemmArgs p) {
                     if (col >= N) continue;
                     float v = acc[mb][c][r];
                     if (EPI == EPI_BIAS && p.bias != nullptr) v = v + p.bias[col];
+                    if (EPI == EPI_BIAS && p.resid != nullptr) v = v + p.resid[row * p.ldc + col];
                     Cb[row * p.ldc + col] = v;
                 }
             }
@@ -1671,6 +1726,7 @@ void launch_batched_cfg(const GemmArgs& args, int batches, hipStream_t s) {
 
 void launch_gemm_batched(const GemmArgs& a, bool nn, int batches, hipStream_t s) {
     if (batches <= 0 || a.M <= 0 || a.N <= 0) return;
+    if (a.resid != nullptr) throw Unsupported("batched GEMM with a residual");
     auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
     const bool ok = a.K % 16 == 0 && a.lda % 4 == 0 && a.ldb % 4 == 0 && al(a.A) && al(a.B0) &&
                     (!nn || a.N % 4 == 0) && a.a_so % 4 == 0 && a.a_si % 4 == 0 &&
@@ -1807,6 +1863,8 @@ void launch_gemm(const GemmArgs& args, bool nn, bool grouped, int epi, bool vec,
         a.k_split_len = a.K;
         a.c_split_stride = 0;
     }
+    if (a.resid != nullptr && (grouped || a.k_splits > 1))
+        throw Unsupported("a residual needs a dense GEMM without K splits");
     if (!grouped) {
         if (epi != EPI_BIAS) throw Unsupported("dense GEMM epilogue");
         switch (a.tile) {

@@ -166,8 +166,9 @@ class DecoderModel:
                  table=ctx.rope_table(c.rope_theta, c.head_dim, seq_len))
         ctx.attention(q, k, v, attn, batch, seq_len, c.heads, c.kv_heads, c.head_dim,
                       c.window)
-        ctx.sgemm_nt(attn, L["o_w"], h, bias=L["o_b"])
-        ctx.add(h, x)  # h = o_proj(attn) + x, the reference's add_inplace(attn, x)
+        # h = o_proj(attn) + x (the reference's add_inplace(attn, x)), the
+        # residual added in the GEMM's store
+        ctx.sgemm_nt(attn, L["o_w"], h, bias=L["o_b"], residual=x)
         moe = {"gate_w": L["gate_w"], "w1": L["w1"], "w3": L["w3"], "w2": L["w2"],
                "norm_w": L["post_norm_w"], "norm_b": L["post_norm_b"]}
         ctx.layer_forward(self.moe_desc(T), moe, h, y, topk_idx, topk_w)
@@ -206,8 +207,7 @@ class DecoderModel:
         ctx.rope(q_l, None, batch, 1, c.heads, 0, c.head_dim, table=table, first_pos=seq_len - 1)
         ctx.attention_last(q_l, k, v, a_l, batch, seq_len, c.heads, c.kv_heads, c.head_dim,
                            c.window)
-        ctx.sgemm_nt(a_l, L["o_w"], h_l, bias=L["o_b"])
-        ctx.add(h_l, x_l)
+        ctx.sgemm_nt(a_l, L["o_w"], h_l, bias=L["o_b"], residual=x_l)
         moe = {"gate_w": L["gate_w"], "w1": L["w1"], "w3": L["w3"], "w2": L["w2"],
                "norm_w": L["post_norm_w"], "norm_b": L["post_norm_b"]}
         ctx.layer_forward(self.moe_desc(batch), moe, h_l, y_last, topk_idx)

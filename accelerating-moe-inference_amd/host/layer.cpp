@@ -69,6 +69,15 @@ void sgemm_nt(const float* a, const DeviceBuffer& w, const std::shared_ptr<const
                        nullptr));
 }
 
+// c = a w^T + b + resid, the residual added in the GEMM's store
+void sgemm_nt_residual(const float* a, const DeviceBuffer& w,
+                       const std::shared_ptr<const DeviceBuffer>& b, const float* resid, float* c,
+                       std::size_t m, std::size_t n, std::size_t k) {
+    check(moe_sgemm_nt_residual(moe_dropin::context(), a, w.as<float>(),
+                                b ? b->as<float>() : nullptr, resid, c, static_cast<int64_t>(m),
+                                static_cast<int64_t>(n), static_cast<int64_t>(k), nullptr));
+}
+
 }  // namespace
 
 // ------------------------------------------------------------------ Linear
@@ -300,8 +309,8 @@ void PhiAttention::forward(const Tensor& x, Tensor& y) const {
     moe_dropin::to_host(y.data(), dy, s * hidden_ * sizeof(float));
 }
 
-void PhiAttention::forward_nodes(const float* dn, float* dy, const NodeRows& nb, bool tail,
-                                 moe_dropin::Scratch& sc) const {
+void PhiAttention::forward_nodes(const float* dn, float* dy, const float* resid,
+                                 const NodeRows& nb, bool tail, moe_dropin::Scratch& sc) const {
     const std::size_t H = apss26::NUM_ATTENTION_HEADS, KVH = apss26::NUM_KV_HEADS,
                       hd = apss26::HEAD_DIM;
     const std::size_t rows = nb.rows, nq = tail ? nb.tail_rows : rows;
@@ -335,7 +344,7 @@ void PhiAttention::forward_nodes(const float* dn, float* dy, const NodeRows& nb,
                               static_cast<int64_t>(nb.key_total), static_cast<int64_t>(H),
                               static_cast<int64_t>(KVH), static_cast<int64_t>(hd),
                               static_cast<int64_t>(apss26::SLIDING_WINDOW), nullptr));
-    sgemm_nt(a, *wo_, bo_, dy, nq, hidden_, H * hd);
+    sgemm_nt_residual(a, *wo_, bo_, resid, dy, nq, hidden_, H * hd);
 }
 
 // --------------------------------------------------------- PhiDecoderLayer
@@ -400,15 +409,16 @@ void PhiDecoderLayer::forward_nodes(const float* dx, float* dy, const NodeRows& 
     check(moe_layer_norm(ctx, dx, in_w_->as<float>(), in_b_->as<float>(), apss26::NORM_EPS,
                          static_cast<int64_t>(rows), static_cast<int64_t>(h), MOE_CONTRACT_FMA, dn,
                          nullptr, nullptr, nullptr));
-    attention_.forward_nodes(dn, da, nb, tail, sc);
+    // h = x + attention(norm(x)): the residual rows (the tail rows' gathered
+    // from x) are added in the o-projection's store
+    const float* resid = dx;
     if (tail) {
         float* dr = sc.f32(kSlotTailResid, n * h);
         check(moe_embed(ctx, dx, nb.tail_nodes, static_cast<int64_t>(n), static_cast<int64_t>(h),
                         static_cast<int64_t>(rows), dr, nullptr));
-        check(moe_add(ctx, da, dr, static_cast<int64_t>(n * h), nullptr));
-    } else {
-        check(moe_add(ctx, da, dx, static_cast<int64_t>(n * h), nullptr));
+        resid = dr;
     }
+    attention_.forward_nodes(dn, da, resid, nb, tail, sc);
     moe_.forward_device(da, dy, n, MOE_NORM_LAYER, post_w_->as<float>(), post_b_->as<float>(), 1,
                         nullptr);
 }

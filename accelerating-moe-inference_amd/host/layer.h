@@ -117,9 +117,11 @@ public:
     // s rounded up to the attention kernels' 16-row granule.
     static std::size_t padded_rows(std::size_t s) { return (s + 15) / 16 * 16; }
     // Trie rows (an extension): dn [rows, hidden] normalised input; dy gets
-    // o_proj(attention) for every node, or (tail) for the tail rows only.
-    void forward_nodes(const float* dn, float* dy, const NodeRows& nb, bool tail,
-                       moe_dropin::Scratch& sc) const;
+    // o_proj(attention) + resid for every node, or (tail) for the tail rows
+    // only (resid: the residual rows, added in the o-projection's store as
+    // src/model.cu:1965 does).
+    void forward_nodes(const float* dn, float* dy, const float* resid, const NodeRows& nb,
+                       bool tail, moe_dropin::Scratch& sc) const;
     std::size_t hidden() const { return hidden_; }
 
 private:

@@ -13,6 +13,7 @@
  *   moe_sgemm_nt        tensor_ops::matmul_transposed     src/tensor.cu:136-148
  *                       and the GPU gemm_nt_body/gemm_nt_bias src/model.cu:182-460
  *   moe_sgemm_nn        tensor_ops::matmul (declared only) include/tensor.h:61
+ *   moe_sgemm_nt_residual  DeviceLinear::forward_resid     src/model.cu:1417-1427
  *   moe_gate_logits     router gate GEMM                   src/layer.cu:84,
  *                       gemm_gate                          src/model.cu:505-616
  *   moe_route           PhiMoE::route                      src/layer.cu:47-70,
@@ -148,6 +149,15 @@ int moe_sgemm_nt(moe_ctx* ctx, const float* A, const float* B,
 int moe_sgemm_nn(moe_ctx* ctx, const float* A, const float* B,
                  const float* bias, float* C, int64_t M, int64_t N, int64_t K,
                  void* stream);
+/* NT with the residual add folded into the GEMM's store: C = (A B^T + bias)
+ * + R, R[M,N] (R == C is allowed), bit-identical to moe_sgemm_nt followed by
+ * moe_add(C, R) (tensor_ops::add_inplace after the o-projection,
+ * src/layer.cu:156).  Replaces DeviceLinear::forward_resid /
+ * gemm_nt_bias_resid (src/model.cu:1417-1427, include/model.h:50-51), the
+ * o-projection of the reference's generate() (src/model.cu:1965). */
+int moe_sgemm_nt_residual(moe_ctx* ctx, const float* A, const float* B,
+                          const float* bias, const float* R, float* C, int64_t M,
+                          int64_t N, int64_t K, void* stream);
 
 /* ---- elementwise ops of the expert MLP, bit-identical to the CPU loops:
  * moe_silu: y = x / (1 + float(exp(double(-x))))  tensor_ops::silu, src/tensor.cu:169-173

@@ -163,6 +163,37 @@ def test_sgemm_k_groups(ctx, torch, orc, layout, m, n, k):
     assert_close(host(c), ref + bias, what=layout + "+bias")
 
 
+@pytest.mark.parametrize("m,n,k", [(16, 1000, 512), (48, 2048, 1024), (1024, 1024, 1024),
+                                   (600, 700, 1000), (300, 257, 37), (2048, 4096, 512), (5, 7, 0)])
+def test_sgemm_nt_residual(ctx, torch, orc, m, n, k):
+    """moe_sgemm_nt_residual on shapes that reach the skinny kernel, split K,
+    the K-group and 256-row tiles, the register-staged and scalar paths and
+    K = 0: bit-identical to moe_sgemm_nt followed by the add (the residual is
+    added after the bias in the store, or in the split reduction), within
+    tolerance of the oracle, and in place (R == C)."""
+    print(f"sgemm_nt_residual {m}x{n}x{k}", flush=True)
+    rng = np.random.default_rng(m * 13 + n * 7 + k)
+    a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    b = rng.uniform(-1, 1, (n, k)).astype(np.float32)
+    bias = rng.uniform(-1, 1, n).astype(np.float32)
+    r = rng.uniform(-4, 4, (m, n)).astype(np.float32)
+    da, db, dbias, dr = dev(torch, a), dev(torch, b), dev(torch, bias), dev(torch, r)
+    plain = torch.empty((m, n), device="cuda")
+    ctx.sgemm_nt(da, db, plain, bias=dbias)
+    two_step = plain + dr
+    fused = torch.empty((m, n), device="cuda")
+    ctx.sgemm_nt(da, db, fused, bias=dbias, residual=dr)
+    assert torch.equal(fused, two_step), "fused residual differs from GEMM + add"
+    inplace = dr.clone()
+    ctx.sgemm_nt(da, db, inplace, bias=dbias, residual=inplace)
+    assert torch.equal(inplace, two_step), "in-place residual"
+    ref = orc.matmul_nt(a, b) + bias + r
+    if k == 0:
+        assert np.array_equal(host(fused), (bias + r).astype(np.float32))
+    else:
+        assert_close(host(fused), ref, what="nt+bias+residual")
+
+
 @pytest.mark.parametrize("n", [4096, 8192])
 def test_sgemm_square_config2_row_sample(ctx, torch, orc, n):
     """Config-2 squares 4096^3 and 8192^3 through moe_sgemm_nn / moe_sgemm_nt
