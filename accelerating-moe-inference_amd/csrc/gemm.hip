@@ -632,6 +632,25 @@ __device__ __forceinline__ void store_block(const GemmArgs& p, float* Cb, int sp
     const int wm = wave % C::WM, wn = wave / C::WM;
     const int lr = lane & 31, lh = lane >> 5;
     const int arow0 = wm * (C::BM / C::WM), bcol0 = wn * (C::BN / C::WN);
+    if constexpr (EPI == EPI_BIAS) {
+        // the lane's column is the same for all 16 values: its bias is
+        // loaded once (C may alias it as far as the compiler knows, so a
+        // load per store would wait behind each store)
+        const int64_t n = n0 + bcol0 + bj * 32 + lr;
+        if (n >= p.N) return;
+        const bool hb = p.bias != nullptr;
+        const float bn = hb ? p.bias[n] : 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int i = arow0 + bi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+            if (i >= rows) continue;
+            float v = a0[r];
+            if (hb) v = v + bn;
+            if (p.resid != nullptr) v = v + p.resid[(row0 + i) * p.ldc + n];
+            Cb[split * p.c_split_stride + (row0 + i) * p.ldc + n] = v;
+        }
+        return;
+    }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         const int i = arow0 + bi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
@@ -653,6 +672,13 @@ __device__ __forceinline__ void store_tile(const GemmArgs& p, float* Cb, int spl
             const int wm = wave % C::WM, wn = wave / C::WM;
             const int lr = lane & 31, lh = lane >> 5;
             const int arow0 = wm * (C::BM / C::WM), bcol0 = wn * (C::BN / C::WN);
+            const bool hb = p.bias != nullptr;
+            float bn[C::FN];
+#pragma unroll
+            for (int bj = 0; bj < C::FN; ++bj) {
+                const int64_t n = n0 + bcol0 + bj * 32 + lr;
+                bn[bj] = hb && n < p.N ? p.bias[n] : 0.0f;
+            }
 #pragma unroll
             for (int bi = 0; bi < C::FM; ++bi) {
                 float rv[C::FN][16];
@@ -672,7 +698,7 @@ __device__ __forceinline__ void store_tile(const GemmArgs& p, float* Cb, int spl
                         const int64_t n = n0 + bcol0 + bj * 32 + lr;
                         if (i < rows && n < p.N) {
                             float v = acc[0][bi][bj][r];
-                            if (p.bias != nullptr) v = v + p.bias[n];
+                            if (hb) v = v + bn[bj];
                             Cb[split * p.c_split_stride + (row0 + i) * p.ldc + n] = v + rv[bj][r];
                         }
                     }
@@ -1259,6 +1285,11 @@ __device__ __forceinline__ void direct_tile(const GemmArgs& p, int mt, int nt, i
         const int64_t nc = n0 + bcol0 + FN * lr;
         const bool vecw = nc + FN - 1 < N && p.ldc % FN == 0 && p.c_split_stride % FN == 0 &&
                           (reinterpret_cast<uintptr_t>(Cb) & (4 * FN - 1)) == 0;
+        // the lane's FN columns' bias, loaded once (see store_block)
+        const bool hb = EPI == EPI_BIAS && p.bias != nullptr;
+        f32xw bv;
+#pragma unroll
+        for (int bj = 0; bj < FN; ++bj) bv[bj] = hb && vecw ? p.bias[nc + bj] : 0.0f;
 #pragma unroll
         for (int bi = 0; bi < FM; ++bi) {
             // the residual of this row of blocks, loaded before its stores
@@ -1282,7 +1313,7 @@ __device__ __forceinline__ void direct_tile(const GemmArgs& p, int mt, int nt, i
 #pragma unroll
                     for (int bj = 0; bj < FN; ++bj) {
                         v[bj] = acc[0][bi][bj][r];
-                        if (EPI == EPI_BIAS && p.bias != nullptr) v[bj] = v[bj] + p.bias[nc + bj];
+                        if (hb) v[bj] = v[bj] + bv[bj];
                         if (EPI == EPI_BIAS && p.resid != nullptr) v[bj] = v[bj] + rv[r][bj];
                     }
                     *reinterpret_cast<f32xw*>(&Cb[split * p.c_split_stride + (row0 + i) * p.ldc + nc]) = v;
@@ -1555,8 +1586,16 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(const GemmArgs p) {
         }
     }
 
-    // epilogue: split partials (no bias) or the output with bias
+    // epilogue: split partials (no bias) or the output with bias; the bias
+    // of the lane's columns is loaded once (see store_block)
     float* Cb = p.C + split * p.c_split_stride;
+    const bool hb = EPI == EPI_BIAS && p.bias != nullptr;
+    float bcol[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int64_t col = NN ? n0 + 4 * j + c : n0 + 16 * c + j;
+        bcol[c] = hb && col < N ? p.bias[col] : 0.0f;
+    }
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
@@ -1567,9 +1606,9 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(const GemmArgs p) {
                 const int64_t col = n0 + 4 * j;
                 if (col >= N) continue;
                 f32x4s v{acc[mb][0][r], acc[mb][1][r], acc[mb][2][r], acc[mb][3][r]};
-                if (EPI == EPI_BIAS && p.bias != nullptr)
+                if (hb)
 #pragma unroll
-                    for (int c = 0; c < 4; ++c) v[c] = v[c] + p.bias[col + c];
+                    for (int c = 0; c < 4; ++c) v[c] = v[c] + bcol[c];
                 if (EPI == EPI_BIAS && p.resid != nullptr)
 #pragma unroll
                     for (int c = 0; c < 4; ++c) v[c] = v[c] + p.resid[row * p.ldc + col + c];
@@ -1580,7 +1619,7 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(const GemmArgs p) {
                     const int64_t col = n0 + 16 * c + j;
                     if (col >= N) continue;
                     float v = acc[mb][c][r];
-                    if (EPI == EPI_BIAS && p.bias != nullptr) v = v + p.bias[col];
+                    if (hb) v = v + bcol[c];
                     if (EPI == EPI_BIAS && p.resid != nullptr) v = v + p.resid[row * p.ldc + col];
                     Cb[row * p.ldc + col] = v;
                 }
