@@ -279,7 +279,12 @@ __global__ __launch_bounds__(256) void attn_paths_wave_kernel(
     const int32_t* __restrict__ key_beg, const int32_t* __restrict__ key_end, int64_t nq,
     int64_t kv_rows, int64_t key_total, int64_t KVH, int64_t hd, int64_t window, float scale) {
     const int lane = threadIdx.x & 63;
-    const int64_t gw = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    // the wave's (query, key head), wave-uniform by construction: readfirstlane
+    // lets the compiler see that, so q (the same for every lane) is read
+    // through scalar loads and fed to the chains as scalar operands instead of
+    // 64 lanes' vector loads of one address
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int64_t gw = static_cast<int64_t>(blockIdx.x) * 4 + wave;
     if (gw >= nq * KVH) return;  // no barrier in this kernel
     const int64_t i = gw / KVH, kh = gw % KVH, H = KVH * G;
     const int64_t kw = KVH * hd;
@@ -306,15 +311,25 @@ __global__ __launch_bounds__(256) void attn_paths_wave_kernel(
         float acc[G];
 #pragma unroll
         for (int g = 0; g < G; ++g) acc[g] = 0.0f;
-        for (int64_t d = 0; d < hd; d += 4) {
-            const float4 c = *reinterpret_cast<const float4*>(kr + d);
+        // 32 columns of the key row at a time, all 8 loads issued before
+        // the chain consumes them (one memory round trip per chunk)
+        for (int64_t d0 = 0; d0 < hd; d0 += 32) {
+            float4 c[8];
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const float4 a = *reinterpret_cast<const float4*>(qi + g * hd + d);
-                acc[g] += a.x * c.x;
-                acc[g] += a.y * c.y;
-                acc[g] += a.z * c.z;
-                acc[g] += a.w * c.w;
+            for (int u = 0; u < 8; ++u)
+                c[u] = d0 + 4 * u < hd ? *reinterpret_cast<const float4*>(kr + d0 + 4 * u)
+                                       : float4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                if (d0 + 4 * u >= hd) break;
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    const float4 a = *reinterpret_cast<const float4*>(qi + g * hd + d0 + 4 * u);
+                    acc[g] += a.x * c[u].x;
+                    acc[g] += a.y * c[u].y;
+                    acc[g] += a.z * c[u].z;
+                    acc[g] += a.w * c[u].w;
+                }
             }
         }
 #pragma unroll
@@ -332,21 +347,45 @@ __global__ __launch_bounds__(256) void attn_paths_wave_kernel(
         for (int64_t t = 0; t < len; ++t) dsum += __shfl(sc[g], static_cast<int>(t), 64);
         den[g] = dsum;
     }
-    for (int64_t d = lane; d < hd; d += 64) {
-        float value[G];
+    // key t's weight exp_t / den, divided once on its own lane (the same
+    // operands and rounding as dividing on every lane that uses it)
+    float pw[G];
 #pragma unroll
-        for (int g = 0; g < G; ++g) value[g] = 0.0f;
-        for (int64_t t = 0; t < len; ++t) {
-            const int64_t r = __shfl(my_row, static_cast<int>(t), 64);
-            const float vv = v[r * kw + kh * hd + d];
+    for (int g = 0; g < G; ++g) pw[g] = sc[g] / den[g];
+    // output columns d = d0 + lane and d0 + 64 + lane together; the value
+    // rows of 16 keys at a time are loaded before their t-ascending chains
+    // consume them (one memory round trip per 16 keys, not per key)
+    for (int64_t d0 = 0; d0 < hd; d0 += 128) {
+        const int64_t da = d0 + lane, db = d0 + 64 + lane;
+        const bool ina = da < hd, inb = db < hd;
+        float va[G], vb[G];
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const float pr = __shfl(sc[g], static_cast<int>(t), 64);
-                value[g] += pr / den[g] * vv;
+        for (int g = 0; g < G; ++g) va[g] = vb[g] = 0.0f;
+        for (int64_t t0 = 0; t0 < len; t0 += 16) {
+            float xa[16], xb[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                const int64_t t = t0 + u < len ? t0 + u : t0;  // wave-uniform
+                const float* vr = v + __shfl(my_row, static_cast<int>(t), 64) * kw + kh * hd;
+                xa[u] = ina ? vr[da] : 0.0f;
+                xb[u] = inb ? vr[db] : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                if (t0 + u >= len) break;  // wave-uniform
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    const float pr = __shfl(pw[g], static_cast<int>(t0 + u), 64);
+                    va[g] += pr * xa[u];
+                    vb[g] += pr * xb[u];
+                }
             }
         }
 #pragma unroll
-        for (int g = 0; g < G; ++g) o[g * hd + d] = value[g];
+        for (int g = 0; g < G; ++g) {
+            if (ina) o[g * hd + da] = va[g];
+            if (inb) o[g * hd + db] = vb[g];
+        }
     }
 }
 
