@@ -135,11 +135,15 @@ __global__ __launch_bounds__(256) void attn_last_kernel(
     }
     __syncthreads();
     const float den = red[0];
+    // each weight divided once (the same operands and rounding as dividing
+    // in every output chain that uses it)
+    for (int64_t ki = lo + tid; ki < S; ki += blockDim.x) sc[ki] = sc[ki] / den;
+    __syncthreads();
     float* o = out + b * H * hd + h * hd;
     for (int64_t d = tid; d < hd; d += blockDim.x) {
         float value = 0.0f;
 #pragma unroll 8
-        for (int64_t ki = lo; ki < S; ++ki) value += sc[ki] / den * vb[ki * kw + d];
+        for (int64_t ki = lo; ki < S; ++ki) value += sc[ki] * vb[ki * kw + d];
         o[d] = value;
     }
 }
@@ -253,10 +257,13 @@ __global__ __launch_bounds__(256) void attn_paths_kernel(
     }
     __syncthreads();
     const float den = red[0];
+    // each weight divided once (as in attn_last_kernel)
+    for (int64_t t = tid; t < len; t += blockDim.x) sc[t] = sc[t] / den;
+    __syncthreads();
     for (int64_t d = tid; d < hd; d += blockDim.x) {
         float value = 0.0f;
 #pragma unroll 8
-        for (int64_t t = 0; t < len; ++t) value += sc[t] / den * v[key_row(t) * kw + kh * hd + d];
+        for (int64_t t = 0; t < len; ++t) value += sc[t] * v[key_row(t) * kw + kh * hd + d];
         o[d] = value;
     }
 }
