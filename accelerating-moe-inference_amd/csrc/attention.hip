@@ -38,6 +38,59 @@ __global__ __launch_bounds__(256) void rope_kernel(float* __restrict__ q, float*
     }
 }
 
+// The same rotation, 4 adjacent pairs per thread with 16-byte loads and
+// stores, and 32-bit index arithmetic (the launcher takes it when
+// head_dim % 8 == 0, the buffers are 16-byte aligned and the pair count /
+// 4 fits 31 bits): each element's two products and sum are the ones above,
+// so the results are bit-identical.  ROWS: positions[r] clamped into the
+// table (rope_rows_kernel); else first_pos + r % seq_len (rope_kernel).
+template <bool ROWS>
+__global__ __launch_bounds__(256) void rope4_kernel(float* __restrict__ q, float* __restrict__ k,
+                                                    const float* __restrict__ table,
+                                                    int64_t table_positions,
+                                                    const int32_t* __restrict__ positions,
+                                                    uint32_t seq_len, int64_t first_pos,
+                                                    uint32_t rows, uint32_t q_heads,
+                                                    uint32_t kv_heads, uint32_t head_dim) {
+    const uint32_t half = head_dim / 2, h4 = half / 4, heads = q_heads + kv_heads;
+    const uint32_t n4 = rows * heads * h4;
+    const uint32_t stride = gridDim.x * blockDim.x;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
+        const uint32_t t = i / h4, j = 4 * (i - t * h4);
+        const uint32_t r = t / heads, hh = t - r * heads;
+        float* x = hh < q_heads ? q + (static_cast<int64_t>(r) * q_heads + hh) * head_dim
+                                : k + (static_cast<int64_t>(r) * kv_heads + (hh - q_heads)) * head_dim;
+        int64_t pos;
+        if (ROWS) {
+            pos = positions[r];
+            pos = pos < 0 ? 0 : (pos >= table_positions ? table_positions - 1 : pos);
+        } else {
+            pos = first_pos + r % seq_len;
+        }
+        const float4* trig = reinterpret_cast<const float4*>(table + (pos * half + j) * 2);
+        const float4 t01 = trig[0], t23 = trig[1];  // (cos, sin) of pairs j .. j + 3
+        const float4 a = *reinterpret_cast<const float4*>(x + j);
+        const float4 b = *reinterpret_cast<const float4*>(x + j + half);
+        const float c[4] = {t01.x, t01.z, t23.x, t23.z}, sn[4] = {t01.y, t01.w, t23.y, t23.w};
+        const float x0[4] = {a.x, a.y, a.z, a.w}, x1[4] = {b.x, b.y, b.z, b.w};
+        float y0[4], y1[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            y0[u] = x0[u] * c[u] - x1[u] * sn[u];
+            y1[u] = x1[u] * c[u] + x0[u] * sn[u];
+        }
+        *reinterpret_cast<float4*>(x + j) = float4{y0[0], y0[1], y0[2], y0[3]};
+        *reinterpret_cast<float4*>(x + j + half) = float4{y1[0], y1[1], y1[2], y1[3]};
+    }
+}
+
+bool rope4_ok(const float* q, const float* k, const float* table, int64_t rows, int64_t heads,
+              int64_t head_dim) {
+    auto al = [](const void* p) { return p == nullptr || reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    return head_dim % 8 == 0 && al(q) && al(k) && al(table) &&
+           rows * heads * (head_dim / 8) < (int64_t(1) << 31) && rows < (int64_t(1) << 31);
+}
+
 __device__ __forceinline__ float wave_max(float v) {
     for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
     return v;
@@ -440,6 +493,14 @@ void launch_rope(float* q, float* k, const float* table, int64_t rows, int64_t s
                  hipStream_t s) {
     const int64_t n = rows * (q_heads + kv_heads) * (head_dim / 2);
     if (n <= 0) return;
+    if (rope4_ok(q, k, table, rows, q_heads + kv_heads, head_dim) && seq_len > 0 &&
+        seq_len < (int64_t(1) << 31)) {
+        hipLaunchKernelGGL((rope4_kernel<false>), dim3(grid_for(n / 4)), dim3(256), 0, s, q, k,
+                           table, int64_t(0), nullptr, static_cast<uint32_t>(seq_len), first_pos,
+                           static_cast<uint32_t>(rows), static_cast<uint32_t>(q_heads),
+                           static_cast<uint32_t>(kv_heads), static_cast<uint32_t>(head_dim));
+        return;
+    }
     hipLaunchKernelGGL(rope_kernel, dim3(grid_for(n)), dim3(256), 0, s, q, k, table, rows,
                        seq_len, first_pos, q_heads, kv_heads, head_dim);
 }
@@ -477,6 +538,13 @@ void launch_rope_rows(float* q, float* k, const float* table, int64_t table_posi
                       int64_t head_dim, hipStream_t s) {
     const int64_t n = rows * (q_heads + kv_heads) * (head_dim / 2);
     if (n <= 0) return;
+    if (rope4_ok(q, k, table, rows, q_heads + kv_heads, head_dim)) {
+        hipLaunchKernelGGL((rope4_kernel<true>), dim3(grid_for(n / 4)), dim3(256), 0, s, q, k,
+                           table, table_positions, positions, uint32_t(1), int64_t(0),
+                           static_cast<uint32_t>(rows), static_cast<uint32_t>(q_heads),
+                           static_cast<uint32_t>(kv_heads), static_cast<uint32_t>(head_dim));
+        return;
+    }
     hipLaunchKernelGGL(rope_rows_kernel, dim3(grid_for(n)), dim3(256), 0, s, q, k, table,
                        table_positions, positions, rows, q_heads, kv_heads, head_dim);
 }
