@@ -420,9 +420,16 @@ __global__ __launch_bounds__(256) void norm_apply4_kernel(
         int64_t h, float* __restrict__ y) {
     const int64_t h4 = h >> 2, n4 = rows * h4;
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    // 32-bit row division when every index fits (the launch grid-strides
+    // at most 2^24 past n4): a 64-bit division costs a long instruction
+    // sequence per 16 bytes moved
+    const bool narrow = n4 < (int64_t(1) << 31);
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n4;
          i += stride) {
-        const int64_t r = i / h4, j = 4 * (i - r * h4);
+        const int64_t r = narrow ? static_cast<int64_t>(static_cast<uint32_t>(i) /
+                                                        static_cast<uint32_t>(h4))
+                                 : i / h4;
+        const int64_t j = 4 * (i - r * h4);
         const f32x4 v = reinterpret_cast<const f32x4*>(x)[i];
         const f32x4 wv = *reinterpret_cast<const f32x4*>(w + j);
         const f32x4 bv = RMS ? wv : *reinterpret_cast<const f32x4*>(b + j);
