@@ -40,7 +40,7 @@ EXPORTS = (
     "moe_add_bias", "moe_embed", "moe_gate_logits",
     "moe_route", "moe_permute", "moe_expert_ffn_grouped", "moe_combine",
     "moe_layer_forward", "moe_layer_forward_noalloc", "moe_layer_w2_splits",
-    "moe_ctx_set_stream_k",
+    "moe_ctx_set_stream_k", "moe_ctx_workspace_bytes", "moe_launch_floor",
 )
 
 
@@ -125,6 +125,8 @@ def load_library(path: str = LIB_PATH):
         "moe_layer_w2_splits": ([P, ctypes.POINTER(LayerDesc), ctypes.POINTER(ctypes.c_int32)],
                                 I),
         "moe_ctx_set_stream_k": ([P, I], I),
+        "moe_ctx_workspace_bytes": ([P, ctypes.POINTER(ctypes.c_int64)], I),
+        "moe_launch_floor": ([P, P], I),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -214,6 +216,17 @@ class Context:
 
     def reserve(self, desc: LayerDesc):
         _check(_lib.moe_ctx_reserve(self.handle, ctypes.byref(desc)))
+
+    def workspace_bytes(self) -> int:
+        """moe_ctx_workspace_bytes: the context's workspace as it stands."""
+        out = ctypes.c_int64(0)
+        _check(_lib.moe_ctx_workspace_bytes(self.handle, ctypes.byref(out)))
+        return out.value
+
+    def launch_floor(self):
+        """moe_launch_floor: one empty kernel on the current stream (timed
+        as "empty" when timing is on)."""
+        _check(_lib.moe_launch_floor(self.handle, _stream()))
 
     # ---- operators
     def sgemm_nt(self, A, B, C, bias=None, residual=None):

@@ -660,7 +660,6 @@ void layer_forward(moe_ctx* ctx, const moe_layer_desc& D, const moe_layer_weight
     LayerWs ws = carve_layer(base, D, plan);
     int32_t* idx = topk_idx_out != nullptr ? topk_idx_out : ws.idx;
     float* w = topk_w_out != nullptr ? topk_w_out : ws.w;
-    const int64_t nb = moe::ceil_div(D.T, moe::kPermTokens);
 
     // The experts' input: x, or its normalised copy (written once, read
     // by the gate and the w1/w3 GEMM; the residual stays x).
@@ -677,12 +676,12 @@ void layer_forward(moe_ctx* ctx, const moe_layer_desc& D, const moe_layer_weight
     ctx->launch("gate_logits", s, [&] {
         moe::launch_gate_logits(xin, weights.gate_w, ws.logits, D.T, D.d, D.E, D.contract, s);
     });
-    ctx->launch(D.router == MOE_ROUTER_PHI_QUANT ? "route_phi" : "route_softmax", s, [&] {
-        moe::launch_route(ws.logits, weights.expert_bias, D.T, D.E, D.k, D.router, D.quantum,
-                          D.tie_eps, idx, w, s);
+    // routing, the per-block expert counts and their scan: one launch
+    ctx->launch("route_count", s, [&] {
+        moe::launch_route_count(ws.logits, weights.expert_bias, D.T, D.E, D.k, D.router,
+                                D.quantum, D.tie_eps, idx, w, ws.counts, ws.offsets, ctx->sync,
+                                s);
     });
-    ctx->launch("perm_count", s, [&] { moe::launch_perm_count(idx, D.T, D.k, D.E, ws.counts, s); });
-    ctx->launch("perm_scan", s, [&] { moe::launch_perm_scan(ws.counts, nb, D.E, ws.offsets, s); });
     ctx->launch("perm_place", s, [&] {
         moe::launch_perm_place(idx, D.T, D.k, D.E, ws.counts, ws.perm, ws.inv, s);
     });
@@ -756,10 +755,21 @@ int moe_ctx_create(int device, moe_ctx** out) {
             DeviceScope dev(device);
             scr = bind_scratch(device);
         }
+        uint32_t* sync = nullptr;
+        {
+            DeviceScope dev(device);
+            moe::hip_check(hipMalloc(&sync, 256), "hipMalloc counters");
+            const hipError_t e = hipMemset(sync, 0, 256);
+            if (e != hipSuccess) {
+                (void)hipFree(sync);
+                moe::hip_check(e, "hipMemset counters");
+            }
+        }
         auto* c = new moe_ctx();
         c->device = device;
         c->cus = prop.multiProcessorCount;
         c->scratch = scr;
+        c->sync = sync;
         *out = c;
     });
 }
@@ -775,6 +785,7 @@ int moe_ctx_destroy(moe_ctx* ctx) {
             (void)hipEventDestroy(e.second);
         }
         if (ctx->ws != nullptr) (void)hipFree(ctx->ws);
+        if (ctx->sync != nullptr) (void)hipFree(ctx->sync);
         delete ctx;
     });
 }
@@ -787,6 +798,14 @@ int moe_ctx_reserve(moe_ctx* ctx, const moe_layer_desc* desc) {
         const FfnPlan plan =
             choose_ffn_plan(ctx, desc->T * desc->k, desc->d, desc->d_ff, desc->E);
         ctx->workspace(carve_layer(nullptr, *desc, plan).bytes);
+    });
+}
+
+int moe_ctx_workspace_bytes(moe_ctx* ctx, int64_t* bytes) {
+    return guarded([&] {
+        check_ctx(ctx);
+        check_ptr(bytes, "bytes");
+        *bytes = static_cast<int64_t>(ctx->ws_bytes);
     });
 }
 
@@ -853,6 +872,15 @@ int moe_sgemm_nt_residual(moe_ctx* ctx, const float* A, const float* B, const fl
     return guarded([&] {
         if (M > 0 && N > 0) check_ptr(R, "R");
         sgemm(ctx, false, A, B, bias, C, M, N, K, stream, R);
+    });
+}
+
+int moe_launch_floor(moe_ctx* ctx, void* stream) {
+    return guarded([&] {
+        check_ctx(ctx);
+        DeviceScope dev(ctx->device);
+        hipStream_t s = as_stream(stream);
+        ctx->launch("empty", s, [&] { moe::launch_empty(s); });
     });
 }
 

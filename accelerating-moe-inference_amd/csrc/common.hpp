@@ -187,6 +187,12 @@ void launch_gate_logits(const float* x, const float* w, float* logits,
 void launch_route(const float* logits, const float* bias, int64_t T, int64_t E,
                   int64_t k, int mode, float quantum, float tie_eps,
                   int32_t* idx, float* w, hipStream_t s);
+// Routing + per-block counts + their scan (offsets) in one launch; `done`: a
+// device counter that is 0 between launches (the last block resets it).
+void launch_route_count(const float* logits, const float* bias, int64_t T, int64_t E,
+                        int64_t k, int mode, float quantum, float tie_eps, int32_t* idx,
+                        float* w, int32_t* counts, int32_t* offsets, uint32_t* done,
+                        hipStream_t s);
 void launch_perm_count(const int32_t* idx, int64_t T, int64_t k, int64_t E,
                        int32_t* counts, hipStream_t s);
 void launch_perm_scan(int32_t* counts, int64_t nblocks, int64_t E,
@@ -194,6 +200,7 @@ void launch_perm_scan(int32_t* counts, int64_t nblocks, int64_t E,
 void launch_perm_place(const int32_t* idx, int64_t T, int64_t k, int64_t E,
                        const int32_t* base, int32_t* perm, int32_t* inv,
                        hipStream_t s);
+void launch_empty(hipStream_t s);
 void launch_silu(const float* x, float* y, int64_t n, hipStream_t s);
 void launch_mul(const float* a, const float* b, float* c, int64_t n, hipStream_t s);
 // c[rows, cols] (contiguous) = sum over `splits` partials part_stride apart,
@@ -231,6 +238,9 @@ struct moe_ctx {
     void* ws = nullptr;
     size_t ws_bytes = 0;
     void* scratch = nullptr;   // this device's no-alloc scratch (moe_layer_forward_noalloc)
+    // device counters of the single-launch scans (route_count's `done`): 0
+    // between launches; allocated and zeroed when the context is created
+    uint32_t* sync = nullptr;
     bool timing = false;
     struct Pending {
         const char* name;

@@ -48,6 +48,10 @@ __global__ __launch_bounds__(256) void split_sum_kernel(const float* __restrict_
     }
 }
 
+// Does nothing: the launch-latency floor that the small routing and
+// permutation kernels are measured against.
+__global__ __launch_bounds__(64) void empty_kernel() {}
+
 unsigned grid_for(int64_t n) {
     const int64_t blocks = ceil_div(n, 256);
     return static_cast<unsigned>(blocks < 65536 ? blocks : 65536);
@@ -69,6 +73,10 @@ void launch_split_sum(const float* parts, int splits, int64_t part_stride, const
     else
         hipLaunchKernelGGL(split_sum_kernel<1>, dim3(grid_for(n)), dim3(256), 0, s, parts, splits,
                            part_stride, bias, resid, c, n, cols);
+}
+
+void launch_empty(hipStream_t s) {
+    hipLaunchKernelGGL(empty_kernel, dim3(1), dim3(64), 0, s);
 }
 
 void launch_silu(const float* x, float* y, int64_t n, hipStream_t s) {

@@ -454,15 +454,13 @@ __device__ __forceinline__ float quantise(float score, float quantum) {
 // (src/layer.cu:56-69): ascending scan, take e when nothing is held or when
 // it beats the held score by more than tie_eps; repeat excluding the picks.
 // The rule is order-dependent (not a reduction), so it stays sequential.
-__global__ __launch_bounds__(256) void route_phi_kernel(
-        const float* __restrict__ logits, const float* __restrict__ bias,
-        int64_t T, int64_t E, int64_t k, float quantum, float tie_eps,
-        int32_t* __restrict__ idx, float* __restrict__ w) {
-    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (t >= T) return;
-    const float* row = logits + t * E;
+// Writes token t's k picks and weights; picks[] receives the experts.
+__device__ __forceinline__ void route_phi_token(const float* __restrict__ row,
+                                                const float* __restrict__ bias, int64_t E,
+                                                int64_t k, float quantum, float tie_eps,
+                                                int32_t* __restrict__ idx_t,
+                                                float* __restrict__ w_t, int32_t* picks) {
     const float weight = 1.0f / static_cast<float>(k);
-    int32_t picks[kMaxTopK];
     for (int s = 0; s < k; ++s) {
         int best = -1;
         float best_value = -INFINITY;
@@ -478,9 +476,19 @@ __global__ __launch_bounds__(256) void route_phi_kernel(
             }
         }
         picks[s] = best;
-        idx[t * k + s] = best;
-        w[t * k + s] = weight;
+        idx_t[s] = best;
+        w_t[s] = weight;
     }
+}
+
+__global__ __launch_bounds__(256) void route_phi_kernel(
+        const float* __restrict__ logits, const float* __restrict__ bias,
+        int64_t T, int64_t E, int64_t k, float quantum, float tie_eps,
+        int32_t* __restrict__ idx, float* __restrict__ w) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= T) return;
+    int32_t picks[kMaxTopK];
+    route_phi_token(logits + t * E, bias, E, k, quantum, tie_eps, idx + t * k, w + t * k, picks);
 }
 
 // SOFTMAX_TOPK: a group of G lanes (a power of two, <= 64) per token; lane j
@@ -492,15 +500,16 @@ __device__ __forceinline__ bool beats(float av, int ai, float bv, int bi) {
     return av > bv || (av == bv && ai < bi);
 }
 
-__global__ __launch_bounds__(256) void route_softmax_kernel(
-        const float* __restrict__ logits, const float* __restrict__ bias,
-        int64_t T, int64_t E, int64_t k, int G,
-        int32_t* __restrict__ idx, float* __restrict__ w) {
-    const int lane = threadIdx.x & 63;
-    const int sub = lane & (G - 1);
-    const int64_t t = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / G;
-    const bool live = t < T;
-    const float* row = logits + (live ? t : 0) * E;
+// Token t's top-k by the group of G lanes this lane belongs to (sub: the
+// lane's index in it); every lane of the group must call it, live or not.
+// The group's first lane writes idx_t / w_t and, when `mask` is not null,
+// sets bit `bit` of each picked expert's 256-bit block mask in LDS.
+__device__ __forceinline__ void route_softmax_group(const float* __restrict__ row,
+                                                    const float* __restrict__ bias, int64_t E,
+                                                    int64_t k, int G, int sub, bool live,
+                                                    int32_t* __restrict__ idx_t,
+                                                    float* __restrict__ w_t,
+                                                    unsigned long long* mask, int bit) {
     // experts of this lane: sub + G*j, j < per_lane (<= kMaxExperts / G)
     const int per_lane = static_cast<int>((E + G - 1) / G);
     uint32_t picked = 0;  // bit j: expert sub + G*j already selected (per_lane <= 32)
@@ -525,18 +534,33 @@ __global__ __launch_bounds__(256) void route_softmax_kernel(
         }
         if (live && bi != INT_MAX && (bi % G) == sub) picked |= 1u << (bi / G);
         if (live && sub == 0) {
-            idx[t * k + s] = bi;
+            idx_t[s] = bi;
             if (s == 0) top = static_cast<double>(bv);
             sum += exp(static_cast<double>(bv) - top);
-            w[t * k + s] = bv;  // the selected value, turned into a weight below
+            w_t[s] = bv;  // the selected value, turned into a weight below
+            if (mask != nullptr && bi >= 0 && bi < E)
+                atomicOr(&mask[bi * 4 + (bit >> 6)], 1ull << (bit & 63));
         }
     }
     if (live && sub == 0) {
         for (int s = 0; s < k; ++s) {
-            const double ex = exp(static_cast<double>(w[t * k + s]) - top);
-            w[t * k + s] = static_cast<float>(ex / sum);
+            const double ex = exp(static_cast<double>(w_t[s]) - top);
+            w_t[s] = static_cast<float>(ex / sum);
         }
     }
+}
+
+__global__ __launch_bounds__(256) void route_softmax_kernel(
+        const float* __restrict__ logits, const float* __restrict__ bias,
+        int64_t T, int64_t E, int64_t k, int G,
+        int32_t* __restrict__ idx, float* __restrict__ w) {
+    const int lane = threadIdx.x & 63;
+    const int sub = lane & (G - 1);
+    const int64_t t = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / G;
+    const bool live = t < T;
+    const int64_t tt = live ? t : 0;
+    route_softmax_group(logits + tt * E, bias, E, k, G, sub, live, idx + tt * k, w + tt * k,
+                        nullptr, 0);
 }
 
 // ---------------------------------------------------------- permutation
@@ -576,18 +600,18 @@ __global__ __launch_bounds__(256) void perm_count_kernel(
     }
 }
 
-// Exclusive scan of counts[E * nb] in place (one workgroup of 1024 threads),
-// then the per-expert offsets.
-__global__ __launch_bounds__(1024) void perm_scan_kernel(
-        int32_t* __restrict__ counts, int64_t nb, int64_t E,
-        int32_t* __restrict__ offsets) {
-    __shared__ int32_t wave_sums[16];
+// Exclusive scan of counts[E * nb] in place by one workgroup of THREADS
+// threads, then the per-expert offsets.
+template <int THREADS>
+__device__ void scan_counts(int32_t* __restrict__ counts, int64_t nb, int64_t E,
+                            int32_t* __restrict__ offsets) {
+    __shared__ int32_t wave_sums[THREADS / 64];
     __shared__ int32_t carry;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     if (tid == 0) carry = 0;
     __syncthreads();
     const int64_t n = E * nb;
-    for (int64_t base = 0; base < n; base += 1024) {
+    for (int64_t base = 0; base < n; base += THREADS) {
         const int64_t i = base + tid;
         const int32_t v = i < n ? counts[i] : 0;
         int32_t incl = v;  // inclusive scan within the wave
@@ -601,12 +625,81 @@ __global__ __launch_bounds__(1024) void perm_scan_kernel(
         for (int j = 0; j < wv; ++j) before += wave_sums[j];
         if (i < n) counts[i] = before + incl - v;
         __syncthreads();
-        if (tid == 1023) carry = before + incl;
+        if (tid == THREADS - 1) carry = before + incl;
         __syncthreads();
     }
     // offsets[e] = base of (e, block 0); offsets[E] = total pairs
-    for (int64_t e = tid; e < E; e += 1024) offsets[e] = nb > 0 ? counts[e * nb] : 0;
+    for (int64_t e = tid; e < E; e += THREADS) offsets[e] = nb > 0 ? counts[e * nb] : 0;
     if (tid == 0) offsets[E] = carry;
+}
+
+__global__ __launch_bounds__(1024) void perm_scan_kernel(
+        int32_t* __restrict__ counts, int64_t nb, int64_t E,
+        int32_t* __restrict__ offsets) {
+    scan_counts<1024>(counts, nb, E, offsets);
+}
+
+// Routing, the block counts and their scan in one launch, as the
+// reference's route_count routes each token and counts it in one launch
+// (src/model.cu:921-942).  Block b routes its kPermTokens tokens (PHI_QUANT:
+// a thread per token; SOFTMAX_TOPK: groups of G lanes, 256 / G tokens per
+// round), records each pick in the block's per-expert 256-bit masks in LDS
+// (as perm_count does) and writes counts[e][b].  Then each block makes its
+// counts visible (a device-scope release fence) and takes a ticket from
+// `done`; the block holding the last ticket fences (acquire), scans every
+// block's counts into the offsets and puts `done` back to 0 for the next
+// launch.  No block waits for another: the scan is done by whichever block
+// finishes last.  `done` must be 0 before the first launch.
+template <int MODE>
+__global__ __launch_bounds__(256) void route_count_kernel(
+        const float* __restrict__ logits, const float* __restrict__ bias, int64_t T,
+        int64_t E, int64_t k, int G, float quantum, float tie_eps,
+        int32_t* __restrict__ idx, float* __restrict__ w, int32_t* __restrict__ counts,
+        int32_t* __restrict__ offsets, uint32_t* __restrict__ done) {
+    __shared__ unsigned long long masks[kMaxExperts * 4];
+    __shared__ int last;
+    const int tid = threadIdx.x;
+    const int64_t b = blockIdx.x, nb = gridDim.x;
+    const int64_t tb = b * kPermTokens;
+    for (int i = tid; i < E * 4; i += blockDim.x) masks[i] = 0ull;
+    __syncthreads();
+    if (MODE == MOE_ROUTER_PHI_QUANT) {
+        const int64_t t = tb + tid;
+        if (tid < kPermTokens && t < T) {
+            int32_t picks[kMaxTopK];
+            route_phi_token(logits + t * E, bias, E, k, quantum, tie_eps, idx + t * k,
+                            w + t * k, picks);
+            for (int s = 0; s < k; ++s) {
+                const int e = picks[s];
+                if (e >= 0 && e < E) atomicOr(&masks[e * 4 + (tid >> 6)], 1ull << (tid & 63));
+            }
+        }
+    } else {
+        const int sub = (tid & 63) & (G - 1);
+        const int per_round = 256 / G;
+        for (int r = 0; r < kPermTokens; r += per_round) {
+            const int j = r + tid / G;  // token of this lane's group, within the block
+            const int64_t t = tb + j;
+            const bool live = j < kPermTokens && t < T;
+            const int64_t tt = live ? t : 0;
+            route_softmax_group(logits + tt * E, bias, E, k, G, sub, live, idx + tt * k,
+                                w + tt * k, masks, j);
+        }
+    }
+    __syncthreads();
+    for (int e = tid; e < E; e += blockDim.x) {
+        const int c = __popcll(masks[e * 4]) + __popcll(masks[e * 4 + 1]) +
+                      __popcll(masks[e * 4 + 2]) + __popcll(masks[e * 4 + 3]);
+        counts[e * nb + b] = c;  // expert-major: the scan below is a plain scan
+    }
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) last = atomicAdd(done, 1u) == static_cast<uint32_t>(nb - 1);
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    scan_counts<256>(counts, nb, E, offsets);
+    if (tid == 0) *done = 0u;
 }
 
 __global__ __launch_bounds__(256) void perm_place_kernel(
@@ -842,6 +935,22 @@ void launch_route(const float* logits, const float* bias, int64_t T, int64_t E,
     const int64_t threads = T * G;
     hipLaunchKernelGGL(route_softmax_kernel, dim3(static_cast<unsigned>(ceil_div(threads, 256))),
                        dim3(256), 0, s, logits, bias, T, E, k, G, idx, w);
+}
+
+void launch_route_count(const float* logits, const float* bias, int64_t T, int64_t E,
+                        int64_t k, int mode, float quantum, float tie_eps, int32_t* idx,
+                        float* w, int32_t* counts, int32_t* offsets, uint32_t* done,
+                        hipStream_t s) {
+    const int64_t nb = ceil_div(T, kPermTokens);
+    if (nb == 0) return;
+    int G = 1;
+    while (G < E && G < 64) G <<= 1;
+    auto go = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(nb)), dim3(256), 0, s, logits,
+                           bias, T, E, k, G, quantum, tie_eps, idx, w, counts, offsets, done);
+    };
+    if (mode == MOE_ROUTER_PHI_QUANT) go(route_count_kernel<MOE_ROUTER_PHI_QUANT>);
+    else go(route_count_kernel<MOE_ROUTER_SOFTMAX_TOPK>);
 }
 
 void launch_perm_count(const int32_t* idx, int64_t T, int64_t k, int64_t E,

@@ -125,11 +125,6 @@ struct Staging {
     hipEvent_t done[2] = {nullptr, nullptr};  // the last DMA out of / into each half
     bool pending[2] = {false, false};
     Scratch io;
-    ~Staging() {
-        if (host != nullptr) (void)hipHostFree(host);
-        for (hipEvent_t e : done)
-            if (e != nullptr) (void)hipEventDestroy(e);
-    }
     // Grow the pinned halves to min(bytes, 32 MiB) each.
     void reserve(std::size_t bytes) {
         constexpr std::size_t kMaxHalf = std::size_t(32) << 20;
@@ -152,8 +147,13 @@ struct Staging {
     }
 };
 
+// Built on first use and never destroyed: a static's destructor would run
+// at process exit, after the HIP runtime may have torn down its own state,
+// so hipHostFree / hipEventDestroy / hipFree from there could crash or hang.
+// The pinned halves, events and device slots are released by the process's
+// end instead.
 Staging& staging() {
-    static Staging s;
+    static Staging& s = *new Staging;
     return s;
 }
 

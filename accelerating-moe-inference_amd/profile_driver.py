@@ -27,7 +27,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("what", choices=["copy", "layer", "sgemm"])
     ap.add_argument("--mib", type=int, default=1024)
-    ap.add_argument("--config", default="c3", choices=["c3", "c4", "c5", "ref"])
+    ap.add_argument("--config", default="c3", choices=["c1", "c3", "c4", "c5", "ref"])
     ap.add_argument("--steps", type=int, default=2)
     args = ap.parse_args()
 
@@ -64,21 +64,8 @@ def main():
         ctx.close()
         return
     cfg = bench.CONFIGS[args.config]
-    T, d, E, k, d_ff = cfg["T"], cfg["d"], cfg["E"], cfg["k"], cfg["d_ff"]
-    g = torch.Generator(device="cuda").manual_seed(0)
-    x = torch.randn((T, d), device="cuda", generator=g)
-    weights = {
-        "gate_w": torch.randn((E, d), device="cuda", generator=g) * 0.02,
-        "w1": torch.randn((E, d_ff, d), device="cuda", generator=g) * 0.02,
-        "w3": torch.randn((E, d_ff, d), device="cuda", generator=g) * 0.02,
-        "w2": torch.randn((E, d, d_ff), device="cuda", generator=g) * 0.02,
-        "expert_bias": None,
-    }
-    if cfg["zipf"] is not None:
-        weights["expert_bias"] = torch.from_numpy(bench.zipf_bias(E, cfg["zipf"])).cuda()
-    y = torch.empty((T, d), device="cuda")
-    router = pkg.ROUTER_PHI_QUANT if cfg.get("router") == "phi_quant" else pkg.ROUTER_SOFTMAX_TOPK
-    desc = pkg.make_desc(T, d, E, k, d_ff, act=pkg.ACT_SWIGLU, router=router)
+    x, weights, y, idx, w, desc = bench.build_layer(pkg, cfg, cfg["T"], False,
+                                                    torch.device("cuda:0"))
     ctx = pkg.Context(0)
     ctx.reserve(desc)
     for i in range(1 + args.steps):

@@ -1,8 +1,9 @@
-"""Benchmark of the MoE layer forward on one MI355X.
+"""Benchmark of the MoE forward hot path on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--config c3|c4|c5|ref] [--block]
-                    [--cpu-seconds S] [--no-extra]
-    python bench.py --sgemm        (config 2: the SGEMM sweep, a line per shape)
+    python bench.py [--steps K] [--warmup W]          (the default run, below)
+    python bench.py --config c1|c3|c4|c5|ref [--block] [--tokens T] [--no-extra]
+                    [--cpu-seconds S]                  (one layer configuration)
+    python bench.py --sgemm        (config 2: the SGEMM sweep, NN and NT, a line per shape)
     python bench.py --decoder      (config 5: the whole 4-layer decoder prefill)
     python bench.py --dropin       (the C++ drop-in PhiMoE::forward, host tensors,
                                     at the reference's layer shape)
@@ -11,18 +12,22 @@
 
 A step is one moe_layer_forward (gate -> route -> permute -> grouped expert
 FFN -> combine) over one batch of synthetic tokens whose inputs and weights
-are already resident in HBM.  The default workload is config 3 of the
+are already resident in HBM.  The headline workload is config 3 of the
 baseline: the Mixtral-shaped fp32 layer, 4096 tokens x d_model 4096, 8
 experts top-2, SwiGLU d_ff 14336, weights N(0, 0.02), inputs N(0, 1),
 softmax over the selected logits.
 
-Prints ONE JSON line: tokens/s of the whole layer, the roofline of the
-dominant kernel (the grouped w1/w3 SwiGLU GEMM, fp32 MFMA bound) measured
-with HIP events on the stream the kernels run on, and the CPU path (the
-oracle restatement of the reference's PhiMoE::forward) timed on a bounded
-token sample on this host's cores.  The default run (config 3) then times
-the other layer shapes (config 5's MoE FFN, the reference's own layer,
-config 4) the same way, without CPU legs, under `other_layer_shapes`.
+The default run prints ONE JSON line: config 3's tokens/s, the roofline of
+its dominant kernel (the grouped w1/w3 SwiGLU GEMM, fp32 MFMA bound)
+measured with HIP events on the stream the kernels run on, and the CPU path
+(the oracle restatement of the reference's PhiMoE::forward, built for this
+host with -march=native, on every core this process is given) timed on a
+bounded token sample; then, under `configs`, every other configuration of
+the baseline measured the same way in the same run, each with its roofline
+and its CPU leg: config 1 (GPU and the whole CPU layer), config 2's eight NN
+SGEMM shapes, config 4, config 5's MoE FFN, the reference's own layer shape,
+config 5's whole decoder prefill, and the drop-in PhiTinyMoEModel::generate
+on the reference's model shape.
 """
 from __future__ import annotations
 
@@ -32,6 +37,7 @@ import json
 import math
 import os
 import sys
+import tempfile
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -40,9 +46,15 @@ FP32_MFMA_PEAK_TFLOPS = 157.3
 HBM_PEAK_GBS = 8000.0
 NORM_EPS = 1e-5
 SPINUP_S = 1.0
+# per-element tolerance rule of the parity figures (tests/helpers.py):
+# |gpu - cpu| <= REL_TOL * max(|cpu|, rms(cpu)) elementwise
+REL_TOL = 1e-4
 
 CONFIGS = {
     # name: T, d, E, k, d_ff, router bias (Zipf s) or None
+    # config 1: the CPU-reference layer (SiLU-MLP experts, no w3)
+    "c1": dict(T=64, d=512, E=4, k=2, d_ff=1024, zipf=None, norm="layer", act="silu_mlp",
+               workload="cpu_reference_moe_layer_fp32"),
     "c3": dict(T=4096, d=4096, E=8, k=2, d_ff=14336, zipf=None, norm="layer",
                workload="mixtral_moe_layer_fp32"),
     "c4": dict(T=16384, d=2048, E=64, k=8, d_ff=1408, zipf=1.2, norm="layer",
@@ -65,59 +77,21 @@ REF_GEMM_MS = {"expert_w13_swiglu": 363.0 / 32, "expert_w2": 191.0 / 32}
 SGEMM_SHAPES = [(1024, 1024, 1024), (2048, 2048, 2048), (4096, 4096, 4096), (8192, 8192, 8192),
                 (16, 14336, 4096), (64, 14336, 4096), (256, 14336, 4096), (512, 14336, 4096)]
 
+# CPU-leg budgets of the default run (seconds of CPU work per configuration)
+CPU_S_EXTRA_LAYER = 6.0
+CPU_S_SGEMM = 0.6
+CPU_S_DECODER = 8.0
+CPU_S_MODEL = 10.0
 
-def sgemm_sweep(args):
-    """One JSON line per config-2 shape: TFLOP/s against the fp32 MFMA peak
-    and the HBM roofline (max of flop time and byte time).  Each shape runs
-    untimed for a while first (SPINUP_S before the first shape, a fifth of
-    it before the others) so that every line is measured at the clock a
-    loaded GPU holds, as the layer bench is; the warm-up calls follow."""
-    import torch
-    pkg = load_pkg()
-    ctx = pkg.Context(0)
-    g = torch.Generator(device="cuda").manual_seed(0)
-    first = True
-    for layout in ("nn", "nt"):
-        for M, N, K in SGEMM_SHAPES:
-            a = torch.rand((M, K), device="cuda", generator=g) * 2 - 1
-            b = (torch.rand((K, N), device="cuda", generator=g) * 2 - 1) if layout == "nn" else \
-                (torch.rand((N, K), device="cuda", generator=g) * 2 - 1)
-            c = torch.empty((M, N), device="cuda")
-            fn = ctx.sgemm_nn if layout == "nn" else ctx.sgemm_nt
-            spin = SPINUP_S if first else SPINUP_S / 5
-            first = False
-            t_spin = time.perf_counter()
-            while time.perf_counter() - t_spin < spin:
-                for _ in range(4):
-                    fn(a, b, c)
-                torch.cuda.synchronize()
-            for _ in range(args.warmup):
-                fn(a, b, c)
-            ctx.reset_timing()
-            ctx.set_timing(True)
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            for _ in range(args.steps):
-                fn(a, b, c)
-            torch.cuda.synchronize()
-            wall = (time.perf_counter() - t0) / args.steps
-            ctx.set_timing(False)
-            ms, n = ctx.kernel_times()[f"sgemm_{layout}"]
-            t = ms / n * 1e-3
-            flops = 2.0 * M * N * K
-            nbytes = 4.0 * (M * K + K * N + M * N)
-            floor = max(flops / (FP32_MFMA_PEAK_TFLOPS * 1e12), nbytes / (HBM_PEAK_GBS * 1e9))
-            print(json.dumps({"workload": "sgemm", "layout": layout, "M": M, "N": N, "K": K,
-                              "kernel_ms": t * 1e3, "wall_ms": wall * 1e3,
-                              "tflops": flops / t / 1e12,
-                              "frac_fp32_mfma_peak": flops / t / 1e12 / FP32_MFMA_PEAK_TFLOPS,
-                              "frac_of_roofline_time": floor / t}), flush=True)
-            del a, b, c
-    ctx.close()
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
 def load_pkg():
     pkg_dir = os.path.join(ROOT, "accelerating-moe-inference_amd")
+    if "moe_amd" in sys.modules:
+        return sys.modules["moe_amd"]
     spec = importlib.util.spec_from_file_location(
         "moe_amd", os.path.join(pkg_dir, "__init__.py"), submodule_search_locations=[pkg_dir])
     mod = importlib.util.module_from_spec(spec)
@@ -133,40 +107,47 @@ def zipf_bias(E, s):
     return np.log(p).astype(np.float32)
 
 
-def hbm_kernel_rates(avg, T, d, E, k, block, w2_splits):
-    """Achieved HBM rate of the routing, permutation, combine and norm kernels
-    against the 8 TB/s peak: algorithmic bytes (each operand read once, each
-    result written once) over the kernel's HIP-event time.  The combine reads
-    the w2_splits K-split partial row buffers the layer's w2 wrote."""
-    nb = -(-T // 256)
-    pairs = T * k
-    algo = {
-        "gate_logits": 4 * (T * d + E * d + T * E),
-        "route_softmax": 4 * (T * E + E) + 8 * pairs,
-        "route_phi": 4 * (T * E + E) + 8 * pairs,
-        "perm_count": 4 * pairs + 4 * E * nb,
-        "perm_scan": 8 * E * nb + 4 * (E + 1),
-        "perm_place": 4 * pairs + 4 * E * nb + 8 * pairs,
-        "layer_norm": 8 * T * d + 8 * T,
-        "rms_norm": 8 * T * d + 4 * T,
-    }
-    out = {}
-    for name, b in algo.items():
-        if name in avg:
-            gbs = b / (avg[name] * 1e-3) / 1e9
-            out[name] = {"bytes": b, "ms": round(avg[name], 5), "GB/s": round(gbs, 1),
-                         "frac": round(gbs / HBM_PEAK_GBS, 4)}
-    if "combine" in avg:
-        S = w2_splits
-        b = 4 * S * pairs * d + 12 * pairs + 4 * T * d * (2 if block else 1)
-        gbs = b / (avg["combine"] * 1e-3) / 1e9
-        out["combine"] = {"bytes": b, "ms": round(avg["combine"], 5), "GB/s": round(gbs, 1),
-                          "frac": round(gbs / HBM_PEAK_GBS, 4), "w2_splits": S}
-    return out
+# --------------------------------------------------------------- the CPU side
+_CPU_SHARE = None
+
+
+def cpu_share():
+    """(threads, description): every CPU this process may run on -- its
+    affinity set, capped by a cgroup CPU quota and by OMP_NUM_THREADS when
+    either is set (the GPU box gives each GPU's process a share of the
+    host).  Taken once, before the oracle's OpenMP runtime starts: with
+    OMP_PROC_BIND it pins the main thread to one CPU, after which the
+    affinity set reads 1."""
+    global _CPU_SHARE
+    if _CPU_SHARE is None:
+        _CPU_SHARE = _cpu_share()
+    return _CPU_SHARE
+
+
+def _cpu_share():
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    why = [f"{n} in the affinity set"]
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            quota, period = f.read().split()[:2]
+        if quota != "max":
+            q = max(1, int(math.ceil(int(quota) / int(period))))
+            why.append(f"cgroup quota {q}")
+            n = min(n, q)
+    except (OSError, ValueError):
+        pass
+    env = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    if env > 0:
+        why.append(f"OMP_NUM_THREADS {env}")
+        n = min(n, env)
+    return n, ", ".join(why)
 
 
 def host_cpu():
-    """The host's CPU model and logical core count (the CPU baseline's hardware)."""
+    """The host's CPU model and core counts (the CPU baseline's hardware)."""
     model = "unknown"
     try:
         with open("/proc/cpuinfo") as f:
@@ -176,7 +157,49 @@ def host_cpu():
                     break
     except OSError:
         pass
-    return f"{model}, {os.cpu_count()} logical cores on the host"
+    n, why = cpu_share()
+    return f"{model}; {os.cpu_count()} logical CPUs visible, {n} used ({why})"
+
+
+_ORACLE = None
+
+
+def cpu_oracle():
+    """The oracle (test infrastructure: the checker and the CPU baseline,
+    never the measured GPU path), compiled once per run for this host with
+    -march=native (the reference Makefile's host flags), OpenMP on every
+    core of this process's share.  Returns (module, build description)."""
+    global _ORACLE
+    if _ORACLE is None:
+        threads, _ = cpu_share()
+        os.environ.setdefault("OMP_PROC_BIND", "close")
+        sys.path.insert(0, ROOT)
+        import oracle
+        try:
+            path = oracle.build_native(tempfile.mkdtemp(prefix="moe_oracle_"))
+            oracle.lib(path)
+            build = "gcc -O3 -march=native -fopenmp -ffp-contract=off, built on this host"
+        except Exception as e:  # no gcc on the host: the prebuilt x86-64-v3 library
+            oracle.lib()
+            build = f"prebuilt gcc -O3 -march=x86-64-v3 -fopenmp (native build failed: {e})"
+        oracle.set_threads(threads)
+        _ORACLE = (oracle, build)
+    return _ORACLE
+
+
+def parity_errors(got, ref):
+    """Normwise max|d| / max|ref| and the per-element rule's max
+    |d| / max(|ref|, rms(ref))."""
+    import numpy as np
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    scale = float(np.max(np.abs(ref))) or 1.0
+    rms = float(np.sqrt(np.mean(ref * ref))) or 1.0
+    d = np.abs(got - ref)
+    return {"max_rel_err": float(np.max(d)) / scale,
+            "max_elem_rel_err": float(np.max(d / np.maximum(np.abs(ref), rms))),
+            "within_1e-4": bool(float(np.max(d / np.maximum(np.abs(ref), rms))) <= REL_TOL
+                                and float(np.max(d)) / scale <= REL_TOL)}
 
 
 def tile_cover_sample(gidx, E, bm=128, block=32):
@@ -203,28 +226,26 @@ def tile_cover_sample(gidx, E, bm=128, block=32):
     return np.concatenate([cover, rest]), len(cover)
 
 
-def cpu_baseline(x, weights, cfg, pkg_outputs, target_s):
+def cpu_baseline(x, weights, cfg, pkg_outputs, target_s, block):
     """The oracle's PhiMoE::forward restatement on a token sample sized to
     about target_s seconds of CPU work (at least the tokens that cover every
-    m-tile of every expert), checked against the GPU's rows; and the oracle's
-    gate and router on every token, checked against the GPU's routing.  Test
-    infrastructure: timed here as the reported CPU baseline, never part of
-    the GPU measurement."""
+    m-tile of every expert; every token when target_s is None), checked
+    against the GPU's rows; and the oracle's gate and router on every token,
+    checked against the GPU's routing.  Test infrastructure: timed here as
+    the reported CPU baseline, never part of the GPU measurement."""
     import numpy as np
-    sys.path.insert(0, ROOT)
-    import oracle
-
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
-    oracle.set_threads(threads)
-    gw, w1, w3, w2, bias = (weights[n] for n in ("gate_w", "w1", "w3", "w2", "expert_bias"))
+    oracle, build = cpu_oracle()
+    gw, w1, w3, w2, bias = (weights.get(n) for n in ("gate_w", "w1", "w3", "w2", "expert_bias"))
     nw, nb = weights.get("norm_w"), weights.get("norm_b")
     k = cfg["k"]
+    act = oracle.ACT_SILU_MLP if cfg.get("act") == "silu_mlp" else oracle.ACT_SWIGLU
     router = (oracle.ROUTER_PHI_QUANT if cfg.get("router") == "phi_quant"
               else oracle.ROUTER_SOFTMAX_TOPK)
     gy, gidx = pkg_outputs
+    T = x.shape[0]
 
     def normed(xs):
-        if nw is None:
+        if not block:
             return xs
         if nb is None:
             return oracle.rms_norm(xs, nw, NORM_EPS, oracle.CONTRACT_FMA)[0]
@@ -232,61 +253,398 @@ def cpu_baseline(x, weights, cfg, pkg_outputs, target_s):
 
     def run(toks):
         t0 = time.perf_counter()
-        y, idx, w = oracle.moe_forward(normed(x[toks]), gw, w1, w3, w2, k,
-                                       act=oracle.ACT_SWIGLU, router_mode=router,
-                                       expert_bias=bias)
-        if nw is not None:  # the decoder block: y = x + MoE(norm(x))
+        y, idx, w = oracle.moe_forward(normed(x[toks]), gw, w1, w3, w2, k, act=act,
+                                       router_mode=router, expert_bias=bias)
+        if block:  # the decoder block: y = x + MoE(norm(x))
             y = y + x[toks]
         return time.perf_counter() - t0, y, idx
 
     order, n_cover = tile_cover_sample(gidx, cfg["E"])
-    # Grow the sample until it takes about target_s: small samples leave
-    # most of the threads idle (the reference parallelises over an expert's
-    # rows), so the per-token time only settles once experts hold >= threads
-    # rows each.
-    n = max(16, n_cover)
-    while True:
-        toks = np.sort(order[:n])
+    if target_s is None:
+        # the whole layer, repeated until a second of CPU time has passed
+        toks = np.arange(T)
         dt, y, idx = run(toks)
-        if dt >= 0.5 * target_s or n >= cfg["T"]:
-            break
-        n = int(min(cfg["T"], max(2 * n, round(0.9 * n * target_s / max(dt, 1e-9)))))
-    ref_scale = float(np.max(np.abs(y))) or 1.0
+        reps, total = 1, dt
+        while total < 1.0:
+            dt, y, idx = run(toks)
+            reps += 1
+            total += dt
+        dt, n = total / reps, T
+        what = f"all {T} tokens (the whole layer), mean of {reps} runs"
+    else:
+        # Grow the sample until it takes about target_s: small samples leave
+        # most of the threads idle (the reference parallelises over an
+        # expert's rows), so the per-token time only settles once experts
+        # hold >= threads rows each.
+        n = max(16, n_cover)
+        while True:
+            toks = np.sort(order[:n])
+            dt, y, idx = run(toks)
+            if dt >= 0.5 * target_s or n >= T:
+                break
+            n = int(min(T, max(2 * n, round(0.9 * n * target_s / max(dt, 1e-9)))))
+        what = (f"{n} of {T} tokens of the same layer (same weights; routing is per token): "
+                f"the {n_cover} whose packed rows cover every 128-row m-tile of every "
+                f"expert, then the lowest-numbered others")
     all_idx, _ = oracle.route(oracle.matmul_nt(normed(x), gw, oracle.CONTRACT_FMA), k,
                               mode=router, expert_bias=bias)
-    parity = {
-        "tokens": n,
-        "tile_covering_tokens": n_cover,
-        "routing_bit_exact": bool(np.array_equal(gidx[toks], idx)),
-        "routing_bit_exact_all_tokens": bool(np.array_equal(gidx, all_idx)),
-        "max_rel_err": float(np.max(np.abs(gy[toks] - y)) / ref_scale),
-    }
+    parity = {"tokens": n, "tile_covering_tokens": n_cover,
+              "routing_bit_exact": bool(np.array_equal(gidx[toks], idx)),
+              "routing_bit_exact_all_tokens": bool(np.array_equal(gidx, all_idx))}
+    parity.update(parity_errors(gy[toks], y))
     return {
         "value": n / dt,
         "unit": "tokens/s",
         "cores": oracle.get_threads(),
         "kind": "port",
         "host": host_cpu(),
-        "sample": (f"{n} of {cfg['T']} tokens of the same layer (same weights; routing is "
-                   f"per token): the {n_cover} whose packed rows cover every 128-row m-tile "
-                   f"of every expert, then the lowest-numbered others; {dt:.1f} s on "
-                   f"{oracle.get_threads()} threads"),
+        "build": build,
+        "sample": f"{what}; {dt:.2f} s on {oracle.get_threads()} threads",
     }, parity
 
 
+# ------------------------------------------------------------- layer configs
+def hbm_kernel_rates(avg, T, d, E, k, block, w2_splits, floor_ms):
+    """Achieved HBM rate of the routing, permutation, combine and norm kernels
+    against the 8 TB/s peak: algorithmic bytes (each operand read once, each
+    result written once) over the kernel's HIP-event time; and that time
+    against the launch floor (an empty kernel timed the same way in the same
+    run), since the small launches sit on it rather than on HBM.  The combine
+    reads the w2_splits K-split partial row buffers the layer's w2 wrote."""
+    nb = -(-T // 256)
+    pairs = T * k
+    algo = {
+        "gate_logits": 4 * (T * d + E * d + T * E),
+        "route_softmax": 4 * (T * E + E) + 8 * pairs,
+        "route_phi": 4 * (T * E + E) + 8 * pairs,
+        "perm_count": 4 * pairs + 4 * E * nb,
+        "perm_scan": 8 * E * nb + 4 * (E + 1),
+        "perm_place": 4 * pairs + 4 * E * nb + 8 * pairs,
+        # routing, block counts and their scan in one launch: logits read,
+        # picks and weights written, counts written, scanned and offsets out
+        "route_count": 4 * (T * E + E) + 8 * pairs + 12 * E * nb + 4 * (E + 1),
+        "layer_norm": 8 * T * d + 8 * T,
+        "rms_norm": 8 * T * d + 4 * T,
+        "combine": 4 * w2_splits * pairs * d + 12 * pairs + 4 * T * d * (2 if block else 1),
+    }
+    out = {}
+    for name, b in algo.items():
+        if name in avg:
+            gbs = b / (avg[name] * 1e-3) / 1e9
+            out[name] = {"bytes": b, "ms": round(avg[name], 5), "GB/s": round(gbs, 1),
+                         "frac": round(gbs / HBM_PEAK_GBS, 4)}
+            if floor_ms:
+                out[name]["x_launch_floor"] = round(avg[name] / floor_ms, 2)
+    if "combine" in out:
+        out["combine"]["w2_splits"] = w2_splits
+    return out
+
+
+def load_traffic(name, key="expert_w13_swiglu_bytes_per_launch"):
+    """HBM bytes per launch of a configuration's dominant kernel, from the
+    committed rocprofv3 counter summary (profiles/traffic_<name>.json), or
+    None."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{name}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get(key)
+
+
+def build_layer(pkg, cfg, T, block, dev):
+    """Seeded inputs, weights, outputs and the descriptor of one layer shape."""
+    import torch
+    d, E, k, d_ff = cfg["d"], cfg["E"], cfg["k"], cfg["d_ff"]
+    swiglu = cfg.get("act", "swiglu") == "swiglu"
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn((T, d), device=dev, generator=g)
+    weights = {
+        "gate_w": torch.randn((E, d), device=dev, generator=g) * 0.02,
+        "w1": torch.randn((E, d_ff, d), device=dev, generator=g) * 0.02,
+        "w3": torch.randn((E, d_ff, d), device=dev, generator=g) * 0.02 if swiglu else None,
+        "w2": torch.randn((E, d, d_ff), device=dev, generator=g) * 0.02,
+        "expert_bias": None,
+    }
+    if cfg["zipf"] is not None:
+        weights["expert_bias"] = torch.from_numpy(zipf_bias(E, cfg["zipf"])).to(dev)
+    rms = cfg["norm"] == "rms"
+    if block:
+        weights["norm_w"] = 1 + 0.1 * torch.randn(d, device=dev, generator=g)
+        weights["norm_b"] = None if rms else 0.1 * torch.randn(d, device=dev, generator=g)
+    y = torch.empty((T, d), device=dev)
+    idx = torch.empty((T, k), dtype=torch.int32, device=dev)
+    w = torch.empty((T, k), device=dev)
+    desc = pkg.make_desc(T, d, E, k, d_ff, act=pkg.ACT_SWIGLU if swiglu else pkg.ACT_SILU_MLP,
+                         router=(pkg.ROUTER_PHI_QUANT if cfg.get("router") == "phi_quant"
+                                 else pkg.ROUTER_SOFTMAX_TOPK), contract=pkg.CONTRACT_FMA,
+                         norm=(pkg.NORM_RMS if rms else pkg.NORM_LAYER) if block
+                         else pkg.NORM_NONE,
+                         norm_eps=NORM_EPS, residual=block)
+    return x, weights, y, idx, w, desc
+
+
+def time_layer(ctx, desc, weights, x, y, idx, w, warmup, steps, spin_s=SPINUP_S):
+    """Spin-up, warm-up, `steps` timed forwards without per-kernel events,
+    then as many with HIP events around every launch (on the stream the
+    kernels run on), each followed by one empty kernel timed the same way
+    (the launch floor).  Returns (spin-up forwards, timed seconds,
+    instrumented seconds, per-kernel times)."""
+    import torch
+    # spin-up: the GPU takes about a second of load to reach its full clock
+    # (durations of short layers fall 10-20 % over the first second), so
+    # forwards run for at least spin_s before the warm-up steps
+    spin_steps, t_spin = 0, time.perf_counter()
+    while time.perf_counter() - t_spin < spin_s:
+        ctx.layer_forward(desc, weights, x, y, idx, w)
+        torch.cuda.synchronize()
+        spin_steps += 1
+    for _ in range(warmup):
+        ctx.layer_forward(desc, weights, x, y, idx, w)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        ctx.layer_forward(desc, weights, x, y, idx, w)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ctx.reset_timing()
+    ctx.set_timing(True)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    for _ in range(steps):
+        ctx.layer_forward(desc, weights, x, y, idx, w)
+        ctx.launch_floor()
+    torch.cuda.synchronize()
+    instrumented = time.perf_counter() - t1
+    ctx.set_timing(False)
+    return spin_steps, elapsed, instrumented, ctx.kernel_times()
+
+
+def layer_entry(pkg, name, dev, warmup, steps, cpu_seconds, block=False, tokens=None,
+                spin_s=SPINUP_S):
+    """One layer configuration measured in full: tokens/s of the whole layer,
+    the expert GEMMs' fraction of the fp32 MFMA peak, the w1/w3 roofline
+    (HIP events; HBM traffic from the committed counter summary), the small
+    kernels against HBM and the launch floor, and the CPU path on a bounded
+    sample (cpu_seconds; None = the whole layer; 0 = skip)."""
+    import numpy as np
+    import torch
+    cfg = CONFIGS[name]
+    T, d, E, k, d_ff = cfg["T"], cfg["d"], cfg["E"], cfg["k"], cfg["d_ff"]
+    if tokens is not None:
+        T = tokens  # a batch-size point of the configuration's layer shape
+    swiglu = cfg.get("act", "swiglu") == "swiglu"
+    rms = cfg["norm"] == "rms"
+    x, weights, y, idx, w, desc = build_layer(pkg, cfg, T, block, dev)
+    ctx = pkg.Context(0)
+    ctx.reserve(desc)
+    spin_steps, elapsed, instrumented, kt = time_layer(ctx, desc, weights, x, y, idx, w,
+                                                       warmup, steps, spin_s)
+    splits = ctx.w2_splits(desc)
+    ctx.close()
+
+    counts = np.bincount(idx.cpu().numpy().ravel(), minlength=E)
+    pairs = T * k
+    n13 = 2 if swiglu else 1
+    flops_w13 = 2.0 * pairs * d * d_ff * n13
+    flops_w2 = 2.0 * pairs * d_ff * d
+    avg = {n: ms / c for n, (ms, c) in kt.items()}
+    floor = avg.pop("empty", None)
+    w13_name = "expert_w13_swiglu" if swiglu else "expert_w1_silu"
+    w13_ms, w2_ms = avg[w13_name], avg["expert_w2"]
+    w13_tflops = flops_w13 / (w13_ms * 1e-3) / 1e12
+    expert_tflops = (flops_w13 + flops_w2) / ((w13_ms + w2_ms) * 1e-3) / 1e12
+    entry = {
+        "workload": cfg["workload"],
+        "config": {"workload": cfg["workload"], "tokens": T, "d_model": d, "experts": E,
+                   "top_k": k, "d_ff": d_ff,
+                   "router": ("quantised top-2, weights 1/2 (PhiMoE::route)"
+                              if cfg.get("router") == "phi_quant"
+                              else "softmax over selected top-k"),
+                   "expert": "SwiGLU" if swiglu else "SiLU-MLP (Linear, SiLU, Linear)",
+                   "router_bias": f"zipf(s={cfg['zipf']})" if cfg["zipf"] else None,
+                   "block": (f"y = x + MoE({'rms_norm' if rms else 'layer_norm'}(x))"
+                             if block else None)},
+        "value": T * steps / elapsed,
+        "unit": "tokens/s",
+        "ms_per_step": 1e3 * elapsed / steps,
+        "steps": steps,
+        "warmup": warmup,
+        "expert_gemm_tflops": expert_tflops,
+        "expert_gemm_frac_fp32_mfma_peak": expert_tflops / FP32_MFMA_PEAK_TFLOPS,
+        "roofline": {
+            "kernel": w13_name,
+            "bound": "mfma",
+            "achieved": w13_tflops,
+            "peak": FP32_MFMA_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": w13_tflops / FP32_MFMA_PEAK_TFLOPS,
+            "traffic": (load_traffic(name, f"{w13_name}_bytes_per_launch")
+                        if (tokens is None and not block) else None),
+            "flops_per_launch": flops_w13,
+        },
+        "kernel_avg_ms": {n: round(v, 5) for n, v in sorted(avg.items())},
+        "launch_floor_ms": None if floor is None else round(floor, 5),
+        "hbm_kernels": hbm_kernel_rates(avg, T, d, E, k, block, splits, floor),
+        "expert_rows": counts.tolist(),
+        "spinup": f"{spin_steps} untimed forwards over {spin_s:.1f} s before the warm-up steps",
+        "timing": (f"ms_per_step from {steps} steps without per-kernel events; "
+                   f"kernel_avg_ms and the roofline from HIP events over {steps} more "
+                   f"steps ({1e3 * instrumented / steps:.3f} ms per instrumented step)"),
+    }
+    if name == "ref":
+        # the reference's own per-layer expert GEMM times at this shape (RTX 3090)
+        entry["reference_gpu_gemm_ms"] = {n: round(v, 3) for n, v in REF_GEMM_MS.items()}
+        entry["speedup_vs_reference_gpu_gemms"] = {
+            n: round(REF_GEMM_MS[n] / avg[n], 2) for n in REF_GEMM_MS if n in avg}
+    entry["cpu_baseline"] = entry["cpu_sample_parity"] = None
+    if cpu_seconds is None or cpu_seconds > 0:
+        host = {n: (None if v is None else v.cpu().numpy()) for n, v in weights.items()}
+        cpu, parity = cpu_baseline(x.cpu().numpy(), host, cfg,
+                                   (y.cpu().numpy(), idx.cpu().numpy()), cpu_seconds, block)
+        # the expert-GEMM rate of the CPU path: its FLOPs per token
+        cpu["expert_gemm_gflops"] = cpu["value"] * k * d * d_ff * 2 * (n13 + 1) / 1e9
+        entry["cpu_baseline"], entry["cpu_sample_parity"] = cpu, parity
+    del x, weights, y, idx, w
+    torch.cuda.empty_cache()
+    return entry
+
+
+# ------------------------------------------------------------------ config 2
+def sgemm_time(ctx, fn, a, b, c, warmup, steps, spin_s):
+    """Time (s) per SGEMM call after a spin-up and warm-up: one HIP event
+    pair on the stream the kernels run on around `steps` back-to-back calls
+    (a split-K plan's reduction launch included), so that an event's own
+    overhead -- microseconds, against a 1024^3 product's 20-odd -- is not
+    charged to every call; and the host wall time per call."""
+    import torch
+    t_spin = time.perf_counter()
+    while time.perf_counter() - t_spin < spin_s:
+        for _ in range(4):
+            fn(a, b, c)
+        torch.cuda.synchronize()
+    for _ in range(warmup):
+        fn(a, b, c)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        fn(a, b, c)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
+    return e0.elapsed_time(e1) * 1e-3 / steps, wall
+
+
+def sgemm_roofline(M, N, K, t):
+    flops = 2.0 * M * N * K
+    nbytes = 4.0 * (M * K + K * N + M * N)
+    t_flop = flops / (FP32_MFMA_PEAK_TFLOPS * 1e12)
+    t_byte = nbytes / (HBM_PEAK_GBS * 1e9)
+    hbm = t_byte > t_flop
+    return {"bound": "hbm" if hbm else "mfma",
+            "achieved": (nbytes / t / 1e9) if hbm else flops / t / 1e12,
+            "peak": HBM_PEAK_GBS if hbm else FP32_MFMA_PEAK_TFLOPS,
+            "unit": "GB/s" if hbm else "TFLOP/s",
+            "frac": max(t_flop, t_byte) / t}
+
+
+def sgemm_entries(pkg, warmup, steps, cpu_seconds):
+    """Config 2 as the baseline states it: C = A B, row-major, no transpose,
+    A and B ~ U[-1, 1], each shape's kernel time from HIP events, its
+    TFLOP/s, fraction of the fp32 peak and fraction of its roofline time
+    max(flop time, byte time); HBM traffic from the committed counter
+    summary; and the CPU path (the oracle's matmul, the k-ascending loop of
+    the reference's matmul_transposed over B's columns) on a row sample of
+    the same operands, whose rows are checked against the GPU's."""
+    import numpy as np
+    import torch
+    ctx = pkg.Context(0)
+    g = torch.Generator(device="cuda").manual_seed(0)
+    traffic = {}
+    tpath = os.path.join(ROOT, "profiles", "traffic_c2.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f)
+    oracle, build = cpu_oracle() if cpu_seconds > 0 else (None, None)
+    out = []
+    for i, (M, N, K) in enumerate(SGEMM_SHAPES):
+        a = torch.rand((M, K), device="cuda", generator=g) * 2 - 1
+        b = torch.rand((K, N), device="cuda", generator=g) * 2 - 1
+        c = torch.empty((M, N), device="cuda")
+        t, wall = sgemm_time(ctx, ctx.sgemm_nn, a, b, c, warmup, steps,
+                             SPINUP_S if i == 0 else SPINUP_S / 5)
+        flops = 2.0 * M * N * K
+        e = {"layout": "nn", "M": M, "N": N, "K": K, "ms_per_call": t * 1e3, "wall_ms": wall * 1e3,
+             "tflops": flops / t / 1e12,
+             "frac_fp32_mfma_peak": flops / t / 1e12 / FP32_MFMA_PEAK_TFLOPS}
+        roof = sgemm_roofline(M, N, K, t)
+        e["frac_of_roofline_time"] = roof["frac"]
+        e["roofline"] = dict(roof, traffic=traffic.get(f"nn {M}x{N}x{K}"))
+        if oracle is not None:
+            threads = oracle.get_threads()
+            rows = min(M, max(threads, int(math.ceil(cpu_seconds * 3e9 / (2.0 * N * K)))))
+            sel = np.linspace(0, M - 1, rows).round().astype(np.int64)
+            ah, bh = a[sel].cpu().numpy(), b.cpu().numpy()
+            t0 = time.perf_counter()
+            ref = oracle.matmul_nn(ah, bh, oracle.CONTRACT_FMA)
+            dt = time.perf_counter() - t0
+            e["cpu_baseline"] = {
+                "value": 2.0 * rows * N * K / dt / 1e9, "unit": "GFLOP/s", "cores": threads,
+                "kind": "port", "build": build,
+                "sample": f"{rows} of {M} rows of C (evenly spaced), {dt:.2f} s"}
+            e["cpu_sample_parity"] = parity_errors(c[sel].cpu().numpy(), ref)
+        out.append(e)
+        del a, b, c
+    ctx.close()
+    torch.cuda.empty_cache()
+    return out
+
+
+def sgemm_sweep(args):
+    """One JSON line per config-2 shape, NN then NT: TFLOP/s against the
+    fp32 MFMA peak and the roofline (max of flop time and byte time).  Each
+    shape runs untimed for a while first (SPINUP_S before the first shape, a
+    fifth of it before the others) so that every line is measured at the
+    clock a loaded GPU holds, as the layer bench is; the warm-up calls
+    follow."""
+    import torch
+    pkg = load_pkg()
+    ctx = pkg.Context(0)
+    g = torch.Generator(device="cuda").manual_seed(0)
+    first = True
+    for layout in ("nn", "nt"):
+        for M, N, K in SGEMM_SHAPES:
+            a = torch.rand((M, K), device="cuda", generator=g) * 2 - 1
+            b = (torch.rand((K, N), device="cuda", generator=g) * 2 - 1) if layout == "nn" else \
+                (torch.rand((N, K), device="cuda", generator=g) * 2 - 1)
+            c = torch.empty((M, N), device="cuda")
+            fn = ctx.sgemm_nn if layout == "nn" else ctx.sgemm_nt
+            t, wall = sgemm_time(ctx, fn, a, b, c, args.warmup, args.steps,
+                                 SPINUP_S if first else SPINUP_S / 5)
+            first = False
+            flops = 2.0 * M * N * K
+            print(json.dumps({"workload": "sgemm", "layout": layout, "M": M, "N": N, "K": K,
+                              "ms_per_call": t * 1e3, "wall_ms": wall * 1e3,
+                              "tflops": flops / t / 1e12,
+                              "frac_fp32_mfma_peak": flops / t / 1e12 / FP32_MFMA_PEAK_TFLOPS,
+                              "frac_of_roofline_time": sgemm_roofline(M, N, K, t)["frac"]}),
+                  flush=True)
+            del a, b, c
+    ctx.close()
+
+
+# ------------------------------------------------------------------ config 5
 def decoder_cpu_baseline(tokens, W, cfg, gpu_hidden, target_s):
     """The oracle decoder (oracle/decoder.py) on a sample of the batch sized
     to about target_s seconds of CPU work: a prefix of sequence 0 while one
     sequence is more than enough, else the first m whole sequences.
     Attention is causal and sequences are independent, so the sample's rows
     are exactly those rows of the full prefill."""
-    import numpy as np
-    sys.path.insert(0, ROOT)
-    import oracle
+    oracle, build = cpu_oracle()
     from oracle import decoder as od
 
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
-    oracle.set_threads(threads)
     B, S = tokens.shape
     m, n = 1, 16
     while True:
@@ -300,8 +658,10 @@ def decoder_cpu_baseline(tokens, W, cfg, gpu_hidden, target_s):
         else:
             m = int(min(B, max(m + 1, round(0.9 * m * target_s / max(dt, 1e-9)))))
     ref = gpu_hidden.reshape(B, S, -1)[:m, :n].reshape(m * n, -1)
-    parity = {"tokens": m * n,
-              "hidden_max_rel_err": float(np.max(np.abs(ref - x)) / (np.max(np.abs(x)) or 1.0))}
+    err = parity_errors(ref, x)
+    parity = {"tokens": m * n, "hidden_max_rel_err": err["max_rel_err"],
+              "hidden_max_elem_rel_err": err["max_elem_rel_err"],
+              "within_1e-4": err["within_1e-4"]}
     what = (f"first {n} positions of sequence 0" if m == 1 and n < S
             else f"the first {m} whole sequences")
     return {
@@ -310,12 +670,150 @@ def decoder_cpu_baseline(tokens, W, cfg, gpu_hidden, target_s):
         "cores": oracle.get_threads(),
         "kind": "port",
         "host": host_cpu(),
+        "build": build,
         "sample": (f"{what} of {B} x {S} (all {cfg.layers} layers, same weights; causal "
                    f"attention, so these rows are those of the full prefill), {dt:.1f} s on "
                    f"{oracle.get_threads()} threads"),
     }, parity
 
 
+def decoder_entry(pkg, warmup, steps, cpu_seconds, graph=True):
+    """Config 5 as a whole: the 4-layer decoder prefill of 8 x 512 tokens
+    (embedding, per layer RMS norm, q/k/v projections, RoPE, causal
+    attention, o projection + residual, the MoE block with its norm and
+    residual; final norm and lm_head on the last row of every sequence)."""
+    import torch
+
+    B, S = 8, 512
+    cfg = pkg.DecoderConfig()
+    dev = torch.device("cuda:0")
+    W = pkg.random_weights(cfg, dev, seed=0)
+    g = torch.Generator(device="cpu").manual_seed(1)
+    tokens = torch.randint(0, cfg.vocab, (B, S), generator=g, dtype=torch.int32).to(dev)
+    ctx = pkg.Context(0)
+    model = pkg.DecoderModel(ctx, cfg, W)
+    model.reserve(B, S)
+    logits = torch.empty((B, cfg.vocab), device=dev)
+    # spin-up: prefills for at least SPINUP_S, so every timed step runs at the
+    # clock a loaded GPU holds; then the warm-up steps
+    t_spin = time.perf_counter()
+    while time.perf_counter() - t_spin < SPINUP_S:
+        model.generate(tokens, logits)
+        torch.cuda.synchronize()
+    for _ in range(warmup):
+        model.generate(tokens, logits)
+    torch.cuda.synchronize()
+    # per-kernel HIP events over K eager steps (the breakdown and the roofline)
+    ctx.reset_timing()
+    ctx.set_timing(True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        model.generate(tokens, logits)
+    torch.cuda.synchronize()
+    eager_s = time.perf_counter() - t0
+    ctx.set_timing(False)
+    kt = ctx.kernel_times()
+    elapsed = eager_s
+    graph_note = None
+    if graph:
+        # the timed steps: the same prefill captured once in a HIP graph and
+        # replayed (one host launch per step instead of ~70)
+        from moe_amd.decoder import CapturedPrefill
+        cap = CapturedPrefill(model, B, S, warmup=warmup)
+        cap.tokens.copy_(tokens)
+        for _ in range(warmup):
+            cap.replay()
+        torch.cuda.synchronize()
+        check = cap.replay().clone()
+        model.generate(tokens, logits)
+        torch.cuda.synchronize()
+        assert torch.equal(check, logits), "graph replay differs from the eager prefill"
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            cap.replay()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        cap.close()
+        graph_note = (f"timed steps are HIP-graph replays of the prefill; the per-kernel times "
+                      f"come from HIP events over {steps} eager steps "
+                      f"({1e3 * eager_s / steps:.3f} ms per eager step)")
+    T = B * S
+    per_step = {n: ms / steps for n, (ms, _) in kt.items()}
+    avg = {n: ms / c for n, (ms, c) in kt.items()}
+    pairs = T * cfg.top_k
+    # w13 launches differ in size (the pruned last layer has B*k pairs), so
+    # the roofline is the step's w13 FLOPs over the step's w13 time
+    full = cfg.layers - 1 if model.prune_last else cfg.layers
+    tail_pairs = B * cfg.top_k if model.prune_last else 0
+    flops_w13 = 2.0 * (full * pairs + tail_pairs) * cfg.d * cfg.d_ff * 2
+    w13_tflops = flops_w13 / (per_step["expert_w13_swiglu"] * 1e-3) / 1e12
+    qw, kw = cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
+    tail_rows = B if model.prune_last else 0
+    proj_flops = (2.0 * full * T * cfg.d * (qw + 2 * kw + qw) + 2.0 * tail_rows * cfg.d * (qw + qw)
+                  + 2.0 * (cfg.layers - full) * T * cfg.d * 2 * kw + 2.0 * B * cfg.d * cfg.vocab)
+    # causal attention: S(S+1)/2 (query, key) pairs per sequence and head, 2 products;
+    # the pruned layer's last rows see S keys each
+    attn_flops = (full * B * cfg.heads * 2 * (2.0 * cfg.head_dim * S * (S + 1) / 2)
+                  + tail_rows * cfg.heads * 2 * (2.0 * cfg.head_dim * S))
+    moe_flops = 2.0 * (full * pairs + tail_pairs) * cfg.d * cfg.d_ff * 3
+    cpu = parity = None
+    if cpu_seconds > 0:
+        hidden = model.hidden(tokens).cpu().numpy()
+        Wh = {k: (None if v is None else v.cpu().numpy()) for k, v in W.items() if k != "layers"}
+        Wh["layers"] = [{k: (None if v is None else v.cpu().numpy()) for k, v in L.items()}
+                        for L in W["layers"]]
+        cpu, parity = decoder_cpu_baseline(tokens.cpu().numpy(), Wh, cfg, hidden, cpu_seconds)
+    ms_per_step = 1e3 * elapsed / steps
+    out = {
+        "metric": "decoder prefill tokens/sec (config 5), 1 MI355X",
+        "value": T * steps / elapsed,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": ("synthetic (seeded: token ids uniform over the vocabulary, embedding "
+                 "N(0,1), weights N(0,0.02), norm weights 1 + N(0,0.1))"),
+        "config": {"workload": "decoder_prefill_fp32", "batch": B, "seq_len": S,
+                   "layers": cfg.layers, "d_model": cfg.d, "heads": cfg.heads,
+                   "kv_heads": cfg.kv_heads, "experts": cfg.experts, "top_k": cfg.top_k,
+                   "d_ff": cfg.d_ff, "vocab": cfg.vocab, "norm": "rms", "rope_theta":
+                   cfg.rope_theta, "router": "softmax over selected top-k",
+                   "lm_head": "last position of each sequence"},
+        "model_tflops": (proj_flops + attn_flops + moe_flops) / (ms_per_step * 1e-3) / 1e12,
+        "roofline": {
+            "kernel": "expert_w13_swiglu",
+            "bound": "mfma",
+            "achieved": w13_tflops,
+            "peak": FP32_MFMA_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": w13_tflops / FP32_MFMA_PEAK_TFLOPS,
+            "traffic": load_traffic("c5"),
+            "flops_per_step": flops_w13,
+            "launches_per_step": cfg.layers,
+            "note": (f"achieved = the step's w13 FLOPs ({full} layers x {pairs} pairs + "
+                     f"{tail_pairs} pairs of the pruned layer) over the step's w13 HIP-event "
+                     f"time; traffic = one full layer's w13 launch (config 5's MoE FFN)"),
+        },
+        "kernel_ms_per_step": {n: round(v, 4) for n, v in sorted(per_step.items())},
+        "kernel_avg_ms": {n: round(v, 5) for n, v in sorted(avg.items())},
+        "cpu_baseline": cpu,
+        "cpu_sample_parity": parity,
+        "timing": graph_note or "timed steps are eager, with HIP events around every kernel",
+        "eager_ms_per_step": 1e3 * eager_s / steps,
+    }
+    ctx.close()
+    del model, W, tokens, logits
+    torch.cuda.empty_cache()
+    return out
+
+
+# ------------------------------------------------------ the drop-in C++ API
 def write_model_bin(path, tensors):
     """The reference's model.bin layout (src/model_loader.cu:14-30): u32 count;
     per tensor u32 name length, name, u32 ndim, u32 dims, u64 offset, u64
@@ -342,7 +840,6 @@ def dropin_bench(args):
     C shim the drop-in tests use (tests/cpp/libdropin_shim.so): weights in a
     model.bin of the reference's format, 15,583 rows of d 4096."""
     import ctypes
-    import tempfile
     import numpy as np
     cfg = CONFIGS["ref"]
     T, d, E, d_ff = cfg["T"], cfg["d"], cfg["E"], cfg["d_ff"]
@@ -378,20 +875,14 @@ def dropin_bench(args):
     }))
 
 
-def model_bench(args):
-    """The C++ drop-in's PhiTinyMoEModel::generate (the reference's timed
-    end-to-end call, src/main.cpp:584-601) on the reference's model shape
-    (Phi-tiny-MoE: 32 layers, d 4096, 16 query / 4 key heads of 128, 16
-    experts of d_ff 448, vocabulary 32064; random weights) over a batch
-    shaped like the reference's contest input: 1024 sequences, 10-29 tokens
-    each, whose first 4 tokens come from 64 shared prefixes, so the prefix
-    trie removes about a fifth of the rows (the reference's input: 19,803
-    tokens, 15,583 trie rows).  Host token lists in, host logits out."""
-    import ctypes
-    import struct
-    import tempfile
-    import numpy as np
-    L_, h, E, ff, vocab, qw, kw = 32, 4096, 16, 448, 32064, 16 * 128, 4 * 128
+# The reference's model (Phi-tiny-MoE) as the drop-in loads it.
+PHI = dict(layers=32, d=4096, E=16, d_ff=448, vocab=32064, heads=16, kv_heads=4, head_dim=128)
+
+
+def phi_tensor_specs():
+    """(name, shape, scale, shift) of every tensor of the reference's model."""
+    L_, h, E, ff, vocab = PHI["layers"], PHI["d"], PHI["E"], PHI["d_ff"], PHI["vocab"]
+    qw, kw = PHI["heads"] * PHI["head_dim"], PHI["kv_heads"] * PHI["head_dim"]
     specs = [("model.embed_tokens.weight", (vocab, h), 1.0, 0.0),
              ("model.norm.weight", (h,), 0.1, 1.0), ("model.norm.bias", (h,), 0.1, 0.0),
              ("lm_head.weight", (vocab, h), 0.02, 0.0), ("lm_head.bias", (vocab,), 0.02, 0.0)]
@@ -410,206 +901,220 @@ def model_bench(args):
             specs += [(f"{p}.block_sparse_moe.experts.{e}.w1.weight", (ff, h), 0.02, 0.0),
                       (f"{p}.block_sparse_moe.experts.{e}.w3.weight", (ff, h), 0.02, 0.0),
                       (f"{p}.block_sparse_moe.experts.{e}.w2.weight", (h, ff), 0.02, 0.0)]
-    # every tensor is a window of one seeded N(0,1) pool (64 MiB), at its own
-    # offset, scaled and shifted; each gate gets its own fresh draws
+    return specs
+
+
+def write_phi_model(path):
+    """model.bin of the reference's model with seeded random weights: every
+    tensor is a window of one seeded N(0,1) pool (64 MiB), at its own
+    offset, scaled and shifted; each gate gets its own fresh draws.
+    Returns {name: (byte offset, shape)}."""
+    import struct
+    import numpy as np
+    specs = phi_tensor_specs()
     rng = np.random.default_rng(0)
     pool = rng.standard_normal(1 << 24).astype(np.float32)
     sizes = [int(np.prod(shape)) for _, shape, _, _ in specs]
     header = 4 + sum(4 + len(n.encode()) + 4 + 4 * len(shape) + 16 for n, shape, _, _ in specs)
-    # the batch: 1024 sequences, lengths 10..29, the first 4 tokens from one
-    # of 64 shared prefixes
+    where = {}
+    with open(path, "wb") as f:
+        blob = bytearray(struct.pack("<I", len(specs)))
+        off = header
+        for (name, shape, _, _), n in zip(specs, sizes):
+            nb = name.encode()
+            blob += struct.pack("<I", len(nb)) + nb + struct.pack("<I", len(shape))
+            blob += struct.pack(f"<{len(shape)}I", *shape) + struct.pack("<QQ", off, 4 * n)
+            where[name] = (off, shape)
+            off += 4 * n
+        f.write(bytes(blob))
+        for i, ((name, shape, scale, shift), n) in enumerate(zip(specs, sizes)):
+            if ".gate." in name:
+                a = rng.standard_normal(n).astype(np.float32)
+            else:
+                a = np.resize(np.roll(pool, -((i * 7919 * 4096) % pool.size)), n)
+            (a * np.float32(scale) + np.float32(shift)).astype(np.float32).tofile(f)
+    return where, off
+
+
+def phi_batch():
+    """A batch shaped like the reference's contest input: 1024 sequences,
+    10-29 tokens each, whose first 4 tokens come from 64 shared prefixes, so
+    the prefix trie removes about a fifth of the rows (the reference's input:
+    19,803 tokens, 15,583 trie rows)."""
+    import numpy as np
     tr = np.random.default_rng(1)
     prefixes = tr.integers(0, 32000, (64, 4))
     lens = tr.integers(10, 30, 1024).astype(np.int32)
     seqs = [np.concatenate([prefixes[tr.integers(0, 64)], tr.integers(0, 32000, n - 4)])
             for n in lens]
+    return seqs, lens
+
+
+def phi_oracle_weights(path, where):
+    """The oracle decoder's weights (oracle/decoder.py names) read from the
+    model.bin, memory-mapped; expert matrices stacked per layer."""
+    import types
+    import numpy as np
+    sys.path.insert(0, ROOT)
+    import oracle
+    mm = np.memmap(path, dtype=np.uint8, mode="r")
+
+    def t(name):
+        off, shape = where[name]
+        n = int(np.prod(shape))
+        return np.frombuffer(mm, dtype=np.float32, count=n, offset=off).reshape(shape)
+
+    layers = []
+    for li in range(PHI["layers"]):
+        p = f"model.layers.{li}"
+        L = {"input_norm_w": t(f"{p}.input_layernorm.weight"),
+             "input_norm_b": t(f"{p}.input_layernorm.bias"),
+             "post_norm_w": t(f"{p}.post_attention_layernorm.weight"),
+             "post_norm_b": t(f"{p}.post_attention_layernorm.bias"),
+             "gate_w": t(f"{p}.block_sparse_moe.gate.weight")}
+        for n in ("q", "k", "v", "o"):
+            L[f"{n}_w"] = t(f"{p}.self_attn.{n}_proj.weight")
+            L[f"{n}_b"] = t(f"{p}.self_attn.{n}_proj.bias")
+        for n in ("w1", "w3", "w2"):
+            L[n] = np.stack([t(f"{p}.block_sparse_moe.experts.{e}.{n}.weight")
+                             for e in range(PHI["E"])])
+        layers.append(L)
+    W = {"embed": t("model.embed_tokens.weight"), "final_norm_w": t("model.norm.weight"),
+         "final_norm_b": t("model.norm.bias"), "lm_head_w": t("lm_head.weight"),
+         "lm_head_b": t("lm_head.bias"), "layers": layers}
+    cfg = types.SimpleNamespace(norm="layer", norm_eps=1e-5, heads=PHI["heads"],
+                                kv_heads=PHI["kv_heads"], head_dim=PHI["head_dim"],
+                                rope_theta=10000.0, window=2047, top_k=2,
+                                router=oracle.ROUTER_PHI_QUANT, contract=oracle.CONTRACT_FMA,
+                                layers=PHI["layers"])
+    return W, cfg
+
+
+def model_entry(warmup, steps, cpu_seconds):
+    """The C++ drop-in's PhiTinyMoEModel::generate (the reference's timed
+    end-to-end call, src/main.cpp:584-601) on the reference's model shape
+    (Phi-tiny-MoE: 32 layers, d 4096, 16 query / 4 key heads of 128, 16
+    experts of d_ff 448, vocabulary 32064; random weights) over a batch
+    shaped like the reference's contest input.  Host token lists in, host
+    logits out.  The CPU leg runs the oracle decoder on the first sequences
+    of the batch, one at a time, and checks their logits."""
+    import ctypes
+    import numpy as np
+    seqs, lens = phi_batch()
     nodes = len({tuple(sq[:i + 1]) for sq in seqs for i in range(len(sq))})
     ids = np.concatenate(seqs).astype(np.int32)
     shim = ctypes.CDLL(os.path.join(ROOT, "tests", "cpp", "libdropin_shim.so"))
     shim.shim_error.restype = ctypes.c_char_p
     I, D = ctypes.c_int64, ctypes.c_double
     load_s, ms = D(0.0), D(0.0)
+    logits = np.empty((len(lens), PHI["vocab"]), np.float32)
     t0 = time.perf_counter()
     with tempfile.TemporaryDirectory() as tmp:
         path = os.path.join(tmp, "model.bin")
-        with open(path, "wb") as f:
-            blob = bytearray(struct.pack("<I", len(specs)))
-            off = header
-            for (name, shape, _, _), n in zip(specs, sizes):
-                nb = name.encode()
-                blob += struct.pack("<I", len(nb)) + nb + struct.pack("<I", len(shape))
-                blob += struct.pack(f"<{len(shape)}I", *shape) + struct.pack("<QQ", off, 4 * n)
-                off += 4 * n
-            f.write(bytes(blob))
-            for i, ((name, shape, scale, shift), n) in enumerate(zip(specs, sizes)):
-                if ".gate." in name:
-                    a = rng.standard_normal(n).astype(np.float32)
-                else:
-                    a = np.resize(np.roll(pool, -((i * 7919 * 4096) % pool.size)), n)
-                (a * np.float32(scale) + np.float32(shift)).astype(np.float32).tofile(f)
+        where, nbytes = write_phi_model(path)
         write_s = time.perf_counter() - t0
-        print(f"model.bin written ({off / 2**30:.1f} GiB, {write_s:.0f} s); timing generate()",
-              file=sys.stderr, flush=True)
+        log(f"model.bin written ({nbytes / 2**30:.1f} GiB, {write_s:.0f} s); timing generate()")
         # at least SPINUP_S of untimed calls (a call takes about 0.3 s), so the
         # timed calls run at the clock a loaded GPU holds
-        warm = max(args.warmup, int(math.ceil(SPINUP_S / 0.25)))
+        warm = max(warmup, int(math.ceil(SPINUP_S / 0.25)))
         rc = shim.shim_model_time(path.encode(), lens.ctypes.data_as(ctypes.c_void_p),
                                   ids.ctypes.data_as(ctypes.c_void_p), I(len(lens)),
-                                  I(warm), I(args.steps), ctypes.byref(load_s),
-                                  ctypes.byref(ms))
-    if rc != 0:
-        raise RuntimeError(f"shim_model_time: {shim.shim_error().decode()}")
-    seq_s = len(lens) / (ms.value * 1e-3)
-    print(json.dumps({
+                                  I(warm), I(steps), ctypes.byref(load_s), ctypes.byref(ms),
+                                  logits.ctypes.data_as(ctypes.c_void_p))
+        if rc != 0:
+            raise RuntimeError(f"shim_model_time: {shim.shim_error().decode()}")
+        cpu = parity = None
+        if cpu_seconds > 0:
+            oracle, build = cpu_oracle()
+            from oracle import decoder as od
+            W, cfg = phi_oracle_weights(path, where)
+            done, errs, t_cpu = 0, [], 0.0
+            while done < len(seqs) and (done == 0 or t_cpu < cpu_seconds):
+                t1 = time.perf_counter()
+                ref, _, _ = od.generate(np.asarray(seqs[done])[None, :], W, cfg)
+                t_cpu += time.perf_counter() - t1
+                errs.append(parity_errors(logits[done], ref[0]))
+                done += 1
+            toks = int(sum(len(s) for s in seqs[:done]))
+            cpu = {"value": done / t_cpu, "unit": "seq/s", "cores": oracle.get_threads(),
+                   "kind": "port", "host": host_cpu(), "build": build,
+                   "tokens_per_s": toks / t_cpu,
+                   "sample": (f"the first {done} of {len(seqs)} sequences ({toks} tokens), each "
+                              f"alone through the oracle decoder (no prefix sharing), "
+                              f"{t_cpu:.1f} s")}
+            parity = {"sequences": done,
+                      "logits_max_rel_err": max(e["max_rel_err"] for e in errs),
+                      "logits_max_elem_rel_err": max(e["max_elem_rel_err"] for e in errs),
+                      "within_1e-4": all(e["within_1e-4"] for e in errs)}
+    h, L_ = PHI["d"], PHI["layers"]
+    qw, kw = PHI["heads"] * PHI["head_dim"], PHI["kv_heads"] * PHI["head_dim"]
+    # algorithmic FLOPs of one call over the trie rows (the last layer pruned
+    # to each sequence's last node): projections, experts, lm_head
+    B = len(lens)
+    per_row = 2.0 * h * (qw + 2 * kw + qw) + 2.0 * 2 * h * PHI["d_ff"] * 3
+    flops = (L_ - 1) * nodes * per_row + nodes * 2.0 * h * 2 * kw \
+        + B * (2.0 * h * (qw + qw) + 2.0 * 2 * h * PHI["d_ff"] * 3) + B * 2.0 * h * PHI["vocab"]
+    return {
         "metric": "drop-in PhiTinyMoEModel::generate sequences/sec (prefill, logits of the last "
                   "position), 1 MI355X",
-        "value": seq_s, "unit": "seq/s", "ms_per_call": ms.value, "steps": args.steps,
-        "warmup": warm, "dtype": "f32",
+        "value": B / (ms.value * 1e-3), "unit": "seq/s", "ms_per_call": ms.value,
+        "steps": steps, "warmup": warm, "dtype": "f32",
         "data": "synthetic (seeded random weights; random token ids with 64 shared prefixes)",
-        "config": {"workload": "phi_tiny_moe_generate_fp32", "sequences": int(len(lens)),
+        "config": {"workload": "phi_tiny_moe_generate_fp32", "sequences": int(B),
                    "tokens": int(lens.sum()), "trie_rows": nodes, "layers": L_, "d_model": h,
-                   "experts": E, "top_k": 2, "d_ff": ff, "vocab": vocab,
+                   "experts": PHI["E"], "top_k": 2, "d_ff": PHI["d_ff"], "vocab": PHI["vocab"],
                    "router": "quantised top-2, weights 1/2 (PhiMoE::route)"},
+        "model_tflops": flops / (ms.value * 1e-3) / 1e12,
+        "model_frac_fp32_mfma_peak": flops / (ms.value * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS,
+        "flops_note": ("projections, experts and lm_head over the prefix-trie rows; attention "
+                       "(under 1 % of the FLOPs) left out; host-to-device token copy and "
+                       "device-to-host logits copy inside the time"),
         "reference_gpu_seq_s": 687.8,
         "reference_note": "the reference's end-to-end figure on one RTX 3090, 1024 sequences / "
                           "19,803 tokens of its contest input (docs/report/report.html:96)",
         "model_load_s": load_s.value,
-    }))
+        "cpu_baseline": cpu,
+        "cpu_sample_parity": parity,
+    }
+
+
+def model_bench(args):
+    print(json.dumps(model_entry(args.warmup, args.steps, args.cpu_seconds)))
 
 
 def decoder_bench(args, pkg):
-    """Config 5 as a whole: the 4-layer decoder prefill of 8 x 512 tokens
-    (embedding, per layer RMS norm, q/k/v projections, RoPE, causal
-    attention, o projection + residual, the MoE block with its norm and
-    residual; final norm and lm_head on the last row of every sequence)."""
-    import numpy as np
-    import torch
+    print(json.dumps(decoder_entry(pkg, args.warmup, args.steps, args.cpu_seconds,
+                                   graph=not args.no_graph)))
 
-    B, S = 8, 512
-    cfg = pkg.DecoderConfig()
-    dev = torch.device("cuda:0")
-    W = pkg.random_weights(cfg, dev, seed=0)
-    g = torch.Generator(device="cpu").manual_seed(1)
-    tokens = torch.randint(0, cfg.vocab, (B, S), generator=g, dtype=torch.int32).to(dev)
-    ctx = pkg.Context(0)
-    model = pkg.DecoderModel(ctx, cfg, W)
-    model.reserve(B, S)
-    logits = torch.empty((B, cfg.vocab), device=dev)
-    # spin-up: prefills for at least SPINUP_S, so every timed step runs at the
-    # clock a loaded GPU holds; then the warm-up steps
-    t_spin = time.perf_counter()
-    while time.perf_counter() - t_spin < SPINUP_S:
-        model.generate(tokens, logits)
-        torch.cuda.synchronize()
-    for _ in range(args.warmup):
-        model.generate(tokens, logits)
-    torch.cuda.synchronize()
-    # per-kernel HIP events over K eager steps (the breakdown and the roofline)
-    ctx.reset_timing()
-    ctx.set_timing(True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        model.generate(tokens, logits)
-    torch.cuda.synchronize()
-    eager_s = time.perf_counter() - t0
-    ctx.set_timing(False)
-    kt = ctx.kernel_times()
-    elapsed = eager_s
-    graph_note = None
-    if not args.no_graph:
-        # the timed steps: the same prefill captured once in a HIP graph and
-        # replayed (one host launch per step instead of ~70)
-        from moe_amd.decoder import CapturedPrefill
-        cap = CapturedPrefill(model, B, S, warmup=args.warmup)
-        cap.tokens.copy_(tokens)
-        for _ in range(args.warmup):
-            cap.replay()
-        torch.cuda.synchronize()
-        check = cap.replay().clone()
-        model.generate(tokens, logits)
-        torch.cuda.synchronize()
-        assert torch.equal(check, logits), "graph replay differs from the eager prefill"
+
+# ----------------------------------------------------------------------- main
+def other_configs(pkg, dev, warmup, steps):
+    """Every other configuration of the baseline, measured in this run."""
+    import torch
+    out = {}
+    plan = [
+        ("c1", lambda: layer_entry(pkg, "c1", dev, warmup, steps, None, spin_s=SPINUP_S / 5)),
+        ("c2_sgemm_nn", lambda: sgemm_entries(pkg, warmup, steps, CPU_S_SGEMM)),
+        ("c4", lambda: layer_entry(pkg, "c4", dev, warmup, min(steps, 10), CPU_S_EXTRA_LAYER,
+                                   spin_s=SPINUP_S / 2)),
+        ("c5_moe_ffn", lambda: layer_entry(pkg, "c5", dev, warmup, steps, CPU_S_EXTRA_LAYER,
+                                           spin_s=SPINUP_S / 2)),
+        ("ref_layer", lambda: layer_entry(pkg, "ref", dev, warmup, steps, CPU_S_EXTRA_LAYER,
+                                          spin_s=SPINUP_S / 2)),
+        ("c5_prefill", lambda: decoder_entry(pkg, warmup, steps, CPU_S_DECODER)),
+        ("generate", lambda: model_entry(min(warmup, 2), min(steps, 10), CPU_S_MODEL)),
+    ]
+    for name, fn in plan:
         t0 = time.perf_counter()
-        for _ in range(args.steps):
-            cap.replay()
+        log(f"{name} ...")
+        try:
+            out[name] = fn()
+        except Exception as e:  # keep the other configurations' figures
+            out[name] = {"error": f"{type(e).__name__}: {e}"}
         torch.cuda.synchronize()
-        elapsed = time.perf_counter() - t0
-        cap.close()
-        graph_note = (f"timed steps are HIP-graph replays of the prefill; the per-kernel times "
-                      f"come from HIP events over {args.steps} eager steps "
-                      f"({1e3 * eager_s / args.steps:.3f} ms per eager step)")
-    T = B * S
-    per_step = {n: ms / args.steps for n, (ms, _) in kt.items()}
-    avg = {n: ms / c for n, (ms, c) in kt.items()}
-    pairs = T * cfg.top_k
-    # w13 launches differ in size (the pruned last layer has B*k pairs), so
-    # the roofline is the step's w13 FLOPs over the step's w13 time
-    full = cfg.layers - 1 if model.prune_last else cfg.layers
-    tail_pairs = B * cfg.top_k if model.prune_last else 0
-    flops_w13 = 2.0 * (full * pairs + tail_pairs) * cfg.d * cfg.d_ff * 2
-    w13_tflops = flops_w13 / (per_step["expert_w13_swiglu"] * 1e-3) / 1e12
-    qw, kw = cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
-    tail_rows = B if model.prune_last else 0
-    proj_flops = (2.0 * full * T * cfg.d * (qw + 2 * kw + qw) + 2.0 * tail_rows * cfg.d * (qw + qw)
-                  + 2.0 * (cfg.layers - full) * T * cfg.d * 2 * kw + 2.0 * B * cfg.d * cfg.vocab)
-    # causal attention: S(S+1)/2 (query, key) pairs per sequence and head, 2 products;
-    # the pruned layer's last rows see S keys each
-    attn_flops = (full * B * cfg.heads * 2 * (2.0 * cfg.head_dim * S * (S + 1) / 2)
-                  + tail_rows * cfg.heads * 2 * (2.0 * cfg.head_dim * S))
-    moe_flops = 2.0 * (full * pairs + tail_pairs) * cfg.d * cfg.d_ff * 3
-    cpu = parity = None
-    if args.cpu_seconds > 0:
-        hidden = model.hidden(tokens).cpu().numpy()
-        Wh = {k: (None if v is None else v.cpu().numpy()) for k, v in W.items() if k != "layers"}
-        Wh["layers"] = [{k: (None if v is None else v.cpu().numpy()) for k, v in L.items()}
-                        for L in W["layers"]]
-        cpu, parity = decoder_cpu_baseline(tokens.cpu().numpy(), Wh, cfg, hidden,
-                                           args.cpu_seconds)
-    ms_per_step = 1e3 * elapsed / args.steps
-    out = {
-        "metric": "decoder prefill tokens/sec (config 5), 1 MI355X",
-        "value": T * args.steps / elapsed,
-        "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": ms_per_step,
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "data": ("synthetic (seeded: token ids uniform over the vocabulary, embedding "
-                 "N(0,1), weights N(0,0.02), norm weights 1 + N(0,0.1))"),
-        "config": {"workload": "decoder_prefill_fp32", "batch": B, "seq_len": S,
-                   "layers": cfg.layers, "d_model": cfg.d, "heads": cfg.heads,
-                   "kv_heads": cfg.kv_heads, "experts": cfg.experts, "top_k": cfg.top_k,
-                   "d_ff": cfg.d_ff, "vocab": cfg.vocab, "norm": "rms", "rope_theta":
-                   cfg.rope_theta, "router": "softmax over selected top-k",
-                   "lm_head": "last position of each sequence"},
-        "model_tflops": (proj_flops + attn_flops + moe_flops) / (ms_per_step * 1e-3) / 1e12,
-        "roofline": {
-            "kernel": "expert_w13_swiglu",
-            "bound": "mfma",
-            "achieved": w13_tflops,
-            "peak": FP32_MFMA_PEAK_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": w13_tflops / FP32_MFMA_PEAK_TFLOPS,
-            "traffic": None,
-            "flops_per_step": flops_w13,
-            "launches_per_step": cfg.layers,
-            "note": (f"achieved = the step's w13 FLOPs ({full} layers x {pairs} pairs + "
-                     f"{tail_pairs} pairs of the pruned layer) over the step's w13 HIP-event time"),
-        },
-        "kernel_ms_per_step": {n: round(v, 4) for n, v in sorted(per_step.items())},
-        "kernel_avg_ms": {n: round(v, 5) for n, v in sorted(avg.items())},
-        "cpu_baseline": cpu,
-        "cpu_sample_parity": parity,
-        "timing": graph_note or "timed steps are eager, with HIP events around every kernel",
-        "eager_ms_per_step": 1e3 * eager_s / args.steps,
-    }
-    ctx.close()
-    print(json.dumps(out))
+        torch.cuda.empty_cache()
+        log(f"{name} done in {time.perf_counter() - t0:.1f} s")
+    return out
 
 
 def main():
@@ -632,9 +1137,9 @@ def main():
                     help="--decoder: time eager steps instead of HIP-graph replays")
     ap.add_argument("--model", action="store_true",
                     help="the C++ drop-in PhiTinyMoEModel::generate on the reference's model "
-                         "shape (32 layers; writes a ~15 GiB model.bin to a temporary directory)")
+                         "shape (32 layers; writes a ~14 GiB model.bin to a temporary directory)")
     ap.add_argument("--no-extra", action="store_true",
-                    help="config 3: skip timing the other layer shapes after the headline")
+                    help="config 3: skip measuring the other configurations after the headline")
     ap.add_argument("--dropin", action="store_true",
                     help="the C++ drop-in PhiMoE::forward at the reference's layer shape, host "
                          "tensors in and out (PCIe-inclusive)")
@@ -658,198 +1163,34 @@ def main():
         model_bench(args)
         return
 
-    import numpy as np
     import torch
 
-    cfg = CONFIGS[args.config]
-    T, d, E, k, d_ff = cfg["T"], cfg["d"], cfg["E"], cfg["k"], cfg["d_ff"]
-    if args.tokens is not None:
-        T = args.tokens  # a batch-size point of the configuration's layer shape
     pkg = load_pkg()
     dev = torch.device("cuda:0")
-    rms = cfg["norm"] == "rms"
-    x, weights, y, idx, w, desc = build_layer(pkg, cfg, T, args.block, dev)
-    ctx = pkg.Context(0)
-    ctx.reserve(desc)
-    spin_steps, elapsed, instrumented, kt = time_layer(ctx, desc, weights, x, y, idx, w,
-                                                       args.warmup, args.steps)
-
-    ms_per_step = 1e3 * elapsed / args.steps
-    tokens_per_s = T * args.steps / elapsed
-    counts = np.bincount(idx.cpu().numpy().ravel(), minlength=E)
-    pairs = T * k
-    flops_w13 = 2.0 * pairs * d * d_ff * 2
-    flops_w2 = 2.0 * pairs * d_ff * d
-    avg = {name: ms / n for name, (ms, n) in kt.items()}
-    hbm = hbm_kernel_rates(avg, T, d, E, k, args.block, ctx.w2_splits(desc))
-    w13_ms = avg["expert_w13_swiglu"]
-    w2_ms = avg["expert_w2"]
-    w13_tflops = flops_w13 / (w13_ms * 1e-3) / 1e12
-    expert_tflops = (flops_w13 + flops_w2) / ((w13_ms + w2_ms) * 1e-3) / 1e12
-
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", f"traffic_{args.config}.json")
-    if os.path.exists(tpath):
-        with open(tpath) as f:
-            traffic = json.load(f).get("expert_w13_swiglu_bytes_per_launch")
-
-    cpu = None
-    parity = None
-    if args.cpu_seconds > 0:
-        host = {n: (None if v is None else v.cpu().numpy()) for n, v in weights.items()}
-        cpu, parity = cpu_baseline(x.cpu().numpy(), host, cfg,
-                                   (y.cpu().numpy(), idx.cpu().numpy()), args.cpu_seconds)
-
+    log(f"{args.config} (headline) ...")
+    e = layer_entry(pkg, args.config, dev, args.warmup, args.steps,
+                    None if args.config == "c1" else args.cpu_seconds, block=args.block,
+                    tokens=args.tokens)
     out = {
         "metric": METRIC,
-        "value": tokens_per_s,
-        "unit": "tokens/s",
+        "value": e.pop("value"),
+        "unit": e.pop("unit"),
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": ms_per_step,
+        "steps": e.pop("steps"),
+        "warmup": e.pop("warmup"),
+        "ms_per_step": e.pop("ms_per_step"),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded torch.randn: x ~ N(0,1), weights ~ N(0,0.02))",
-        "config": {"workload": cfg["workload"], "tokens": T, "d_model": d, "experts": E,
-                   "top_k": k, "d_ff": d_ff,
-                   "router": ("quantised top-2, weights 1/2 (PhiMoE::route)"
-                              if cfg.get("router") == "phi_quant"
-                              else "softmax over selected top-k"),
-                   "expert": "SwiGLU", "router_bias": (f"zipf(s={cfg['zipf']})"
-                                                       if cfg["zipf"] else None),
-                   "block": (f"y = x + MoE({'rms_norm' if rms else 'layer_norm'}(x))"
-                             if args.block else None)},
-        "expert_gemm_tflops": expert_tflops,
-        "expert_gemm_frac_fp32_mfma_peak": expert_tflops / FP32_MFMA_PEAK_TFLOPS,
-        "roofline": {
-            "kernel": "expert_w13_swiglu",
-            "bound": "mfma",
-            "achieved": w13_tflops,
-            "peak": FP32_MFMA_PEAK_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": w13_tflops / FP32_MFMA_PEAK_TFLOPS,
-            "traffic": traffic,
-            "flops_per_launch": flops_w13,
-        },
-        "kernel_avg_ms": {n: round(v, 5) for n, v in sorted(avg.items())},
-        "hbm_kernels": hbm,
-        "expert_rows": counts.tolist(),
-        "cpu_baseline": cpu,
-        "cpu_sample_parity": parity,
-        "spinup": f"{spin_steps} untimed forwards over {SPINUP_S:.1f} s before the warm-up steps",
-        "timing": (f"ms_per_step from {args.steps} steps without per-kernel events; "
-                   f"kernel_avg_ms and the roofline from HIP events over {args.steps} more "
-                   f"steps ({1e3 * instrumented / args.steps:.3f} ms per instrumented step)"),
+        "config": e.pop("config"),
     }
-    if args.config == "ref":
-        # the reference's own per-layer expert GEMM times at this shape (RTX 3090)
-        out["reference_gpu_gemm_ms"] = {n: round(v, 3) for n, v in REF_GEMM_MS.items()}
-        out["speedup_vs_reference_gpu_gemms"] = {
-            n: round(REF_GEMM_MS[n] / avg[n], 2) for n in REF_GEMM_MS if n in avg}
-    ctx.close()
+    e.pop("workload")
+    out.update(e)
     if args.config == "c3" and args.tokens is None and not args.block and not args.no_extra:
-        # the other layer shapes of the configurations, timed the same way in
-        # this run (no CPU leg): the short-K expert GEMMs of config 5 and of the
-        # reference's own layer, and config 4's skewed 64 experts
-        del x, weights, y, idx, w
-        torch.cuda.empty_cache()
-        out["other_layer_shapes"] = {c: layer_point(pkg, c, dev, args.warmup, min(args.steps, 10))
-                                     for c in ("c5", "ref", "c4")}
+        out["configs"] = other_configs(pkg, dev, args.warmup, args.steps)
     print(json.dumps(out))
-
-
-def build_layer(pkg, cfg, T, block, dev):
-    """Seeded inputs, weights, outputs and the descriptor of one layer shape."""
-    import torch
-    d, E, k, d_ff = cfg["d"], cfg["E"], cfg["k"], cfg["d_ff"]
-    g = torch.Generator(device=dev).manual_seed(0)
-    x = torch.randn((T, d), device=dev, generator=g)
-    weights = {
-        "gate_w": torch.randn((E, d), device=dev, generator=g) * 0.02,
-        "w1": torch.randn((E, d_ff, d), device=dev, generator=g) * 0.02,
-        "w3": torch.randn((E, d_ff, d), device=dev, generator=g) * 0.02,
-        "w2": torch.randn((E, d, d_ff), device=dev, generator=g) * 0.02,
-        "expert_bias": None,
-    }
-    if cfg["zipf"] is not None:
-        weights["expert_bias"] = torch.from_numpy(zipf_bias(E, cfg["zipf"])).to(dev)
-    rms = cfg["norm"] == "rms"
-    if block:
-        weights["norm_w"] = 1 + 0.1 * torch.randn(d, device=dev, generator=g)
-        weights["norm_b"] = None if rms else 0.1 * torch.randn(d, device=dev, generator=g)
-    y = torch.empty((T, d), device=dev)
-    idx = torch.empty((T, k), dtype=torch.int32, device=dev)
-    w = torch.empty((T, k), device=dev)
-    desc = pkg.make_desc(T, d, E, k, d_ff, act=pkg.ACT_SWIGLU,
-                         router=(pkg.ROUTER_PHI_QUANT if cfg.get("router") == "phi_quant"
-                                 else pkg.ROUTER_SOFTMAX_TOPK), contract=pkg.CONTRACT_FMA,
-                         norm=(pkg.NORM_RMS if rms else pkg.NORM_LAYER) if block
-                         else pkg.NORM_NONE,
-                         norm_eps=NORM_EPS, residual=block)
-    return x, weights, y, idx, w, desc
-
-
-def time_layer(ctx, desc, weights, x, y, idx, w, warmup, steps):
-    """Spin-up, warm-up, `steps` timed forwards without per-kernel events,
-    then as many with HIP events around every launch (on the stream the
-    kernels run on).  Returns (spin-up forwards, timed seconds, instrumented
-    seconds, per-kernel times)."""
-    import torch
-    # spin-up: the GPU takes about a second of load to reach its full clock
-    # (durations of short layers fall 10-20 % over the first second), so
-    # forwards run for at least SPINUP_S before the warm-up steps
-    spin_steps, t_spin = 0, time.perf_counter()
-    while time.perf_counter() - t_spin < SPINUP_S:
-        ctx.layer_forward(desc, weights, x, y, idx, w)
-        torch.cuda.synchronize()
-        spin_steps += 1
-    for _ in range(warmup):
-        ctx.layer_forward(desc, weights, x, y, idx, w)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        ctx.layer_forward(desc, weights, x, y, idx, w)
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    ctx.reset_timing()
-    ctx.set_timing(True)
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    for _ in range(steps):
-        ctx.layer_forward(desc, weights, x, y, idx, w)
-    torch.cuda.synchronize()
-    instrumented = time.perf_counter() - t1
-    ctx.set_timing(False)
-    return spin_steps, elapsed, instrumented, ctx.kernel_times()
-
-
-def layer_point(pkg, name, dev, warmup, steps):
-    """One configuration's layer timed as the headline one is: tokens/s, the
-    expert GEMMs' fraction of the fp32 MFMA peak, the w1/w3 roofline."""
-    import torch
-    cfg = CONFIGS[name]
-    T, d, k, d_ff = cfg["T"], cfg["d"], cfg["k"], cfg["d_ff"]
-    x, weights, y, idx, w, desc = build_layer(pkg, cfg, T, False, dev)
-    ctx = pkg.Context(0)
-    ctx.reserve(desc)
-    _, elapsed, _, kt = time_layer(ctx, desc, weights, x, y, idx, w, warmup, steps)
-    ctx.close()
-    avg = {n: ms / c for n, (ms, c) in kt.items()}
-    pairs = T * k
-    f13, f2 = 2.0 * pairs * d * d_ff * 2, 2.0 * pairs * d_ff * d
-    w13, w2 = avg["expert_w13_swiglu"], avg["expert_w2"]
-    del x, weights, y, idx, w
-    torch.cuda.empty_cache()
-    return {"workload": cfg["workload"], "tokens": T, "ms_per_step": round(1e3 * elapsed / steps, 4),
-            "tokens_per_s": round(T * steps / elapsed),
-            "expert_gemm_frac_fp32_mfma_peak":
-                round((f13 + f2) / ((w13 + w2) * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4),
-            "w13_frac_fp32_mfma_peak": round(f13 / (w13 * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4),
-            "kernel_avg_ms": {"expert_w13_swiglu": round(w13, 4), "expert_w2": round(w2, 4)},
-            "steps": steps}
 
 
 if __name__ == "__main__":

@@ -126,8 +126,14 @@ typedef struct moe_layer_weights {
  * device before the old buffer is freed. */
 int moe_ctx_create(int device, moe_ctx** out);
 int moe_ctx_destroy(moe_ctx* ctx);
-/* Grow the workspace so that moe_layer_forward(desc) allocates nothing. */
+/* Grow the workspace so that moe_layer_forward(desc) allocates nothing.
+ * It also covers moe_expert_ffn_grouped on the same (T, k, d, d_ff, E) and
+ * the sgemm / attention calls of that size or smaller. */
 int moe_ctx_reserve(moe_ctx* ctx, const moe_layer_desc* desc);
+/* The bytes of the context's workspace as it stands (0 before any call
+ * that needed one).  No reference counterpart: an introspection query for
+ * tests and tools (e.g. that moe_layer_forward_noalloc leaves it at 0). */
+int moe_ctx_workspace_bytes(moe_ctx* ctx, int64_t* bytes);
 /* Kernel timing (the reference's APS_PROFILE stage timers,
  * src/model.cu:1584-1622): when on, every launch is bracketed by HIP events
  * on its stream.  moe_ctx_kernel_times() synchronises, then returns the
@@ -137,6 +143,11 @@ int moe_ctx_set_timing(moe_ctx* ctx, int enabled);
 int moe_ctx_kernel_times(moe_ctx* ctx, const char** names, double* total_ms,
                          int64_t* launches, int cap);
 int moe_ctx_reset_timing(moe_ctx* ctx);
+/* Launches one empty kernel (one wave, no work) on `stream`, timed like any
+ * other launch under moe_ctx_set_timing (name "empty").  No reference
+ * counterpart: the launch-latency floor that the small routing and
+ * permutation kernels are reported against. */
+int moe_launch_floor(moe_ctx* ctx, void* stream);
 const char* moe_last_error(void);
 const char* moe_version(void);
 
@@ -284,7 +295,12 @@ int moe_permute(moe_ctx* ctx, const int32_t* topk_idx, int64_t T, int64_t k,
  * Packed row r of expert e (expert_offsets[e] <= r < expert_offsets[e+1])
  * reads x[perm[r], :].  h[T*k, d_ff] is the hidden activation (written),
  * out_rows[T*k, d] the expert outputs in packed order.
- * w1, w3: [E, d_ff, d]; w2: [E, d, d_ff]; w3 is ignored for SILU_MLP. */
+ * w1, w3: [E, d_ff, d]; w2: [E, d, d_ff]; w3 is ignored for SILU_MLP.
+ * Where the planner runs a projection stream-K, its partial tiles go to the
+ * context's workspace, which the call grows if it is too small (a device
+ * synchronisation, a free and an allocation: not allowed under graph
+ * capture).  moe_ctx_reserve with a desc of the same T, k, d, d_ff and E
+ * sizes it beforehand, after which the call allocates nothing. */
 int moe_expert_ffn_grouped(moe_ctx* ctx, const float* x, const int32_t* perm,
                            const int32_t* expert_offsets, const float* w1,
                            const float* w3, const float* w2, int act,

@@ -35,12 +35,29 @@ def build(force: bool = False) -> str:
     return LIB_PATH
 
 
-def lib():
+def build_native(out_dir: str) -> str:
+    """Compile the oracle for this host's CPU (-march=native, the reference
+    Makefile's host flags) into out_dir and return the library's path.
+    Raises CalledProcessError when the host has no working gcc."""
+    out = os.path.join(out_dir, "liboracle_moe_native.so")
+    subprocess.run(["make", "-s", "-B", "-C", HERE, "MARCH=native", f"OUT={out}"],
+                   check=True, capture_output=True)
+    return out
+
+
+def lib(path: str = None):
+    """The loaded oracle library: the prebuilt one, or `path` when given on
+    the first call (bench.py's native build).  A later call with another
+    path is an error: ctypes keeps the first library loaded."""
     global _lib
+    if _lib is not None and path is not None and path != _lib._name:
+        raise RuntimeError(f"oracle already loaded from {_lib._name}")
     if _lib is None:
-        if not os.path.exists(LIB_PATH):
-            build()
-        L = ctypes.CDLL(LIB_PATH)
+        if path is None:
+            path = LIB_PATH
+            if not os.path.exists(path):
+                build()
+        L = ctypes.CDLL(path)
         P = ctypes.c_void_p
         S = ctypes.c_size_t
         I = ctypes.c_int

@@ -348,10 +348,10 @@ int shim_model_generate(const char* path, const int32_t* lens, const int32_t* id
 }
 
 // Times PhiTinyMoEModel: construction from the file (load_s, seconds) and
-// generate() over the batch (ms per call, after `warmup` calls); nodes: the
-// rows of the batch's prefix trie (distinct prefixes).
+// generate() over the batch (ms per call, after `warmup` calls).  When
+// `logits` is not null it receives the last call's [batch, vocab] logits.
 int shim_model_time(const char* path, const int32_t* lens, const int32_t* ids, int64_t batch,
-                    int64_t warmup, int64_t iters, double* load_s, double* ms) {
+                    int64_t warmup, int64_t iters, double* load_s, double* ms, float* logits) {
     return guarded([&] {
         if (iters <= 0 || warmup < 0)
             throw std::invalid_argument("iters must be > 0 and warmup >= 0");
@@ -366,6 +366,7 @@ int shim_model_time(const char* path, const int32_t* lens, const int32_t* ids, i
         for (int64_t i = 0; i < iters; ++i) m.generate(seqs, L);
         const auto t3 = std::chrono::steady_clock::now();
         *ms = std::chrono::duration<double, std::milli>(t3 - t2).count() / double(iters);
+        if (logits != nullptr) std::memcpy(logits, L.data(), L.size() * sizeof(float));
     });
 }
 

@@ -12,10 +12,18 @@ PKG_DIR = os.path.join(ROOT, "accelerating-moe-inference_amd")
 HEADER = os.path.join(ROOT, "include", "moe_amd.h")
 
 # Activations must match the CPU path within this relative error (fp32),
-# measured normwise: max|gpu - cpu| / max|cpu| over the tensor.  (A
-# per-element relative error is ill-posed where the reference value is near
-# zero.)  Routing indices, expert assignment, offsets and permutations are
-# compared bit-for-bit.
+# measured two ways, both asserted:
+#   normwise:    max|gpu - cpu| / max|cpu| over the tensor;
+#   per element: every element within REL_TOL of itself OR within an
+#                absolute floor of REL_TOL * rms(cpu) -- the reference's own
+#                validation rule (an element fails only when both its
+#                absolute and its relative error pass the threshold,
+#                src/main.cpp:321-363) with the absolute threshold scaled to
+#                the tensor, so that elements near zero, whose relative error
+#                a different summation order makes arbitrarily large, are
+#                held to a floor 4-5x tighter than the normwise bound.
+# Routing indices, expert assignment, offsets and permutations are compared
+# bit-for-bit.
 REL_TOL = 1e-4
 
 _pkg = None
@@ -51,10 +59,28 @@ def rel_err(got, ref):
     return float(np.max(np.abs(got - ref)) / scale)
 
 
+def elem_rel_err(got, ref, tol=REL_TOL):
+    """Largest per-element error relative to max(|ref_i|, rms(ref)): an
+    element passes `tol` when its error is within tol of itself or within
+    tol * rms(ref) absolutely."""
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    if ref.size == 0:
+        return 0.0
+    floor = float(np.sqrt(np.mean(ref * ref)))
+    denom = np.maximum(np.abs(ref), floor)
+    if floor == 0.0:
+        return float(np.max(np.abs(got)))
+    return float(np.max(np.abs(got - ref) / denom))
+
+
 def assert_close(got, ref, tol=REL_TOL, what=""):
     e = rel_err(got, ref)
     assert np.all(np.isfinite(np.asarray(got))), f"{what}: non-finite output"
     assert e <= tol, f"{what}: normwise relative error {e:.3e} > {tol:.0e}"
+    ee = elem_rel_err(got, ref, tol)
+    assert ee <= tol, (f"{what}: per-element relative error {ee:.3e} > {tol:.0e} "
+                       f"(absolute floor {tol:.0e} x rms of the reference)")
     return e
 
 

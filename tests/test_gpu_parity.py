@@ -286,14 +286,14 @@ def test_silu_mul_bit_exact(ctx, torch, orc):
 @pytest.mark.parametrize("contract", [0, 1])
 # E <= 8 with 16-byte rows takes the ring kernel (64 x 512 x 4; 33 x 100 x 7:
 # a partial last stage and a one-token last wave; 4096 x 1024 x 8, config
-# 5's gate; 100 x 256 x 2: fewer experts than the lane block); E of 9-16 and
-# 33-64 with 16-byte rows the workgroup ring (300 x 4096 x 16 and 1037 x 4096
-# x 16: the reference's expert count, the latter with a partial last
-# workgroup; 45 x 196 x 11: a partial last stage, 5 experts masked; 1000 x
-# 2048 x 64; 77 x 452 x 100: two expert blocks, the second 36 wide, a
-# partial stage and a partial workgroup; 16 x 4 x 16: one 4-column stage);
-# the rest the staged kernel (70 x 130 x 130: rows of 130 floats; 5 x 1 x 3;
-# 50 x 1024 x 32)
+# 5's gate; 100 x 256 x 2: fewer experts than the lane block); E of 9-16 with
+# 16-byte rows the workgroup ring (300 x 4096 x 16 and 1037 x 4096 x 16: the
+# reference's expert count, the latter with a partial last workgroup; 45 x
+# 196 x 11: a partial last stage, 5 experts masked; 16 x 4 x 16: one
+# 4-column stage); every other shape the staged kernel: E above 16 (1000 x
+# 2048 x 64, config 4's expert count, 4 tokens per thread; 77 x 452 x 100:
+# two 64-expert blocks, the second 36 wide; 50 x 1024 x 32) and rows that
+# are not 16-byte multiples (70 x 130 x 130; 5 x 1 x 3)
 @pytest.mark.parametrize("T,d,E", [(64, 512, 4), (300, 4096, 16), (1000, 2048, 64),
                                    (33, 100, 7), (5, 1, 3), (70, 130, 130), (4096, 1024, 8),
                                    (100, 256, 2), (1037, 4096, 16), (45, 196, 11),
@@ -369,6 +369,51 @@ def test_route_phi_hand_cases(ctx, torch, orc):
     w = torch.empty((6, 2), device="cuda")
     ctx.route(dev(torch, rows), 2, idx, w)
     assert host(idx).tolist() == [[1, 2], [0, 1], [1, 0], [0, 1], [1, 2], [0, 1]]
+
+
+# The layer routes, counts and scans in one launch (route_count: each block
+# routes its 256 tokens into LDS bitmasks, the last block to finish scans the
+# counts).  Its routing, and through the outputs its offsets and permutation,
+# against the oracle: one token, a partial block, exactly one block, a block
+# plus one token, and 274 blocks; 1 to 1024 experts (softmax groups of 1 to
+# 64 lanes, 4 to 256 tokens per round), k up to 32; the Zipf bias at E = 64.
+# Every case runs twice on the context: the second launch must find the
+# completion counter reset by the first.
+@pytest.mark.parametrize("T,E,k,mode", [(1, 4, 2, 1), (255, 8, 2, 1), (256, 16, 2, 0),
+                                        (257, 64, 8, 1), (70000, 64, 8, 1), (70000, 16, 2, 0),
+                                        (3001, 1, 1, 1), (1000, 100, 3, 0), (900, 1024, 32, 1),
+                                        (600, 1024, 4, 0), (513, 3, 3, 1)])
+def test_layer_fused_routing_vs_oracle(ctx, pkg, torch, orc, T, E, k, mode):
+    print(f"layer routing T={T} E={E} k={k} mode={mode}", flush=True)
+    rng = np.random.default_rng(T + 7 * E + k)
+    d, d_ff = 64, 32
+    x = normal(rng, (T, d))
+    gw = normal(rng, (E, d), 0.3)
+    w1 = normal(rng, (E, d_ff, d), 0.05)
+    w3 = normal(rng, (E, d_ff, d), 0.05)
+    w2 = normal(rng, (E, d, d_ff), 0.05)
+    bias = zipf_bias(E) if E == 64 else None
+    W = {"gate_w": dev(torch, gw), "w1": dev(torch, w1), "w3": dev(torch, w3),
+         "w2": dev(torch, w2), "expert_bias": None if bias is None else dev(torch, bias)}
+    desc = pkg.make_desc(T, d, E, k, d_ff, act=pkg.ACT_SWIGLU, router=mode)
+    xt = dev(torch, x)
+    outs = []
+    for _ in range(2):
+        y = torch.empty((T, d), device="cuda")
+        idx = torch.empty((T, k), dtype=torch.int32, device="cuda")
+        w = torch.empty((T, k), device="cuda")
+        ctx.layer_forward(desc, W, xt, y, idx, w)
+        outs.append((host(y), host(idx), host(w)))
+    ry, ridx, rw = orc.moe_forward(x, gw, w1, w3, w2, k, router_mode=mode, expert_bias=bias)
+    for y, idx, w in outs:
+        assert np.array_equal(idx, ridx)
+        if mode == 0:
+            assert np.array_equal(w, rw)
+        else:
+            diff = np.abs(w.view(np.int32).astype(np.int64) - rw.view(np.int32))
+            assert diff.max() <= 1, "softmax weights beyond 1 ulp"
+        assert_close(y, ry, what=f"T={T} E={E} k={k}")
+    assert np.array_equal(outs[0][0], outs[1][0]), "second launch differs"
 
 
 # ------------------------------------------------------------ permutation

@@ -1,8 +1,12 @@
 """moe_layer_forward_noalloc (the layer on the library's fixed per-GPU
 scratch, allocating nothing) against moe_layer_forward on the same inputs:
 two calls in a row, the second with fewer tokens, each identical bit for bit
-to the allocating entry point (the same kernels run on the same inputs);
-and a layer too large for the scratch is rejected before any GPU work."""
+to the allocating entry point (the same kernels run on the same inputs).
+The no-alloc calls come first on a fresh context and must leave its
+workspace at 0 bytes; one is captured in a HIP graph and replayed, with
+other no-alloc calls between the replays, each replay matching the eager
+call; and a layer too large for the scratch is rejected before any GPU
+work."""
 import numpy as np
 import pytest
 
@@ -55,18 +59,66 @@ def test_noalloc_matches_layer_forward(torch, d, E, k, d_ff, router, norm, resid
                                  residual=residual)
             x = x_all[:T].contiguous()
             outs = []
-            for noalloc in (False, True):
+            # the no-alloc call first: on this fresh context it must leave
+            # the workspace unallocated (the allocating call then grows it)
+            for noalloc in (True, False):
                 y = torch.full((T, d), float("nan"), device="cuda")
                 idx = torch.full((T, k), -1, dtype=torch.int32, device="cuda")
                 w = torch.full((T, k), float("nan"), device="cuda")
+                ws_before = ctx.workspace_bytes()
                 ctx.layer_forward(desc, W, x, y, idx, w, noalloc=noalloc)
+                if noalloc:
+                    assert ctx.workspace_bytes() == ws_before, f"T={T}: no-alloc grew the workspace"
+                    if T == T1:
+                        assert ws_before == 0
                 outs.append((y, idx, w))
             torch.cuda.synchronize()
-            (y0, i0, w0), (y1, i1, w1) = outs
+            (y1, i1, w1), (y0, i0, w0) = outs
             assert torch.equal(i0, i1), f"T={T}: routing"
             assert torch.equal(w0, w1), f"T={T}: routing weights"
             assert torch.equal(y0, y1), f"T={T}: layer output"
             assert bool(torch.isfinite(y1).all())
+    finally:
+        ctx.close()
+
+
+def test_noalloc_replays_under_graph_capture(torch):
+    # the reference's layer block (layer norm + residual, quantised top-2 of
+    # 16 experts, d_ff 448) at d 512: one no-alloc call captured in a graph;
+    # between its replays other no-alloc calls (other tokens, fewer of them)
+    # overwrite the shared scratch, and every replay must still give the
+    # eager call's result bit for bit
+    pkg = load_pkg()
+    d, E, k, d_ff, T, T2 = 512, 16, 2, 448, 700, 251
+    print(f"noalloc graph d={d} E={E} T={T} (between replays T={T2})", flush=True)
+    rng = np.random.default_rng(77)
+    W = _weights(torch, rng, d, E, d_ff, True)
+    x = _dev(torch, normal(rng, (T, d)))
+    x2 = _dev(torch, normal(rng, (T2, d)))
+    desc = pkg.make_desc(T, d, E, k, d_ff, act=pkg.ACT_SWIGLU, router=0, norm=pkg.NORM_LAYER,
+                         residual=True)
+    desc2 = pkg.make_desc(T2, d, E, k, d_ff, act=pkg.ACT_SWIGLU, router=0,
+                          norm=pkg.NORM_LAYER, residual=True)
+    ctx = pkg.Context(0)
+    try:
+        ref = torch.empty((T, d), device="cuda")
+        ctx.layer_forward(desc, W, x, ref, noalloc=True)
+        y = torch.empty((T, d), device="cuda")
+        y2 = torch.empty((T2, d), device="cuda")
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            ctx.layer_forward(desc, W, x, y, noalloc=True)
+        torch.cuda.synchronize()
+        for rep in range(3):
+            ctx.layer_forward(desc2, W, x2, y2, noalloc=True)
+            y.fill_(float("nan"))
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(y, ref), f"replay {rep} differs from the eager call"
+        assert ctx.workspace_bytes() == 0
+        del g
     finally:
         ctx.close()
 
