@@ -673,18 +673,30 @@ void layer_forward(moe_ctx* ctx, const moe_layer_desc& D, const moe_layer_weight
         xin = ws.xnorm;
     }
 
+    // the gate also clears the counts route_count adds into
+    const int64_t nb = moe::ceil_div(D.T, moe::kPermTokens);
     ctx->launch("gate_logits", s, [&] {
-        moe::launch_gate_logits(xin, weights.gate_w, ws.logits, D.T, D.d, D.E, D.contract, s);
+        moe::launch_gate_logits(xin, weights.gate_w, ws.logits, D.T, D.d, D.E, D.contract, s,
+                                reinterpret_cast<uint32_t*>(ws.counts), D.E * nb);
     });
-    // routing, the per-block expert counts and their scan: one launch
+    // routing and the per-block expert counts: one launch
     ctx->launch("route_count", s, [&] {
         moe::launch_route_count(ws.logits, weights.expert_bias, D.T, D.E, D.k, D.router,
-                                D.quantum, D.tie_eps, idx, w, ws.counts, ws.offsets, ctx->sync,
-                                s);
+                                D.quantum, D.tie_eps, idx, w, ws.counts, s);
     });
-    ctx->launch("perm_place", s, [&] {
-        moe::launch_perm_place(idx, D.T, D.k, D.E, ws.counts, ws.perm, ws.inv, s);
-    });
+    if (D.E * nb <= moe::kPlaceScanMax) {
+        // the scan folded into the placement: one launch
+        ctx->launch("perm_place", s, [&] {
+            moe::launch_perm_place_scan(idx, D.T, D.k, D.E, ws.counts, ws.perm, ws.inv,
+                                        ws.offsets, s);
+        });
+    } else {
+        ctx->launch("perm_scan", s,
+                    [&] { moe::launch_perm_scan(ws.counts, nb, D.E, ws.offsets, s); });
+        ctx->launch("perm_place", s, [&] {
+            moe::launch_perm_place(idx, D.T, D.k, D.E, ws.counts, ws.perm, ws.inv, s);
+        });
+    }
     expert_ffn(ctx, xin, ws.perm, ws.offsets, weights.w1, weights.w3, weights.w2, D.act, D.T, D.k,
                D.d, D.d_ff, D.E, ws.h, ws.out_rows, s, plan, ws.sk_part);
     ctx->launch("combine", s, [&] {
@@ -755,21 +767,10 @@ int moe_ctx_create(int device, moe_ctx** out) {
             DeviceScope dev(device);
             scr = bind_scratch(device);
         }
-        uint32_t* sync = nullptr;
-        {
-            DeviceScope dev(device);
-            moe::hip_check(hipMalloc(&sync, 256), "hipMalloc counters");
-            const hipError_t e = hipMemset(sync, 0, 256);
-            if (e != hipSuccess) {
-                (void)hipFree(sync);
-                moe::hip_check(e, "hipMemset counters");
-            }
-        }
         auto* c = new moe_ctx();
         c->device = device;
         c->cus = prop.multiProcessorCount;
         c->scratch = scr;
-        c->sync = sync;
         *out = c;
     });
 }
@@ -785,7 +786,6 @@ int moe_ctx_destroy(moe_ctx* ctx) {
             (void)hipEventDestroy(e.second);
         }
         if (ctx->ws != nullptr) (void)hipFree(ctx->ws);
-        if (ctx->sync != nullptr) (void)hipFree(ctx->sync);
         delete ctx;
     });
 }

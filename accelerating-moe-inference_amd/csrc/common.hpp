@@ -181,18 +181,27 @@ void launch_add(float* a, const float* b, int64_t n, hipStream_t s);
 void launch_add_bias(float* a, const float* bias, int64_t rows, int64_t cols, hipStream_t s);
 void launch_embed(const float* table, const int32_t* tokens, int64_t n, int64_t d,
                   int64_t vocab, float* out, hipStream_t s);
+// zero / nzero: words the launch also sets to 0 (the routing counters of
+// the launch that follows), or null / 0.
 void launch_gate_logits(const float* x, const float* w, float* logits,
                         int64_t T, int64_t d, int64_t E, int contract,
-                        hipStream_t s);
+                        hipStream_t s, uint32_t* zero = nullptr, int64_t nzero = 0);
 void launch_route(const float* logits, const float* bias, int64_t T, int64_t E,
                   int64_t k, int mode, float quantum, float tie_eps,
                   int32_t* idx, float* w, hipStream_t s);
-// Routing + per-block counts + their scan (offsets) in one launch; `done`: a
-// device counter that is 0 between launches (the last block resets it).
+// The layer's routing and permutation in two launches.  route_count: the
+// routing and the per-block expert counts, added into counts[E *
+// ceil(T / kPermTokens)], which must be 0 when it starts (the gate's zero
+// region).  perm_place_scan: perm and inv from those raw counts (each block
+// scans them itself) and the expert offsets; for E * blocks up to
+// kPlaceScanMax (past it: perm_scan, then perm_place).
+constexpr int64_t kPlaceScanMax = 16384;
 void launch_route_count(const float* logits, const float* bias, int64_t T, int64_t E,
                         int64_t k, int mode, float quantum, float tie_eps, int32_t* idx,
-                        float* w, int32_t* counts, int32_t* offsets, uint32_t* done,
-                        hipStream_t s);
+                        float* w, int32_t* counts, hipStream_t s);
+void launch_perm_place_scan(const int32_t* idx, int64_t T, int64_t k, int64_t E,
+                            const int32_t* counts, int32_t* perm, int32_t* inv,
+                            int32_t* offsets, hipStream_t s);
 void launch_perm_count(const int32_t* idx, int64_t T, int64_t k, int64_t E,
                        int32_t* counts, hipStream_t s);
 void launch_perm_scan(int32_t* counts, int64_t nblocks, int64_t E,
@@ -238,9 +247,6 @@ struct moe_ctx {
     void* ws = nullptr;
     size_t ws_bytes = 0;
     void* scratch = nullptr;   // this device's no-alloc scratch (moe_layer_forward_noalloc)
-    // device counters of the single-launch scans (route_count's `done`): 0
-    // between launches; allocated and zeroed when the context is created
-    uint32_t* sync = nullptr;
     bool timing = false;
     struct Pending {
         const char* name;

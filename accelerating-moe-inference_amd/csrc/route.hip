@@ -40,15 +40,28 @@ __device__ __forceinline__ float mac(float acc, float a, float b) {
     return acc + prod;
 }
 
+// Zeroes zero[0 .. nzero) with every thread of the launch (2D grids
+// included): the layer's routing counters, cleared by the launch before the
+// one that adds into them.  A no-op when zero is null.
+__device__ __forceinline__ void zero_words(uint32_t* __restrict__ zero, int64_t nzero) {
+    if (zero == nullptr) return;
+    const int64_t nthreads = int64_t(gridDim.x) * gridDim.y * blockDim.x;
+    for (int64_t i = (int64_t(blockIdx.y) * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x;
+         i < nzero; i += nthreads)
+        zero[i] = 0u;
+}
+
 template <int CONTRACT, int EB, int TB>
 __global__ __launch_bounds__(256) void gate_logits_kernel(
         const float* __restrict__ x, const float* __restrict__ w,
-        float* __restrict__ logits, int64_t T, int64_t d, int64_t E) {
+        float* __restrict__ logits, int64_t T, int64_t d, int64_t E,
+        uint32_t* __restrict__ zero, int64_t nzero) {
     constexpr int R = TB * (256 / EB);        // token rows per workgroup
     constexpr int ROWS = R + EB;              // staged rows: x rows, then w rows
     constexpr int PER = ROWS * GATE_KC / 256; // staged floats per thread
     typedef float f4 __attribute__((ext_vector_type(4)));
     __shared__ __align__(16) float tile[2][ROWS * GATE_LDS];
+    zero_words(zero, nzero);
 
     const int tid = threadIdx.x;
     const int64_t t0 = static_cast<int64_t>(blockIdx.x) * R;
@@ -171,7 +184,8 @@ __device__ __forceinline__ void gate_static_for(std::integer_sequence<int, I...>
 template <int CONTRACT, int EB>
 __global__ __launch_bounds__(64) void gate_ring_kernel(
         const float* __restrict__ x, const float* __restrict__ w,
-        float* __restrict__ logits, int64_t T, int64_t d, int64_t E) {
+        float* __restrict__ logits, int64_t T, int64_t d, int64_t E,
+        uint32_t* __restrict__ zero, int64_t nzero) {
     constexpr int R = 64 / EB;                     // token rows per wave
     constexpr int ROWS = R + EB;                   // staged rows: tokens, then experts
     constexpr int STAGE = ROWS * kGateRingCols;    // floats per stage
@@ -193,6 +207,7 @@ __global__ __launch_bounds__(64) void gate_ring_kernel(
         else return r7;
     };
 
+    zero_words(zero, nzero);
     const int lane = threadIdx.x;
     const int64_t t0 = static_cast<int64_t>(blockIdx.x) * R;
     const int64_t nt = T - t0 < R ? T - t0 : R;  // tokens of this wave (>= 1)
@@ -310,7 +325,8 @@ __global__ __launch_bounds__(64) void gate_ring_kernel(
 template <int CONTRACT, int EB, int TB, int RING>
 __global__ __launch_bounds__(256, MOE_GATE_OCC) void gate_wg_ring_kernel(
         const float* __restrict__ x, const float* __restrict__ w,
-        float* __restrict__ logits, int64_t T, int64_t d, int64_t E) {
+        float* __restrict__ logits, int64_t T, int64_t d, int64_t E,
+        uint32_t* __restrict__ zero, int64_t nzero) {
     constexpr int R = TB * (256 / EB);             // token rows per workgroup
     constexpr int ROWS = R + EB;                   // staged rows: tokens, then experts
     constexpr int STAGE = ROWS * kGateRingCols;    // floats per stage
@@ -332,6 +348,7 @@ __global__ __launch_bounds__(256, MOE_GATE_OCC) void gate_wg_ring_kernel(
         else return r7;
     };
 
+    zero_words(zero, nzero);
     const int tid = threadIdx.x;
     const int64_t t0 = static_cast<int64_t>(blockIdx.x) * R;
     const int64_t e0 = static_cast<int64_t>(blockIdx.y) * EB;
@@ -502,19 +519,22 @@ __device__ __forceinline__ bool beats(float av, int ai, float bv, int bi) {
 
 // Token t's top-k by the group of G lanes this lane belongs to (sub: the
 // lane's index in it); every lane of the group must call it, live or not.
-// The group's first lane writes idx_t / w_t and, when `mask` is not null,
-// sets bit `bit` of each picked expert's 256-bit block mask in LDS.
-__device__ __forceinline__ void route_softmax_group(const float* __restrict__ row,
+// Round s takes every lane's best unpicked expert and reduces over the group
+// with xor-shuffles, so every lane learns pick s; lane s keeps it (k <= E <=
+// G).  Then lane s forms exp(v_s - v_0) in double, the group's first lane
+// adds the k of them in pick order (the oracle's sum), and lane s writes
+// pick s and its weight exp(v_s - v_0) / sum, rounded once.  Returns pick
+// `sub` on the lanes that hold one (live, sub < k), else -1.
+__device__ __forceinline__ int route_softmax_group(const float* __restrict__ row,
                                                     const float* __restrict__ bias, int64_t E,
                                                     int64_t k, int G, int sub, bool live,
                                                     int32_t* __restrict__ idx_t,
-                                                    float* __restrict__ w_t,
-                                                    unsigned long long* mask, int bit) {
+                                                    float* __restrict__ w_t) {
     // experts of this lane: sub + G*j, j < per_lane (<= kMaxExperts / G)
     const int per_lane = static_cast<int>((E + G - 1) / G);
     uint32_t picked = 0;  // bit j: expert sub + G*j already selected (per_lane <= 32)
-    double top = 0.0;
-    double sum = 0.0;
+    float my_v = -INFINITY;
+    int my_i = INT_MAX;
     for (int s = 0; s < k; ++s) {
         float bv = -INFINITY;
         int bi = INT_MAX;
@@ -533,21 +553,21 @@ __device__ __forceinline__ void route_softmax_group(const float* __restrict__ ro
             if (beats(ov, oi, bv, bi)) { bv = ov; bi = oi; }
         }
         if (live && bi != INT_MAX && (bi % G) == sub) picked |= 1u << (bi / G);
-        if (live && sub == 0) {
-            idx_t[s] = bi;
-            if (s == 0) top = static_cast<double>(bv);
-            sum += exp(static_cast<double>(bv) - top);
-            w_t[s] = bv;  // the selected value, turned into a weight below
-            if (mask != nullptr && bi >= 0 && bi < E)
-                atomicOr(&mask[bi * 4 + (bit >> 6)], 1ull << (bit & 63));
+        if (sub == s) {
+            my_v = bv;
+            my_i = bi;
         }
     }
-    if (live && sub == 0) {
-        for (int s = 0; s < k; ++s) {
-            const double ex = exp(static_cast<double>(w_t[s]) - top);
-            w_t[s] = static_cast<float>(ex / sum);
-        }
+    const double top = static_cast<double>(__shfl(my_v, 0, G));
+    const double ex = exp(static_cast<double>(my_v) - top);
+    double sum = 0.0;
+    for (int s = 0; s < k; ++s) sum += __shfl(ex, s, G);  // pick order, on every lane
+    if (live && sub < k) {
+        idx_t[sub] = my_i;
+        w_t[sub] = static_cast<float>(ex / sum);
+        return my_i;
     }
+    return -1;
 }
 
 __global__ __launch_bounds__(256) void route_softmax_kernel(
@@ -559,8 +579,7 @@ __global__ __launch_bounds__(256) void route_softmax_kernel(
     const int64_t t = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / G;
     const bool live = t < T;
     const int64_t tt = live ? t : 0;
-    route_softmax_group(logits + tt * E, bias, E, k, G, sub, live, idx + tt * k, w + tt * k,
-                        nullptr, 0);
+    route_softmax_group(logits + tt * E, bias, E, k, G, sub, live, idx + tt * k, w + tt * k);
 }
 
 // ---------------------------------------------------------- permutation
@@ -639,67 +658,136 @@ __global__ __launch_bounds__(1024) void perm_scan_kernel(
     scan_counts<1024>(counts, nb, E, offsets);
 }
 
-// Routing, the block counts and their scan in one launch, as the
-// reference's route_count routes each token and counts it in one launch
-// (src/model.cu:921-942).  Block b routes its kPermTokens tokens (PHI_QUANT:
-// a thread per token; SOFTMAX_TOPK: groups of G lanes, 256 / G tokens per
-// round), records each pick in the block's per-expert 256-bit masks in LDS
-// (as perm_count does) and writes counts[e][b].  Then each block makes its
-// counts visible (a device-scope release fence) and takes a ticket from
-// `done`; the block holding the last ticket fences (acquire), scans every
-// block's counts into the offsets and puts `done` back to 0 for the next
-// launch.  No block waits for another: the scan is done by whichever block
-// finishes last.  `done` must be 0 before the first launch.
-template <int MODE>
-__global__ __launch_bounds__(256) void route_count_kernel(
+// Routing and the per-block expert counts in one launch, as the reference's
+// route_count routes each token and counts it in one launch
+// (src/model.cu:921-942).  The routing keeps the standalone routers' full
+// parallelism: a thread per token (PHI_QUANT) or a group of G lanes per
+// token (SOFTMAX_TOPK), RC_THREADS threads per workgroup.  A workgroup's
+// tokens fill one or more permutation blocks of kPermTokens, or part of one;
+// it counts its picks per (permutation block, expert) in LDS and adds each
+// non-zero count into counts[e][b], which the launch before this one (the
+// gate) zeroed.  Nothing here waits for the other workgroups: the counts are
+// read by the next launch (perm_place_scan_kernel), after this one ends.
+template <int MODE, int RC_THREADS>
+__global__ __launch_bounds__(RC_THREADS) void route_count_kernel(
         const float* __restrict__ logits, const float* __restrict__ bias, int64_t T,
         int64_t E, int64_t k, int G, float quantum, float tie_eps,
-        int32_t* __restrict__ idx, float* __restrict__ w, int32_t* __restrict__ counts,
-        int32_t* __restrict__ offsets, uint32_t* __restrict__ done) {
-    __shared__ unsigned long long masks[kMaxExperts * 4];
-    __shared__ int last;
+        int32_t* __restrict__ idx, float* __restrict__ w, int32_t* __restrict__ counts) {
+    // tokens per workgroup: RC_THREADS (PHI_QUANT) or RC_THREADS / G, in pb
+    // permutation blocks (RC_THREADS / kPermTokens for a thread per token,
+    // 1 when a workgroup holds kPermTokens tokens or fewer)
+    constexpr int PBMAX = RC_THREADS / kPermTokens;
+    __shared__ int32_t hist[PBMAX * kMaxExperts];
     const int tid = threadIdx.x;
-    const int64_t b = blockIdx.x, nb = gridDim.x;
-    const int64_t tb = b * kPermTokens;
-    for (int i = tid; i < E * 4; i += blockDim.x) masks[i] = 0ull;
+    const int64_t nb = (T + kPermTokens - 1) / kPermTokens;
+    const int tpw = MODE == MOE_ROUTER_PHI_QUANT ? RC_THREADS : RC_THREADS / G;
+    const int64_t tw = static_cast<int64_t>(blockIdx.x) * tpw;  // first token
+    const int pb = tpw >= kPermTokens ? tpw / kPermTokens : 1;
+    for (int i = tid; i < pb * E; i += RC_THREADS) hist[i] = 0;
     __syncthreads();
     if (MODE == MOE_ROUTER_PHI_QUANT) {
-        const int64_t t = tb + tid;
-        if (tid < kPermTokens && t < T) {
+        const int64_t t = tw + tid;
+        if (t < T) {
             int32_t picks[kMaxTopK];
             route_phi_token(logits + t * E, bias, E, k, quantum, tie_eps, idx + t * k,
                             w + t * k, picks);
+            const int hb = tid / kPermTokens;
             for (int s = 0; s < k; ++s) {
                 const int e = picks[s];
-                if (e >= 0 && e < E) atomicOr(&masks[e * 4 + (tid >> 6)], 1ull << (tid & 63));
+                if (e >= 0 && e < E) atomicAdd(&hist[hb * E + e], 1);
             }
         }
     } else {
         const int sub = (tid & 63) & (G - 1);
-        const int per_round = 256 / G;
-        for (int r = 0; r < kPermTokens; r += per_round) {
-            const int j = r + tid / G;  // token of this lane's group, within the block
-            const int64_t t = tb + j;
-            const bool live = j < kPermTokens && t < T;
-            const int64_t tt = live ? t : 0;
-            route_softmax_group(logits + tt * E, bias, E, k, G, sub, live, idx + tt * k,
-                                w + tt * k, masks, j);
+        const int64_t t = tw + tid / G;
+        const bool live = t < T;
+        const int64_t tt = live ? t : 0;
+        // lane s of the group holds pick s: its count
+        const int e = route_softmax_group(logits + tt * E, bias, E, k, G, sub, live,
+                                          idx + tt * k, w + tt * k);
+        if (e >= 0 && e < E) {
+            const int hb = static_cast<int>((t - tw) / kPermTokens);
+            atomicAdd(&hist[hb * E + e], 1);
         }
     }
     __syncthreads();
-    for (int e = tid; e < E; e += blockDim.x) {
-        const int c = __popcll(masks[e * 4]) + __popcll(masks[e * 4 + 1]) +
-                      __popcll(masks[e * 4 + 2]) + __popcll(masks[e * 4 + 3]);
-        counts[e * nb + b] = c;  // expert-major: the scan below is a plain scan
+    const int64_t b0 = tw / kPermTokens;
+    for (int i = tid; i < pb * E; i += RC_THREADS) {
+        const int hb = i / static_cast<int>(E), e = i % static_cast<int>(E);
+        if (hist[i] != 0 && b0 + hb < nb) atomicAdd(&counts[e * nb + b0 + hb], hist[i]);
     }
-    __threadfence();
+}
+
+// perm_place with the scan folded in, for the layer: block b computes the
+// bases it needs from the raw per-block counts (counts[e][b'] of every
+// block, as route_count_kernel left them) -- for each expert the count of
+// its pairs in blocks before b and in all blocks -- then the experts'
+// offsets as an exclusive scan of those totals, so base(e, b) = offset(e) +
+// pairs of e in blocks before b, the value perm_scan_kernel would have
+// written.  Block 0 writes the offsets.  Each block reads all E * nb counts,
+// so the layer takes this path only while E * nb is small (kPlaceScanMax).
+__global__ __launch_bounds__(256) void perm_place_scan_kernel(
+        const int32_t* __restrict__ idx, int64_t T, int64_t k, int64_t E,
+        const int32_t* __restrict__ counts, int32_t* __restrict__ perm,
+        int32_t* __restrict__ inv, int32_t* __restrict__ offsets) {
+    __shared__ unsigned long long masks[kMaxExperts * 4];
+    __shared__ int32_t before[kMaxExperts], base[kMaxExperts];
+    __shared__ int32_t wave_sums[4];
+    const int64_t b = blockIdx.x, nb = gridDim.x;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    for (int e = tid; e < E; e += 256) {
+        before[e] = 0;
+        base[e] = 0;
+    }
     __syncthreads();
-    if (tid == 0) last = atomicAdd(done, 1u) == static_cast<uint32_t>(nb - 1);
+    // per expert: pairs in blocks before b (before[]), in all blocks (base[])
+    for (int64_t i = tid; i < E * nb; i += 256) {
+        const int c = counts[i];
+        if (c == 0) continue;
+        const int64_t e = i / nb;
+        atomicAdd(&base[e], c);
+        if (i - e * nb < b) atomicAdd(&before[e], c);
+    }
+    build_masks(idx, T, k, E, b * kPermTokens, masks);  // its barriers order the adds above
+    // exclusive scan of the totals over the experts, 256 at a time
+    int32_t carry = 0;
+    for (int e0 = 0; e0 < E; e0 += 256) {
+        const int e = e0 + tid;
+        const int32_t v = e < E ? base[e] : 0;
+        int32_t incl = v;
+        for (int off = 1; off < 64; off <<= 1) {
+            const int32_t o = __shfl_up(incl, off, 64);
+            if (lane >= off) incl += o;
+        }
+        if (lane == 63) wave_sums[wv] = incl;
+        __syncthreads();
+        int32_t pre = carry;
+        for (int j = 0; j < wv; ++j) pre += wave_sums[j];
+        const int32_t chunk = wave_sums[0] + wave_sums[1] + wave_sums[2] + wave_sums[3];
+        __syncthreads();
+        if (e < E) {
+            const int32_t off = pre + incl - v;
+            if (b == 0) offsets[e] = off;
+            base[e] = off + before[e];
+        }
+        carry += chunk;
+    }
+    if (b == 0 && tid == 0) offsets[E] = carry;
     __syncthreads();
-    if (!last) return;
-    __threadfence();
-    scan_counts<256>(counts, nb, E, offsets);
-    if (tid == 0) *done = 0u;
+    const int64_t t = b * kPermTokens + tid;
+    if (tid < kPermTokens && t < T) {
+        const int word = tid >> 6;
+        const unsigned long long below = (1ull << (tid & 63)) - 1ull;
+        for (int s = 0; s < k; ++s) {
+            const int e = idx[t * k + s];
+            if (e < 0 || e >= E) { inv[t * k + s] = -1; continue; }
+            int rank = __popcll(masks[e * 4 + word] & below);
+            for (int q = 0; q < word; ++q) rank += __popcll(masks[e * 4 + q]);
+            const int32_t pos = base[e] + rank;
+            perm[pos] = static_cast<int32_t>(t);
+            inv[t * k + s] = pos;
+        }
+    }
 }
 
 __global__ __launch_bounds__(256) void perm_place_kernel(
@@ -866,7 +954,7 @@ __global__ __launch_bounds__(256) void combine_kernel(
 
 void launch_gate_logits(const float* x, const float* w, float* logits,
                         int64_t T, int64_t d, int64_t E, int contract,
-                        hipStream_t s) {
+                        hipStream_t s, uint32_t* zero, int64_t nzero) {
     if (T == 0 || E == 0) return;
     auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
     // The ring form for E <= 8 (16 token rows x 4 experts or 8 x 8 per wave).
@@ -878,7 +966,7 @@ void launch_gate_logits(const float* x, const float* w, float* logits,
         const int eb = E <= 4 ? 4 : 8;
         const dim3 grid(static_cast<unsigned>(ceil_div(T, 64 / eb)));
         auto go = [&](auto kernel) {
-            hipLaunchKernelGGL(kernel, grid, dim3(64), 0, s, x, w, logits, T, d, E);
+            hipLaunchKernelGGL(kernel, grid, dim3(64), 0, s, x, w, logits, T, d, E, zero, nzero);
         };
         switch (eb * 2 + (contract ? 1 : 0)) {
             case 8: go(gate_ring_kernel<0, 4>); break;
@@ -895,7 +983,8 @@ void launch_gate_logits(const float* x, const float* w, float* logits,
     if (eb == 16 && d % 4 == 0 && d >= 4 && al(x) && al(w) && d * 16 * 4 < (int64_t(1) << 31)) {
         const dim3 grid(static_cast<unsigned>(ceil_div(T, 16)), static_cast<unsigned>(ceil_div(E, 16)));
         auto go = [&](auto kernel) {
-            hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, x, w, logits, T, d, E);
+            hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, x, w, logits, T, d, E, zero,
+                               nzero);
         };
         if (contract) go(gate_wg_ring_kernel<1, 16, 1, MOE_GATE_RING>);
         else go(gate_wg_ring_kernel<0, 16, 1, MOE_GATE_RING>);
@@ -907,7 +996,7 @@ void launch_gate_logits(const float* x, const float* w, float* logits,
     const dim3 grid(static_cast<unsigned>(ceil_div(T, tb * (256 / eb))),
                     static_cast<unsigned>(ceil_div(E, eb)));
     auto go = [&](auto kernel) {
-        hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, x, w, logits, T, d, E);
+        hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, x, w, logits, T, d, E, zero, nzero);
     };
     switch (eb * 2 + (contract ? 1 : 0)) {
         case 16: go(gate_logits_kernel<0, 8, 1>); break;
@@ -939,18 +1028,33 @@ void launch_route(const float* logits, const float* bias, int64_t T, int64_t E,
 
 void launch_route_count(const float* logits, const float* bias, int64_t T, int64_t E,
                         int64_t k, int mode, float quantum, float tie_eps, int32_t* idx,
-                        float* w, int32_t* counts, int32_t* offsets, uint32_t* done,
-                        hipStream_t s) {
-    const int64_t nb = ceil_div(T, kPermTokens);
-    if (nb == 0) return;
+                        float* w, int32_t* counts, hipStream_t s) {
+    if (T == 0) return;
     int G = 1;
     while (G < E && G < 64) G <<= 1;
+    // Threads per workgroup, measured on MI355X (HIP events, us, 256 / 1024
+    // threads): PHI_QUANT at the reference's 15,583 x 16 11.5 / 18.7 (a
+    // thread per token: the smaller workgroups spread the sequential selects
+    // over 4x the CUs); SOFTMAX_TOPK at config 3 8.8 / 8.0, config 5 8.8 /
+    // 8.0, config 4 (64 experts, top-8) 48.4 / 37.9.
+    const int threads = mode == MOE_ROUTER_PHI_QUANT ? 256 : 1024;
+    const int64_t tpw = mode == MOE_ROUTER_PHI_QUANT ? threads : threads / G;
+    const dim3 grid(static_cast<unsigned>(ceil_div(T, tpw)));
     auto go = [&](auto kernel) {
-        hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(nb)), dim3(256), 0, s, logits,
-                           bias, T, E, k, G, quantum, tie_eps, idx, w, counts, offsets, done);
+        hipLaunchKernelGGL(kernel, grid, dim3(threads), 0, s, logits, bias, T, E, k, G,
+                           quantum, tie_eps, idx, w, counts);
     };
-    if (mode == MOE_ROUTER_PHI_QUANT) go(route_count_kernel<MOE_ROUTER_PHI_QUANT>);
-    else go(route_count_kernel<MOE_ROUTER_SOFTMAX_TOPK>);
+    if (mode == MOE_ROUTER_PHI_QUANT) go(route_count_kernel<MOE_ROUTER_PHI_QUANT, 256>);
+    else go(route_count_kernel<MOE_ROUTER_SOFTMAX_TOPK, 1024>);
+}
+
+void launch_perm_place_scan(const int32_t* idx, int64_t T, int64_t k, int64_t E,
+                            const int32_t* counts, int32_t* perm, int32_t* inv,
+                            int32_t* offsets, hipStream_t s) {
+    const int64_t nb = ceil_div(T, kPermTokens);
+    if (nb == 0) return;
+    hipLaunchKernelGGL(perm_place_scan_kernel, dim3(static_cast<unsigned>(nb)), dim3(256), 0, s,
+                       idx, T, k, E, counts, perm, inv, offsets);
 }
 
 void launch_perm_count(const int32_t* idx, int64_t T, int64_t k, int64_t E,
