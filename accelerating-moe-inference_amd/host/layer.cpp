@@ -320,15 +320,32 @@ void PhiAttention::forward_nodes(const float* dn, float* dy, const float* resid,
     float* v = sc.f32(kSlotV, rows * KVH * hd);
     float* q = sc.f32(kSlotQ, nq * H * hd);
     float* a = sc.f32(kSlotAttn, nq * H * hd);
-    sgemm_nt(dn, *wk_, bk_, k, rows, KVH * hd, hidden_);
-    sgemm_nt(dn, *wv_, bv_, v, rows, KVH * hd, hidden_);
-    if (tail) {  // q of the last node of every sequence only
-        float* dt = sc.f32(kSlotTailIn, nq * hidden_);
-        check(moe_embed(ctx, dn, nb.tail_nodes, static_cast<int64_t>(nq),
-                        static_cast<int64_t>(hidden_), static_cast<int64_t>(rows), dt, nullptr));
-        sgemm_nt(dt, *wq_, bq_, q, nq, H * hd, hidden_);
+    if (nb.urows > 0 && !tail) {
+        // the projections of the distinct tokens' rows, then each node's row
+        // of them (a row gather, moe_embed over the projected table)
+        const std::size_t U = nb.urows;
+        float* uq = sc.f32(kSlotUQ, U * H * hd);
+        float* uk = sc.f32(kSlotUK, U * KVH * hd);
+        float* uv = sc.f32(kSlotUV, U * KVH * hd);
+        sgemm_nt(dn, *wq_, bq_, uq, U, H * hd, hidden_);
+        sgemm_nt(dn, *wk_, bk_, uk, U, KVH * hd, hidden_);
+        sgemm_nt(dn, *wv_, bv_, uv, U, KVH * hd, hidden_);
+        const auto R = static_cast<int64_t>(rows), Ui = static_cast<int64_t>(U);
+        check(moe_embed(ctx, uq, nb.node_u, R, static_cast<int64_t>(H * hd), Ui, q, nullptr));
+        check(moe_embed(ctx, uk, nb.node_u, R, static_cast<int64_t>(KVH * hd), Ui, k, nullptr));
+        check(moe_embed(ctx, uv, nb.node_u, R, static_cast<int64_t>(KVH * hd), Ui, v, nullptr));
     } else {
-        sgemm_nt(dn, *wq_, bq_, q, rows, H * hd, hidden_);
+        sgemm_nt(dn, *wk_, bk_, k, rows, KVH * hd, hidden_);
+        sgemm_nt(dn, *wv_, bv_, v, rows, KVH * hd, hidden_);
+        if (tail) {  // q of the last node of every sequence only
+            float* dt = sc.f32(kSlotTailIn, nq * hidden_);
+            check(moe_embed(ctx, dn, nb.tail_nodes, static_cast<int64_t>(nq),
+                            static_cast<int64_t>(hidden_), static_cast<int64_t>(rows), dt,
+                            nullptr));
+            sgemm_nt(dt, *wq_, bq_, q, nq, H * hd, hidden_);
+        } else {
+            sgemm_nt(dn, *wq_, bq_, q, rows, H * hd, hidden_);
+        }
     }
     const auto P = static_cast<int64_t>(rope_positions_);
     check(moe_rope_rows(ctx, nullptr, k, rope_->as<float>(), P, nb.positions,
@@ -404,11 +421,15 @@ void PhiDecoderLayer::forward_nodes(const float* dx, float* dy, const NodeRows& 
     const std::size_t n = tail ? nb.tail_rows : rows;
     if (rows == 0 || n == 0) return;
     moe_ctx* ctx = moe_dropin::context();
-    float* dn = sc.f32(kSlotNorm, rows * h);
     float* da = sc.f32(kSlotAttnOut, n * h);
-    check(moe_layer_norm(ctx, dx, in_w_->as<float>(), in_b_->as<float>(), apss26::NORM_EPS,
-                         static_cast<int64_t>(rows), static_cast<int64_t>(h), MOE_CONTRACT_FMA, dn,
-                         nullptr, nullptr, nullptr));
+    // the input norm: over the distinct tokens' rows when the batch gives
+    // them (first layer), else over every node
+    const bool distinct = nb.urows > 0 && !tail;
+    const std::size_t nrows = distinct ? nb.urows : rows;
+    float* dn = sc.f32(distinct ? kSlotUNorm : kSlotNorm, nrows * h);
+    check(moe_layer_norm(ctx, distinct ? nb.ux : dx, in_w_->as<float>(), in_b_->as<float>(),
+                         apss26::NORM_EPS, static_cast<int64_t>(nrows), static_cast<int64_t>(h),
+                         MOE_CONTRACT_FMA, dn, nullptr, nullptr, nullptr));
     // h = x + attention(norm(x)): the residual rows (the tail rows' gathered
     // from x) are added in the o-projection's store
     const float* resid = dx;

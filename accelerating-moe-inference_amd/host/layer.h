@@ -30,6 +30,7 @@ class Scratch;
 // Scratch slots of the trie-row path (the model's own start at kSlotModel).
 enum NodeSlot : std::size_t {
     kSlotK, kSlotV, kSlotQ, kSlotAttn, kSlotTailIn, kSlotNorm, kSlotAttnOut, kSlotTailResid,
+    kSlotUNorm, kSlotUQ, kSlotUK, kSlotUV,
     kSlotModel = 16
 };
 
@@ -100,6 +101,15 @@ struct NodeRows {
     const int32_t* tail_positions = nullptr;  // [tail_rows]
     const int32_t* tail_key_beg = nullptr;    // [tail_rows] their root paths in key_rows
     const int32_t* tail_key_end = nullptr;
+    // Distinct-token rows (set for the first layer only, when they are fewer
+    // than the nodes): a first-layer node's input row is its token's
+    // embedding, so the input norm and the q/k/v projections depend on the
+    // token alone (src/model.cu:1682-1705); they run over the distinct
+    // tokens' rows ux[urows, hidden] and node n takes row node_u[n] of each
+    // result (RoPE then at the node's own position).
+    std::size_t urows = 0;
+    const float* ux = nullptr;
+    const int32_t* node_u = nullptr;  // [rows]
 };
 
 class PhiAttention {
@@ -120,6 +130,9 @@ public:
     // o_proj(attention) + resid for every node, or (tail) for the tail rows
     // only (resid: the residual rows, added in the o-projection's store as
     // src/model.cu:1965 does).
+    // With nb.urows set, dn holds the normalised distinct-token rows
+    // [urows, hidden] instead, and the projections are expanded to the
+    // nodes by row gathers (not for the tail).
     void forward_nodes(const float* dn, float* dy, const float* resid, const NodeRows& nb,
                        bool tail, moe_dropin::Scratch& sc) const;
     std::size_t hidden() const { return hidden_; }

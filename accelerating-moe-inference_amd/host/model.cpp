@@ -4,6 +4,9 @@
 #include <cstdint>
 #include <numeric>
 #include <stdexcept>
+#include <string>
+
+#include <hip/hip_runtime.h>
 
 #include "config.h"
 #include "device.h"
@@ -21,7 +24,7 @@ std::shared_ptr<const DeviceBuffer> upload(const Tensor& t) {
 
 enum ModelSlot : std::size_t {
     kX = kSlotModel, kY, kLast, kLastNorm, kLogits, kTok, kPos, kKeys, kOff, kLastIdx, kTailPos,
-    kTailBeg, kTailEnd
+    kTailBeg, kTailEnd, kUTok, kNodeU, kUX
 };
 
 // The prefix trie of a batch: one node (one activation row) per distinct
@@ -81,9 +84,39 @@ Trie build_trie(const std::vector<std::vector<int>>& seqs, std::size_t vocab) {
     return t;
 }
 
+// lm_head row chunks: each chunk's logits go home while the next chunk's
+// product runs (src/model.cu:2031-2050 does the same with 4 chunks)
+constexpr std::size_t kLmChunks = 4;
+
 }  // namespace
 
-PhiTinyMoEModel::PhiTinyMoEModel(const std::string& model_file) : loader_(model_file) {
+// A non-blocking stream of default priority for the logits copies and one
+// event per lm_head chunk, created with the model and destroyed with it.
+struct PhiTinyMoEModel::CopyStream {
+    hipStream_t stream = nullptr;
+    hipEvent_t done[kLmChunks] = {};
+    CopyStream() {
+        check_hip(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreate");
+        for (hipEvent_t& e : done)
+            check_hip(hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreate");
+    }
+    ~CopyStream() {
+        for (hipEvent_t e : done)
+            if (e != nullptr) (void)hipEventDestroy(e);
+        if (stream != nullptr) (void)hipStreamDestroy(stream);
+    }
+    CopyStream(const CopyStream&) = delete;
+    CopyStream& operator=(const CopyStream&) = delete;
+    static void check_hip(hipError_t e, const char* what) {
+        if (e != hipSuccess)
+            throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+    }
+};
+
+PhiTinyMoEModel::PhiTinyMoEModel(const std::string& model_file)
+    : loader_(model_file),
+      pinned_out_({kPinnedOutBytes / sizeof(float)}, Tensor::Alloc::Pinned),
+      copy_(std::make_unique<CopyStream>()) {
     const Tensor emb = loader_.load("model.embed_tokens.weight");
     if (emb.ndim() != 2) throw std::invalid_argument("model.embed_tokens.weight: weight must be 2-D");
     embed_rows_ = emb.size(0);
@@ -160,20 +193,78 @@ void PhiTinyMoEModel::generate(const std::vector<std::vector<int>>& input_ids,
         check(moe_embed(ctx, x, d_last, static_cast<int64_t>(batch), static_cast<int64_t>(h),
                         static_cast<int64_t>(rows), last, nullptr));
     }
+    // The first layer's input norm and q/k/v over the distinct tokens of the
+    // nodes (a node's first-layer input is its token's embedding row), in
+    // order of first appearance (src/model.cu:1682-1705,1905-1935), when
+    // tokens repeat and the first layer is not also the pruned last one.
+    NodeRows nb0 = nb;
+    if (layers_.size() > 1) {
+        std::vector<int32_t> utok, node_u(rows);
+        std::vector<int32_t> first(std::min(vocab_, embed_rows_), -1);
+        for (std::size_t n = 0; n < rows; ++n) {
+            int32_t& u = first[static_cast<std::size_t>(t.token[n])];
+            if (u < 0) {
+                u = static_cast<int32_t>(utok.size());
+                utok.push_back(t.token[n]);
+            }
+            node_u[n] = u;
+        }
+        if (utok.size() < rows) {
+            const std::size_t U = utok.size();
+            float* ux = sc.f32(kUX, U * h);
+            check(moe_embed(ctx, embed_->as<float>(), sc.upload(kUTok, utok.data(), U),
+                            static_cast<int64_t>(U), static_cast<int64_t>(h),
+                            static_cast<int64_t>(embed_rows_), ux, nullptr));
+            nb0.urows = U;
+            nb0.ux = ux;
+            nb0.node_u = sc.upload(kNodeU, node_u.data(), rows);
+        }
+    }
     for (std::size_t l = 0; l < layers_.size(); ++l) {
         const bool tail = l + 1 == layers_.size();
-        layers_[l]->forward_nodes(x, tail ? last : y, nb, tail, sc);
+        layers_[l]->forward_nodes(x, tail ? last : y, l == 0 ? nb0 : nb, tail, sc);
         if (!tail) std::swap(x, y);
     }
     check(moe_layer_norm(ctx, last, norm_w_->as<float>(), norm_b_->as<float>(), apss26::NORM_EPS,
                          static_cast<int64_t>(batch), static_cast<int64_t>(h), MOE_CONTRACT_FMA,
                          last_n, nullptr, nullptr, nullptr));
-    check(moe_sgemm_nt(ctx, last_n, lm_w_->as<float>(), lm_b_ ? lm_b_->as<float>() : nullptr, out,
-                       static_cast<int64_t>(batch), static_cast<int64_t>(vocab_),
-                       static_cast<int64_t>(h), nullptr));
-    // the caller's Tensor is reused when it holds enough elements; the
-    // copy goes through the drop-in's pinned staging
+    // Where the logits land: the caller's Tensor if it is page-locked and
+    // large enough, else the model's page-locked reserve (moved into it, as
+    // the reference's generate() does), else ordinary host memory.
     const std::size_t n = batch * vocab_;
+    const float* lm_b = lm_b_ ? lm_b_->as<float>() : nullptr;
+    const bool caller_pinned = logits.alloc() == Tensor::Alloc::Pinned &&
+                               logits.capacity() >= n && logits.data() != nullptr;
+    if (!caller_pinned && pinned_out_.data() != nullptr && pinned_out_.capacity() >= n)
+        logits = std::move(pinned_out_);
+    if (logits.alloc() == Tensor::Alloc::Pinned && logits.capacity() >= n &&
+        logits.data() != nullptr) {
+        logits.reshape_within_capacity({batch, vocab_});
+        // lm_head in row chunks; chunk c's copy (on the copy stream, after
+        // the chunk's event) overlaps chunk c + 1's product
+        const std::size_t chunk = (batch + kLmChunks - 1) / kLmChunks;
+        CopyStream& cs = *copy_;
+        std::size_t c = 0;
+        for (std::size_t r0 = 0; r0 < batch; r0 += chunk, ++c) {
+            const std::size_t rc = std::min(chunk, batch - r0);
+            check(moe_sgemm_nt(ctx, last_n + r0 * h, lm_w_->as<float>(), lm_b, out + r0 * vocab_,
+                               static_cast<int64_t>(rc), static_cast<int64_t>(vocab_),
+                               static_cast<int64_t>(h), nullptr));
+            CopyStream::check_hip(hipEventRecord(cs.done[c], nullptr), "hipEventRecord lm_head");
+            CopyStream::check_hip(hipStreamWaitEvent(cs.stream, cs.done[c], 0),
+                                  "hipStreamWaitEvent lm_head");
+            CopyStream::check_hip(hipMemcpyAsync(logits.data() + r0 * vocab_, out + r0 * vocab_,
+                                                 rc * vocab_ * sizeof(float),
+                                                 hipMemcpyDeviceToHost, cs.stream),
+                                  "hipMemcpyAsync logits");
+        }
+        CopyStream::check_hip(hipStreamSynchronize(cs.stream), "hipStreamSynchronize logits");
+        return;
+    }
+    check(moe_sgemm_nt(ctx, last_n, lm_w_->as<float>(), lm_b, out, static_cast<int64_t>(batch),
+                       static_cast<int64_t>(vocab_), static_cast<int64_t>(h), nullptr));
+    // pageable output: the caller's Tensor is reused when it holds enough
+    // elements; the copy goes through the drop-in's pinned staging
     if (logits.capacity() >= n && logits.data() != nullptr)
         logits.reshape_within_capacity({batch, vocab_});
     else
@@ -194,11 +285,11 @@ void PhiTinyMoEModel::generate_decode(const std::vector<std::vector<int>>& input
     std::vector<std::vector<int>> prefix = input_ids;
     std::vector<std::size_t> active(batch);
     for (std::size_t b = 0; b < batch; ++b) active[b] = b;
+    Tensor step_logits;  // one buffer for every step (it keeps the page-locked reserve)
     for (std::size_t step = 0; step < max_new_tokens && !active.empty(); ++step) {
         std::vector<std::vector<int>> rows;
         rows.reserve(active.size());
         for (std::size_t b : active) rows.push_back(prefix[b]);
-        Tensor step_logits;
         generate(rows, step_logits);
         std::vector<std::size_t> still;
         for (std::size_t i = 0; i < active.size(); ++i) {

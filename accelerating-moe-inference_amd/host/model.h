@@ -56,4 +56,12 @@ private:
     // before allocates nothing (so, like the reference's generate(), a model
     // is not safe for concurrent calls).
     mutable moe_dropin::Scratch scratch_;
+    // Page-locked output reserve (the reference's pinned_out_,
+    // include/model.h:123): the first generate() whose logits Tensor is not
+    // page-locked and large enough takes it over, so the logits copy runs
+    // at full DMA speed, chunk by chunk behind the lm_head.
+    static constexpr std::size_t kPinnedOutBytes = std::size_t(256) << 20;
+    mutable Tensor pinned_out_;
+    struct CopyStream;  // the copy stream and the lm_head chunks' events
+    std::unique_ptr<CopyStream> copy_;
 };

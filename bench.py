@@ -936,18 +936,35 @@ def write_phi_model(path):
     return where, off
 
 
-def phi_batch():
+def phi_batch(text_like=False):
     """A batch shaped like the reference's contest input: 1024 sequences,
     10-29 tokens each, whose first 4 tokens come from 64 shared prefixes, so
     the prefix trie removes about a fifth of the rows (the reference's input:
-    19,803 tokens, 15,583 trie rows)."""
+    19,803 tokens, 15,583 trie rows).  The other tokens are uniform over the
+    vocabulary (about 78 % of the trie nodes then carry distinct tokens), or
+    (text_like) drawn as words of text are, a Zipf(1.1) rank over a shuffled
+    vocabulary mixed with 7 % uniform draws, which gives the contest input's
+    ratio of distinct tokens to nodes (3,830 of 15,583, 25 %)."""
     import numpy as np
     tr = np.random.default_rng(1)
     prefixes = tr.integers(0, 32000, (64, 4))
     lens = tr.integers(10, 30, 1024).astype(np.int32)
-    seqs = [np.concatenate([prefixes[tr.integers(0, 64)], tr.integers(0, 32000, n - 4)])
-            for n in lens]
+    tz = np.random.default_rng(2)  # the text-like draws (the uniform batch keeps tr's stream)
+    perm = tz.permutation(32000)
+
+    def draw(n):
+        if not text_like:
+            return tr.integers(0, 32000, n)
+        z = perm[np.minimum(tz.zipf(1.1, n) - 1, 31999)]
+        return np.where(tz.random(n) < 0.07, tz.integers(0, 32000, n), z)
+    seqs = [np.concatenate([prefixes[tr.integers(0, 64)], draw(n - 4)]) for n in lens]
     return seqs, lens
+
+
+def trie_stats(seqs):
+    """(trie nodes, distinct tokens among them) of a batch."""
+    nodes = {tuple(sq[:i + 1]) for sq in seqs for i in range(len(sq))}
+    return len(nodes), len({n[-1] for n in nodes})
 
 
 def phi_oracle_weights(path, where):
@@ -1001,7 +1018,7 @@ def model_entry(warmup, steps, cpu_seconds):
     import ctypes
     import numpy as np
     seqs, lens = phi_batch()
-    nodes = len({tuple(sq[:i + 1]) for sq in seqs for i in range(len(sq))})
+    nodes, distinct = trie_stats(seqs)
     ids = np.concatenate(seqs).astype(np.int32)
     shim = ctypes.CDLL(os.path.join(ROOT, "tests", "cpp", "libdropin_shim.so"))
     shim.shim_error.restype = ctypes.c_char_p
@@ -1023,6 +1040,22 @@ def model_entry(warmup, steps, cpu_seconds):
                                   logits.ctypes.data_as(ctypes.c_void_p))
         if rc != 0:
             raise RuntimeError(f"shim_model_time: {shim.shim_error().decode()}")
+        # the same model on a batch with the contest input's share of
+        # distinct tokens (the first layer's norm and q/k/v run over them)
+        tseqs, tlens = phi_batch(text_like=True)
+        tnodes, tdistinct = trie_stats(tseqs)
+        tids = np.concatenate(tseqs).astype(np.int32)
+        tload, tms = D(0.0), D(0.0)
+        rc = shim.shim_model_time(path.encode(), tlens.ctypes.data_as(ctypes.c_void_p),
+                                  tids.ctypes.data_as(ctypes.c_void_p), I(len(tlens)),
+                                  I(warm), I(steps), ctypes.byref(tload), ctypes.byref(tms),
+                                  None)
+        if rc != 0:
+            raise RuntimeError(f"shim_model_time: {shim.shim_error().decode()}")
+        text_like = {"value": len(tlens) / (tms.value * 1e-3), "unit": "seq/s",
+                     "ms_per_call": tms.value, "tokens": int(tlens.sum()), "trie_rows": tnodes,
+                     "distinct_tokens": tdistinct,
+                     "tokens_note": "Zipf(1.1) ranks over a shuffled vocabulary, 7 % uniform"}
         cpu = parity = None
         if cpu_seconds > 0:
             oracle, build = cpu_oracle()
@@ -1061,7 +1094,8 @@ def model_entry(warmup, steps, cpu_seconds):
         "steps": steps, "warmup": warm, "dtype": "f32",
         "data": "synthetic (seeded random weights; random token ids with 64 shared prefixes)",
         "config": {"workload": "phi_tiny_moe_generate_fp32", "sequences": int(B),
-                   "tokens": int(lens.sum()), "trie_rows": nodes, "layers": L_, "d_model": h,
+                   "tokens": int(lens.sum()), "trie_rows": nodes, "distinct_tokens": distinct,
+                   "layers": L_, "d_model": h,
                    "experts": PHI["E"], "top_k": 2, "d_ff": PHI["d_ff"], "vocab": PHI["vocab"],
                    "router": "quantised top-2, weights 1/2 (PhiMoE::route)"},
         "model_tflops": flops / (ms.value * 1e-3) / 1e12,
@@ -1073,6 +1107,7 @@ def model_entry(warmup, steps, cpu_seconds):
         "reference_note": "the reference's end-to-end figure on one RTX 3090, 1024 sequences / "
                           "19,803 tokens of its contest input (docs/report/report.html:96)",
         "model_load_s": load_s.value,
+        "text_like_batch": text_like,
         "cpu_baseline": cpu,
         "cpu_sample_parity": parity,
     }

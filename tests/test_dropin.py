@@ -514,6 +514,37 @@ def test_model_generate_and_decode_vs_oracle(shim, orc, tmp_path):
 
 
 @pytest.mark.gpu
+def test_model_generate_repeated_tokens_vs_oracle(shim, orc, tmp_path):
+    # tokens from a pool of 7, so most trie nodes share their token with
+    # nodes at other depths and in other branches: the first layer's norm
+    # and q/k/v run over the 7 distinct tokens' rows and are expanded to the
+    # nodes (RoPE at each node's own depth); every sequence's logits must
+    # still equal the oracle's run of that sequence alone.  A second batch
+    # without repeats takes the all-nodes path on the same model.
+    from oracle import decoder as od
+    rng = np.random.default_rng(52)
+    L, h, E, ff, V = 3, 256, 4, 64, 32064
+    t = _model_tensors(rng, L, h, E, ff, V)
+    path = str(tmp_path / "model.bin")
+    write_model_bin(path, t)
+    W, cfg = _oracle_model(orc, t, L, E)
+    pool = rng.integers(0, 32000, 7)
+    base = pool[rng.integers(0, 7, 20)]
+    seqs = [base, base[:6], np.concatenate([base[:6], pool[[3, 3, 0]]]), pool[rng.integers(0, 7, 13)],
+            np.full(9, pool[2]), pool[rng.integers(0, 7, 1)]]
+    distinct = [rng.permutation(32000)[:n] for n in (11, 5, 17)]
+    for batch in (seqs, distinct):
+        lens = np.array([len(s) for s in batch], np.int32)
+        ids = np.concatenate(batch).astype(np.int32)
+        got = np.empty((len(batch), V), np.float32)
+        assert shim.shim_model_generate(path.encode(), fptr(lens), fptr(ids), ctypes.c_int64(len(batch)),
+                                        fptr(got), ctypes.c_int64(V)) == 0, err(shim)
+        for b, sq in enumerate(batch):
+            ref, _, _ = od.generate(np.asarray(sq)[None, :], W, cfg)
+            assert_close(got[b], ref[0], what=f"sequence {b}")
+
+
+@pytest.mark.gpu
 def test_model_decode_stops_at_eos_and_rejects_bad_input(shim, orc, tmp_path):
     rng = np.random.default_rng(51)
     L, h, E, ff, V = 1, 256, 4, 64, 32064
