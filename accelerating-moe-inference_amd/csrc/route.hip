@@ -51,14 +51,20 @@ __device__ __forceinline__ void zero_words(uint32_t* __restrict__ zero, int64_t 
         zero[i] = 0u;
 }
 
-template <int CONTRACT, int EB, int TB>
+// TE > 1: each thread runs TB tokens x TE experts (experts el, el + EB/TE,
+// ...: the lanes of a wave then read TE distinct expert rows per read), so a
+// 16-byte LDS read of x feeds TE chains and one of w feeds TB: at 64 experts
+// with TE = 1 the reads, not the multiply-adds, bounded the kernel.
+template <int CONTRACT, int EB, int TB, int TE = 1>
 __global__ __launch_bounds__(256) void gate_logits_kernel(
         const float* __restrict__ x, const float* __restrict__ w,
         float* __restrict__ logits, int64_t T, int64_t d, int64_t E,
         uint32_t* __restrict__ zero, int64_t nzero) {
-    constexpr int R = TB * (256 / EB);        // token rows per workgroup
+    constexpr int EG = EB / TE;               // expert groups (threads per token row group)
+    constexpr int R = TB * (256 / EG);        // token rows per workgroup
     constexpr int ROWS = R + EB;              // staged rows: x rows, then w rows
     constexpr int PER = ROWS * GATE_KC / 256; // staged floats per thread
+    static_assert(EB % TE == 0 && 256 % EG == 0 && ROWS * GATE_KC % 256 == 0, "gate tile");
     typedef float f4 __attribute__((ext_vector_type(4)));
     __shared__ __align__(16) float tile[2][ROWS * GATE_LDS];
     zero_words(zero, nzero);
@@ -66,7 +72,7 @@ __global__ __launch_bounds__(256) void gate_logits_kernel(
     const int tid = threadIdx.x;
     const int64_t t0 = static_cast<int64_t>(blockIdx.x) * R;
     const int64_t e0 = static_cast<int64_t>(blockIdx.y) * EB;
-    const int el = tid % EB, r = tid / EB;
+    const int el = tid % EG, r = tid / EG;
 
     // Staging: element i*256 + tid of the tile -> (row, col); 64 lanes of a
     // wave read 64 consecutive floats of one row (256 contiguous bytes).
@@ -103,9 +109,11 @@ __global__ __launch_bounds__(256) void gate_logits_kernel(
         }
     };
 
-    float acc[TB];
+    float acc[TB][TE];
 #pragma unroll
-    for (int u = 0; u < TB; ++u) acc[u] = 0.0f;
+    for (int u = 0; u < TB; ++u)
+#pragma unroll
+        for (int v = 0; v < TE; ++v) acc[u][v] = 0.0f;
     const int64_t nchunks = (d + GATE_KC - 1) / GATE_KC;
     if (nchunks > 0) {
         gload(0);
@@ -120,30 +128,43 @@ __global__ __launch_bounds__(256) void gate_logits_kernel(
         // CPU's, with no padding term.
         const int kn = static_cast<int>(d - k0 < GATE_KC ? d - k0 : GATE_KC);
         const float* xr = &tile[buf][r * TB * GATE_LDS];  // this thread's TB rows
-        const float* wr = &tile[buf][(R + el) * GATE_LDS];
+        const float* wr = &tile[buf][(R + el) * GATE_LDS];  // its TE rows, EG apart
         int kk = 0;
         for (; kk + 4 <= kn; kk += 4) {
-            const f4 wv = *reinterpret_cast<const f4*>(wr + kk);
+            f4 wv[TE];
+#pragma unroll
+            for (int v = 0; v < TE; ++v)
+                wv[v] = *reinterpret_cast<const f4*>(wr + v * EG * GATE_LDS + kk);
 #pragma unroll
             for (int u = 0; u < TB; ++u) {
                 const f4 xv = *reinterpret_cast<const f4*>(xr + u * GATE_LDS + kk);
-                acc[u] = mac<CONTRACT>(acc[u], xv[0], wv[0]);
-                acc[u] = mac<CONTRACT>(acc[u], xv[1], wv[1]);
-                acc[u] = mac<CONTRACT>(acc[u], xv[2], wv[2]);
-                acc[u] = mac<CONTRACT>(acc[u], xv[3], wv[3]);
+#pragma unroll
+                for (int v = 0; v < TE; ++v) {
+                    acc[u][v] = mac<CONTRACT>(acc[u][v], xv[0], wv[v][0]);
+                    acc[u][v] = mac<CONTRACT>(acc[u][v], xv[1], wv[v][1]);
+                    acc[u][v] = mac<CONTRACT>(acc[u][v], xv[2], wv[v][2]);
+                    acc[u][v] = mac<CONTRACT>(acc[u][v], xv[3], wv[v][3]);
+                }
             }
         }
         for (; kk < kn; ++kk)
 #pragma unroll
-            for (int u = 0; u < TB; ++u) acc[u] = mac<CONTRACT>(acc[u], xr[u * GATE_LDS + kk], wr[kk]);
+            for (int u = 0; u < TB; ++u)
+#pragma unroll
+                for (int v = 0; v < TE; ++v)
+                    acc[u][v] = mac<CONTRACT>(acc[u][v], xr[u * GATE_LDS + kk],
+                                              wr[v * EG * GATE_LDS + kk]);
         if (c + 1 < nchunks) lstore(buf ^ 1);
         __syncthreads();
     }
-    const int64_t e = e0 + el;
 #pragma unroll
-    for (int u = 0; u < TB; ++u) {
-        const int64_t t = t0 + r * TB + u;
-        if (t < T && e < E) logits[t * E + e] = acc[u];
+    for (int v = 0; v < TE; ++v) {
+        const int64_t e = e0 + el + v * EG;
+#pragma unroll
+        for (int u = 0; u < TB; ++u) {
+            const int64_t t = t0 + r * TB + u;
+            if (t < T && e < E) logits[t * E + e] = acc[u][v];
+        }
     }
 }
 
@@ -991,9 +1012,15 @@ void launch_gate_logits(const float* x, const float* w, float* logits,
         return;
     }
     // 4 tokens per thread from 32 experts up (small E keeps one output per
-    // thread: its rows per workgroup are already many, and the grid stays wide)
+    // thread: its rows per workgroup are already many, and the grid stays
+    // wide), and at 64-expert blocks 2 or 4 experts per thread as well: 4
+    // where that still leaves 512 workgroups or more.  Measured on MI355X
+    // (us, 1 / 2 / 4 experts per thread): config 4's 16,384 x 2048 x 64
+    // 189.5 / 100.2 / 137.6; 4096 x 4096 x 64 182.1 / 171.1 / 265.9;
+    // 16,384 x 2048 x 100 (two expert blocks) 300.3 / 182.5 / 146.8.
     const int tb = eb >= 32 ? 4 : 1;
-    const dim3 grid(static_cast<unsigned>(ceil_div(T, tb * (256 / eb))),
+    const int te = eb < 64 ? 1 : (ceil_div(T, 64) * ceil_div(E, 64) >= 512 ? 4 : 2);
+    const dim3 grid(static_cast<unsigned>(ceil_div(T, tb * (256 / (eb / te)))),
                     static_cast<unsigned>(ceil_div(E, eb)));
     auto go = [&](auto kernel) {
         hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, x, w, logits, T, d, E, zero, nzero);
@@ -1005,8 +1032,14 @@ void launch_gate_logits(const float* x, const float* w, float* logits,
         case 33: go(gate_logits_kernel<1, 16, 1>); break;
         case 64: go(gate_logits_kernel<0, 32, 4>); break;
         case 65: go(gate_logits_kernel<1, 32, 4>); break;
-        case 128: go(gate_logits_kernel<0, 64, 4>); break;
-        default: go(gate_logits_kernel<1, 64, 4>); break;
+        case 128:
+            if (te == 4) go(gate_logits_kernel<0, 64, 4, 4>);
+            else go(gate_logits_kernel<0, 64, 4, 2>);
+            break;
+        default:
+            if (te == 4) go(gate_logits_kernel<1, 64, 4, 4>);
+            else go(gate_logits_kernel<1, 64, 4, 2>);
+            break;
     }
 }
 

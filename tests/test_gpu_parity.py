@@ -291,13 +291,16 @@ def test_silu_mul_bit_exact(ctx, torch, orc):
 # reference's expert count, the latter with a partial last workgroup; 45 x
 # 196 x 11: a partial last stage, 5 experts masked; 16 x 4 x 16: one
 # 4-column stage); every other shape the staged kernel: E above 16 (1000 x
-# 2048 x 64, config 4's expert count, 4 tokens per thread; 77 x 452 x 100:
-# two 64-expert blocks, the second 36 wide; 50 x 1024 x 32) and rows that
-# are not 16-byte multiples (70 x 130 x 130; 5 x 1 x 3)
+# 2048 x 64, config 4's expert count, 4 tokens x 2 experts per thread; 77 x
+# 452 x 100: two 64-expert blocks, the second 36 wide; 50 x 1024 x 32; and
+# grids of 512 workgroups or more, 4 tokens x 4 experts per thread: 33000 x
+# 40 x 64 and 16421 x 96 x 100, ragged last workgroup and expert block) and
+# rows that are not 16-byte multiples (70 x 130 x 130; 5 x 1 x 3)
 @pytest.mark.parametrize("T,d,E", [(64, 512, 4), (300, 4096, 16), (1000, 2048, 64),
                                    (33, 100, 7), (5, 1, 3), (70, 130, 130), (4096, 1024, 8),
                                    (100, 256, 2), (1037, 4096, 16), (45, 196, 11),
-                                   (77, 452, 100), (16, 4, 16), (50, 1024, 32)])
+                                   (77, 452, 100), (16, 4, 16), (50, 1024, 32),
+                                   (33000, 40, 64), (16421, 96, 100)])
 def test_gate_logits_bit_exact(ctx, torch, orc, contract, T, d, E):
     print(f"gate {T}x{d}x{E} contract={contract}", flush=True)
     rng = np.random.default_rng(T + d + E)
