@@ -7,7 +7,9 @@
 `copy` launches one elementwise kernel that reads and writes exactly
 --mib MiB (torch.neg into a second buffer): the calibration of the TCC byte
 counters against a known traffic.  `layer` runs --steps MoE layer forwards
-of a bench configuration (same seeded data as bench.py) after one warm-up.
+of a bench configuration (same seeded data as bench.py) after one warm-up;
+with --block, as the decoder's MoE block (the norm in front, the residual
+added).
 `sgemm` runs every config-2 SGEMM shape twice, NN then NT (bench.py's
 SGEMM_SHAPES, A and B ~ U[-1, 1]), printing each shape before its calls so
 dispatches can be matched to shapes.
@@ -29,6 +31,8 @@ def main():
     ap.add_argument("--mib", type=int, default=1024)
     ap.add_argument("--config", default="c3", choices=["c1", "c3", "c4", "c5", "ref"])
     ap.add_argument("--steps", type=int, default=2)
+    ap.add_argument("--block", action="store_true",
+                    help="layer: the MoE block (norm in front, residual added)")
     args = ap.parse_args()
 
     import torch
@@ -64,7 +68,7 @@ def main():
         ctx.close()
         return
     cfg = bench.CONFIGS[args.config]
-    x, weights, y, idx, w, desc = bench.build_layer(pkg, cfg, cfg["T"], False,
+    x, weights, y, idx, w, desc = bench.build_layer(pkg, cfg, cfg["T"], args.block,
                                                     torch.device("cuda:0"))
     ctx = pkg.Context(0)
     ctx.reserve(desc)
