@@ -40,7 +40,7 @@ EXPORTS = (
     "moe_add_bias", "moe_embed", "moe_gate_logits",
     "moe_route", "moe_permute", "moe_expert_ffn_grouped", "moe_combine",
     "moe_layer_forward", "moe_layer_forward_noalloc", "moe_layer_w2_splits",
-    "moe_ctx_set_stream_k", "moe_ctx_workspace_bytes", "moe_launch_floor",
+    "moe_ctx_set_stream_k", "moe_ctx_workspace_bytes", "moe_launch_floor", "moe_sgemm_plan",
 )
 
 
@@ -127,6 +127,8 @@ def load_library(path: str = LIB_PATH):
         "moe_ctx_set_stream_k": ([P, I], I),
         "moe_ctx_workspace_bytes": ([P, ctypes.POINTER(ctypes.c_int64)], I),
         "moe_launch_floor": ([P, P], I),
+        "moe_sgemm_plan": ([P, I, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+                            ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32)], I),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -429,6 +431,14 @@ class Context:
         """moe_ctx_set_stream_k: -1 planner, 0 one tile per workgroup, 1
         stream-K for the grouped expert GEMMs of this context."""
         _check(_lib.moe_ctx_set_stream_k(self.handle, int(mode)))
+
+    def sgemm_plan(self, M: int, N: int, K: int, nn: bool = True) -> dict:
+        """moe_sgemm_plan: the tile shape id and K splits moe_sgemm_nn /
+        moe_sgemm_nt runs M x N x K with on this context's GPU."""
+        t, sp = ctypes.c_int32(0), ctypes.c_int32(0)
+        _check(_lib.moe_sgemm_plan(self.handle, int(bool(nn)), int(M), int(N), int(K),
+                                   ctypes.byref(t), ctypes.byref(sp)))
+        return {"tile": t.value, "splits": sp.value}
 
     def w2_splits(self, desc: LayerDesc) -> int:
         """K splits layer_forward(desc) uses for w2 on this context's GPU."""

@@ -817,6 +817,24 @@ int moe_ctx_set_stream_k(moe_ctx* ctx, int mode) {
     });
 }
 
+int moe_sgemm_plan(moe_ctx* ctx, int nn, int64_t M, int64_t N, int64_t K, int32_t* tile,
+                   int32_t* splits) {
+    return guarded([&] {
+        check_ctx(ctx);
+        check_dims(M, "M");
+        check_dims(N, "N");
+        check_dims(K, "K");
+        check_ptr(tile, "tile");
+        check_ptr(splits, "splits");
+        DeviceScope dev(ctx->device);
+        // the direct-load condition of sgemm() for 16-byte aligned operands
+        const bool direct = K % 16 == 0 && (nn == 0 || N % 4 == 0);
+        const DensePlan plan = plan_dense(ctx, nn != 0, direct, M, N, K);
+        *tile = plan.tile;
+        *splits = plan.splits;
+    });
+}
+
 int moe_ctx_set_timing(moe_ctx* ctx, int enabled) {
     return guarded([&] {
         check_ctx(ctx);

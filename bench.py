@@ -626,6 +626,7 @@ def sgemm_sweep(args):
             first = False
             flops = 2.0 * M * N * K
             print(json.dumps({"workload": "sgemm", "layout": layout, "M": M, "N": N, "K": K,
+                              "plan": ctx.sgemm_plan(M, N, K, nn=layout == "nn"),
                               "ms_per_call": t * 1e3, "wall_ms": wall * 1e3,
                               "tflops": flops / t / 1e12,
                               "frac_fp32_mfma_peak": flops / t / 1e12 / FP32_MFMA_PEAK_TFLOPS,

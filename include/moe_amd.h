@@ -357,6 +357,14 @@ int moe_ctx_set_stream_k(moe_ctx* ctx, int mode);
  * measurement tools. */
 int moe_layer_w2_splits(moe_ctx* ctx, const moe_layer_desc* desc, int32_t* splits);
 
+/* ---- the plan moe_sgemm_nn (nn != 0) or moe_sgemm_nt runs an M x N x K
+ * product with on this context's device, assuming 16-byte aligned operands:
+ * the tile shape id (0 128x128, 1 64x128, 2 32x128, 3 256x128, 4 the skinny
+ * kernel, 5 the K-group tile) and its K splits.  No reference counterpart:
+ * an introspection query for tests and measurement tools. */
+int moe_sgemm_plan(moe_ctx* ctx, int nn, int64_t M, int64_t N, int64_t K, int32_t* tile,
+                   int32_t* splits);
+
 #ifdef __cplusplus
 }
 #endif

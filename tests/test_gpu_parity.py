@@ -149,6 +149,7 @@ def test_sgemm_k_groups(ctx, torch, orc, layout, m, n, k):
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     tiles = -(-m // 32) * -(-n // 128)
     assert 4 * tiles >= 3 * cus and tiles <= cus and k % 64 == 0 and 128 <= k // 4 <= 512
+    assert ctx.sgemm_plan(m, n, k, nn=layout == "nn") == {"tile": 5, "splits": 1}
     print(f"sgemm {layout} {m}x{n}x{k} (K groups)", flush=True)
     rng = np.random.default_rng(m * 3 + n * 5 + k)
     a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
