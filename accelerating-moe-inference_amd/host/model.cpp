@@ -244,6 +244,12 @@ void PhiTinyMoEModel::generate(const std::vector<std::vector<int>>& input_ids,
         // the chunk's event) overlaps chunk c + 1's product
         const std::size_t chunk = (batch + kLmChunks - 1) / kLmChunks;
         CopyStream& cs = *copy_;
+        // every copy enqueued below has ended when this call returns, also
+        // when a later launch throws (the copies write into `logits`)
+        struct Drain {
+            hipStream_t s;
+            ~Drain() { (void)hipStreamSynchronize(s); }
+        } drain{cs.stream};
         std::size_t c = 0;
         for (std::size_t r0 = 0; r0 < batch; r0 += chunk, ++c) {
             const std::size_t rc = std::min(chunk, batch - r0);
@@ -259,7 +265,7 @@ void PhiTinyMoEModel::generate(const std::vector<std::vector<int>>& input_ids,
                                   "hipMemcpyAsync logits");
         }
         CopyStream::check_hip(hipStreamSynchronize(cs.stream), "hipStreamSynchronize logits");
-        return;
+        return;  // (the drain finds the stream idle)
     }
     check(moe_sgemm_nt(ctx, last_n, lm_w_->as<float>(), lm_b, out, static_cast<int64_t>(batch),
                        static_cast<int64_t>(vocab_), static_cast<int64_t>(h), nullptr));
