@@ -5,6 +5,7 @@ Bar: routing indices, expert assignment, offsets, permutations and gate
 logits bit-exact; activations within REL_TOL = 1e-4 normwise relative error
 (helpers.REL_TOL); the combine is bit-exact given identical inputs.
 """
+import ctypes
 import json
 import os
 
@@ -859,6 +860,77 @@ def test_errors_are_reported(ctx, pkg, torch):
     with pytest.raises(pkg.MoeInvalidArgument):
         pkg._check(pkg.load_library().moe_gate_logits(
             ctx.handle, None, None, None, 4, 8, 2000, 1, None))
+
+
+def test_entry_points_reject_invalid_arguments(ctx, pkg, torch):
+    """Every stage's argument checks, through the C ABI on a live context:
+    null pointers at non-zero sizes, sizes out of range, unknown modes and a
+    misaligned output each return MOE_ERR_INVALID with a message, before any
+    launch; the context keeps working afterwards."""
+    L = pkg.load_library()
+    h = ctx.handle
+    f = torch.zeros(64, device="cuda")
+    i = torch.zeros(64, dtype=torch.int32, device="cuda")
+    P, Q = f.data_ptr(), i.data_ptr()
+    desc = pkg.make_desc(4, 8, 4, 2, 8, act=pkg.ACT_SWIGLU, router=0)
+    wts = pkg.LayerWeights(P, None, P, P, P, None, None)
+    bad_desc = pkg.make_desc(4, 8, 4, 2, 8, act=pkg.ACT_SWIGLU, router=0)
+    bad_desc.residual = 2
+    no_gate = pkg.LayerWeights(None, None, P, P, P, None, None)
+    tile, splits = ctypes.c_int32(), ctypes.c_int32()
+    cases = [
+        ("silu", lambda: L.moe_silu(h, None, None, 16, None), "null pointer: x"),
+        ("mul", lambda: L.moe_mul(h, P, P, P, -1, None), "n must be >= 0"),
+        ("gate E=0", lambda: L.moe_gate_logits(h, P, P, P, 4, 8, 0, 1, None), "E must be in"),
+        ("gate contract", lambda: L.moe_gate_logits(h, P, P, P, 4, 8, 4, 7, None), "contract"),
+        ("route k>E", lambda: L.moe_route(h, P, None, 4, 4, 5, 0, 1e-3, 2e-2, Q, P, None),
+         "k must be in"),
+        ("route T", lambda: L.moe_route(h, P, None, 1 << 31, 4, 2, 0, 1e-3, 2e-2, Q, P, None),
+         "T exceeds int32 range"),
+        ("route mode", lambda: L.moe_route(h, P, None, 4, 4, 2, 9, 1e-3, 2e-2, Q, P, None),
+         "router"),
+        ("permute", lambda: L.moe_permute(h, Q, 4, 2, 4, None, Q, Q, None),
+         "null pointer: expert_offsets"),
+        ("ffn act", lambda: L.moe_expert_ffn_grouped(h, P, Q, Q, P, P, P, 7, 4, 2, 8, 8, 4, P,
+                                                     P, None), "unknown act"),
+        ("ffn w3", lambda: L.moe_expert_ffn_grouped(h, P, Q, Q, P, None, P, pkg.ACT_SWIGLU, 4, 2,
+                                                    8, 8, 4, P, P, None), "null pointer: w3"),
+        ("combine k", lambda: L.moe_combine(h, P, Q, P, Q, None, P, 4, 0, 8, 1, None),
+         "k must be in"),
+        ("combine misaligned y", lambda: L.moe_combine(h, P, Q, P, Q, None, P + 4, 4, 2, 8, 1,
+                                                       None), "aligned"),
+        ("layer residual", lambda: L.moe_layer_forward(h, ctypes.byref(bad_desc),
+                                                       ctypes.byref(wts), P, P, None, None, None),
+         "residual must be 0 or 1"),
+        ("layer gate_w", lambda: L.moe_layer_forward(h, ctypes.byref(desc), ctypes.byref(no_gate),
+                                                     P, P, None, None, None),
+         "null pointer: gate_w"),
+        ("attention heads", lambda: L.moe_attention(h, P, P, P, P, 1, 4, 4, 3, 8, 0, None),
+         "heads"),
+        ("rope head_dim", lambda: L.moe_rope(h, P, P, P, 8, 1, 4, 0, 1, 1, 3, None),
+         "head_dim must be even"),
+        ("layer_norm h", lambda: L.moe_layer_norm(h, P, P, P, 1e-5, 4, 0, 1, P, None, None, None),
+         "h must be > 0"),
+        ("sgemm M", lambda: L.moe_sgemm_nt(h, P, P, None, P, -1, 4, 4, None), "M must be >= 0"),
+        ("sgemm N", lambda: L.moe_sgemm_nn(h, P, P, None, P, 4, 1 << 31, 4, None),
+         "N exceeds int32 range"),
+        ("stream-K mode", lambda: L.moe_ctx_set_stream_k(h, 2), "stream-K mode"),
+        ("plan", lambda: L.moe_sgemm_plan(h, 1, 4, 4, 4, None, ctypes.byref(splits)),
+         "null pointer: tile"),
+        ("embed", lambda: L.moe_embed(h, P, Q, -1, 8, 8, P, None), "n must be >= 0"),
+    ]
+    for name, call, msg in cases:
+        rc = call()
+        err = L.moe_last_error().decode()
+        assert rc == pkg.ERR_INVALID, (name, rc, err)
+        assert msg in err, (name, err)
+    torch.cuda.synchronize()
+    # the context still works
+    a = torch.arange(12, dtype=torch.float32, device="cuda").reshape(3, 4)
+    c = torch.empty((3, 3), device="cuda")
+    ctx.sgemm_nt(a, a, c)
+    assert torch.equal(c.cpu(), a.cpu() @ a.cpu().T)
+    assert L.moe_sgemm_plan(h, 1, 4, 4, 4, ctypes.byref(tile), ctypes.byref(splits)) == pkg.OK
 
 
 @pytest.mark.parametrize("router", [0, 1])
