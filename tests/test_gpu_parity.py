@@ -800,6 +800,45 @@ def test_layer_norm_block_vs_oracle(ctx, pkg, torch, orc, d, mode, contract, act
     assert_close(host(y), ry, what="norm block y")
 
 
+# The block at 9-16 experts (the reference's 16 and its workgroup-ring
+# gate): one 64-column stage (d = 64), a partial last stage (d = 200, 1028),
+# one token, a partial workgroup of tokens (T = 37), experts past E in the
+# 16-expert block (E = 9, 12).
+@pytest.mark.parametrize("T,d,E", [(1, 64, 16), (37, 200, 9), (1000, 1028, 12), (600, 4096, 16)])
+@pytest.mark.parametrize("rms,contract", [(False, 1), (False, 0), (True, 1), (True, 0)])
+def test_layer_norm_block_is_its_stages(ctx, pkg, torch, orc, T, d, E, rms, contract):
+    """The block y = x + MoE(norm(x)) in one moe_layer_forward is
+    bit-identical to its stages run apart: moe_layer_norm / moe_rms_norm,
+    then the layer without a norm on the normalised rows, then + x; routing
+    bit-exact against the oracle too."""
+    print(f"norm block stages T={T} d={d} E={E} rms={rms} contract={contract}", flush=True)
+    rng = np.random.default_rng(T + d + E + 7 * rms + 3 * contract)
+    k, d_ff = 2, 96
+    x = (0.5 + 2 * rng.normal(size=(T, d))).astype(np.float32)
+    gw = normal(rng, (E, d), 0.05)
+    w1 = normal(rng, (E, d_ff, d), 0.05)
+    w3 = normal(rng, (E, d_ff, d), 0.05)
+    w2 = normal(rng, (E, d, d_ff), 0.05)
+    nw = (1 + 0.1 * rng.normal(size=d)).astype(np.float32)
+    nb = (0.1 * rng.normal(size=d)).astype(np.float32)
+    dx, dgw, dw1, dw3, dw2, dnw, dnb = (dev(torch, a) for a in (x, gw, w1, w3, w2, nw, nb))
+    norm = pkg.NORM_RMS if rms else pkg.NORM_LAYER
+    y, idx, w = _norm_block(ctx, pkg, torch, dx, dgw, dw1, dw3, dw2, dnw, None if rms else dnb,
+                            k, pkg.ACT_SWIGLU, 0, contract, norm=norm)
+    xn = torch.empty_like(dx)
+    if rms:
+        ctx.rms_norm(dx, dnw, xn, 1e-5, contract)
+    else:
+        ctx.layer_norm(dx, dnw, dnb, xn, 1e-5, contract)
+    y0, idx0, w0 = _norm_block(ctx, pkg, torch, xn, dgw, dw1, dw3, dw2, None, None, k,
+                               pkg.ACT_SWIGLU, 0, contract, residual=False, norm=pkg.NORM_NONE)
+    assert torch.equal(idx, idx0) and torch.equal(w, w0)
+    assert torch.equal(y, y0 + dx), "the block differs from its stages"
+    _, ridx, _ = _norm_block_oracle(orc, x, gw, w1, w3, w2, nw, nb, k, 0, 0, contract,
+                                    residual=True, rms=rms)
+    assert np.array_equal(host(idx), ridx)
+
+
 def test_layer_norm_block_without_residual(ctx, pkg, torch, orc):
     rng = np.random.default_rng(77)
     T, d, E, k, d_ff = 130, 128, 4, 2, 96
