@@ -36,6 +36,7 @@ import importlib.util
 import json
 import math
 import os
+import shutil
 import sys
 import tempfile
 import time
@@ -175,13 +176,17 @@ def cpu_oracle():
         os.environ.setdefault("OMP_PROC_BIND", "close")
         sys.path.insert(0, ROOT)
         import oracle
+        tmp = tempfile.mkdtemp(prefix="moe_oracle_")
         try:
-            path = oracle.build_native(tempfile.mkdtemp(prefix="moe_oracle_"))
+            path = oracle.build_native(tmp)
             oracle.lib(path)
             build = "gcc -O3 -march=native -fopenmp -ffp-contract=off, built on this host"
         except Exception as e:  # no gcc on the host: the prebuilt x86-64-v3 library
             oracle.lib()
             build = f"prebuilt gcc -O3 -march=x86-64-v3 -fopenmp (native build failed: {e})"
+        finally:
+            # the loaded library stays mapped; its directory is not needed
+            shutil.rmtree(tmp, ignore_errors=True)
         oracle.set_threads(threads)
         _ORACLE = (oracle, build)
     return _ORACLE
