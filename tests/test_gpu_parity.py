@@ -376,14 +376,17 @@ def test_route_phi_hand_cases(ctx, torch, orc):
     assert host(idx).tolist() == [[1, 2], [0, 1], [1, 0], [0, 1], [1, 2], [0, 1]]
 
 
-# The layer routes, counts and scans in one launch (route_count: each block
-# routes its 256 tokens into LDS bitmasks, the last block to finish scans the
-# counts).  Its routing, and through the outputs its offsets and permutation,
-# against the oracle: one token, a partial block, exactly one block, a block
-# plus one token, and 274 blocks; 1 to 1024 experts (softmax groups of 1 to
-# 64 lanes, 4 to 256 tokens per round), k up to 32; the Zipf bias at E = 64.
-# Every case runs twice on the context: the second launch must find the
-# completion counter reset by the first.
+# The layer routes and counts in one launch (route_count: each workgroup
+# routes its tokens and adds its per-block expert counts into counters the
+# gate launch zeroed), then places the pairs with the scan of those counts
+# folded in (perm_place_scan; past kPlaceScanMax block counts, the separate
+# scan and placement).  Its routing, and through the outputs its offsets and
+# permutation, against the oracle: one token, a partial block, exactly one
+# block, a block plus one token, and 274 blocks; 1 to 1024 experts (softmax
+# groups of 1 to 64 lanes, 4 to 256 tokens per round), k up to 32; the Zipf
+# bias at E = 64.  Every case runs twice on the context: the second layer
+# must find the counters, which the first left filled in the reused
+# workspace, zeroed again by its own gate.
 @pytest.mark.parametrize("T,E,k,mode", [(1, 4, 2, 1), (255, 8, 2, 1), (256, 16, 2, 0),
                                         (257, 64, 8, 1), (70000, 64, 8, 1), (70000, 16, 2, 0),
                                         (3001, 1, 1, 1), (1000, 100, 3, 0), (900, 1024, 32, 1),
