@@ -19,27 +19,24 @@ void hip(hipError_t e, const char* what) {
         throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
 }
 
-struct CtxHolder {
-    moe_ctx* ctx = nullptr;
-    ~CtxHolder() {
-        if (ctx != nullptr) moe_ctx_destroy(ctx);
-    }
-};
-
 }  // namespace
 
+// The drop-in's one context, created on first use and never destroyed: a
+// destructor of a static would run during process exit, after the HIP
+// runtime's own statics may be gone, so hipFree / hipEventDestroy from there
+// could crash or hang.  Its workspace is released by the process's end.
 moe_ctx* context() {
-    static CtxHolder holder;
+    static moe_ctx* ctx = nullptr;
     static std::once_flag once;
     std::call_once(once, [] {
         const char* env = std::getenv("MOE_DEVICE");
         const int device = env != nullptr ? std::atoi(env) : 0;
         moe_ctx* c = nullptr;
         check(moe_ctx_create(device, &c));
-        holder.ctx = c;
+        ctx = c;
     });
-    if (holder.ctx == nullptr) throw std::runtime_error("moe context unavailable");
-    return holder.ctx;
+    if (ctx == nullptr) throw std::runtime_error("moe context unavailable");
+    return ctx;
 }
 
 void check(int status) {
