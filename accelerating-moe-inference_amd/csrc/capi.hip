@@ -365,16 +365,22 @@ int64_t expected_m_tiles(int64_t pairs, int64_t E, int bm) {
 // way and deals the K steps of the tiles left over to its G workgroups in
 // contiguous ranges, at the price of partial stores and a fix-up launch for
 // the cut tiles and of L2 sharing in the dealt part (its workgroups read
-// unrelated K offsets).  Measured on MI355X at configs 3-5 and the
+// unrelated K offsets).  Measured on MI355X at configs 1, 3-5 and the
 // reference's layer shape with 64 tokens to full size, it wins where the
 // one-tile fill is under 96 % and
-//   w1/w3 (no K splits there): K is at least 128 steps of 16 -- shorter
-//     tiles lose more to the dealt part's start-ups and L2 misses than the
-//     fill gains (config 5, K = 1024);
+//   w1/w3 (no K splits there): always -- also at short K (config 5's
+//     K = 64 steps: 128 / 256 / 512 / 2,048 tokens 0.133 / 0.134 / 0.248 /
+//     0.491 ms one tile per workgroup against 0.099 / 0.112 / 0.161 / 0.415
+//     stream-K; 1,024 tokens, fill 0.86, level; full size, fill 0.97, stays
+//     one tile per workgroup);
 //   w2 (against its best split plan, whose combine reads every split's
 //     partial rows): each workgroup's dealt range is at least 64 K steps.
-// Pieces are kept at 32 K steps or more: with fewer tiles than slots, G is
-// cut to tiles x K-steps / 32 (at least the tiles).  MOE_SK = 0 / 1 (or
+// Pieces are kept at 32 K steps or more (with fewer tiles than slots, G is
+// cut to tiles x K-steps / 32, at least the tiles), except for w1/w3 tiles
+// under 128 K steps, which are dealt to every slot: there the short pieces
+// measured faster (config 1's 64 tokens, 24 tiles of 32 K steps: 0.032 ms
+// on all slots, 0.061 ms cut to whole tiles, 0.041 ms one tile per
+// workgroup; config 5's 128 tokens 0.099 against 0.142 ms).  MOE_SK = 0 / 1 (or
 // moe_ctx_set_stream_k) forces either (1: on every launch the direct
 // buffer-load path applies to, on all slots).  Returns the stream-K grid, 0
 // for one tile per workgroup.
@@ -396,11 +402,11 @@ int choose_sk(moe_ctx* ctx, moe::GemmUse use, int64_t pairs, int64_t E, int64_t 
     const double w = tiles * S / dp_slots;
     if (w / std::ceil(w) >= 0.96) return 0;
     const bool w2 = use == moe::GemmUse::W2 || use == moe::GemmUse::W2Narrow;
-    if (!w2 && nk < 128) return 0;
     const double left = tiles - std::floor(tiles / slots) * slots;
     if (w2 && left * nk / slots < 64) return 0;
     double G = slots;
-    if (tiles < G) G = std::min(G, std::max(tiles, std::floor(tiles * nk / 32.0)));
+    if (tiles < G && (w2 || nk >= 128))
+        G = std::min(G, std::max(tiles, std::floor(tiles * nk / 32.0)));
     return static_cast<int>(G);
 }
 
