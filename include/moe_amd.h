@@ -329,9 +329,12 @@ int moe_layer_forward(moe_ctx* ctx, const moe_layer_desc* desc,
  * layer's workspace (logits, routing, permutation, hidden rows, w2 partials,
  * norm statistics, stream-K partial tiles) lives in a fixed 256 MiB array the
  * library holds on every GPU it runs on, until the process ends; a layer
- * needing more (beyond about 4,800 tokens at config 5's shape, 3,600 at the
- * reference's, 2,500 there behind its layer norm) is rejected with
- * MOE_ERR_INVALID.  The call allocates nothing and records no timing events.
+ * needing more is rejected with MOE_ERR_INVALID.  Every layer up to 4,160
+ * tokens at config 5's shape fits (3,840 behind its RMS norm), up to 3,680
+ * at the reference's (1,552 behind its layer norm); some larger ones fit as
+ * well, since the plan's K splits and stream-K grid change with the token
+ * count (moe_ctx_reserve on a fresh context, then moe_ctx_workspace_bytes,
+ * gives a layer's need).  The call allocates nothing and records no timing events.
  * Every call on one GPU shares that GPU's array, which keeps the last call's
  * contents: calls that overlap on one GPU (two streams, two threads, two
  * contexts) race and must be serialised by the caller.  Same arguments,
