@@ -1478,11 +1478,45 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_sk_fixup_kernel(const Gemm
     // workgroup w - 1 holds the tile's first piece: in its start slot when
     // its range begins at the tile's start, else in its end slot
     add_slot(2 * int64_t(w - 1) + (prev == t0 ? 0 : 1), true);
-    for (int u = w; u < G; ++u) {
-        const int bu = sk_begin(s, u);
-        if (bu >= t1) break;
-        if (sk_begin(s, u + 1) == bu) continue;  // an empty range
-        add_slot(2 * int64_t(u), false);
+    // The later pieces (the start slots of workgroups w, w + 1, ... while
+    // their ranges begin inside the tile), up to 4 at a time: every load of
+    // a batch is issued before its adds, which keep the K order, so a tile
+    // cut into many short pieces costs one memory round trip per 4 pieces,
+    // not per piece.
+    constexpr int PB = 4;
+    bool more = true;
+    for (int u = w; more;) {
+        int64_t slot[PB];
+        int n = 0;
+        while (n < PB) {
+            if (u >= G) { more = false; break; }
+            const int bu = sk_begin(s, u);
+            if (bu >= t1) { more = false; break; }
+            if (sk_begin(s, u + 1) != bu) slot[n++] = 2 * int64_t(u);  // skip empty ranges
+            ++u;
+        }
+        f32x4 v[PB][NB * 4];
+#pragma unroll
+        for (int i = 0; i < PB; ++i) {
+            if (i >= n) break;
+            const f32x4* src = reinterpret_cast<const f32x4*>(p.sk_part + slot[i] * SLOT);
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4)
+                    v[i][nb * 4 + r4] = src[sk_part_index<C, NB>(nb, bi, bj, r4, tid)];
+        }
+#pragma unroll
+        for (int i = 0; i < PB; ++i) {
+            if (i >= n) break;
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        acc[nb][4 * r4 + j] = acc[nb][4 * r4 + j] + v[i][nb * 4 + r4][j];
+        }
     }
     int mt, nt;
     tile_of(t, s.m_tiles, p.n_tiles, s.group, mt, nt);
