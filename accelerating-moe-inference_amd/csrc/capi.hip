@@ -1058,7 +1058,8 @@ int moe_attention(moe_ctx* ctx, const float* q, const float* k, const float* v, 
         // head_dim 64 / 128: one fused pass, any seq_len, no workspace
         // (MOE_ATTN_FLASH=0 keeps the three-launch path, for comparison)
         static const int flash = env_int("MOE_ATTN_FLASH", 1);
-        if (flash != 0 && aligned && (head_dim == 64 || head_dim == 128)) {
+        if (flash != 0 && aligned && (head_dim == 64 || head_dim == 128) &&
+            seq_len <= INT32_MAX) {
             ctx->launch("attn_flash", s, [&] {
                 moe::launch_flash_attention(q, k, v, out, batch, seq_len, q_heads, kv_heads,
                                             head_dim, w, s);
