@@ -37,12 +37,12 @@ constexpr int kQTile = 128;  // queries per workgroup (4 waves x 32)
 constexpr int kKBlock = 32;  // keys per block
 
 template <int HD>
-__global__ __launch_bounds__(256) void flash_attn_kernel(const float* __restrict__ q,
-                                                         const float* __restrict__ k,
-                                                         const float* __restrict__ v,
-                                                         float* __restrict__ out, int64_t S,
-                                                         int64_t H, int64_t KVH, int64_t window,
-                                                         float scale) {
+// at least two waves per SIMD: at most 256 registers a lane, which keeps
+// head_dim 128 at two waves (it took 289 and one wave) and keeps the
+// accumulators in VGPRs, where the rescale needs no AGPR moves
+__global__ __launch_bounds__(256, 2) void flash_attn_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    float* __restrict__ out, int64_t S, int64_t H, int64_t KVH, int64_t window, float scale) {
     static_assert(HD % 32 == 0 && HD <= 128, "head_dim 32, 64, 96 or 128");
     constexpr int LD = HD + 8;      // LDS row stride: the lane halves land 32 banks apart
     constexpr int QK = HD / 2;      // MFMA steps of the score product (2 dims each)
@@ -52,7 +52,8 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(const float* __restrict
     __shared__ __align__(16) float Ks[2][kKBlock * LD];
     __shared__ __align__(16) float Vs[2][kKBlock * LD];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches
     const int lq = lane & 31, half = lane >> 5;
     // Causal work grows with the tile index (tile t walks 4t + 4 key blocks).
     // Workgroups half a grid apart share a CU when the grid fills two per CU
