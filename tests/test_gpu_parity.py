@@ -65,12 +65,13 @@ def host(t):
 # Up to 32 rows with K % 16 == 0 the skinny kernel runs: (1, 1000, 256) one
 # row, (17, 200, 512) a second 16-row block 1 row deep and a last column block
 # past N, (32, 132, 1024) two full row blocks with K splits, (9, 4, 64) one
-# 4-column output.
+# 4-column output; (5, 300, 48) and (20, 600, 1040) have K an odd multiple
+# of 16, which admits no split.
 SGEMM_SHAPES = [(1, 1, 1), (7, 5, 33), (129, 130, 17), (128, 128, 128),
                 (256, 384, 512), (33, 200, 1000), (300, 64, 4), (5, 700, 2),
                 (40, 384, 4096), (100, 300, 512), (64, 1408, 2048), (200, 520, 64),
                 (33, 250, 512), (64, 130, 256), (1, 1000, 256), (17, 200, 512),
-                (32, 132, 1024), (9, 4, 64)]
+                (32, 132, 1024), (9, 4, 64), (5, 300, 48), (20, 600, 1040)]
 
 
 @pytest.mark.parametrize("m,n,k", SGEMM_SHAPES)
@@ -239,6 +240,11 @@ def test_sgemm_skinny_config2_row_sample(ctx, torch, orc, m):
     c2 = torch.empty_like(c)
     ctx.sgemm_nn(a, b, c2)
     assert torch.equal(c, c2)
+    # the same product with B stored [N, K]
+    bt = b.t().contiguous()
+    del b
+    ctx.sgemm_nt(a, bt, c2)
+    assert_close(host(c2)[rows], ref, what=f"skinny nt {m}")
 
 
 def test_sgemm_operands_past_2gib(ctx, torch, orc):
