@@ -36,10 +36,10 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int kQTile = 128;  // queries per workgroup (4 waves x 32)
 constexpr int kKBlock = 32;  // keys per block
 
-template <int HD>
-// at least two waves per SIMD: at most 256 registers a lane, which keeps
+// At least two waves per SIMD: at most 256 registers a lane, which keeps
 // head_dim 128 at two waves (it took 289 and one wave) and keeps the
-// accumulators in VGPRs, where the rescale needs no AGPR moves
+// accumulators in VGPRs, where the rescale needs no AGPR moves.
+template <int HD>
 __global__ __launch_bounds__(256, 2) void flash_attn_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     float* __restrict__ out, int64_t S, int64_t H, int64_t KVH, int64_t window, float scale) {
