@@ -8,13 +8,21 @@ and ragged expert loads that the hand-picked cases leave out.
 
 Bar: routing indices bit-exact, PHI weights bit-exact and softmax weights
 within 1 ulp; activations within REL_TOL normwise relative error.
+
+MOE_RANDOM_CASES (default 48) sets how many cases each test draws and
+MOE_RANDOM_SEED (default 0) shifts the seeds, for a wider sweep by hand.
 """
+import os
+
 import numpy as np
 import pytest
 
 from helpers import assert_close, load_pkg, normal
 
 pytestmark = pytest.mark.gpu
+
+N_CASES = int(os.environ.get("MOE_RANDOM_CASES", "48"))
+SEED = int(os.environ.get("MOE_RANDOM_SEED", "0"))
 
 
 @pytest.fixture(scope="module")
@@ -44,8 +52,8 @@ def host(t):
     return t.detach().cpu().numpy()
 
 
-def _sgemm_cases(n=48, seed=2024):
-    rng = np.random.default_rng(seed)
+def _sgemm_cases(n=N_CASES, seed=2024):
+    rng = np.random.default_rng(seed + SEED)
     cases = []
     for i in range(n):
         M = int(rng.integers(1, 700))
@@ -81,8 +89,8 @@ def test_sgemm_random_shapes(ctx, torch, orc, layout, M, N, K, with_bias):
         assert_close(host(c), ref, what=f"{layout} {M}x{N}x{K}")
 
 
-def _layer_cases(n=48, seed=77):
-    rng = np.random.default_rng(seed)
+def _layer_cases(n=N_CASES, seed=77):
+    rng = np.random.default_rng(seed + SEED)
     cases = []
     while len(cases) < n:
         T = int(rng.integers(1, 900))
@@ -128,3 +136,35 @@ def test_layer_random_shapes(ctx, pkg, torch, orc, T, d, E, k, d_ff, act, router
         assert_close(host(y), ry, what="layer y")
     finally:
         ctx.set_stream_k(-1)
+
+
+def _attention_cases(n=N_CASES // 2, seed=31):
+    rng = np.random.default_rng(seed + SEED)
+    cases = []
+    while len(cases) < n:
+        hd = int(rng.choice([64, 128, 64, 128, 16 * int(rng.integers(1, 9))]))
+        fused = hd in (64, 128)
+        S = int(rng.integers(1, 700)) if fused else 16 * int(rng.integers(1, 40))
+        B = int(rng.integers(1, 5))
+        KVH = int(rng.integers(1, 5))
+        H = KVH * int(rng.integers(1, 5))
+        window = int(rng.integers(1, S + 1)) if rng.random() < 0.4 else 0
+        if B * H * S * S * hd > 2e8:             # keeps the oracle's share to seconds
+            continue
+        cases.append((B, S, H, KVH, hd, window))
+    return cases
+
+
+@pytest.mark.parametrize("B,S,H,KVH,hd,window", _attention_cases())
+def test_attention_random_shapes(ctx, torch, orc, B, S, H, KVH, hd, window):
+    """Causal attention (the fused kernel at head_dim 64 and 128, the batched
+    GEMMs otherwise) on random batch, length, head and window shapes."""
+    print(f"attention B={B} S={S} H={H} KVH={KVH} hd={hd} window={window}", flush=True)
+    rng = np.random.default_rng(B * 1009 + S * 13 + H * 7 + KVH + hd + window)
+    q = normal(rng, (B * S, H * hd))
+    k = normal(rng, (B * S, KVH * hd))
+    v = normal(rng, (B * S, KVH * hd))
+    out = torch.full((B * S, H * hd), float("nan"), device="cuda")
+    ctx.attention(dev(torch, q), dev(torch, k), dev(torch, v), out, B, S, H, KVH, hd, window)
+    ref = orc.attention(q, k, v, B, S, H, KVH, hd, window or None)
+    assert_close(host(out), ref, what="attention")
