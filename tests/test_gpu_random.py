@@ -1,16 +1,18 @@
 """GPU parity on seeded random shapes: the dense SGEMM (NN and NT, with and
-without bias) and the whole MoE layer (both routers, both activations, both
-contraction modes, the planner's tile dealing and both forced ones), each
-against the CPU oracle.  The shapes are drawn once from fixed seeds, so every
+without bias), the whole MoE layer (both routers, both activations, both
+contraction modes, the planner's tile dealing and both forced ones), causal
+attention and the two norms, each against the CPU oracle.  The shapes are drawn once from fixed seeds, so every
 run checks the same cases; they reach the planner's tile shapes and K splits,
 the skinny kernel, the register-staged fallback (K % 16 != 0, unaligned rows)
 and ragged expert loads that the hand-picked cases leave out.
 
 Bar: routing indices bit-exact, PHI weights bit-exact and softmax weights
-within 1 ulp; activations within REL_TOL normwise relative error.
+within 1 ulp, norms bit-exact; activations and attention within REL_TOL
+normwise relative error.
 
-MOE_RANDOM_CASES (default 48) sets how many cases each test draws and
-MOE_RANDOM_SEED (default 0) shifts the seeds, for a wider sweep by hand.
+MOE_RANDOM_CASES (default 48) sets how many cases each test draws (the
+attention and norm tests half as many) and MOE_RANDOM_SEED (default 0)
+shifts the seeds, for a wider sweep by hand.
 """
 import os
 
@@ -168,3 +170,40 @@ def test_attention_random_shapes(ctx, torch, orc, B, S, H, KVH, hd, window):
     ctx.attention(dev(torch, q), dev(torch, k), dev(torch, v), out, B, S, H, KVH, hd, window)
     ref = orc.attention(q, k, v, B, S, H, KVH, hd, window or None)
     assert_close(host(out), ref, what="attention")
+
+
+def _norm_cases(n=N_CASES // 2, seed=53):
+    rng = np.random.default_rng(seed + SEED)
+    cases = []
+    for i in range(n):
+        rows = int(rng.integers(1, 3000))
+        h = int(rng.integers(1, 6000))
+        if i % 2 == 0:
+            h = 4 * max(1, h // 4)               # 16-byte rows: the LDS and ring kernels
+        if rows * h > 6_000_000:
+            rows = max(1, 6_000_000 // h)
+        cases.append((rows, h, bool(i % 3 == 0), i % 2))
+    return cases
+
+
+@pytest.mark.parametrize("rows,h,rms,contract", _norm_cases())
+def test_norm_random_shapes(ctx, torch, orc, rows, h, rms, contract):
+    """Layer norm and RMS norm on random row counts and widths (rows in LDS,
+    the ring kernel, the register-staged pair), bit for bit."""
+    print(f"{'rms' if rms else 'layer'}_norm {rows}x{h} contract={contract}", flush=True)
+    rng = np.random.default_rng(rows * 5 + h * 3 + contract)
+    x = (1 + 3 * rng.normal(size=(rows, h))).astype(np.float32)
+    w = rng.normal(size=h).astype(np.float32)
+    y = torch.empty((rows, h), device="cuda")
+    inv = torch.empty(rows, device="cuda")
+    if rms:
+        ry, ri = orc.rms_norm(x, w, 1e-5, contract)
+        ctx.rms_norm(dev(torch, x), dev(torch, w), y, 1e-5, contract, inv)
+    else:
+        b = rng.normal(size=h).astype(np.float32)
+        ry, rm, ri = orc.layer_norm(x, w, b, 1e-5, contract)
+        mean = torch.empty(rows, device="cuda")
+        ctx.layer_norm(dev(torch, x), dev(torch, w), dev(torch, b), y, 1e-5, contract, mean, inv)
+        assert np.array_equal(host(mean), rm), "mean"
+    assert np.array_equal(host(inv), ri), "inv"
+    assert np.array_equal(host(y), ry), "y"
