@@ -1,8 +1,8 @@
 """moe_layer_forward_noalloc (the layer on the library's fixed per-GPU
 scratch, allocating nothing) against moe_layer_forward on the same inputs:
 two calls in a row, the second with fewer tokens, each identical bit for bit
-to the allocating entry point (the same kernels run on the same inputs).
-The no-alloc calls come first on a fresh context and must leave its
+to the allocating entry point (the same kernels run on the same inputs),
+on three chosen layers and 24 seeded random ones.  The no-alloc calls come first on a fresh context and must leave its
 workspace at 0 bytes; one is captured in a HIP graph and replayed, with
 other no-alloc calls between the replays, each replay matching the eager
 call; and a layer too large for the scratch is rejected before any GPU
@@ -78,6 +78,57 @@ def test_noalloc_matches_layer_forward(torch, d, E, k, d_ff, router, norm, resid
             assert torch.equal(w0, w1), f"T={T}: routing weights"
             assert torch.equal(y0, y1), f"T={T}: layer output"
             assert bool(torch.isfinite(y1).all())
+    finally:
+        ctx.close()
+
+
+def _random_cases(n=24, seed=404):
+    rng = np.random.default_rng(seed)
+    cases = []
+    for _ in range(n):
+        d = int(rng.choice([int(rng.integers(1, 130)), 16 * int(rng.integers(1, 33))]))
+        E = int(rng.integers(1, 80))
+        k = int(rng.integers(1, min(E, 8) + 1))
+        d_ff = int(rng.choice([int(rng.integers(1, 300)), 64 * int(rng.integers(1, 11))]))
+        T1 = int(rng.integers(2, 1200))
+        T2 = int(rng.integers(1, T1))
+        cases.append((d, E, k, d_ff, int(rng.integers(0, 2)), int(rng.integers(0, 2)),
+                      int(rng.integers(0, 3)), bool(rng.integers(0, 2)), T1, T2))
+    return cases
+
+
+# seeded random layers (odd widths, both activations and routers, no norm /
+# layer norm / RMS norm, with and without the residual), each two no-alloc
+# calls in a row against the allocating entry point, bit for bit
+@pytest.mark.parametrize("d,E,k,d_ff,act,router,norm,residual,T1,T2", _random_cases())
+def test_noalloc_random_shapes(torch, d, E, k, d_ff, act, router, norm, residual, T1, T2):
+    pkg = load_pkg()
+    print(f"noalloc random d={d} E={E} k={k} d_ff={d_ff} act={act} router={router} "
+          f"norm={norm} residual={residual} T={T1} then {T2}", flush=True)
+    rng = np.random.default_rng(d * 31 + E * 7 + T1)
+    W = _weights(torch, rng, d, E, d_ff, norm != 0)
+    if act != pkg.ACT_SWIGLU:
+        W["w3"] = None
+    x_all = _dev(torch, normal(rng, (T1, d)))
+    norm_kind = [pkg.NORM_NONE, pkg.NORM_LAYER, pkg.NORM_RMS][norm]
+    ctx = pkg.Context(0)
+    try:
+        for T in (T1, T2):
+            desc = pkg.make_desc(T, d, E, k, d_ff, act=act, router=router, norm=norm_kind,
+                                 residual=residual)
+            x = x_all[:T].contiguous()
+            outs = []
+            for noalloc in (True, False):
+                y = torch.full((T, d), float("nan"), device="cuda")
+                idx = torch.full((T, k), -1, dtype=torch.int32, device="cuda")
+                w = torch.full((T, k), float("nan"), device="cuda")
+                ctx.layer_forward(desc, W, x, y, idx, w, noalloc=noalloc)
+                outs.append((y, idx, w))
+            torch.cuda.synchronize()
+            (y1, i1, w1), (y0, i0, w0) = outs
+            assert torch.equal(i0, i1), f"T={T}: routing"
+            assert torch.equal(w0, w1), f"T={T}: routing weights"
+            assert torch.equal(y0, y1), f"T={T}: layer output"
     finally:
         ctx.close()
 
