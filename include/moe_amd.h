@@ -138,7 +138,8 @@ int moe_ctx_workspace_bytes(moe_ctx* ctx, int64_t* bytes);
  * src/model.cu:1584-1622): when on, every launch is bracketed by HIP events
  * on its stream.  moe_ctx_kernel_times() synchronises, then returns the
  * number of named kernels and fills up to `cap` entries of names / total
- * milliseconds / launch counts accumulated since the last reset. */
+ * milliseconds / launch counts accumulated since the last reset (on an error
+ * it returns minus the MOE_ERR_* status). */
 int moe_ctx_set_timing(moe_ctx* ctx, int enabled);
 int moe_ctx_kernel_times(moe_ctx* ctx, const char** names, double* total_ms,
                          int64_t* launches, int cap);

@@ -72,3 +72,35 @@ def test_rope_table_is_the_oracles_libm_table(lib_path, orc):
     t = np.empty(4, np.float32)
     assert lib.moe_rope_table(10000.0, 3, 1, t.ctypes.data_as(ctypes.c_void_p)) == \
         load_pkg().ERR_INVALID
+
+
+def test_every_entry_point_rejects_a_null_context(lib_path):
+    # each call taking a context checks it before any device work, so a null
+    # one is an invalid-argument error (with the reason) even without a GPU
+    import ctypes as ct
+    pkg = load_pkg()
+    lib = pkg.load_library()
+    skip = {"moe_ctx_create", "moe_rope_table", "moe_last_error", "moe_version"}
+    checked = []
+    for name in header_functions():
+        if name in skip:
+            continue
+        fn = getattr(lib, name)
+        args = []
+        for t in fn.argtypes:
+            if t in (ct.c_float, ct.c_double):
+                args.append(0.0)
+            elif t in (ct.c_int, ct.c_int32, ct.c_int64, ct.c_uint, ct.c_uint32, ct.c_uint64):
+                args.append(1)
+            else:
+                args.append(None)
+        rc = fn(*args)
+        if name == "moe_ctx_destroy":
+            assert rc in (pkg.OK, pkg.ERR_INVALID), name
+            continue
+        if name == "moe_ctx_kernel_times":  # a count, or minus the status
+            rc = -rc
+        assert rc == pkg.ERR_INVALID, f"{name} returned {rc}"
+        assert lib.moe_last_error().decode(), name
+        checked.append(name)
+    assert len(checked) >= 30
