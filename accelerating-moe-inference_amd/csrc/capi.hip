@@ -332,6 +332,8 @@ struct FfnPlan {
     int splits = 1;    // K splits of w2 (1 under stream-K)
     int w2_sk = 0;     // stream-K grid of w2
     int64_t sk_floats = 0;  // partial-tile floats the stream-K launches need
+    bool skinny13 = false;  // w1/w3 on the grouped skinny kernel (choose_skinny)
+    bool skinny2 = false;   // w2 on it
 };
 
 // The K splits of w2 on one w2 tile and their modelled time (choose_w2_split_plan).
@@ -423,6 +425,58 @@ int choose_sk(moe_ctx* ctx, moe::GemmUse use, int64_t pairs, int64_t E, int64_t 
 // 0.522 ms; 15,583 rows equal, wide kept).  MOE_W2_TILE = 0 / 1 overrides.
 // Then stream-K where the one-tile rounds fill badly (choose_sk), else K
 // splits for w2.
+// Few rows per expert (at most 32 on average): a launch whose waves would
+// each run a short K loop goes to the grouped skinny kernel, whose
+// workgroups stream one expert's 16 or 32 rows against 64 columns of its
+// weights, four waves to a quarter of K, instead of 128-row tiles that are
+// mostly empty.  A wave's work is its K steps (K / 64, over S for w2's K
+// splits) times its 16-row blocks times the B operands (2 assumed: w1 and
+// w3).  Measured on MI355X, ms per launch, tiles -> skinny (units):
+//   w1/w3: config 1 (64 tokens) 0.029 -> 0.014 (32); config 5 at 64 tokens
+//     0.083 -> 0.069 (32), its decoder's last rows (16 pairs) about 0.075
+//     -> 0.04 (32); config 5 at 128 tokens 0.101 -> 0.107 (64); the
+//     reference's at 64 tokens 0.117 -> 0.167 (128): up to 32 units.
+//   w2: config 1 0.024 -> 0.014 (8, d 512); the reference's at 64 tokens
+//     0.044 -> 0.034 (7, 8 rows per expert); but at 128 tokens 0.044 ->
+//     0.045 (7, 16 rows per expert, d 4096: 64 column blocks of short
+//     workgroups), at 256 0.063 -> 0.064 (14) and config 5 at 64 tokens
+//     0.037 -> 0.051 (22): up to 12 units, and only with at most 8 rows
+//     per expert or d up to 1024.
+// w2 takes the K splits S that keep about two workgroups per CU, each wave
+// at least 4 K steps.  A context or process that forces the tiles' dealing
+// (moe_ctx_set_stream_k, MOE_SK) keeps the tiles; MOE_FFN_SKINNY = 0 / 1
+// turns the skinny kernel off / on for every launch the shape allows.
+void choose_skinny(moe_ctx* ctx, FfnPlan& f, int64_t pairs, int64_t d, int64_t d_ff, int64_t E) {
+    static const int env_skinny = env_int("MOE_FFN_SKINNY", -1);
+    static const int env_sk = env_int("MOE_SK", -1);
+    const bool sk_forced = (ctx->sk_mode >= 0 ? ctx->sk_mode : env_sk) >= 0;
+    const int64_t rows_wg = pairs <= 16 * E ? 16 : 32;
+    const int64_t rb_max = moe::ceil_div(pairs, rows_wg);
+    if (env_skinny == 0 || sk_forced || d % 16 != 0 || d_ff % 16 != 0 || E * rb_max > 65535 ||
+        (env_skinny != 1 && pairs > 32 * E))
+        return;
+    const int64_t blocks16 = rows_wg / 16;
+    if (env_skinny == 1 || (d / 64) * blocks16 * 2 <= 32) {
+        f.skinny13 = true;
+        f.w13_tile = moe::kGroupedSkinnyTile;
+        f.w13_sk = 0;
+    }
+    // expected row blocks: the pairs' blocks plus a partial one per expert
+    const double blocks = std::min(double(E) * double(rb_max),
+                                   double(pairs) / double(rows_wg) + 0.5 * double(E));
+    const double wgs = blocks * double(moe::ceil_div(d, 64));
+    int S = 1;
+    for (int s2 = 2; s2 <= moe::kMaxW2Splits; s2 *= 2)
+        if (d_ff % (16 * s2) == 0 && d_ff / (64 * s2) >= 4 && wgs * s2 <= 2.0 * ctx->cus) S = s2;
+    if (env_skinny == 1 ||
+        ((d_ff / (64 * S)) * blocks16 <= 12 && (pairs <= 8 * E || d <= 1024))) {
+        f.skinny2 = true;
+        f.tile = moe::kGroupedSkinnyTile;
+        f.w2_sk = 0;
+        f.splits = S;
+    }
+}
+
 FfnPlan choose_ffn_plan(moe_ctx* ctx, int64_t pairs, int64_t d, int64_t d_ff, int64_t E) {
     FfnPlan f;
     static const int env_tile = env_int("MOE_W2_TILE", -1);
@@ -458,6 +512,7 @@ FfnPlan choose_ffn_plan(moe_ctx* ctx, int64_t pairs, int64_t d, int64_t d_ff, in
     }
     f.splits = f.w2_sk > 0 ? 1 : w2.splits;
     const moe::GemmUse u2 = use_of(f.tile);
+    choose_skinny(ctx, f, pairs, d, d_ff, E);
     if (f.w13_sk > 0) f.sk_floats = moe::gemm_sk_part_floats(u13, f.w13_sk);
     if (f.w2_sk > 0) f.sk_floats = std::max(f.sk_floats, moe::gemm_sk_part_floats(u2, f.w2_sk));
     return f;
@@ -543,6 +598,7 @@ void expert_ffn(moe_ctx* ctx, const float* x, const int32_t* perm,
             a.sk_part = sk_part;
         }
         const bool vec = d % 4 == 0 && aligned16(x) && aligned16(w1) && (!swiglu || aligned16(w3));
+        if (f.skinny13 && !vec) a.tile = 0;  // unaligned rows: one 128x128 tile per workgroup
         ctx->launch(swiglu ? "expert_w13_swiglu" : "expert_w1_silu", s, [&] {
             moe::launch_gemm(a, false, true, swiglu ? moe::EPI_SWIGLU : moe::EPI_SILU, vec, s);
         });
@@ -578,6 +634,7 @@ void expert_ffn(moe_ctx* ctx, const float* x, const int32_t* perm,
     moe::require(int64_t(b.m_tiles) * b.n_tiles * std::max(f.splits, 1) <= INT32_MAX,
                  "w2 grid too large");
     const bool vec = d_ff % 4 == 0 && aligned16(h) && aligned16(w2);
+    if (f.skinny2 && !vec) b.tile = 0;  // unaligned rows: the wide tile, the same K splits
     ctx->launch("expert_w2", s, [&] { moe::launch_gemm(b, false, true, moe::EPI_STORE, vec, s); });
 }
 

@@ -79,6 +79,9 @@ int dense_blocks_per_cu(int tile, bool nn);
 // K groups of a dense tile shape (1, or the K-group tiles' count).
 int dense_tile_groups(int tile);
 constexpr int kMaxDenseSplits = 16;  // split-K of a dense SGEMM (partials in the workspace)
+// GemmArgs::tile of the grouped (expert) launches for layers whose experts
+// hold few rows each: the grouped skinny kernel, w1/w3 and w2 alike.
+constexpr int kGroupedSkinnyTile = 2;
 
 // Routing constants.
 constexpr int kPermTokens = 256;    // tokens per permutation block

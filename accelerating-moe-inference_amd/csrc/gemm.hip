@@ -1670,6 +1670,160 @@ void launch_skinny(const GemmArgs& a, hipStream_t s) {
     else hipLaunchKernelGGL((gemm_skinny_kernel<NN, 4, EPI_BIAS>), grid, dim3(256), 0, s, a);
 }
 
+// ---------------------------------------------------------------------------
+// Grouped skinny expert GEMM (NT, w1/w3 or w2) for layers whose experts hold
+// few rows each -- a batch of 64 tokens over 4 experts, a decoder's last rows
+// -- where the tiled kernels' 128-row tiles are mostly empty and the run is a
+// few K steps of load latency per tile.  A workgroup owns one expert's block
+// of 16 * MB packed rows and 64 columns; its four waves take four consecutive
+// quarters of the K range (grid.z: the w2 K splits, each its own partial
+// rows) and stream A and B straight into registers as the skinny dense
+// kernel does (v_mfma_f32_16x16x4_f32, the same lane layout), then meet in
+// LDS: every output is the waves' partials added in wave order, then the
+// epilogue.  grid.y = E * rb, rb the row blocks of the largest expert the
+// launch allows for (rows_limit / (16 * MB), rounded up); blocks past an
+// expert's rows exit at once.  Requires K % 16 == 0 per split and 16-byte
+// aligned rows.
+template <int MB, int NBO, int EPI>
+__global__ __launch_bounds__(256) void gemm_skinny_grouped_kernel(const GemmArgs p, int rb) {
+    constexpr int PF = NBO == 2 ? 2 : 3;  // chunks in flight besides the one computed
+    constexpr int RW = 16 * MB;           // rows of the workgroup
+    constexpr int LDR = 65;               // LDS row stride of a partial (64 columns + 1)
+    __shared__ float red[4][NBO][RW * LDR];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int j = lane & 15, g = lane >> 4;
+    const int e = static_cast<int>(blockIdx.y) / rb, b = static_cast<int>(blockIdx.y) % rb;
+    const int64_t end = p.offsets[e + 1];
+    const int64_t row0 = p.offsets[e] + static_cast<int64_t>(b) * RW;
+    if (row0 >= end) return;  // the whole workgroup (no barrier reached yet)
+    const int64_t N = p.N, n0 = static_cast<int64_t>(blockIdx.x) * 64;
+    const int split = blockIdx.z;
+    const int64_t kbeg = split * p.k_split_len;
+    const int64_t kend = p.K - kbeg < p.k_split_len ? p.K : kbeg + p.k_split_len;
+    const int64_t nch = (kend - kbeg) / 16;
+    const int64_t c0 = nch * wave / 4, c1 = nch * (wave + 1) / 4;  // this wave's chunks
+
+    const float* arow[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+        int64_t r = row0 + 16 * mb + j;
+        r = r < end ? r : end - 1;
+        int64_t t = r;
+        if (p.gather != nullptr) {  // a token row of A, clamped to the rows it has
+            t = p.gather[r];
+            t = t < 0 ? 0 : (t >= p.gather_rows ? p.gather_rows - 1 : t);
+        }
+        arow[mb] = p.A + t * p.lda + 4 * g;
+    }
+    const float* bptr[NBO][4];
+#pragma unroll
+    for (int o = 0; o < NBO; ++o)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            int64_t n = n0 + 16 * q + j;
+            n = n < N ? n : N - 1;
+            bptr[o][q] = (o == 0 ? p.B0 : p.B1) + e * p.b_expert_stride + n * p.ldb + 4 * g;
+        }
+    struct Chunk {
+        f32x4s a[MB], b[NBO][4];
+    };
+    auto load = [&](Chunk& c, int64_t k0) {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) c.a[mb] = *reinterpret_cast<const f32x4s*>(arow[mb] + k0);
+#pragma unroll
+        for (int o = 0; o < NBO; ++o)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                c.b[o][q] = *reinterpret_cast<const f32x4s*>(bptr[o][q] + k0);
+    };
+    f32x4s acc[NBO][MB][4];
+#pragma unroll
+    for (int o = 0; o < NBO; ++o)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[o][mb][c] = f32x4s{0.f, 0.f, 0.f, 0.f};
+    auto compute = [&](const Chunk& c) {
+#pragma unroll
+        for (int st = 0; st < 4; ++st)
+#pragma unroll
+            for (int o = 0; o < NBO; ++o)
+#pragma unroll
+                for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+                    for (int mb = 0; mb < MB; ++mb)
+                        acc[o][mb][cb] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                            c.a[mb][st], c.b[o][cb][st], acc[o][mb][cb], 0, 0, 0);
+    };
+    const int64_t n_my = c1 - c0;
+    Chunk ring[PF + 1];
+#pragma unroll
+    for (int u = 0; u < PF; ++u)
+        if (u < n_my) load(ring[u], kbeg + 16 * (c0 + u));
+    for (int64_t i0 = 0; i0 < n_my; i0 += PF + 1) {
+#pragma unroll
+        for (int u = 0; u <= PF; ++u) {
+            const int64_t ci = i0 + u;
+            if (ci < n_my) {
+                if (ci + PF < n_my) load(ring[(u + PF) % (PF + 1)], kbeg + 16 * (c0 + ci + PF));
+                compute(ring[u]);
+            }
+        }
+    }
+
+    // partials to LDS: lane (j, g), register i of block (mb, cb) is row
+    // 16 mb + 4 g + i, column 16 cb + j
+#pragma unroll
+    for (int o = 0; o < NBO; ++o)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    red[wave][o][(16 * mb + 4 * g + i) * LDR + 16 * cb + j] = acc[o][mb][cb][i];
+    __syncthreads();
+    // every output: the four waves' partials in wave order, then the epilogue
+    float* Cb = p.C;
+    for (int idx = threadIdx.x; idx < RW * 64; idx += 256) {
+        const int r = idx >> 6, c = idx & 63;
+        const int64_t row = row0 + r, n = n0 + c;
+        if (row >= end || n >= N) continue;
+        float v[NBO];
+#pragma unroll
+        for (int o = 0; o < NBO; ++o) {
+            float sum = red[0][o][r * LDR + c];
+#pragma unroll
+            for (int w = 1; w < 4; ++w) sum += red[w][o][r * LDR + c];
+            v[o] = sum;
+        }
+        epi_store<EPI>(p, Cb, split, row, n, v[0], v[NBO - 1]);
+    }
+}
+
+template <int MB>
+void launch_skinny_grouped_mb(const GemmArgs& a, int epi, hipStream_t s) {
+    const int rb = static_cast<int>(ceil_div(a.rows_limit, 16 * MB));
+    const dim3 grid(static_cast<unsigned>(ceil_div(a.N, 64)), static_cast<unsigned>(a.E * rb),
+                    static_cast<unsigned>(a.k_splits));
+    switch (epi) {
+        case EPI_SWIGLU:
+            hipLaunchKernelGGL((gemm_skinny_grouped_kernel<MB, 2, EPI_SWIGLU>), grid, dim3(256), 0,
+                               s, a, rb);
+            break;
+        case EPI_SILU:
+            hipLaunchKernelGGL((gemm_skinny_grouped_kernel<MB, 1, EPI_SILU>), grid, dim3(256), 0,
+                               s, a, rb);
+            break;
+        case EPI_STORE:
+            hipLaunchKernelGGL((gemm_skinny_grouped_kernel<MB, 1, EPI_STORE>), grid, dim3(256), 0,
+                               s, a, rb);
+            break;
+        default: throw Unsupported("grouped skinny epilogue");
+    }
+}
+
 // Whether every byte offset of a SCHED_BUFLDS launch (lane offset from the
 // operand's base plus the K step's scalar offset) stays below 2^31.
 bool buf_offsets_fit(const GemmArgs& a, int bm, int bn, bool nn, bool grouped) {
@@ -1978,6 +2132,21 @@ void launch_gemm(const GemmArgs& args, bool nn, bool grouped, int epi, bool vec,
         return;
     }
     if (nn) throw Unsupported("grouped NN GEMM");
+    if (a.tile == kGroupedSkinnyTile) {
+        // the planner took it for few rows per expert; it checked the shape
+        const int64_t splits = std::max<int64_t>(a.k_splits, 1);
+        if (!vec || a.K % 16 != 0 || a.sk_grid > 0 ||
+            (splits > 1 && a.k_split_len % 16 != 0) ||
+            a.E * ceil_div(a.rows_limit, 16) > 65535 || ceil_div(a.N, 64) > INT32_MAX)
+            throw Unsupported("grouped skinny GEMM shape");
+        GemmArgs g = a;
+        g.k_splits = static_cast<int32_t>(splits);
+        if (splits == 1) g.k_split_len = a.K;
+        // 16 rows per workgroup while the experts average at most 16 rows, else 32
+        if (a.rows_limit <= 16 * int64_t(a.E)) launch_skinny_grouped_mb<1>(g, epi, s);
+        else launch_skinny_grouped_mb<2>(g, epi, s);
+        return;
+    }
     if (a.sk_grid > 0) {
         // stream-K: the host checked the direct path's requirements
         if (a.k_splits != 1 || a.sk_part == nullptr) throw Unsupported("stream-K arguments");

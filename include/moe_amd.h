@@ -350,7 +350,9 @@ int moe_layer_forward_noalloc(moe_ctx* ctx, const moe_layer_desc* desc,
  * tile per workgroup, 1 always runs stream-K (every workgroup the same
  * number of K steps, tiles cut at range boundaries joined by a fix-up
  * launch) wherever the direct-load path applies.  Results of the two differ
- * only in the rounding of the cut tiles' K sums.  No reference counterpart:
+ * only in the rounding of the cut tiles' K sums.  Only the default lets the
+ * planner run layers with few rows per expert (32 or fewer on average) on
+ * the grouped skinny kernel instead of tiles.  No reference counterpart:
  * a tuning and testing control (the environment variable MOE_SK = 0 / 1
  * sets the process default). */
 int moe_ctx_set_stream_k(moe_ctx* ctx, int mode);

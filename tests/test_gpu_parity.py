@@ -515,6 +515,66 @@ def test_expert_ffn_vs_oracle(ctx, torch, orc, request_reset_stream_k, T, d, E, 
     assert_close(host(out), ref, what="expert rows")
 
 
+# Shapes the planner sends to the grouped skinny kernel (few rows per expert,
+# K a multiple of 16; the context's default tile dealing): config 1's experts
+# (32-row workgroups, SiLU), a decoder's last rows (8 tokens, 16-row
+# workgroups, SwiGLU), every token on one expert (several row blocks for it,
+# the others empty), and 16 experts with empty ones among them.  x misaligned
+# by one float takes the tiles instead (same results within rounding).
+@pytest.mark.parametrize("T,d,E,k,d_ff,act,route", [
+    (64, 512, 4, 2, 1024, 1, "random"),
+    (8, 1024, 8, 2, 2816, 0, "random"),
+    (40, 256, 8, 2, 512, 0, "one"),
+    (30, 128, 16, 4, 256, 1, "skew"),
+    (5, 64, 4, 1, 64, 0, "random"),
+])
+@pytest.mark.parametrize("misaligned", [False, True])
+def test_expert_ffn_skinny_vs_oracle(ctx, torch, orc, T, d, E, k, d_ff, act, route, misaligned):
+    print(f"ffn skinny T={T} d={d} E={E} k={k} d_ff={d_ff} act={act} route={route} "
+          f"misaligned={misaligned}", flush=True)
+    rng = np.random.default_rng(T * 3 + d + E + d_ff)
+    x, w1, w3, w2, topk = _ffn_case(rng, T, d, E, k, d_ff, act, route == "skew")
+    if route == "one":
+        topk = np.stack([np.roll(np.arange(E), -(t % 2))[:k] for t in range(T)]).astype(np.int32)
+        topk[:, 0] = 0  # expert 0 takes every token
+    roff, rperm, rinv = orc.permute(topk, E)
+    ref = orc.expert_ffn(x, rperm, roff, w1, w3, w2, act=act)
+    xd = dev(torch, x)
+    if misaligned:
+        buf = torch.empty(T * d + 1, device="cuda")
+        buf[1:].copy_(xd.reshape(-1))
+        xd = buf[1:].view(T, d)
+    h = torch.empty((T * k, d_ff), device="cuda")
+    out = torch.empty((T * k, d), device="cuda")
+    ctx.expert_ffn_grouped(xd, dev(torch, rperm), dev(torch, roff), dev(torch, w1),
+                           None if w3 is None else dev(torch, w3), dev(torch, w2), k, h, out,
+                           act=act)
+    assert_close(host(out), ref, what="expert rows")
+
+
+@pytest.mark.parametrize("T,d,E,k,d_ff,act,splits", [(8, 1024, 8, 2, 2816, 0, 4),
+                                                     (64, 512, 4, 2, 1024, 1, 4),
+                                                     (24, 256, 16, 2, 448, 0, 1)])
+def test_layer_skinny_vs_oracle(ctx, pkg, torch, orc, T, d, E, k, d_ff, act, splits):
+    """Whole layers on the grouped skinny kernel, w2 with the K splits the
+    planner gives it (4 here for the first two, where the tiles would run w2
+    unsplit under stream-K) summed by the combine: a decoder's last rows,
+    config 1, the reference's experts at d 256."""
+    print(f"layer skinny T={T} d={d} E={E} k={k} d_ff={d_ff} act={act}", flush=True)
+    rng = np.random.default_rng(T + d + E)
+    x = normal(rng, (T, d))
+    gw = normal(rng, (E, d), 0.02)
+    w1 = normal(rng, (E, d_ff, d), 0.02)
+    w3 = normal(rng, (E, d_ff, d), 0.02) if act == 0 else None
+    w2 = normal(rng, (E, d, d_ff), 0.02)
+    y, idx, w = _layer(ctx, pkg, torch, dev(torch, x), dev(torch, gw), dev(torch, w1),
+                       None if w3 is None else dev(torch, w3), dev(torch, w2), k, act=act, mode=1)
+    ry, ridx, rw = orc.moe_forward(x, gw, w1, w3, w2, k, act=act, router_mode=1)
+    assert np.array_equal(host(idx), ridx)
+    assert_close(host(y), ry, what="layer y")
+    assert ctx.w2_splits(pkg.make_desc(T, d, E, k, d_ff, act=act, router=1)) == splits
+
+
 def test_expert_ffn_gather_past_2gib(ctx, torch, orc):
     """x of 2 GiB: the w1/w3 row gather's byte offsets pass 2^31, so w1/w3 take
     the kernel's 64-bit address path (w2 reads packed rows from the tile's
