@@ -334,6 +334,7 @@ struct FfnPlan {
     int64_t sk_floats = 0;  // partial-tile floats the stream-K launches need
     bool skinny13 = false;  // w1/w3 on the grouped skinny kernel (choose_skinny)
     bool skinny2 = false;   // w2 on it
+    int w13_splits = 1;     // K splits of the skinny w1/w3 (their raw sums in sk_part)
 };
 
 // The K splits of w2 on one w2 tile and their modelled time (choose_w2_split_plan).
@@ -456,10 +457,23 @@ void choose_skinny(moe_ctx* ctx, FfnPlan& f, int64_t pairs, int64_t d, int64_t d
         (env_skinny != 1 && pairs > 32 * E))
         return;
     const int64_t blocks16 = rows_wg / 16;
-    if (env_skinny == 1 || (d / 64) * blocks16 * 2 <= 32) {
+    // w1/w3: the fewest K splits (1, 2 or 4; each split a multiple of 16
+    // columns and at least 4 K steps per wave) that bring the units to 32 --
+    // splits only while the experts average at most 16 rows (with 32, the
+    // tiles run as fast: config 5 at 128 tokens, 2 splits, 0.104 against
+    // 0.102 ms)
+    int S13 = 0;
+    const int max_s13 = blocks16 == 1 ? 4 : 1;
+    for (int s1 = 1; s1 <= max_s13 && S13 == 0; s1 *= 2)
+        if (d % (16 * s1) == 0 && (s1 == 1 || d / (64 * s1) >= 4) &&
+            (d / (64 * s1)) * blocks16 * 2 <= 32)
+            S13 = s1;
+    if (env_skinny == 1 && S13 == 0) S13 = 1;
+    if (S13 > 0) {
         f.skinny13 = true;
         f.w13_tile = moe::kGroupedSkinnyTile;
         f.w13_sk = 0;
+        f.w13_splits = S13;
     }
     // expected row blocks: the pairs' blocks plus a partial one per expert
     const double blocks = std::min(double(E) * double(rb_max),
@@ -515,6 +529,9 @@ FfnPlan choose_ffn_plan(moe_ctx* ctx, int64_t pairs, int64_t d, int64_t d_ff, in
     choose_skinny(ctx, f, pairs, d, d_ff, E);
     if (f.w13_sk > 0) f.sk_floats = moe::gemm_sk_part_floats(u13, f.w13_sk);
     if (f.w2_sk > 0) f.sk_floats = std::max(f.sk_floats, moe::gemm_sk_part_floats(u2, f.w2_sk));
+    // the skinny w1/w3's split sums: both B operands (the SwiGLU case) per split
+    if (f.skinny13 && f.w13_splits > 1)
+        f.sk_floats = std::max<int64_t>(f.sk_floats, int64_t(f.w13_splits) * pairs * d_ff * 2);
     return f;
 }
 
@@ -597,8 +614,18 @@ void expert_ffn(moe_ctx* ctx, const float* x, const int32_t* perm,
             a.sk_grid = f.w13_sk;
             a.sk_part = sk_part;
         }
+        if (f.skinny13 && f.w13_splits > 1) {
+            a.k_splits = f.w13_splits;
+            a.k_split_len = d / f.w13_splits;
+            a.sk_part = sk_part;
+        }
         const bool vec = d % 4 == 0 && aligned16(x) && aligned16(w1) && (!swiglu || aligned16(w3));
-        if (f.skinny13 && !vec) a.tile = 0;  // unaligned rows: one 128x128 tile per workgroup
+        if (f.skinny13 && !vec) {  // unaligned rows: one 128x128 tile per workgroup, K whole
+            a.tile = 0;
+            a.k_splits = 1;
+            a.k_split_len = 0;
+            a.sk_part = nullptr;
+        }
         ctx->launch(swiglu ? "expert_w13_swiglu" : "expert_w1_silu", s, [&] {
             moe::launch_gemm(a, false, true, swiglu ? moe::EPI_SWIGLU : moe::EPI_SILU, vec, s);
         });

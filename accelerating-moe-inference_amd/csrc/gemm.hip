@@ -1682,8 +1682,11 @@ void launch_skinny(const GemmArgs& a, hipStream_t s) {
 // LDS: every output is the waves' partials added in wave order, then the
 // epilogue.  grid.y = E * rb, rb the row blocks of the largest expert the
 // launch allows for (rows_limit / (16 * MB), rounded up); blocks past an
-// expert's rows exit at once.  Requires K % 16 == 0 per split and 16-byte
-// aligned rows.
+// expert's rows exit at once.  With K splits, an activation launch (SiLU,
+// SwiGLU) stores each split's raw sums of its B operands instead,
+// sk_part[split][row][o * N + n], and skinny_act_fixup_kernel adds them in
+// split order and applies the activation.  Requires K % 16 == 0 per split
+// and 16-byte aligned rows.
 template <int MB, int NBO, int EPI>
 __global__ __launch_bounds__(256) void gemm_skinny_grouped_kernel(const GemmArgs p, int rb) {
     // chunks in flight besides the one computed (3 and 5, or 4 and 6, measured
@@ -1787,7 +1790,9 @@ __global__ __launch_bounds__(256) void gemm_skinny_grouped_kernel(const GemmArgs
                     red[wave][o][(16 * mb + 4 * g + i) * LDR + 16 * cb + j] = acc[o][mb][cb][i];
     __syncthreads();
     // every output: the four waves' partials in wave order, then the epilogue
+    // (or, for an activation split over K, the split's raw sums)
     float* Cb = p.C;
+    const bool raw = EPI != EPI_STORE && p.k_splits > 1;
     for (int idx = threadIdx.x; idx < RW * 64; idx += 256) {
         const int r = idx >> 6, c = idx & 63;
         const int64_t row = row0 + r, n = n0 + c;
@@ -1800,7 +1805,37 @@ __global__ __launch_bounds__(256) void gemm_skinny_grouped_kernel(const GemmArgs
             for (int w = 1; w < 4; ++w) sum += red[w][o][r * LDR + c];
             v[o] = sum;
         }
-        epi_store<EPI>(p, Cb, split, row, n, v[0], v[NBO - 1]);
+        if (raw) {
+#pragma unroll
+            for (int o = 0; o < NBO; ++o)
+                p.sk_part[(split * p.rows_limit + row) * (NBO * N) + o * N + n] = v[o];
+        } else {
+            epi_store<EPI>(p, Cb, split, row, n, v[0], v[NBO - 1]);
+        }
+    }
+}
+
+// The activation of a K-split grouped skinny launch: h[row][n] = act of the
+// splits' sums of each B operand, added in split order.
+template <int NBO, int EPI>
+__global__ __launch_bounds__(256) void skinny_act_fixup_kernel(const float* __restrict__ part,
+                                                               float* __restrict__ h,
+                                                               int64_t rows, int64_t N,
+                                                               int64_t ldh, int splits) {
+    const int64_t total = rows * N;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+         i += stride) {
+        const int64_t row = i / N, n = i % N;
+        float v[NBO];
+#pragma unroll
+        for (int o = 0; o < NBO; ++o) {
+            float sum = part[row * (NBO * N) + o * N + n];
+            for (int sp = 1; sp < splits; ++sp)
+                sum += part[(sp * rows + row) * (NBO * N) + o * N + n];
+            v[o] = sum;
+        }
+        h[row * ldh + n] = EPI == EPI_SWIGLU ? silu_ref(v[0]) * v[NBO - 1] : silu_ref(v[0]);
     }
 }
 
@@ -2141,12 +2176,25 @@ void launch_gemm(const GemmArgs& args, bool nn, bool grouped, int epi, bool vec,
             (splits > 1 && a.k_split_len % 16 != 0) ||
             a.E * ceil_div(a.rows_limit, 16) > 65535 || ceil_div(a.N, 64) > INT32_MAX)
             throw Unsupported("grouped skinny GEMM shape");
+        const bool act_split = splits > 1 && epi != EPI_STORE;
+        if (act_split && a.sk_part == nullptr) throw Unsupported("grouped skinny split partials");
         GemmArgs g = a;
         g.k_splits = static_cast<int32_t>(splits);
         if (splits == 1) g.k_split_len = a.K;
         // 16 rows per workgroup while the experts average at most 16 rows, else 32
         if (a.rows_limit <= 16 * int64_t(a.E)) launch_skinny_grouped_mb<1>(g, epi, s);
         else launch_skinny_grouped_mb<2>(g, epi, s);
+        if (act_split) {
+            const int64_t total = a.rows_limit * a.N;
+            const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(ceil_div(total, 256), 4096));
+            const int sp = static_cast<int>(splits);
+            if (epi == EPI_SWIGLU)
+                hipLaunchKernelGGL((skinny_act_fixup_kernel<2, EPI_SWIGLU>), dim3(blocks), dim3(256), 0,
+                                   s, a.sk_part, a.C, a.rows_limit, a.N, a.ldc, sp);
+            else
+                hipLaunchKernelGGL((skinny_act_fixup_kernel<1, EPI_SILU>), dim3(blocks), dim3(256), 0,
+                                   s, a.sk_part, a.C, a.rows_limit, a.N, a.ldc, sp);
+        }
         return;
     }
     if (a.sk_grid > 0) {

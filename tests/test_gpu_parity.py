@@ -519,7 +519,9 @@ def test_expert_ffn_vs_oracle(ctx, torch, orc, request_reset_stream_k, T, d, E, 
 # K a multiple of 16; the context's default tile dealing): config 1's experts
 # (32-row workgroups, SiLU), a decoder's last rows (8 tokens, 16-row
 # workgroups, SwiGLU), every token on one expert (several row blocks for it,
-# the others empty), and 16 experts with empty ones among them.  x misaligned
+# the others empty), and 16 experts with empty ones among them; w1/w3 split
+# over K with the activation in the fix-up: the reference's experts at 8
+# tokens (4 splits), SwiGLU at d 2048 (2), SiLU at d 2048 (2).  x misaligned
 # by one float takes the tiles instead (same results within rounding).
 @pytest.mark.parametrize("T,d,E,k,d_ff,act,route", [
     (64, 512, 4, 2, 1024, 1, "random"),
@@ -527,6 +529,9 @@ def test_expert_ffn_vs_oracle(ctx, torch, orc, request_reset_stream_k, T, d, E, 
     (40, 256, 8, 2, 512, 0, "one"),
     (30, 128, 16, 4, 256, 1, "skew"),
     (5, 64, 4, 1, 64, 0, "random"),
+    (8, 4096, 16, 2, 448, 0, "random"),
+    (64, 2048, 8, 2, 512, 0, "random"),
+    (16, 2048, 4, 1, 256, 1, "skew"),
 ])
 @pytest.mark.parametrize("misaligned", [False, True])
 def test_expert_ffn_skinny_vs_oracle(ctx, torch, orc, T, d, E, k, d_ff, act, route, misaligned):
@@ -554,12 +559,14 @@ def test_expert_ffn_skinny_vs_oracle(ctx, torch, orc, T, d, E, k, d_ff, act, rou
 
 @pytest.mark.parametrize("T,d,E,k,d_ff,act,splits", [(8, 1024, 8, 2, 2816, 0, 4),
                                                      (64, 512, 4, 2, 1024, 1, 4),
-                                                     (24, 256, 16, 2, 448, 0, 1)])
+                                                     (24, 256, 16, 2, 448, 0, 1),
+                                                     (8, 4096, 16, 2, 448, 0, 1)])
 def test_layer_skinny_vs_oracle(ctx, pkg, torch, orc, T, d, E, k, d_ff, act, splits):
     """Whole layers on the grouped skinny kernel, w2 with the K splits the
     planner gives it (4 here for the first two, where the tiles would run w2
     unsplit under stream-K) summed by the combine: a decoder's last rows,
-    config 1, the reference's experts at d 256."""
+    config 1, the reference's experts at d 256 and at its d 4096 (w1/w3 split
+    four ways over K)."""
     print(f"layer skinny T={T} d={d} E={E} k={k} d_ff={d_ff} act={act}", flush=True)
     rng = np.random.default_rng(T + d + E)
     x = normal(rng, (T, d))
