@@ -468,6 +468,13 @@ void choose_skinny(moe_ctx* ctx, FfnPlan& f, int64_t pairs, int64_t d, int64_t d
         if (d % (16 * s1) == 0 && (s1 == 1 || d / (64 * s1) >= 4) &&
             (d / (64 * s1)) * blocks16 * 2 <= 32)
             S13 = s1;
+    // expected row blocks: the pairs' blocks plus a partial one per expert
+    const double blocks = std::min(double(E) * double(rb_max),
+                                   double(pairs) / double(rows_wg) + 0.5 * double(E));
+    // and at most about four workgroups per CU: with more, the tiles stream
+    // the weights faster (config 3 at 64 tokens, 10,752 workgroups of 16 K
+    // steps: w1/w3 1.151 against 0.931 ms)
+    if (S13 > 0 && blocks * double(moe::ceil_div(d_ff, 64)) * S13 > 4.0 * ctx->cus) S13 = 0;
     if (env_skinny == 1 && S13 == 0) S13 = 1;
     if (S13 > 0) {
         f.skinny13 = true;
@@ -475,9 +482,6 @@ void choose_skinny(moe_ctx* ctx, FfnPlan& f, int64_t pairs, int64_t d, int64_t d
         f.w13_sk = 0;
         f.w13_splits = S13;
     }
-    // expected row blocks: the pairs' blocks plus a partial one per expert
-    const double blocks = std::min(double(E) * double(rb_max),
-                                   double(pairs) / double(rows_wg) + 0.5 * double(E));
     const double wgs = blocks * double(moe::ceil_div(d, 64));
     int S = 1;
     for (int s2 = 2; s2 <= moe::kMaxW2Splits; s2 *= 2)
