@@ -297,8 +297,10 @@ int moe_permute(moe_ctx* ctx, const int32_t* topk_idx, int64_t T, int64_t k,
  * reads x[perm[r], :].  h[T*k, d_ff] is the hidden activation (written),
  * out_rows[T*k, d] the expert outputs in packed order.
  * w1, w3: [E, d_ff, d]; w2: [E, d, d_ff]; w3 is ignored for SILU_MLP.
- * Where the planner runs a projection stream-K, its partial tiles go to the
- * context's workspace, which the call grows if it is too small (a device
+ * Where the planner runs a projection stream-K, or w1/w3 on the grouped
+ * skinny kernel split over K (few rows per expert), its partial tiles or
+ * split sums go to the context's workspace, which the call grows if it is
+ * too small (a device
  * synchronisation, a free and an allocation: not allowed under graph
  * capture).  moe_ctx_reserve with a desc of the same T, k, d, d_ff and E
  * sizes it beforehand, after which the call allocates nothing. */
