@@ -461,7 +461,10 @@ void choose_skinny(moe_ctx* ctx, FfnPlan& f, int64_t pairs, int64_t d, int64_t d
     // columns and at least 4 K steps per wave) that bring the units to 32 --
     // splits only while the experts average at most 16 rows (with 32, the
     // tiles run as fast: config 5 at 128 tokens, 2 splits, 0.104 against
-    // 0.102 ms)
+    // 0.102 ms).  More splits than that lost (config 1, config 5 at 8-64
+    // tokens: 2 or 4 splits 1-29 % slower per launch); fewer left the long K
+    // loops (the reference at 64 tokens: 1 / 2 / 4 splits 0.168 / 0.094 /
+    // 0.077 ms).  MOE_SKINNY_W13_SPLITS = 1 / 2 / 4 pins them for tuning.
     int S13 = 0;
     const int max_s13 = blocks16 == 1 ? 4 : 1;
     for (int s1 = 1; s1 <= max_s13 && S13 == 0; s1 *= 2)
@@ -476,6 +479,9 @@ void choose_skinny(moe_ctx* ctx, FfnPlan& f, int64_t pairs, int64_t d, int64_t d
     // steps: w1/w3 1.151 against 0.931 ms)
     if (S13 > 0 && blocks * double(moe::ceil_div(d_ff, 64)) * S13 > 4.0 * ctx->cus) S13 = 0;
     if (env_skinny == 1 && S13 == 0) S13 = 1;
+    static const int env_s13 = env_int("MOE_SKINNY_W13_SPLITS", 0);
+    if (S13 > 0 && (env_s13 == 1 || env_s13 == 2 || env_s13 == 4) && d % (16 * env_s13) == 0)
+        S13 = env_s13;
     if (S13 > 0) {
         f.skinny13 = true;
         f.w13_tile = moe::kGroupedSkinnyTile;
