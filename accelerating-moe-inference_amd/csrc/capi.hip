@@ -492,6 +492,12 @@ void choose_skinny(moe_ctx* ctx, FfnPlan& f, int64_t pairs, int64_t d, int64_t d
     int S = 1;
     for (int s2 = 2; s2 <= moe::kMaxW2Splits; s2 *= 2)
         if (d_ff % (16 * s2) == 0 && d_ff / (64 * s2) >= 4 && wgs * s2 <= 2.0 * ctx->cus) S = s2;
+    // (measured, µs per w2 launch at S = 1 / 2 / 4 against the tiles: config 1
+    // 18.8 / 13.4 / 14.2 against 24.0; config 5 at 8 tokens 30.4 / 20.2 /
+    // 20.5 against 36.1; the reference at 64 tokens 34.3 / 36.5 / 40.5
+    // against 43.2.)  MOE_SKINNY_W2_SPLITS = 1 / 2 / 4 pins S for tuning.
+    static const int env_s2 = env_int("MOE_SKINNY_W2_SPLITS", 0);
+    if ((env_s2 == 1 || env_s2 == 2 || env_s2 == 4) && d_ff % (16 * env_s2) == 0) S = env_s2;
     if (env_skinny == 1 ||
         ((d_ff / (64 * S)) * blocks16 <= 12 && (pairs <= 8 * E || d <= 1024))) {
         f.skinny2 = true;
