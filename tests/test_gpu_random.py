@@ -97,6 +97,8 @@ def _layer_cases(n=N_CASES, seed=77):
     while len(cases) < n:
         T = int(rng.integers(1, 900))
         d = int(rng.choice([int(rng.integers(1, 130)), 16 * int(rng.integers(1, 33))]))
+        if rng.random() < 0.15:                  # wide rows, few tokens: split-K skinny w1/w3
+            d, T = 1024 * int(rng.integers(1, 5)), int(rng.integers(1, 40))
         E = int(rng.integers(1, 80))
         k = int(rng.integers(1, min(E, 8) + 1))
         d_ff = int(rng.choice([int(rng.integers(1, 300)), 64 * int(rng.integers(1, 11))]))
