@@ -336,15 +336,13 @@ __global__ __launch_bounds__(64) void gate_ring_kernel(
 // Ring depth and the waves per SIMD the register budget is set for
 // (measured on MI355X at the reference's 15,583 x 4096 x 16: 3 stages at 4
 // waves 84 us; 4 stages at 3 waves 132 us, at 4 waves 217 us; 6 at 2, 112 us;
-// 8 at 2, 242 us; the staged kernel 110 us in the same runs).
-#ifndef MOE_GATE_RING
-#define MOE_GATE_RING 3
-#endif
-#ifndef MOE_GATE_OCC
-#define MOE_GATE_OCC 4
-#endif
-template <int CONTRACT, int EB, int TB, int RING>
-__global__ __launch_bounds__(256, MOE_GATE_OCC) void gate_wg_ring_kernel(
+// 8 at 2, 242 us; the staged kernel 110 us in the same runs).  A grid of at
+// most one workgroup per CU (up to 4,096 tokens at 16 experts) is bound by
+// each workgroup's stage round trips instead: 5 stages at 2 waves there
+// (8 / 1,024 / 4,096 tokens: 45.0 / 47.2 / 48.5 us against 62-65 us at 3
+// stages; 4 stages 45.7-50.0, 6 stages 46.5-50.5, 7 stages 63-66).
+template <int CONTRACT, int EB, int TB, int RING, int OCC>
+__global__ __launch_bounds__(256, OCC) void gate_wg_ring_kernel(
         const float* __restrict__ x, const float* __restrict__ w,
         float* __restrict__ logits, int64_t T, int64_t d, int64_t E,
         uint32_t* __restrict__ zero, int64_t nzero) {
@@ -974,7 +972,7 @@ __global__ __launch_bounds__(256) void combine_kernel(
 }  // namespace
 
 void launch_gate_logits(const float* x, const float* w, float* logits,
-                        int64_t T, int64_t d, int64_t E, int contract,
+                        int64_t T, int64_t d, int64_t E, int contract, int cus,
                         hipStream_t s, uint32_t* zero, int64_t nzero) {
     if (T == 0 || E == 0) return;
     auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
@@ -1007,8 +1005,14 @@ void launch_gate_logits(const float* x, const float* w, float* logits,
             hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, x, w, logits, T, d, E, zero,
                                nzero);
         };
-        if (contract) go(gate_wg_ring_kernel<1, 16, 1, MOE_GATE_RING>);
-        else go(gate_wg_ring_kernel<0, 16, 1, MOE_GATE_RING>);
+        const bool few = int64_t(grid.x) * grid.y <= cus;
+        if (few) {
+            if (contract) go(gate_wg_ring_kernel<1, 16, 1, 5, 2>);
+            else go(gate_wg_ring_kernel<0, 16, 1, 5, 2>);
+        } else {
+            if (contract) go(gate_wg_ring_kernel<1, 16, 1, 3, 4>);
+            else go(gate_wg_ring_kernel<0, 16, 1, 3, 4>);
+        }
         return;
     }
     // 4 tokens per thread from 32 experts up (small E keeps one output per
