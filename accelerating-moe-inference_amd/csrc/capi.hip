@@ -782,8 +782,8 @@ void layer_forward(moe_ctx* ctx, const moe_layer_desc& D, const moe_layer_weight
     // the gate also clears the counts route_count adds into
     const int64_t nb = moe::ceil_div(D.T, moe::kPermTokens);
     ctx->launch("gate_logits", s, [&] {
-        moe::launch_gate_logits(xin, weights.gate_w, ws.logits, D.T, D.d, D.E, D.contract,
-                                ctx->cus, s, reinterpret_cast<uint32_t*>(ws.counts), D.E * nb);
+        moe::launch_gate_logits(xin, weights.gate_w, ws.logits, D.T, D.d, D.E, D.contract, s,
+                                reinterpret_cast<uint32_t*>(ws.counts), D.E * nb);
     });
     // routing and the per-block expert counts: one launch
     ctx->launch("route_count", s, [&] {
@@ -1053,7 +1053,7 @@ int moe_gate_logits(moe_ctx* ctx, const float* x, const float* gate_w, float* lo
         DeviceScope dev(ctx->device);
         hipStream_t s = as_stream(stream);
         ctx->launch("gate_logits", s, [&] {
-            moe::launch_gate_logits(x, gate_w, logits, T, d, E, contract, ctx->cus, s);
+            moe::launch_gate_logits(x, gate_w, logits, T, d, E, contract, s);
         });
     });
 }

@@ -185,10 +185,9 @@ void launch_add_bias(float* a, const float* bias, int64_t rows, int64_t cols, hi
 void launch_embed(const float* table, const int32_t* tokens, int64_t n, int64_t d,
                   int64_t vocab, float* out, hipStream_t s);
 // zero / nzero: words the launch also sets to 0 (the routing counters of
-// the launch that follows), or null / 0.  cus: the GPU's compute units (the
-// kernel's ring depth depends on how many workgroups each holds).
+// the launch that follows), or null / 0.
 void launch_gate_logits(const float* x, const float* w, float* logits,
-                        int64_t T, int64_t d, int64_t E, int contract, int cus,
+                        int64_t T, int64_t d, int64_t E, int contract,
                         hipStream_t s, uint32_t* zero = nullptr, int64_t nzero = 0);
 void launch_route(const float* logits, const float* bias, int64_t T, int64_t E,
                   int64_t k, int mode, float quantum, float tie_eps,

@@ -183,6 +183,14 @@ __global__ __launch_bounds__(256) void gate_logits_kernel(
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 constexpr int kGateRingCols = 64;
 constexpr int kGateRing = 8;
+// Up to this many token x expert logits, 9-64 experts take the per-wave ring
+// with expert blocks (gate_ring_kernel over grid.y); measured on MI355X, us,
+// expert blocks against the workgroup ring / staged kernel: the reference's
+// E = 16 at d 4096, 1 / 64 / 1,024 / 4,096 tokens 39.2 / 38.9 / 40.1 / 43.9
+// against 45.3 / 47.1 / 47.6 / 48.9, at 15,583 tokens 209.9 against 88.8;
+// config 4's E = 64 at d 2048, 16 / 1,024 tokens 23.1 / 25.9 against 86.6 /
+// 91.3, 4,096 86.9 against 88.2, 16,384 352.6 against 105.6.
+constexpr int64_t kGateFewLogits = 65536;
 
 typedef __attribute__((address_space(3))) void gate_lds_t;
 
@@ -232,6 +240,8 @@ __global__ __launch_bounds__(64) void gate_ring_kernel(
     const int lane = threadIdx.x;
     const int64_t t0 = static_cast<int64_t>(blockIdx.x) * R;
     const int64_t nt = T - t0 < R ? T - t0 : R;  // tokens of this wave (>= 1)
+    const int64_t e0 = static_cast<int64_t>(blockIdx.y) * EB;  // this wave's expert block
+    const int64_t ne = E - e0 < EB ? E - e0 : EB;                // its experts (>= 1)
     const int64_t nst = (d + kGateRingCols - 1) / kGateRingCols;
 
     // instruction i: rows 4i .. 4i + 3 of the stage, one matrix each
@@ -246,8 +256,8 @@ __global__ __launch_bounds__(64) void gate_ring_kernel(
             ibase[i] = x + t0 * d;
             ioff[i] = static_cast<uint32_t>((rr * d + 4 * chunk) * 4);
         } else {          // expert rows
-            const int64_t e = row - R < E ? row - R : E - 1;
-            ibase[i] = w;
+            const int64_t e = row - R < ne ? row - R : ne - 1;
+            ibase[i] = w + e0 * d;
             ioff[i] = static_cast<uint32_t>((e * d + 4 * chunk) * 4);
         }
     }
@@ -312,7 +322,7 @@ __global__ __launch_bounds__(64) void gate_ring_kernel(
             }
         });
     }
-    if (r < nt && e < E) logits[(t0 + r) * E + e] = acc;
+    if (r < nt && e < ne) logits[(t0 + r) * E + e0 + e] = acc;
 }
 
 // E of 9-16: the ring form with the workgroup sharing each stage.  A wave of
@@ -337,10 +347,10 @@ __global__ __launch_bounds__(64) void gate_ring_kernel(
 // (measured on MI355X at the reference's 15,583 x 4096 x 16: 3 stages at 4
 // waves 84 us; 4 stages at 3 waves 132 us, at 4 waves 217 us; 6 at 2, 112 us;
 // 8 at 2, 242 us; the staged kernel 110 us in the same runs).  A grid of at
-// most one workgroup per CU (up to 4,096 tokens at 16 experts) is bound by
-// each workgroup's stage round trips instead: 5 stages at 2 waves there
-// (8 / 1,024 / 4,096 tokens: 45.0 / 47.2 / 48.5 us against 62-65 us at 3
-// stages; 4 stages 45.7-50.0, 6 stages 46.5-50.5, 7 stages 63-66).
+// most one workgroup per CU is bound by each workgroup's stage round trips
+// instead (62-67 us from 1 to 4,096 tokens at 16 experts; 5 stages at 2
+// waves 45-49 us): such small batches take the per-wave ring with expert
+// blocks (kGateFewLogits), faster still.
 template <int CONTRACT, int EB, int TB, int RING, int OCC>
 __global__ __launch_bounds__(256, OCC) void gate_wg_ring_kernel(
         const float* __restrict__ x, const float* __restrict__ w,
@@ -972,7 +982,7 @@ __global__ __launch_bounds__(256) void combine_kernel(
 }  // namespace
 
 void launch_gate_logits(const float* x, const float* w, float* logits,
-                        int64_t T, int64_t d, int64_t E, int contract, int cus,
+                        int64_t T, int64_t d, int64_t E, int contract,
                         hipStream_t s, uint32_t* zero, int64_t nzero) {
     if (T == 0 || E == 0) return;
     auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
@@ -995,6 +1005,23 @@ void launch_gate_logits(const float* x, const float* w, float* logits,
         }
         return;
     }
+    // A few tokens over 9-64 experts: the per-wave ring above with 4 experts
+    // per wave and E / 4 expert blocks over grid.y, so that many waves
+    // stream the expert rows at once (the workgroup ring below runs every
+    // expert of a 16-token block in one workgroup, bound by its stages'
+    // round trips while the grid is small); the 16 token rows a wave holds
+    // are re-read once per expert block, which only pays while they are few.
+    if (E > 8 && E <= 64 && T * E <= kGateFewLogits && d % 4 == 0 && d >= 4 && al(x) && al(w) &&
+        d * 16 * 4 < (int64_t(1) << 31)) {
+        const dim3 grid(static_cast<unsigned>(ceil_div(T, 16)), static_cast<unsigned>(ceil_div(E, 4)));
+        if (contract)
+            hipLaunchKernelGGL((gate_ring_kernel<1, 4>), grid, dim3(64), 0, s, x, w, logits, T, d, E,
+                               zero, nzero);
+        else
+            hipLaunchKernelGGL((gate_ring_kernel<0, 4>), grid, dim3(64), 0, s, x, w, logits, T, d, E,
+                               zero, nzero);
+        return;
+    }
     int eb = 8;
     while (eb < E && eb < 64) eb <<= 1;
     // E of 9-16: the workgroup ring, when rows are 16-byte aligned and every
@@ -1005,14 +1032,8 @@ void launch_gate_logits(const float* x, const float* w, float* logits,
             hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, x, w, logits, T, d, E, zero,
                                nzero);
         };
-        const bool few = int64_t(grid.x) * grid.y <= cus;
-        if (few) {
-            if (contract) go(gate_wg_ring_kernel<1, 16, 1, 5, 2>);
-            else go(gate_wg_ring_kernel<0, 16, 1, 5, 2>);
-        } else {
-            if (contract) go(gate_wg_ring_kernel<1, 16, 1, 3, 4>);
-            else go(gate_wg_ring_kernel<0, 16, 1, 3, 4>);
-        }
+        if (contract) go(gate_wg_ring_kernel<1, 16, 1, 3, 4>);
+        else go(gate_wg_ring_kernel<0, 16, 1, 3, 4>);
         return;
     }
     // 4 tokens per thread from 32 experts up (small E keeps one output per

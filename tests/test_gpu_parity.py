@@ -294,21 +294,24 @@ def test_silu_mul_bit_exact(ctx, torch, orc):
 @pytest.mark.parametrize("contract", [0, 1])
 # E <= 8 with 16-byte rows takes the ring kernel (64 x 512 x 4; 33 x 100 x 7:
 # a partial last stage and a one-token last wave; 4096 x 1024 x 8, config
-# 5's gate; 100 x 256 x 2: fewer experts than the lane block); E of 9-16 with
-# 16-byte rows the workgroup ring (300 x 4096 x 16 and 1037 x 4096 x 16: the
-# reference's expert count, the latter with a partial last workgroup; 45 x
-# 196 x 11: a partial last stage, 5 experts masked; 16 x 4 x 16: one
-# 4-column stage); every other shape the staged kernel: E above 16 (1000 x
-# 2048 x 64, config 4's expert count, 4 tokens x 2 experts per thread; 77 x
-# 452 x 100: two 64-expert blocks, the second 36 wide; 50 x 1024 x 32; and
-# grids of 512 workgroups or more, 4 tokens x 4 experts per thread: 33000 x
-# 40 x 64 and 16421 x 96 x 100, ragged last workgroup and expert block) and
-# rows that are not 16-byte multiples (70 x 130 x 130; 5 x 1 x 3)
+# 5's gate; 100 x 256 x 2: fewer experts than the lane block); E of 9-64 with
+# 16-byte rows and at most 65,536 logits the same ring with 4-expert blocks
+# over grid.y (300 x 4096 x 16 and 1037 x 4096 x 16: the reference's expert
+# count, the latter with a partial last wave; 45 x 196 x 11: a partial last
+# stage and expert block; 16 x 4 x 16: one 4-column stage; 1000 x 2048 x 64,
+# config 4's expert count; 50 x 1024 x 32; 1 x 4096 x 16, one token); E of
+# 9-16 with more logits the workgroup ring (4500 x 512 x 16, a partial last
+# workgroup; 7000 x 260 x 10, 6 experts masked); every other shape the staged
+# kernel: E above 64 (77 x 452 x 100: two 64-expert blocks, the second 36
+# wide; grids of 512 workgroups or more, 4 tokens x 4 experts per thread:
+# 33000 x 40 x 64 and 16421 x 96 x 100, ragged last workgroup and expert
+# block) and rows that are not 16-byte multiples (70 x 130 x 130; 5 x 1 x 3)
 @pytest.mark.parametrize("T,d,E", [(64, 512, 4), (300, 4096, 16), (1000, 2048, 64),
                                    (33, 100, 7), (5, 1, 3), (70, 130, 130), (4096, 1024, 8),
                                    (100, 256, 2), (1037, 4096, 16), (45, 196, 11),
                                    (77, 452, 100), (16, 4, 16), (50, 1024, 32),
-                                   (33000, 40, 64), (16421, 96, 100)])
+                                   (33000, 40, 64), (16421, 96, 100), (1, 4096, 16),
+                                   (4500, 512, 16), (7000, 260, 10)])
 def test_gate_logits_bit_exact(ctx, torch, orc, contract, T, d, E):
     print(f"gate {T}x{d}x{E} contract={contract}", flush=True)
     rng = np.random.default_rng(T + d + E)
