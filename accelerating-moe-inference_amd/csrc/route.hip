@@ -289,13 +289,23 @@ __global__ __launch_bounds__(64) void gate_ring_kernel(
         const float* wr = stage + (R + e) * kGateRingCols;
         const int64_t j0 = st * kGateRingCols;
         if (j0 + kGateRingCols <= d) {
+            // the stage's 32 LDS reads first, then the 64-step chain: the
+            // chain no longer waits on a read every 4 steps (bit-identical;
+            // the reference's gate at 1 and 64 tokens 39.6 / 38.6 -> 35.3 /
+            // 34.2 us, config 4's at 64 tokens 24.1 -> 20.7, config 3's 41.3
+            // -> 39.9).  In the workgroup ring below, at four waves per SIMD,
+            // the same 128 registers spilled: 81 -> 428 us at the
+            // reference's 15,583 tokens.
+            f32x4_t xs[16], ws[16];
 #pragma unroll
             for (int q = 0; q < 16; ++q) {
-                const f32x4_t xv = *reinterpret_cast<const f32x4_t*>(xr + 4 * (q ^ xsw));
-                const f32x4_t wv = *reinterpret_cast<const f32x4_t*>(wr + 4 * (q ^ wsw));
-#pragma unroll
-                for (int c = 0; c < 4; ++c) acc = mac<CONTRACT>(acc, xv[c], wv[c]);
+                xs[q] = *reinterpret_cast<const f32x4_t*>(xr + 4 * (q ^ xsw));
+                ws[q] = *reinterpret_cast<const f32x4_t*>(wr + 4 * (q ^ wsw));
             }
+#pragma unroll
+            for (int q = 0; q < 16; ++q)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) acc = mac<CONTRACT>(acc, xs[q][c], ws[q][c]);
         } else {
             for (int q = 0; q < 16; ++q) {
                 const f32x4_t xv = *reinterpret_cast<const f32x4_t*>(xr + 4 * (q ^ xsw));
