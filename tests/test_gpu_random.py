@@ -1,17 +1,17 @@
 """GPU parity on seeded random shapes: the dense SGEMM (NN and NT, with and
 without bias), the whole MoE layer (both routers, both activations, both
-contraction modes, the planner's tile dealing and both forced ones), causal
-attention and the two norms, each against the CPU oracle.  The shapes are drawn once from fixed seeds, so every
+contraction modes, the planner's tile dealing and both forced ones), the
+router gate, causal attention and the two norms, each against the CPU oracle.  The shapes are drawn once from fixed seeds, so every
 run checks the same cases; they reach the planner's tile shapes and K splits,
 the skinny kernel, the register-staged fallback (K % 16 != 0, unaligned rows)
 and ragged expert loads that the hand-picked cases leave out.
 
 Bar: routing indices bit-exact, PHI weights bit-exact and softmax weights
-within 1 ulp, norms bit-exact; activations and attention within REL_TOL
+within 1 ulp, gate logits and norms bit-exact; activations and attention within REL_TOL
 normwise relative error.
 
 MOE_RANDOM_CASES (default 48) sets how many cases each test draws (the
-attention and norm tests half as many) and MOE_RANDOM_SEED (default 0)
+gate, attention and norm tests half as many) and MOE_RANDOM_SEED (default 0)
 shifts the seeds, for a wider sweep by hand.
 """
 import os
@@ -172,6 +172,42 @@ def test_attention_random_shapes(ctx, torch, orc, B, S, H, KVH, hd, window):
     ctx.attention(dev(torch, q), dev(torch, k), dev(torch, v), out, B, S, H, KVH, hd, window)
     ref = orc.attention(q, k, v, B, S, H, KVH, hd, window or None)
     assert_close(host(out), ref, what="attention")
+
+
+def _gate_cases(n=N_CASES // 2, seed=71):
+    rng = np.random.default_rng(seed + SEED)
+    cases = []
+    for i in range(n):
+        lo, hi = [(1, 8), (9, 16), (17, 80)][i % 3]
+        E = int(rng.integers(lo, hi + 1))
+        d = int(rng.integers(1, 4200))
+        if i % 5 != 4:
+            d = 4 * max(1, d // 4)               # 16-byte rows: the ring kernels
+        few = 65536 // E                         # tokens of 65,536 logits
+        T = int(rng.integers(1, few + 1)) if i % 2 == 0 else int(rng.integers(few + 1, 4 * few + 2))
+        T = min(T, 40000)
+        if T * d > 8_000_000:                    # x within 32 MB
+            d = max(4, (8_000_000 // T) // 4 * 4)
+        if T * E * d > 120_000_000:              # the oracle's chains, a second or so
+            d = max(4, (120_000_000 // (T * E)) // 4 * 4)
+        cases.append((T, d, E, (i // 2) % 2))
+    return cases
+
+
+@pytest.mark.parametrize("T,d,E,contract", _gate_cases())
+def test_gate_random_shapes(ctx, torch, orc, T, d, E, contract):
+    """The router gate on random shapes on both sides of every dispatch
+    boundary (up to 8 experts: the per-wave ring; 9-64 with at most 65,536
+    logits: the per-wave ring over expert blocks; 9-16 beyond: the workgroup
+    ring; otherwise the staged kernel), rows aligned or not, bit for bit."""
+    print(f"gate {T}x{d}x{E} contract={contract}", flush=True)
+    rng = np.random.default_rng(T * 7 + d * 3 + E)
+    x = normal(rng, (T, d))
+    w = normal(rng, (E, d), 0.02)
+    logits = torch.empty((T, E), device="cuda")
+    ctx.gate_logits(dev(torch, x), dev(torch, w), logits, contract=contract)
+    ref = orc.matmul_nt(x, w, contract=contract)
+    assert np.array_equal(host(logits).view(np.int32), ref.view(np.int32))
 
 
 def _norm_cases(n=N_CASES // 2, seed=53):
