@@ -779,29 +779,39 @@ void layer_forward(moe_ctx* ctx, const moe_layer_desc& D, const moe_layer_weight
         xin = ws.xnorm;
     }
 
-    // the gate also clears the counts route_count adds into
+    // the gate also clears the counts route_count adds into (none for one block)
     const int64_t nb = moe::ceil_div(D.T, moe::kPermTokens);
+    const bool one_block = moe::route_place_one_fits(D.T, D.E, D.k, D.router);
     ctx->launch("gate_logits", s, [&] {
         moe::launch_gate_logits(xin, weights.gate_w, ws.logits, D.T, D.d, D.E, D.contract, s,
-                                reinterpret_cast<uint32_t*>(ws.counts), D.E * nb);
+                                reinterpret_cast<uint32_t*>(ws.counts), one_block ? 0 : D.E * nb);
     });
-    // routing and the per-block expert counts: one launch
-    ctx->launch("route_count", s, [&] {
-        moe::launch_route_count(ws.logits, weights.expert_bias, D.T, D.E, D.k, D.router,
-                                D.quantum, D.tie_eps, idx, w, ws.counts, s);
-    });
-    if (D.E * nb <= moe::kPlaceScanMax) {
-        // the scan folded into the placement: one launch
-        ctx->launch("perm_place", s, [&] {
-            moe::launch_perm_place_scan(idx, D.T, D.k, D.E, ws.counts, ws.perm, ws.inv,
+    if (one_block) {
+        // one permutation block: routing, offsets and placement in one launch
+        ctx->launch("route_place", s, [&] {
+            moe::launch_route_place_one(ws.logits, weights.expert_bias, D.T, D.E, D.k, D.router,
+                                        D.quantum, D.tie_eps, idx, w, ws.perm, ws.inv,
                                         ws.offsets, s);
         });
     } else {
-        ctx->launch("perm_scan", s,
-                    [&] { moe::launch_perm_scan(ws.counts, nb, D.E, ws.offsets, s); });
-        ctx->launch("perm_place", s, [&] {
-            moe::launch_perm_place(idx, D.T, D.k, D.E, ws.counts, ws.perm, ws.inv, s);
+        // routing and the per-block expert counts: one launch
+        ctx->launch("route_count", s, [&] {
+            moe::launch_route_count(ws.logits, weights.expert_bias, D.T, D.E, D.k, D.router,
+                                    D.quantum, D.tie_eps, idx, w, ws.counts, s);
         });
+        if (D.E * nb <= moe::kPlaceScanMax) {
+            // the scan folded into the placement: one launch
+            ctx->launch("perm_place", s, [&] {
+                moe::launch_perm_place_scan(idx, D.T, D.k, D.E, ws.counts, ws.perm, ws.inv,
+                                            ws.offsets, s);
+            });
+        } else {
+            ctx->launch("perm_scan", s,
+                        [&] { moe::launch_perm_scan(ws.counts, nb, D.E, ws.offsets, s); });
+            ctx->launch("perm_place", s, [&] {
+                moe::launch_perm_place(idx, D.T, D.k, D.E, ws.counts, ws.perm, ws.inv, s);
+            });
+        }
     }
     expert_ffn(ctx, xin, ws.perm, ws.offsets, weights.w1, weights.w3, weights.w2, D.act, D.T, D.k,
                D.d, D.d_ff, D.E, ws.h, ws.out_rows, s, plan, ws.sk_part);

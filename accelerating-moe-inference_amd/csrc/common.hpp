@@ -205,6 +205,14 @@ void launch_route_count(const float* logits, const float* bias, int64_t T, int64
 void launch_perm_place_scan(const int32_t* idx, int64_t T, int64_t k, int64_t E,
                             const int32_t* counts, int32_t* perm, int32_t* inv,
                             int32_t* offsets, hipStream_t s);
+// A layer of one permutation block (T <= kPermTokens): the two launches
+// above as one (routing, offsets, perm and inv; no counts), where
+// route_place_one_fits says so.
+bool route_place_one_fits(int64_t T, int64_t E, int64_t k, int mode);
+void launch_route_place_one(const float* logits, const float* bias, int64_t T, int64_t E,
+                            int64_t k, int mode, float quantum, float tie_eps, int32_t* idx,
+                            float* w, int32_t* perm, int32_t* inv, int32_t* offsets,
+                            hipStream_t s);
 void launch_perm_count(const int32_t* idx, int64_t T, int64_t k, int64_t E,
                        int32_t* counts, hipStream_t s);
 void launch_perm_scan(int32_t* counts, int64_t nblocks, int64_t E,

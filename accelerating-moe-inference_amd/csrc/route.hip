@@ -854,6 +854,99 @@ __global__ __launch_bounds__(256) void perm_place_kernel(
 }
 
 
+
+// A layer whose tokens fill one permutation block (T <= kPermTokens): the
+// routing, the block's expert masks, the offsets and the placement in one
+// workgroup -- route_count_kernel and perm_place_scan_kernel as one launch,
+// each pick kept in LDS instead of passing through the block counts in
+// global memory.  The picks, weights, offsets and positions are those of the
+// two launches: position = the expert's offset + the rank of the token among
+// the expert's tokens (ascending token order, the reference's
+// assignments[e], src/layer.cu:86-92).  SOFTMAX_TOPK routes THREADS / G
+// tokens per round (the layer takes this path for at most two rounds).
+template <int MODE, int THREADS>
+__global__ __launch_bounds__(THREADS) void route_place_one_kernel(
+        const float* __restrict__ logits, const float* __restrict__ bias, int64_t T,
+        int64_t E, int64_t k, int G, float quantum, float tie_eps,
+        int32_t* __restrict__ idx, float* __restrict__ w, int32_t* __restrict__ perm,
+        int32_t* __restrict__ inv, int32_t* __restrict__ offsets) {
+    constexpr int NW = THREADS / 64;
+    __shared__ unsigned long long masks[kMaxExperts * 4];
+    __shared__ int32_t picks[kPermTokens * kMaxTopK];
+    __shared__ int32_t base[kMaxExperts];
+    __shared__ int32_t wave_sums[NW];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    for (int i = tid; i < E * 4; i += THREADS) masks[i] = 0ull;
+    __syncthreads();
+    // pick s of token t (t < kPermTokens): kept, and its token's bit set
+    auto mark = [&](int64_t t, int64_t s, int e) {
+        picks[t * k + s] = e;
+        if (e >= 0 && e < E) atomicOr(&masks[e * 4 + (t >> 6)], 1ull << (t & 63));
+    };
+    if (MODE == MOE_ROUTER_PHI_QUANT) {
+        for (int64_t t = tid; t < T; t += THREADS) {
+            int32_t p[kMaxTopK];
+            route_phi_token(logits + t * E, bias, E, k, quantum, tie_eps, idx + t * k,
+                            w + t * k, p);
+            for (int64_t s2 = 0; s2 < k; ++s2) mark(t, s2, p[s2]);
+        }
+    } else {
+        const int sub = lane & (G - 1);
+        const int per = THREADS / G;  // tokens per round
+        for (int64_t t0 = 0; t0 < T; t0 += per) {  // every lane calls the group routine
+            const int64_t t = t0 + tid / G;
+            const bool live = t < T;
+            const int64_t tt = live ? t : 0;
+            const int e = route_softmax_group(logits + tt * E, bias, E, k, G, sub, live,
+                                              idx + tt * k, w + tt * k);
+            if (live && sub < k) mark(t, sub, e);
+        }
+    }
+    __syncthreads();
+    // offsets: exclusive scan of the experts' pair counts, THREADS at a time
+    int32_t carry = 0;
+    for (int64_t e0 = 0; e0 < E; e0 += THREADS) {
+        const int64_t e = e0 + tid;
+        const int32_t v = e < E ? __popcll(masks[e * 4]) + __popcll(masks[e * 4 + 1]) +
+                                      __popcll(masks[e * 4 + 2]) + __popcll(masks[e * 4 + 3])
+                                : 0;
+        int32_t incl = v;
+        for (int off = 1; off < 64; off <<= 1) {
+            const int32_t o = __shfl_up(incl, off, 64);
+            if (lane >= off) incl += o;
+        }
+        if (lane == 63) wave_sums[wv] = incl;
+        __syncthreads();
+        int32_t pre = carry, chunk = 0;
+        for (int j = 0; j < NW; ++j) {
+            if (j < wv) pre += wave_sums[j];
+            chunk += wave_sums[j];
+        }
+        __syncthreads();
+        if (e < E) {
+            offsets[e] = pre + incl - v;
+            base[e] = pre + incl - v;
+        }
+        carry += chunk;
+    }
+    if (tid == 0) offsets[E] = carry;
+    __syncthreads();
+    for (int64_t i = tid; i < T * k; i += THREADS) {
+        const int64_t t = i / k;
+        const int e = picks[i];
+        if (e < 0 || e >= E) {
+            inv[i] = -1;
+            continue;
+        }
+        const int word = static_cast<int>(t >> 6);
+        int rank = __popcll(masks[e * 4 + word] & ((1ull << (t & 63)) - 1ull));
+        for (int q = 0; q < word; ++q) rank += __popcll(masks[e * 4 + q]);
+        const int32_t pos = base[e] + rank;
+        perm[pos] = static_cast<int32_t>(t);
+        inv[i] = pos;
+    }
+}
+
 // -------------------------------------------------------------- combine
 // One workgroup per token.  The token's slots are ordered by ascending
 // expert (ties by slot), then y = 0 + w*row, + w*row, ... in that order: the
@@ -1123,6 +1216,34 @@ void launch_perm_place_scan(const int32_t* idx, int64_t T, int64_t k, int64_t E,
     if (nb == 0) return;
     hipLaunchKernelGGL(perm_place_scan_kernel, dim3(static_cast<unsigned>(nb)), dim3(256), 0, s,
                        idx, T, k, E, counts, perm, inv, offsets);
+}
+
+bool route_place_one_fits(int64_t T, int64_t E, int64_t k, int mode) {
+    if (T <= 0 || T > kPermTokens || k < 1 || k > kMaxTopK || E < 1 || E > kMaxExperts)
+        return false;
+    if (mode == MOE_ROUTER_PHI_QUANT) return true;
+    // each round of the softmax router is one token per G-lane group; past two
+    // rounds the two-launch path's parallel workgroups are faster
+    int64_t G = 1;
+    while (G < E && G < 64) G <<= 1;
+    return T * G <= 2 * 1024;
+}
+
+void launch_route_place_one(const float* logits, const float* bias, int64_t T, int64_t E,
+                            int64_t k, int mode, float quantum, float tie_eps, int32_t* idx,
+                            float* w, int32_t* perm, int32_t* inv, int32_t* offsets,
+                            hipStream_t s) {
+    if (!route_place_one_fits(T, E, k, mode)) throw Unsupported("one-block routing shape");
+    int G = 1;
+    while (G < E && G < 64) G <<= 1;
+    if (mode == MOE_ROUTER_PHI_QUANT)
+        hipLaunchKernelGGL((route_place_one_kernel<MOE_ROUTER_PHI_QUANT, 256>), dim3(1), dim3(256),
+                           0, s, logits, bias, T, E, k, G, quantum, tie_eps, idx, w, perm, inv,
+                           offsets);
+    else
+        hipLaunchKernelGGL((route_place_one_kernel<MOE_ROUTER_SOFTMAX_TOPK, 1024>), dim3(1),
+                           dim3(1024), 0, s, logits, bias, T, E, k, G, quantum, tie_eps, idx, w,
+                           perm, inv, offsets);
 }
 
 void launch_perm_count(const int32_t* idx, int64_t T, int64_t k, int64_t E,

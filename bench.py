@@ -328,6 +328,8 @@ def hbm_kernel_rates(avg, T, d, E, k, block, w2_splits, floor_ms):
         # routing, block counts and their scan in one launch: logits read,
         # picks and weights written, counts written, scanned and offsets out
         "route_count": 4 * (T * E + E) + 8 * pairs + 12 * E * nb + 4 * (E + 1),
+        # one permutation block: routing, offsets and placement in one launch
+        "route_place": 4 * (T * E + E) + 8 * pairs + 8 * pairs + 4 * (E + 1),
         "layer_norm": 8 * T * d + 8 * T,
         "rms_norm": 8 * T * d + 4 * T,
         "combine": 4 * w2_splits * pairs * d + 12 * pairs + 4 * T * d * (2 if block else 1),

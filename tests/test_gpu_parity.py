@@ -389,17 +389,23 @@ def test_route_phi_hand_cases(ctx, torch, orc):
 # routes its tokens and adds its per-block expert counts into counters the
 # gate launch zeroed), then places the pairs with the scan of those counts
 # folded in (perm_place_scan; past kPlaceScanMax block counts, the separate
-# scan and placement).  Its routing, and through the outputs its offsets and
-# permutation, against the oracle: one token, a partial block, exactly one
-# block, a block plus one token, and 274 blocks; 1 to 1024 experts (softmax
-# groups of 1 to 64 lanes, 4 to 256 tokens per round), k up to 32; the Zipf
-# bias at E = 64.  Every case runs twice on the context: the second layer
-# must find the counters, which the first left filled in the reused
-# workspace, zeroed again by its own gate.
+# scan and placement).  A layer of one permutation block (up to 256 tokens;
+# for the softmax router at most two rounds of its lane groups) routes,
+# scans and places in a single launch (route_place_one) instead.  Its
+# routing, and through the outputs its offsets and permutation, against the
+# oracle: one token, a partial block, exactly one block, a block plus one
+# token, and 274 blocks; 1 to 1024 experts (softmax groups of 1 to 64 lanes,
+# 4 to 256 tokens per round), k up to 32; the Zipf bias at E = 64; the
+# one-block launch at 1, 16, 32, 100, 255 and 256 tokens with 1 to 1024
+# experts.  Every case runs twice on the context: the second layer must find
+# the counters, which the first left filled in the reused workspace, zeroed
+# again by its own gate.
 @pytest.mark.parametrize("T,E,k,mode", [(1, 4, 2, 1), (255, 8, 2, 1), (256, 16, 2, 0),
                                         (257, 64, 8, 1), (70000, 64, 8, 1), (70000, 16, 2, 0),
                                         (3001, 1, 1, 1), (1000, 100, 3, 0), (900, 1024, 32, 1),
-                                        (600, 1024, 4, 0), (513, 3, 3, 1)])
+                                        (600, 1024, 4, 0), (513, 3, 3, 1), (1, 1, 1, 0),
+                                        (100, 1024, 32, 0), (32, 64, 8, 1), (16, 1024, 4, 1),
+                                        (200, 5, 3, 0)])
 def test_layer_fused_routing_vs_oracle(ctx, pkg, torch, orc, T, E, k, mode):
     print(f"layer routing T={T} E={E} k={k} mode={mode}", flush=True)
     rng = np.random.default_rng(T + 7 * E + k)
