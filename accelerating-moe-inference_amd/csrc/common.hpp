@@ -38,10 +38,14 @@ constexpr int kNumXcd = 8;  // MI355X: 8 XCDs, workgroups dealt round-robin
 // Default GEMM raster group (m-tiles per n-sweep; 0 = every m-tile, i.e.
 // m-fastest): 8, so each XCD's ~64 resident workgroups cover about 8
 // m-tiles x 8 n-tiles and share every A and B panel 8 ways in its L2.
-// Measured best on MI355X for the grouped expert GEMMs at configs 3 and 5
-// and the reference's layer shape (config 4 is 1 % faster m-fastest), and
+// Measured best on MI355X for the grouped expert GEMMs at config 3, config
+// 5's w2 and the reference's layer shape (config 4 is 1 % faster m-fastest), and
 // for the large dense shapes (8192^3 NT 128 -> 136 TFLOP/s).
 constexpr int kGemmGroupM = 8;
+// ... and for the grouped w1/w3 launches with at most 1024 K columns: 4 (same box, three
+// runs each, config 5's layer 1.172 -> 1.164 ms, its K = 1024 w1/w3 1 % faster; the
+// reference's w2 at K = 448, tried with it, was level or 0.2 % slower and keeps 8)
+constexpr int kGemmGroupMShortK = 4;
 
 // The GEMM uses whose tile shape the host needs for grid sizing.
 // W2Narrow: the w2 GEMM on the 128x128 tile (GemmArgs::tile = 1 on the

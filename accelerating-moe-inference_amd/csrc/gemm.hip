@@ -2119,7 +2119,9 @@ void launch_gemm(const GemmArgs& args, bool nn, bool grouped, int epi, bool vec,
         const char* v = std::getenv("MOE_GEMM_GROUP_M");
         return v != nullptr ? std::atoi(v) : 0;
     }();
-    int group = env_group != 0 ? env_group : kGemmGroupM;
+    int group = env_group != 0
+                    ? env_group
+                    : (grouped && epi != EPI_STORE && a.K <= 1024 ? kGemmGroupMShortK : kGemmGroupM);
     if (group < 1 || group > a.m_tiles) group = a.m_tiles;
     a.group_m = group;
     if (a.k_splits <= 1) {
