@@ -2122,6 +2122,10 @@ void launch_gemm(const GemmArgs& args, bool nn, bool grouped, int epi, bool vec,
     int group = env_group != 0
                     ? env_group
                     : (grouped && epi != EPI_STORE && a.K <= 1024 ? kGemmGroupMShortK : kGemmGroupM);
+    // the grouped w2 over many experts: m-fastest (config 4's 64 experts, same box, w2
+    // per launch 5.57 -> 5.46 ms at 16,384 tokens, 1.61 -> 1.51 ms at 4,096, 0.59 -> 0.52 ms
+    // at 1,024, 0.38 -> 0.22 ms at 256; bit-identical; its w1/w3 measured level or slower)
+    if (env_group == 0 && grouped && epi == EPI_STORE && a.E >= 32) group = 0;
     if (group < 1 || group > a.m_tiles) group = a.m_tiles;
     a.group_m = group;
     if (a.k_splits <= 1) {
