@@ -349,11 +349,16 @@ W2SplitPlan choose_w2_split_plan(moe_ctx* ctx, int64_t pairs, int64_t d, int64_t
 // The w1/w3 tile: 128 rows x 128 columns of each operand, or, when d_ff is
 // a multiple of 64 but not of 128 (the reference's 448), 256 rows x 64
 // columns, so the n-tiles cover d_ff exactly instead of leaving the last one
-// half empty.  MOE_W13_TILE = 0 / 1 overrides.
-int choose_w13_tile(int64_t d_ff) {
+// half empty -- while the experts average more than 128 rows: with fewer the
+// 256-row tiles run mostly empty (same box, ms per layer, 256 x 64 -> 128 x
+// 128: the reference's layer at 256 / 512 / 1,024 tokens 0.290 / 0.333 / 0.398
+// -> 0.271-0.283 / 0.267 / 0.346; at 1,536 tokens, 192 rows per expert,
+// 0.435 -> 0.439, and level from 2,048 tokens up).
+// MOE_W13_TILE = 0 / 1 overrides.
+int choose_w13_tile(int64_t d_ff, int64_t pairs, int64_t E) {
     static const int env_tile = env_int("MOE_W13_TILE", -1);
     if (env_tile == 0 || env_tile == 1) return env_tile;
-    return (d_ff % 128 != 0 && d_ff % 64 == 0) ? 1 : 0;
+    return (d_ff % 128 != 0 && d_ff % 64 == 0 && pairs > 128 * E) ? 1 : 0;
 }
 
 // Expected real m-tiles of a grouped launch: ceil(pairs / BM) plus half a
@@ -513,7 +518,7 @@ FfnPlan choose_ffn_plan(moe_ctx* ctx, int64_t pairs, int64_t d, int64_t d_ff, in
     const bool tile_pinned = env_tile == 0 || env_tile == 1;
     f.tile = moe::ceil_div(d, moe::gemm_tile(moe::GemmUse::W2).bn) <= 4 ? 1 : 0;
     if (tile_pinned) f.tile = env_tile;
-    f.w13_tile = choose_w13_tile(d_ff);
+    f.w13_tile = choose_w13_tile(d_ff, pairs, E);
     if (d_ff == 0 || d == 0) {
         f.splits = 1;
         return f;
